@@ -1,0 +1,185 @@
+/**
+ * vitna_hip.h - The engine's GPU forward-step interface, served on an AMD
+ * Instinct MI355X (gfx950) by libvitna_hip.so.
+ *
+ * The first part restates engine/include/model_cuda.h (the `vitna_cuda_*`
+ * C ABI that engine/src/model.c calls under VITNA_CUDA) with the same names,
+ * argument meanings and error convention, so model.c links against this
+ * library unchanged: every call returns false (or 0) and writes a sentence
+ * into err[err_len] when it cannot do what was asked; the caller then asks
+ * vitna_cuda_lost whether the device can still be used. Each declaration
+ * cites the line of model_cuda.h it replaces.
+ *
+ * Differences of behaviour, each deliberate:
+ *  - every expert of every layer is resident in device memory (288 GB of HBM
+ *    holds the largest configuration several times over), so
+ *    expert_cache_bytes and the guess arguments are accepted and unused, and
+ *    vitna_cuda_cpu_experts (a PCIe workaround) is refused;
+ *  - the dense-model entry points (vitna_cuda_step, _steps, _rows) refuse, as
+ *    the reference's refuse a mixture of experts; this library serves the
+ *    mixture-of-experts path only.
+ *
+ * The second part (vitna_hip_*) has no counterpart in the reference: a
+ * device-resident decode step that routes on the GPU (no host round trip per
+ * layer), single-layer entry points for benchmarking one MoE FFN, the grouped
+ * prefill of one MoE layer, and key-value cache access for tests.
+ */
+
+#ifndef VITNA_HIP_H
+#define VITNA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <stdbool.h>
+#include "vitna_model.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* model_cuda.h:21-25 */
+typedef struct {
+    int32_t token;
+    int32_t pos;
+    int32_t seq;
+} vitna_cuda_row_t;
+
+/* model_cuda.h:31-36 */
+typedef struct {
+    char name[128];
+    size_t total_bytes;
+    size_t free_bytes;
+    int major, minor;
+} vitna_cuda_device_t;
+
+/* model_cuda.h:28 */
+bool vitna_cuda_probe(char* err, size_t err_len);
+/* model_cuda.h:39 */
+int vitna_cuda_devices(vitna_cuda_device_t* out, int max);
+/* model_cuda.h:56-57 */
+struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, const float* cos_tab, const float* sin_tab, size_t expert_cache_bytes,
+                                           char* err, size_t err_len);
+/* model_cuda.h:77-78 */
+bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, size_t layer, float* logits, float* next,
+                          char* err, size_t err_len);
+/* model_cuda.h:90-91 */
+bool vitna_cuda_moe_experts(struct vitna_cuda_model* g, size_t layer, const int32_t* ids, const float* weights, size_t k,
+                            const int32_t* guess, char* err, size_t err_len);
+/* model_cuda.h:94 */
+bool vitna_cuda_moe_head(struct vitna_cuda_model* g, float* logits, char* err, size_t err_len);
+/* model_cuda.h:97 */
+const char* vitna_cuda_moe_report(const struct vitna_cuda_model* g, char* buf, size_t len);
+/* model_cuda.h:100 */
+int vitna_cuda_kv_layers(const struct vitna_cuda_model* g);
+/* model_cuda.h:103 */
+void vitna_cuda_test_long_from(struct vitna_cuda_model* g, size_t n);
+/* model_cuda.h:106 */
+void vitna_cuda_test_fast_rows(struct vitna_cuda_model* g, size_t n);
+/* model_cuda.h:121 */
+bool vitna_cuda_cpu_experts(struct vitna_cuda_model* g, size_t threads, char* err, size_t err_len);
+/* model_cuda.h:136 */
+size_t vitna_cuda_moe_rows_max(const struct vitna_cuda_model* g);
+/* model_cuda.h:145-146 */
+bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, size_t layer, float* logits, float* next,
+                               char* err, size_t err_len);
+/* model_cuda.h:157-158 */
+bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t layer, size_t n, const int32_t* ids, const float* weights, size_t k,
+                                 const int32_t* guess, char* err, size_t err_len);
+/* model_cuda.h:161 */
+bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, float* const* logits, char* err, size_t err_len);
+/* model_cuda.h:169 */
+bool vitna_cuda_step(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, float* logits, char* err, size_t err_len);
+/* model_cuda.h:175 */
+size_t vitna_cuda_prompt_min(const struct vitna_cuda_model* g);
+/* model_cuda.h:183 */
+size_t vitna_cuda_prompt_piece_min(const struct vitna_cuda_model* g);
+/* model_cuda.h:190 */
+size_t vitna_cuda_exact_max(const struct vitna_cuda_model* g);
+/* model_cuda.h:201-202 */
+bool vitna_cuda_rows(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t count, float* const* logits, char* err,
+                     size_t err_len);
+/* model_cuda.h:213-214 */
+bool vitna_cuda_steps(struct vitna_cuda_model* g, size_t seq, const int32_t* tokens, size_t count, size_t pos, float* logits, size_t rows,
+                      char* err, size_t err_len);
+/* model_cuda.h:217 */
+const char* vitna_cuda_device_name(const struct vitna_cuda_model* g);
+/* model_cuda.h:220 */
+void vitna_cuda_wait(struct vitna_cuda_model* g);
+/* model_cuda.h:231 */
+bool vitna_cuda_lost(struct vitna_cuda_model* g, char* err, size_t err_len);
+/* model_cuda.h:233 */
+void vitna_cuda_free(struct vitna_cuda_model* g);
+/* model_cuda.h:244 */
+bool vitna_cuda_widen(const vitna_matrix_t* m, float* out, char* err, size_t err_len);
+/* model_cuda.h:254-255 */
+bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_matrix_t* up, const vitna_matrix_t* down, const float* norm_w,
+                             const float* x, float eps, float* xs, float* act, float* y, char* err, size_t err_len);
+
+/* ---------------------------------------------------------------------------
+ * Extensions (no counterpart in the reference's interface).
+ * ------------------------------------------------------------------------- */
+
+/** One whole decode step of the token at position pos of sequence seq on the
+    device, routing included (the reference's router, top-k and weights,
+    engine/src/model.c:626-703, computed on the GPU, bit-exact in the expert
+    choice): embedding, every layer, the head. Vocab logits to logits unless
+    NULL. The steps are captured once into a HIP graph and replayed. */
+bool vitna_hip_moe_step(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, float* logits, char* err, size_t err_len);
+
+/** Device-resident step as vitna_hip_moe_step, enqueued without waiting and
+    with the logits left on the device (vitna_hip_logits_device). For
+    throughput measurement. */
+bool vitna_hip_moe_step_async(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, char* err, size_t err_len);
+
+/** The mixture-of-experts half of layer (RMSNorm, router, top-k on the
+    device, experts, weighted sum) on residual row 0, in place, enqueued. */
+bool vitna_hip_moe_ffn(struct vitna_cuda_model* g, size_t layer, char* err, size_t err_len);
+
+/** Residual row row (hidden floats) from or to the host, synchronously. */
+bool vitna_hip_residual(struct vitna_cuda_model* g, size_t row, float* host, bool to_device, char* err, size_t err_len);
+
+/** The latest routing of row row: router logits (n_experts), the choice
+    largest first (K), the experts in order of id (K) and their weights (K).
+    Any pointer may be NULL. Synchronous. */
+bool vitna_hip_routing(struct vitna_cuda_model* g, size_t row, float* logits, int32_t* chosen, int32_t* ids, float* weights, char* err,
+                       size_t err_len);
+
+/** Keys and values of positions pos0 .. pos0 + n - 1 of one layer of one
+    sequence, n x (n_kv_heads * head_dim) each, to (write) or from the device. */
+bool vitna_hip_kv(struct vitna_cuda_model* g, size_t seq, size_t layer, size_t pos0, size_t n, float* k, float* v, bool write, char* err,
+                  size_t err_len);
+
+/** Fill every sequence's cache, every layer, positions 0 .. n_pos[seq] - 1,
+    with seeded N(0, 1) values generated on the device. */
+bool vitna_hip_kv_fill(struct vitna_cuda_model* g, uint64_t seed, const size_t* n_pos, char* err, size_t err_len);
+
+/** Wait for the model's stream; false, with the reason, on a device error. */
+bool vitna_hip_sync(struct vitna_cuda_model* g, char* err, size_t err_len);
+
+/** The HIP stream every kernel of the model runs on (a hipStream_t). */
+void* vitna_hip_stream(struct vitna_cuda_model* g);
+
+/** Device pointer of the vocab logits of row 0 of the last head. */
+const float* vitna_hip_logits_device(struct vitna_cuda_model* g);
+
+/** Prefill of n tokens through the mixture-of-experts half of layer: x is
+    n x hidden on the host; each row is normalized, routed (bit-exact expert
+    choice), run through its experts as a grouped bf16 MFMA GEMM with fp32
+    accumulation, and its weighted sum added to it in place. */
+bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, char* err, size_t err_len);
+
+/** Average duration in microseconds of one launch of a kernel of the decode
+    path, timed with HIP events on the model's stream over reps launches
+    after warmup launches: which = 0 experts gate/up, 1 experts down, 2 router,
+    3 attention projections q/k/v, 4 attention, 5 o-projection, 6 LM head.
+    The layer advances with each launch (layer i % n_layers), so a working
+    set larger than the last-level cache is streamed. Also reports the
+    algorithmic bytes one launch reads and writes. */
+bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int reps, int warmup, double* avg_us, double* bytes, char* err,
+                           size_t err_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,124 @@
+"""The drop-in boundary, checked without a GPU.
+
+* include/vitna_model.h lays out the engine's structs exactly as the
+  reference's model.h does (offsets recorded from the reference's own header
+  by tests/golden/make_golden.py into ref_layout.json), and the ctypes mirror
+  in vitna_amd agrees with both.
+* libvitna_hip.so loads and exports every function include/vitna_hip.h
+  declares.
+* The host-side refusals the reference makes are made (no compute call runs
+  without a GPU).
+"""
+import ctypes as C
+import json
+import os
+import re
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+import vitna_amd as va
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys_path = os.path.join(ROOT, "tests", "golden")
+
+
+def probe_ours():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("make_golden", os.path.join(ROOT, "tests", "golden", "make_golden.py"))
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    return mg.probe_layout(os.path.join(ROOT, "include", "vitna_model.h"), [])
+
+
+def test_struct_layout_matches_reference():
+    with open(os.path.join(ROOT, "tests", "golden", "ref_layout.json")) as f:
+        ref = json.load(f)
+    ours = probe_ours()
+    assert ours == ref
+
+
+def test_ctypes_mirror_matches_reference():
+    with open(os.path.join(ROOT, "tests", "golden", "ref_layout.json")) as f:
+        ref = json.load(f)
+    mirror = {"vitna_llama_config_t": va.Config, "vitna_matrix_t": va.Matrix, "vitna_expert_t": va.Expert,
+              "vitna_llama_layer_t": va.Layer, "vitna_llama_t": va.Llama}
+    for name, cls in mirror.items():
+        assert C.sizeof(cls) == ref[name]["sizeof"], name
+        for field, off in ref[name].items():
+            if field != "sizeof":
+                assert getattr(cls, field).offset == off, (name, field)
+
+
+def declared_functions():
+    with open(os.path.join(ROOT, "include", "vitna_hip.h")) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vitna_(?:cuda|hip)_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    assert os.path.exists(va.HIP_LIB), "build first: python vitna-anchor_amd/build.py"
+    names = declared_functions()
+    assert len(names) >= 39
+    out = subprocess.run(["nm", "-D", "--defined-only", va.HIP_LIB], capture_output=True, text=True, check=True).stdout
+    exported = set(line.split()[-1] for line in out.splitlines() if " T " in line)
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    lib = va.hip()
+    for n in names:
+        assert getattr(lib, n) is not None
+
+
+def test_library_is_gfx950():
+    out = subprocess.run(["/opt/rocm/bin/roc-obj-ls", va.HIP_LIB], capture_output=True, text=True)
+    if out.returncode != 0:
+        pytest.skip("roc-obj-ls unavailable")
+    assert "gfx950" in out.stdout
+
+
+def test_dense_entry_points_refuse():
+    lib = va.hip()
+    err = C.create_string_buffer(256)
+    lib.vitna_cuda_step.restype = C.c_bool
+    assert not lib.vitna_cuda_step(None, 0, 0, 0, None, err, 256)
+    assert b"mixture of experts" in err.value
+    lib.vitna_cuda_cpu_experts.restype = C.c_bool
+    assert not lib.vitna_cuda_cpu_experts(None, 4, err, 256)
+    lib.vitna_cuda_prompt_min.restype = C.c_size_t
+    assert lib.vitna_cuda_prompt_min(None) == 2 ** 64 - 1
+
+
+def test_create_refuses_bad_shapes_before_touching_a_device():
+    """check_shapes runs before any HIP call: a dense model, and an expert width the kernels do not take."""
+    lib = va.hip()
+    m = va.Model(va.shape(n_layers=1, hidden=256, intermediate=256, n_experts=8, n_experts_used=2, attention=0,
+                          dt_gate_up=va.Q8_0, dt_down=va.Q8_0), 1)
+    try:
+        err = C.create_string_buffer(256)
+        m.m.cfg.n_experts = 0
+        assert not lib.vitna_cuda_create(m.ptr, None, None, 0, err, 256)
+        assert b"dense" in err.value
+        m.m.cfg.n_experts = 8
+        m.m.layers[0].router.dtype = va.F16
+        assert not lib.vitna_cuda_create(m.ptr, None, None, 0, err, 256)
+        assert b"router must be F32" in err.value
+        m.m.layers[0].router.dtype = va.F32
+        m.m.layers[0].experts[3].down.dtype = va.Q4_K
+        assert not lib.vitna_cuda_create(m.ptr, None, None, 0, err, 256)
+        assert b"share a dtype" in err.value
+    finally:
+        m.m.layers[0].experts[3].down.dtype = va.Q8_0
+        m.free()
+
+
+def test_probe_without_gpu_says_why():
+    import torch
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is present")
+    lib = va.hip()
+    err = C.create_string_buffer(256)
+    assert not lib.vitna_cuda_probe(err, 256)
+    assert err.value

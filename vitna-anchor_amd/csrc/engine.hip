@@ -1,0 +1,977 @@
+/**
+ * engine.hip - libvitna_hip's host side: the vitna_cuda_* C ABI of
+ * engine/include/model_cuda.h (the reference's boundary, model_cuda.cu
+ * :3537-5536) over HIP on one MI355X, and the vitna_hip_* extensions.
+ *
+ * Upload (vitna_cuda_create, reference model_cuda.cu:3761): shapes are
+ * checked first (check_shapes, reference :3558), then every weight goes to the
+ * device once: GGUF blocks are copied to a staging buffer and split into
+ * planes (vitna_hip_internal.h) by repack_kernel; every expert of every layer
+ * is resident, one allocation a layer. The key-value cache is
+ * [seq][layer][ctx][n_kv * head_dim] float32, as the reference's.
+ *
+ * Every kernel runs on one stream. A device-routed decode step
+ * (vitna_hip_moe_step) is captured once into a HIP graph; its token, position
+ * and sequence live in device memory (rows_dev[0]) and are copied in before
+ * each replay, so one graph serves every position.
+ */
+
+#include "vitna_kernels.h"
+#include "../../include/vitna_hip.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+#include <algorithm>
+
+#define ROWS_MAX 256
+
+struct dlayer {
+    qmat q, k, v, o;
+    float *attn_norm, *mlp_norm, *q_norm, *k_norm;
+    float* router;
+    qmat gate, up, down;
+};
+
+struct vitna_cuda_model {
+    int device;
+    char name[320];
+    hipStream_t stream;
+    const vitna_llama_t* m;
+    int H, I, E, K, NL, nh, nkv, hd, V, ctx, seqs, renorm, attention;
+    float eps;
+    std::vector<void*> allocs;
+    std::vector<dlayer> L;
+    qmat embed, head;
+    float* final_norm;
+    float *cos_tab, *sin_tab, *k_cache, *v_cache;
+    size_t layer_kv;  /* floats of one (sequence, layer) cache */
+    int splits_max;
+    /* scratch, ROWS_MAX rows */
+    float *x, *xn, *q, *k, *v, *qp, *att, *act, *ypart, *rlogits, *vocab, *partial;
+    route_out* rt;
+    unsigned *route_ctr, *attn_ctr;
+    row_rec* rows_dev;
+    row_rec* rows_host; /* pinned */
+    hipEvent_t rows_copied;
+    float* h_logits;    /* pinned, 2 * ROWS_MAX * E */
+    hipGraphExec_t step_graph;
+    bool graph_ready;
+    bool lost;
+    size_t fast_rows, long_from;
+    int rows_n;         /* rows of the pass in flight (vitna_cuda_moe_rows_*) */
+};
+
+static bool fail(char* err, size_t len, const char* fmt, ...) {
+    if (err && len) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(err, len, fmt, ap);
+        va_end(ap);
+    }
+    return false;
+}
+
+static bool fail_hip(char* err, size_t len, const char* what, hipError_t e) {
+    return fail(err, len, "%s: %s (%s)", what, hipGetErrorString(e), hipGetErrorName(e));
+}
+
+#define HIP_TRY(call, what)                                          \
+    do {                                                             \
+        hipError_t e_ = (call);                                      \
+        if (e_ != hipSuccess) return fail_hip(err, err_len, what, e_); \
+    } while (0)
+
+static const char* dtype_name(int t) {
+    switch (t) {
+        case VITNA_DTYPE_F32: return "F32";
+        case VITNA_DTYPE_F16: return "F16";
+        case VITNA_DTYPE_BF16: return "BF16";
+        case VITNA_DTYPE_Q8_0: return "Q8_0";
+        case VITNA_DTYPE_Q2_K: return "Q2_K";
+        case VITNA_DTYPE_Q3_K: return "Q3_K";
+        case VITNA_DTYPE_Q4_K: return "Q4_K";
+        case VITNA_DTYPE_Q5_K: return "Q5_K";
+        case VITNA_DTYPE_Q6_K: return "Q6_K";
+        default: return "an unsupported dtype";
+    }
+}
+
+static bool quant_ok(int t) { return t == VITNA_DTYPE_Q8_0 || t == VITNA_DTYPE_Q4_K || t == VITNA_DTYPE_Q6_K; }
+
+/* widths the GEMV kernels are built for: 32 * {4, 8, ..., 256} */
+static bool width_ok(size_t cols) {
+    const size_t s = cols / 32;
+    return cols % 32 == 0 && (s == 4 || s == 8 || s == 16 || s == 32 || s == 64 || s == 128 || s == 256);
+}
+
+static bool matrix_ok(const vitna_matrix_t* w, size_t rows, size_t cols, const char* what, char* err, size_t err_len) {
+    if (!w->data) return fail(err, err_len, "%s has no data", what);
+    if (w->rows != rows || w->cols != cols)
+        return fail(err, err_len, "%s is %zu x %zu where %zu x %zu is needed", what, w->rows, w->cols, rows, cols);
+    if (!quant_ok(w->dtype))
+        return fail(err, err_len, "%s is %s; this device path reads Q8_0, Q4_K and Q6_K", what, dtype_name(w->dtype));
+    if (!vitna_matrix_row_bytes(w->dtype, cols)) return fail(err, err_len, "%s: %zu columns are not whole %s blocks", what, cols, dtype_name(w->dtype));
+    if (!width_ok(cols)) return fail(err, err_len, "%s: width %zu is not one the kernels take (32 x 4 .. 256, powers of two)", what, cols);
+    return true;
+}
+
+/* The reference's check_shapes (model_cuda.cu:3558), for what these kernels assume. */
+static bool check_shapes(const vitna_llama_t* m, char* err, size_t err_len) {
+    const vitna_llama_config_t* c = &m->cfg;
+    if (!c->n_experts) return fail(err, err_len, "this device path serves a mixture of experts, and the model is dense");
+    if (c->n_experts > ROUTE_E_MAX) return fail(err, err_len, "%zu experts; at most %d are routed on the device", c->n_experts, ROUTE_E_MAX);
+    if (c->n_experts_used < 1 || c->n_experts_used > ROUTE_K_MAX || c->n_experts_used > c->n_experts)
+        return fail(err, err_len, "%zu experts a token; 1 to %d, and no more than the experts, are supported", c->n_experts_used, ROUTE_K_MAX);
+    if (c->hidden % 256 || c->hidden > 8192) return fail(err, err_len, "hidden width %zu: a multiple of 256, at most 8192, is needed", c->hidden);
+    const size_t S = c->intermediate / 32;
+    if (c->intermediate % 256 || (c->n_experts_used * S + 63) / 64 > 8 || (c->n_experts_used * S + 63) / 64 == 7)
+        return fail(err, err_len, "expert width %zu with %zu experts a token is not a shape the down kernel takes", c->intermediate,
+                    c->n_experts_used);
+    if (!m->ctx || !m->seqs) return fail(err, err_len, "the model has no key-value cache shape (ctx %zu, seqs %zu)", m->ctx, m->seqs);
+    char what[96];
+    for (size_t l = 0; l < c->n_layers; l++) {
+        const vitna_llama_layer_t* L = &m->layers[l];
+        if (!L->mlp_norm) return fail(err, err_len, "layer %zu has no MLP norm", l);
+        if (!L->router.data || L->router.dtype != VITNA_DTYPE_F32 || L->router.rows != c->n_experts || L->router.cols != c->hidden)
+            return fail(err, err_len, "layer %zu: the router must be F32, %zu x %zu", l, c->n_experts, c->hidden);
+        if (!L->experts) return fail(err, err_len, "layer %zu has no experts", l);
+        const int gdt = L->experts[0].gate.dtype, ddt = L->experts[0].down.dtype;
+        for (size_t e = 0; e < c->n_experts; e++) {
+            const vitna_expert_t* x = &L->experts[e];
+            snprintf(what, sizeof(what), "layer %zu expert %zu gate", l, e);
+            if (!matrix_ok(&x->gate, c->intermediate, c->hidden, what, err, err_len)) return false;
+            snprintf(what, sizeof(what), "layer %zu expert %zu up", l, e);
+            if (!matrix_ok(&x->up, c->intermediate, c->hidden, what, err, err_len)) return false;
+            snprintf(what, sizeof(what), "layer %zu expert %zu down", l, e);
+            if (!matrix_ok(&x->down, c->hidden, c->intermediate, what, err, err_len)) return false;
+            if (x->gate.dtype != gdt || x->up.dtype != gdt || x->down.dtype != ddt)
+                return fail(err, err_len, "layer %zu: every expert's gate and up, and every expert's down, must share a dtype", l);
+        }
+        if (c->n_heads) {
+            const size_t qd = c->n_heads * c->head_dim, kd = c->n_kv_heads * c->head_dim;
+            snprintf(what, sizeof(what), "layer %zu q", l);
+            if (!matrix_ok(&L->q, qd, c->hidden, what, err, err_len)) return false;
+            snprintf(what, sizeof(what), "layer %zu k", l);
+            if (!matrix_ok(&L->k, kd, c->hidden, what, err, err_len)) return false;
+            snprintf(what, sizeof(what), "layer %zu v", l);
+            if (!matrix_ok(&L->v, kd, c->hidden, what, err, err_len)) return false;
+            snprintf(what, sizeof(what), "layer %zu o", l);
+            if (!matrix_ok(&L->o, c->hidden, qd, what, err, err_len)) return false;
+            if (!L->attn_norm) return fail(err, err_len, "layer %zu has no attention norm", l);
+            if (c->qk_norm && (!c->qk_norm_per_head || !L->q_norm || !L->k_norm))
+                return fail(err, err_len, "layer %zu: only the per-head QK-norm (Qwen3) is served on the device", l);
+        }
+    }
+    if (c->n_heads) {
+        if (c->head_dim != 64 && c->head_dim != 128) return fail(err, err_len, "head width %zu: 64 or 128 is needed", c->head_dim);
+        if (c->n_heads % c->n_kv_heads || c->n_heads / c->n_kv_heads > 8)
+            return fail(err, err_len, "%zu query heads over %zu key-value heads: at most 8 a group", c->n_heads, c->n_kv_heads);
+        if (!matrix_ok(&m->embed, c->vocab, c->hidden, "the embedding", err, err_len)) return false;
+        if (!matrix_ok(&m->lm_head, c->vocab, c->hidden, "the output projection", err, err_len)) return false;
+        if (!m->final_norm) return fail(err, err_len, "the model has no final norm");
+    }
+    return true;
+}
+
+template <typename T>
+static bool dalloc(vitna_cuda_model* g, T** p, size_t bytes, const char* what, char* err, size_t err_len) {
+    void* q = nullptr;
+    const hipError_t e = hipMalloc(&q, bytes ? bytes : 256);
+    if (e != hipSuccess) return fail(err, err_len, "device memory for %s (%zu bytes): %s", what, bytes, hipGetErrorString(e));
+    g->allocs.push_back(q);
+    *p = (T*)q;
+    return true;
+}
+
+/* Planes of n matrices (experts) of one shape, back to back: qmat over the
+   first, estride from one to the next. */
+static size_t set_bytes(int dtype, size_t rows, size_t cols, size_t n) {
+    size_t t = 0;
+    for (int i = 0; i < 4; i++) t += align256(n * plane_bytes(dtype, i, rows, cols));
+    return t;
+}
+
+static qmat place(uint8_t* base, int dtype, size_t rows, size_t cols, size_t n) {
+    qmat q;
+    memset(&q, 0, sizeof(q));
+    size_t off = 0;
+    for (int i = 0; i < 4; i++) {
+        const size_t pb = plane_bytes(dtype, i, rows, cols);
+        q.p[i] = pb ? base + off : nullptr;
+        q.estride[i] = pb;
+        off += align256(n * pb);
+    }
+    q.rows = (int)rows;
+    q.cols = (int)cols;
+    q.nb = (int)(cols / (dtype == VITNA_DTYPE_Q8_0 ? 32 : 256));
+    q.dtype = dtype;
+    return q;
+}
+
+/* n host matrices of one shape into planes at q (experts e0..): each copied to
+   staging, then one repack over all of them. */
+static bool upload_set(vitna_cuda_model* g, const vitna_matrix_t* const* mats, size_t n, const qmat& q, uint8_t* staging,
+                       size_t staging_bytes, char* err, size_t err_len) {
+    const size_t rb = vitna_matrix_row_bytes(mats[0]->dtype, mats[0]->cols), mb = rb * mats[0]->rows;
+    const size_t per = staging_bytes / mb;
+    if (per == 0) return fail(err, err_len, "internal: staging buffer too small");
+    for (size_t e0 = 0; e0 < n; e0 += per) {
+        const size_t cnt = std::min(per, n - e0);
+        for (size_t e = 0; e < cnt; e++)
+            HIP_TRY(hipMemcpyAsync(staging + e * mb, mats[e0 + e]->data, mb, hipMemcpyHostToDevice, g->stream), "copying weights to the device");
+        qmat part = q;
+        for (int i = 0; i < 4; i++)
+            if (part.p[i]) part.p[i] += e0 * q.estride[i];
+        part.rows = (int)(cnt * mats[0]->rows);
+        HIP_TRY(launch_repack(staging, part, g->stream), "splitting blocks into planes");
+        HIP_TRY(hipStreamSynchronize(g->stream), "uploading weights");
+    }
+    return true;
+}
+
+static bool upload_f32(vitna_cuda_model* g, float** out, const float* host, size_t n, const char* what, char* err, size_t err_len) {
+    if (!dalloc(g, out, n * 4, what, err, err_len)) return false;
+    HIP_TRY(hipMemcpy(*out, host, n * 4, hipMemcpyHostToDevice), what);
+    return true;
+}
+
+static bool upload_matrix(vitna_cuda_model* g, qmat* out, const vitna_matrix_t* w, uint8_t* staging, size_t staging_bytes, const char* what,
+                          char* err, size_t err_len) {
+    uint8_t* mem;
+    if (!dalloc(g, &mem, set_bytes(w->dtype, w->rows, w->cols, 1), what, err, err_len)) return false;
+    *out = place(mem, w->dtype, w->rows, w->cols, 1);
+    const vitna_matrix_t* one[1] = {w};
+    return upload_set(g, one, 1, *out, staging, staging_bytes, err, err_len);
+}
+
+extern "C" bool vitna_cuda_probe(char* err, size_t err_len) {
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return fail_hip(err, err_len, "the HIP runtime finds no device", e);
+    if (n < 1) return fail(err, err_len, "the HIP runtime finds no device");
+    return true;
+}
+
+extern "C" int vitna_cuda_devices(vitna_cuda_device_t* out, int max) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    int k = 0;
+    for (int d = 0; d < n && k < max; d++) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, d) != hipSuccess) continue;
+        vitna_cuda_device_t* o = &out[k++];
+        memset(o, 0, sizeof(*o));
+        snprintf(o->name, sizeof(o->name), "%s (%s)", p.name, p.gcnArchName);
+        o->total_bytes = p.totalGlobalMem;
+        size_t fr = 0, tot = 0;
+        if (hipSetDevice(d) == hipSuccess && hipMemGetInfo(&fr, &tot) == hipSuccess) o->free_bytes = fr;
+        o->major = p.major;
+        o->minor = p.minor;
+    }
+    return k;
+}
+
+extern "C" void vitna_cuda_free(struct vitna_cuda_model* g) {
+    if (!g) return;
+    hipSetDevice(g->device);
+    if (g->stream) hipStreamSynchronize(g->stream);
+    if (g->graph_ready) hipGraphExecDestroy(g->step_graph);
+    for (void* p : g->allocs) hipFree(p);
+    if (g->rows_host) hipHostFree(g->rows_host);
+    if (g->h_logits) hipHostFree(g->h_logits);
+    if (g->rows_copied) hipEventDestroy(g->rows_copied);
+    if (g->stream) hipStreamDestroy(g->stream);
+    delete g;
+}
+
+extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, const float* cos_tab, const float* sin_tab,
+                                                      size_t expert_cache_bytes, char* err, size_t err_len) {
+    (void)expert_cache_bytes;
+    if (!m) { fail(err, err_len, "no model"); return nullptr; }
+    if (!check_shapes(m, err, err_len)) return nullptr;
+    const vitna_llama_config_t* c = &m->cfg;
+    if (c->n_heads && (!cos_tab || !sin_tab)) { fail(err, err_len, "the rotary tables are missing"); return nullptr; }
+    if (!vitna_cuda_probe(err, err_len)) return nullptr;
+    vitna_cuda_model* g = new vitna_cuda_model(); /* value-initialized: every plain member zero */
+    g->device = 0;
+    g->m = m;
+    g->H = (int)c->hidden; g->I = (int)c->intermediate; g->E = (int)c->n_experts; g->K = (int)c->n_experts_used;
+    g->NL = (int)c->n_layers; g->nh = (int)c->n_heads; g->nkv = (int)c->n_kv_heads; g->hd = (int)c->head_dim;
+    g->V = (int)c->vocab; g->ctx = (int)m->ctx; g->seqs = (int)m->seqs; g->renorm = c->renormalize; g->attention = c->n_heads != 0;
+    g->eps = c->rms_eps;
+    g->fast_rows = 64;
+    g->long_from = 1024;
+    g->embed = {}; g->head = {};
+    g->final_norm = nullptr;
+    g->graph_ready = false;
+    g->lost = false;
+    g->rows_n = 0;
+    auto bail = [&]() -> vitna_cuda_model* { vitna_cuda_free(g); return nullptr; };
+    if (hipSetDevice(0) != hipSuccess) { fail(err, err_len, "cannot select device 0"); return bail(); }
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, 0) == hipSuccess) snprintf(g->name, sizeof(g->name), "%s (%s)", p.name, p.gcnArchName);
+    if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess) { fail(err, err_len, "cannot create a stream"); return bail(); }
+    if (hipEventCreateWithFlags(&g->rows_copied, hipEventDisableTiming) != hipSuccess) { fail(err, err_len, "cannot create an event"); return bail(); }
+
+    /* staging for the largest set of one layer's experts of one part */
+    const vitna_llama_layer_t* L0 = &m->layers[0];
+    size_t staging_bytes = 64u << 20;
+    for (size_t l = 0; l < c->n_layers; l++) {
+        const vitna_expert_t* x = &m->layers[l].experts[0];
+        const size_t gb = vitna_matrix_row_bytes(x->gate.dtype, x->gate.cols) * x->gate.rows;
+        const size_t db = vitna_matrix_row_bytes(x->down.dtype, x->down.cols) * x->down.rows;
+        staging_bytes = std::max(staging_bytes, std::max(gb, db) * 16);
+    }
+    if (g->attention) {
+        staging_bytes = std::max(staging_bytes, vitna_matrix_row_bytes(m->lm_head.dtype, m->lm_head.cols) * m->lm_head.rows);
+        staging_bytes = std::max(staging_bytes, vitna_matrix_row_bytes(m->embed.dtype, m->embed.cols) * m->embed.rows);
+    }
+    (void)L0;
+    uint8_t* staging = nullptr;
+    if (hipMalloc(&staging, staging_bytes) != hipSuccess) { fail(err, err_len, "device memory for staging (%zu bytes)", staging_bytes); return bail(); }
+    bool ok = true;
+    g->L.resize(c->n_layers);
+    std::vector<const vitna_matrix_t*> mats(c->n_experts);
+    for (size_t l = 0; ok && l < c->n_layers; l++) {
+        const vitna_llama_layer_t* L = &m->layers[l];
+        dlayer& d = g->L[l];
+        memset(&d, 0, sizeof(d));
+        ok = upload_f32(g, &d.mlp_norm, L->mlp_norm, c->hidden, "the MLP norm", err, err_len) &&
+             upload_f32(g, &d.router, (const float*)L->router.data, c->n_experts * c->hidden, "the router", err, err_len);
+        const vitna_expert_t* x0 = &L->experts[0];
+        const size_t E = c->n_experts;
+        const size_t gbytes = set_bytes(x0->gate.dtype, x0->gate.rows, x0->gate.cols, E);
+        const size_t dbytes = set_bytes(x0->down.dtype, x0->down.rows, x0->down.cols, E);
+        uint8_t* mem = nullptr;
+        ok = ok && dalloc(g, &mem, 2 * gbytes + dbytes, "a layer's experts", err, err_len);
+        if (!ok) break;
+        d.gate = place(mem, x0->gate.dtype, x0->gate.rows, x0->gate.cols, E);
+        d.up = place(mem + gbytes, x0->up.dtype, x0->up.rows, x0->up.cols, E);
+        d.down = place(mem + 2 * gbytes, x0->down.dtype, x0->down.rows, x0->down.cols, E);
+        for (size_t e = 0; e < E; e++) mats[e] = &L->experts[e].gate;
+        ok = upload_set(g, mats.data(), E, d.gate, staging, staging_bytes, err, err_len);
+        for (size_t e = 0; ok && e < E; e++) mats[e] = &L->experts[e].up;
+        ok = ok && upload_set(g, mats.data(), E, d.up, staging, staging_bytes, err, err_len);
+        for (size_t e = 0; ok && e < E; e++) mats[e] = &L->experts[e].down;
+        ok = ok && upload_set(g, mats.data(), E, d.down, staging, staging_bytes, err, err_len);
+        if (ok && g->attention) {
+            ok = upload_matrix(g, &d.q, &L->q, staging, staging_bytes, "q", err, err_len) &&
+                 upload_matrix(g, &d.k, &L->k, staging, staging_bytes, "k", err, err_len) &&
+                 upload_matrix(g, &d.v, &L->v, staging, staging_bytes, "v", err, err_len) &&
+                 upload_matrix(g, &d.o, &L->o, staging, staging_bytes, "o", err, err_len) &&
+                 upload_f32(g, &d.attn_norm, L->attn_norm, c->hidden, "the attention norm", err, err_len);
+            if (ok && c->qk_norm)
+                ok = upload_f32(g, &d.q_norm, L->q_norm, c->head_dim, "the q norm", err, err_len) &&
+                     upload_f32(g, &d.k_norm, L->k_norm, c->head_dim, "the k norm", err, err_len);
+        }
+    }
+    if (ok && g->attention) {
+        ok = upload_matrix(g, &g->embed, &m->embed, staging, staging_bytes, "the embedding", err, err_len) &&
+             upload_matrix(g, &g->head, &m->lm_head, staging, staging_bytes, "the output projection", err, err_len) &&
+             upload_f32(g, &g->final_norm, m->final_norm, c->hidden, "the final norm", err, err_len);
+        const size_t half = c->head_dim / 2;
+        ok = ok && upload_f32(g, &g->cos_tab, cos_tab, m->ctx * half, "the rotary cosines", err, err_len) &&
+             upload_f32(g, &g->sin_tab, sin_tab, m->ctx * half, "the rotary sines", err, err_len);
+    }
+    hipFree(staging);
+    if (!ok) return bail();
+
+    /* key-value cache and scratch */
+    const size_t H = c->hidden, R = ROWS_MAX, E = c->n_experts, K = c->n_experts_used;
+    const size_t qd = c->n_heads * c->head_dim, kd = c->n_kv_heads * c->head_dim;
+    g->layer_kv = m->ctx * kd;
+    g->splits_max = (int)((m->ctx + ATTN_CHUNK - 1) / ATTN_CHUNK);
+    const size_t G = c->n_kv_heads ? c->n_heads / c->n_kv_heads : 1;
+    ok = dalloc(g, &g->x, R * H * 4, "the residual", err, err_len) && dalloc(g, &g->xn, R * H * 4, "scratch", err, err_len) &&
+         dalloc(g, &g->act, R * K * c->intermediate * 4, "scratch", err, err_len) &&
+         dalloc(g, &g->ypart, R * K * H * 4, "scratch", err, err_len) &&
+         dalloc(g, &g->rlogits, 2 * R * E * 4, "scratch", err, err_len) && dalloc(g, &g->rt, R * sizeof(route_out), "scratch", err, err_len) &&
+         dalloc(g, &g->route_ctr, R * 4, "scratch", err, err_len) && dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len);
+    if (ok && g->attention) {
+        ok = dalloc(g, &g->q, R * qd * 4, "scratch", err, err_len) && dalloc(g, &g->qp, R * qd * 4, "scratch", err, err_len) &&
+             dalloc(g, &g->k, R * kd * 4, "scratch", err, err_len) && dalloc(g, &g->v, R * kd * 4, "scratch", err, err_len) &&
+             dalloc(g, &g->att, R * qd * 4, "scratch", err, err_len) &&
+             dalloc(g, &g->vocab, R * c->vocab * 4, "the logits", err, err_len) &&
+             dalloc(g, &g->partial, (size_t)R * c->n_kv_heads * g->splits_max * G * (c->head_dim + 2) * 4, "attention partials", err, err_len) &&
+             dalloc(g, &g->attn_ctr, R * c->n_kv_heads * 4, "scratch", err, err_len) &&
+             dalloc(g, &g->k_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the key cache", err, err_len) &&
+             dalloc(g, &g->v_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the value cache", err, err_len);
+    }
+    if (!ok) return bail();
+    if (hipMemset(g->route_ctr, 0, R * 4) != hipSuccess || (g->attn_ctr && hipMemset(g->attn_ctr, 0, R * c->n_kv_heads * 4) != hipSuccess) ||
+        hipMemset(g->x, 0, R * H * 4) != hipSuccess || hipMemset(g->rt, 0, R * sizeof(route_out)) != hipSuccess) {
+        fail(err, err_len, "clearing device scratch failed");
+        return bail();
+    }
+    if (hipHostMalloc((void**)&g->rows_host, R * sizeof(row_rec), 0) != hipSuccess ||
+        hipHostMalloc((void**)&g->h_logits, 2 * R * E * 4, 0) != hipSuccess) {
+        fail(err, err_len, "page-locked host memory for the rows and logits");
+        return bail();
+    }
+    if (hipDeviceSynchronize() != hipSuccess) { fail(err, err_len, "the device failed during upload"); return bail(); }
+    return g;
+}
+
+/* ---- per-layer enqueues ---------------------------------------------- */
+
+static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, bool prepared) {
+    const dlayer& d = g->L[layer];
+    gemv_args ga;
+    memset(&ga, 0, sizeof(ga));
+    ga.w[0] = d.q; ga.w[1] = d.k; ga.w[2] = d.v;
+    ga.y[0] = g->q; ga.y[1] = g->k; ga.y[2] = g->v;
+    ga.n = 3;
+    ga.x = g->x;
+    ga.norm_w = d.attn_norm;
+    ga.eps = g->eps;
+    if (n_rows != 1) return hipErrorInvalidValue; /* several rows: enqueue_rows_attention */
+    hipError_t e = launch_gemv(ga, g->stream);
+    if (e != hipSuccess) return e;
+    attn_args a;
+    memset(&a, 0, sizeof(a));
+    a.q_raw = g->q; a.k_raw = g->k; a.v_raw = g->v;
+    a.q_norm = d.q_norm; a.k_norm = d.k_norm;
+    a.cos_tab = g->cos_tab; a.sin_tab = g->sin_tab;
+    a.k_cache = g->k_cache + (size_t)layer * g->layer_kv;
+    a.v_cache = g->v_cache + (size_t)layer * g->layer_kv;
+    a.seq_stride = (size_t)g->NL * g->layer_kv;
+    a.rows = g->rows_dev;
+    a.n_rows = 1;
+    a.partial = g->partial;
+    a.counter = g->attn_ctr;
+    a.att = g->att;
+    a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx; a.splits_max = g->splits_max;
+    a.eps = g->eps;
+    a.prepared = prepared ? 1 : 0;
+    e = launch_attention(a, g->stream);
+    if (e != hipSuccess) return e;
+    gemv_args go;
+    memset(&go, 0, sizeof(go));
+    go.w[0] = d.o;
+    go.y[0] = g->x;
+    go.n = 1;
+    go.x = g->att;
+    go.add = 1;
+    return launch_gemv(go, g->stream);
+}
+
+static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, bool topk, int n_rows, const float* x) {
+    const dlayer& d = g->L[layer];
+    route_args r;
+    memset(&r, 0, sizeof(r));
+    r.x = x;
+    r.norm_w = d.mlp_norm;
+    r.router = d.router;
+    r.xn_out = g->xn;
+    r.logits = logits;
+    r.out = g->rt;
+    r.counter = g->route_ctr;
+    r.H = g->H; r.E = g->E; r.K = g->K; r.renorm = g->renorm; r.topk = topk ? 1 : 0; r.n_rows = n_rows;
+    r.eps = g->eps;
+    return launch_route(r, g->stream);
+}
+
+static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, float* y, int add) {
+    const dlayer& d = g->L[layer];
+    experts_in_args ai;
+    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.act = g->act; ai.K = g->K;
+    hipError_t e = launch_experts_in(ai, g->stream);
+    if (e != hipSuccess) return e;
+    experts_down_args ad;
+    ad.down = d.down; ad.act = g->act; ad.rt = g->rt; ad.y = y; ad.K = g->K; ad.add = add;
+    return launch_experts_down(ad, g->stream);
+}
+
+static hipError_t enqueue_head(vitna_cuda_model* g) {
+    gemv_args gh;
+    memset(&gh, 0, sizeof(gh));
+    gh.w[0] = g->head;
+    gh.y[0] = g->vocab;
+    gh.n = 1;
+    gh.x = g->x;
+    gh.norm_w = g->final_norm;
+    gh.eps = g->eps;
+    return launch_gemv(gh, g->stream);
+}
+
+static bool check_launch(vitna_cuda_model* g, hipError_t e, const char* what, char* err, size_t err_len) {
+    if (e == hipSuccess) return true;
+    if (e == hipErrorInvalidValue) return fail(err, err_len, "%s: a kernel was asked for a shape it does not take", what);
+    (void)g;
+    return fail_hip(err, err_len, what, e);
+}
+
+static bool set_row(vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, char* err, size_t err_len) {
+    if (seq >= (size_t)g->seqs) return fail(err, err_len, "sequence %zu: the cache holds %d", seq, g->seqs);
+    if (pos >= (size_t)g->ctx) return fail(err, err_len, "position %zu: the cache holds %d", pos, g->ctx);
+    if (g->attention && (token < 0 || token >= g->V)) return fail(err, err_len, "token %d is outside the vocabulary of %d", token, g->V);
+    /* the previous copy out of the page-locked row must have run */
+    HIP_TRY(hipEventSynchronize(g->rows_copied), "waiting for the previous row copy");
+    g->rows_host[0] = {token, (int32_t)pos, (int32_t)seq};
+    HIP_TRY(hipMemcpyAsync(g->rows_dev, g->rows_host, sizeof(row_rec), hipMemcpyHostToDevice, g->stream), "copying the row");
+    HIP_TRY(hipEventRecord(g->rows_copied, g->stream), "recording the row copy");
+    return true;
+}
+
+/* ---- the reference's MoE ABI ----------------------------------------- */
+
+extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, size_t layer, float* logits,
+                                     float* next, char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    if (!g->attention) return fail(err, err_len, "this model has no attention; use vitna_hip_moe_ffn");
+    if (!set_row(g, seq, token, pos, err, err_len)) return false;
+    hipError_t e = hipSuccess;
+    if (layer == 0) e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
+    if (e == hipSuccess) e = enqueue_attention(g, (int)layer, 1, false);
+    if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, false, 1, g->x);
+    const bool nx = next && layer + 1 < (size_t)g->NL;
+    if (e == hipSuccess && nx) {
+        /* the next layer's router on the same residual; its norm must not replace this layer's */
+        const dlayer& d = g->L[layer + 1];
+        route_args r;
+        memset(&r, 0, sizeof(r));
+        r.x = g->x; r.norm_w = d.mlp_norm; r.router = d.router; r.xn_out = nullptr; r.logits = g->rlogits + g->E;
+        r.out = g->rt; r.counter = g->route_ctr; r.H = g->H; r.E = g->E; r.K = g->K; r.topk = 0; r.n_rows = 1; r.eps = g->eps;
+        e = launch_route(r, g->stream);
+    }
+    if (!check_launch(g, e, "the layer up to its router", err, err_len)) return false;
+    HIP_TRY(hipMemcpyAsync(g->h_logits, g->rlogits, (nx ? 2 : 1) * g->E * 4, hipMemcpyDeviceToHost, g->stream), "copying the router's logits");
+    HIP_TRY(hipStreamSynchronize(g->stream), "running the layer up to its router");
+    memcpy(logits, g->h_logits, g->E * 4);
+    if (nx) memcpy(next, g->h_logits + g->E, g->E * 4);
+    return true;
+}
+
+static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const float* weights, size_t k, char* err, size_t err_len) {
+    if (k != (size_t)g->K) return fail(err, err_len, "%zu experts given; the model routes to %d", k, g->K);
+    std::vector<route_out> ro(n);
+    for (size_t t = 0; t < n; t++) {
+        memset(&ro[t], 0, sizeof(route_out));
+        for (size_t i = 0; i < k; i++) {
+            const int32_t e = ids[t * k + i];
+            if (e < 0 || e >= g->E) return fail(err, err_len, "expert %d is outside the layer's %d", e, g->E);
+            for (size_t j = 0; j < i; j++)
+                if (ids[t * k + j] == e) return fail(err, err_len, "expert %d is named twice", e);
+            ro[t].ids[i] = e;
+            ro[t].weights[i] = weights[t * k + i];
+            ro[t].chosen[i] = e;
+        }
+    }
+    /* pageable source: the copy has taken the bytes when this returns */
+    HIP_TRY(hipMemcpyAsync(g->rt, ro.data(), n * sizeof(route_out), hipMemcpyHostToDevice, g->stream), "copying the routing");
+    HIP_TRY(hipStreamSynchronize(g->stream), "copying the routing");
+    return true;
+}
+
+extern "C" bool vitna_cuda_moe_experts(struct vitna_cuda_model* g, size_t layer, const int32_t* ids, const float* weights, size_t k,
+                                       const int32_t* guess, char* err, size_t err_len) {
+    (void)guess;
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    if (!put_routing(g, 1, ids, weights, k, err, err_len)) return false;
+    return check_launch(g, enqueue_experts(g, (int)layer, g->x, 1), "the experts", err, err_len);
+}
+
+extern "C" bool vitna_cuda_moe_head(struct vitna_cuda_model* g, float* logits, char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!g->attention) return fail(err, err_len, "this model has no output projection");
+    if (!check_launch(g, enqueue_head(g), "the head", err, err_len)) return false;
+    if (logits) HIP_TRY(hipMemcpyAsync(logits, g->vocab, (size_t)g->V * 4, hipMemcpyDeviceToHost, g->stream), "copying the logits");
+    HIP_TRY(hipStreamSynchronize(g->stream), "running the head");
+    return true;
+}
+
+extern "C" const char* vitna_cuda_moe_report(const struct vitna_cuda_model* g, char* buf, size_t len) {
+    if (len == 0) return buf;
+    if (!g) { buf[0] = 0; return buf; }
+    snprintf(buf, len, "experts: all %d of each of %d layers resident on the device; nothing copied per token", g->E, g->NL);
+    return buf;
+}
+
+extern "C" int vitna_cuda_kv_layers(const struct vitna_cuda_model* g) { return g ? g->NL : 0; }
+extern "C" void vitna_cuda_test_long_from(struct vitna_cuda_model* g, size_t n) { if (g) g->long_from = n; }
+extern "C" void vitna_cuda_test_fast_rows(struct vitna_cuda_model* g, size_t n) { if (g) g->fast_rows = n; }
+
+extern "C" bool vitna_cuda_cpu_experts(struct vitna_cuda_model* g, size_t threads, char* err, size_t err_len) {
+    (void)g; (void)threads;
+    return fail(err, err_len, "every expert is resident on the device, so none run on the CPU beside it");
+}
+
+extern "C" bool vitna_cuda_step(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, float* logits, char* err, size_t err_len) {
+    (void)g; (void)seq; (void)token; (void)pos; (void)logits;
+    return fail(err, err_len, "a mixture of experts runs a layer at a time (vitna_cuda_moe_route and vitna_cuda_moe_experts)");
+}
+
+extern "C" size_t vitna_cuda_prompt_min(const struct vitna_cuda_model* g) { (void)g; return SIZE_MAX; }
+extern "C" size_t vitna_cuda_prompt_piece_min(const struct vitna_cuda_model* g) { (void)g; return 1; }
+extern "C" size_t vitna_cuda_exact_max(const struct vitna_cuda_model* g) { return g ? ROWS_MAX : 0; }
+
+extern "C" bool vitna_cuda_rows(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t count, float* const* logits, char* err,
+                                size_t err_len) {
+    (void)g; (void)rows; (void)count; (void)logits;
+    return fail(err, err_len, "a mixture of experts runs rows a layer at a time (vitna_cuda_moe_rows_*)");
+}
+
+extern "C" bool vitna_cuda_steps(struct vitna_cuda_model* g, size_t seq, const int32_t* tokens, size_t count, size_t pos, float* logits,
+                                 size_t rows, char* err, size_t err_len) {
+    (void)g; (void)seq; (void)tokens; (void)count; (void)pos; (void)logits; (void)rows;
+    return fail(err, err_len, "a mixture of experts runs a prompt as rows (vitna_cuda_moe_rows_*)");
+}
+
+extern "C" const char* vitna_cuda_device_name(const struct vitna_cuda_model* g) { return g ? g->name : ""; }
+
+extern "C" void vitna_cuda_wait(struct vitna_cuda_model* g) {
+    if (g) hipStreamSynchronize(g->stream);
+}
+
+extern "C" bool vitna_cuda_lost(struct vitna_cuda_model* g, char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no device model") || true;
+    (void)hipGetLastError();
+    const hipError_t e = hipStreamSynchronize(g->stream);
+    if (e != hipSuccess) {
+        g->lost = true;
+        fail_hip(err, err_len, "the device", e);
+        return true;
+    }
+    return false;
+}
+
+/* ---- checkers ---------------------------------------------------------- */
+
+extern "C" bool vitna_cuda_widen(const vitna_matrix_t* w, float* out, char* err, size_t err_len) {
+    if (!w || !w->data || !out) return fail(err, err_len, "no matrix");
+    if (!quant_ok(w->dtype) && w->dtype != VITNA_DTYPE_F32) return fail(err, err_len, "%s is not read on the device", dtype_name(w->dtype));
+    const size_t rb = vitna_matrix_row_bytes(w->dtype, w->cols);
+    if (!rb) return fail(err, err_len, "%zu columns are not whole %s blocks", w->cols, dtype_name(w->dtype));
+    const size_t bytes = rb * w->rows, n = w->rows * w->cols;
+    uint8_t *src = nullptr, *planes = nullptr;
+    float *o1 = nullptr, *o2 = nullptr;
+    bool ok = true;
+    const size_t pb = w->dtype == VITNA_DTYPE_F32 ? bytes : set_bytes(w->dtype, w->rows, w->cols, 1);
+    if (hipMalloc(&src, bytes) != hipSuccess || hipMalloc(&planes, pb) != hipSuccess || hipMalloc(&o1, n * 4) != hipSuccess ||
+        hipMalloc(&o2, n * 4) != hipSuccess)
+        ok = fail(err, err_len, "device memory for widening %zu weights", n);
+    if (ok && hipMemcpy(src, w->data, bytes, hipMemcpyHostToDevice) != hipSuccess) ok = fail(err, err_len, "copying the matrix");
+    if (ok) {
+        qmat q;
+        if (w->dtype == VITNA_DTYPE_F32) {
+            memset(&q, 0, sizeof(q));
+            q.p[0] = src; q.rows = (int)w->rows; q.cols = (int)w->cols; q.dtype = VITNA_DTYPE_F32;
+        } else {
+            q = place(planes, w->dtype, w->rows, w->cols, 1);
+            if (launch_repack(src, q, 0) != hipSuccess) ok = fail(err, err_len, "splitting the blocks");
+        }
+        if (ok && (launch_widen_planes(q, 0, o1, 0) != hipSuccess || launch_widen_blocks(src, w->dtype, w->rows, w->cols, o2, 0) != hipSuccess))
+            ok = fail(err, err_len, "widening");
+        if (ok && hipDeviceSynchronize() != hipSuccess) ok = fail(err, err_len, "the device failed widening");
+    }
+    std::vector<float> a, b;
+    if (ok) {
+        a.resize(n);
+        b.resize(n);
+        if (hipMemcpy(a.data(), o1, n * 4, hipMemcpyDeviceToHost) != hipSuccess || hipMemcpy(b.data(), o2, n * 4, hipMemcpyDeviceToHost) != hipSuccess)
+            ok = fail(err, err_len, "copying the widened weights back");
+    }
+    if (ok && memcmp(a.data(), b.data(), n * 4) != 0) ok = fail(err, err_len, "the two ways of reading the blocks disagree");
+    if (ok) memcpy(out, a.data(), n * 4);
+    hipFree(src); hipFree(planes); hipFree(o1); hipFree(o2);
+    return ok;
+}
+
+extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_matrix_t* up, const vitna_matrix_t* down, const float* norm_w,
+                                        const float* x, float eps, float* xs, float* act, float* y, char* err, size_t err_len) {
+    if (!gate || !up || !down || !norm_w || !x) return fail(err, err_len, "missing arguments");
+    const size_t H = gate->cols, I = gate->rows;
+    if (!matrix_ok(gate, I, H, "gate", err, err_len) || !matrix_ok(up, I, H, "up", err, err_len) ||
+        !matrix_ok(down, H, I, "down", err, err_len))
+        return false;
+    if (gate->dtype != up->dtype) return fail(err, err_len, "gate and up must share a dtype");
+    if (H % 16 || H > 8192) return fail(err, err_len, "width %zu", H);
+    hipStream_t s = 0;
+    std::vector<void*> mem;
+    auto dm = [&](size_t b) -> void* { void* p = nullptr; if (hipMalloc(&p, b) != hipSuccess) return nullptr; mem.push_back(p); return p; };
+    bool ok = true;
+    uint8_t* gm = (uint8_t*)dm(set_bytes(gate->dtype, I, H, 1));
+    uint8_t* um = (uint8_t*)dm(set_bytes(up->dtype, I, H, 1));
+    uint8_t* dmem = (uint8_t*)dm(set_bytes(down->dtype, H, I, 1));
+    const size_t stb = std::max(vitna_matrix_row_bytes(gate->dtype, H) * I, vitna_matrix_row_bytes(down->dtype, I) * H);
+    uint8_t* st = (uint8_t*)dm(stb);
+    float* dx = (float*)dm(H * 4);
+    float* dw = (float*)dm(H * 4);
+    float* dxn = (float*)dm(H * 4);
+    float* dl = (float*)dm(4 * 4);
+    float* drouter = (float*)dm(H * 4);
+    float* dact = (float*)dm(I * 4);
+    float* dy = (float*)dm(H * 4);
+    route_out* drt = (route_out*)dm(sizeof(route_out));
+    unsigned* dctr = (unsigned*)dm(16);
+    for (void* p : mem) ok = ok && p;
+    if (!ok) { for (void* p : mem) hipFree(p); return fail(err, err_len, "device memory for the expert check"); }
+    qmat qg = place(gm, gate->dtype, I, H, 1), qu = place(um, up->dtype, I, H, 1), qd = place(dmem, down->dtype, H, I, 1);
+    auto up_one = [&](const vitna_matrix_t* w, const qmat& q) {
+        const size_t b = vitna_matrix_row_bytes(w->dtype, w->cols) * w->rows;
+        return hipMemcpy(st, w->data, b, hipMemcpyHostToDevice) == hipSuccess && launch_repack(st, q, s) == hipSuccess &&
+               hipDeviceSynchronize() == hipSuccess;
+    };
+    ok = up_one(gate, qg) && up_one(up, qu) && up_one(down, qd);
+    route_out r;
+    memset(&r, 0, sizeof(r));
+    r.weights[0] = 1.0f;
+    ok = ok && hipMemcpy(dx, x, H * 4, hipMemcpyHostToDevice) == hipSuccess && hipMemcpy(dw, norm_w, H * 4, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(drt, &r, sizeof(r), hipMemcpyHostToDevice) == hipSuccess && hipMemset(dctr, 0, 16) == hipSuccess &&
+         hipMemset(drouter, 0, H * 4) == hipSuccess;
+    if (ok) {
+        /* the norm a step uses (the router kernel's, with a one-row router) */
+        route_args ra;
+        memset(&ra, 0, sizeof(ra));
+        ra.x = dx; ra.norm_w = dw; ra.router = drouter; ra.xn_out = dxn; ra.logits = dl; ra.out = drt; ra.counter = dctr;
+        ra.H = (int)H; ra.E = 1; ra.K = 1; ra.topk = 0; ra.n_rows = 1; ra.eps = eps;
+        experts_in_args ai;
+        ai.gate = qg; ai.up = qu; ai.xn = dxn; ai.rt = drt; ai.act = dact; ai.K = 1;
+        experts_down_args ad;
+        ad.down = qd; ad.act = dact; ad.rt = drt; ad.y = dy; ad.K = 1; ad.add = 0;
+        ok = launch_route(ra, s) == hipSuccess && launch_experts_in(ai, s) == hipSuccess && launch_experts_down(ad, s) == hipSuccess &&
+             hipDeviceSynchronize() == hipSuccess;
+        if (!ok) fail(err, err_len, "the expert's kernels failed or do not take this shape");
+    } else {
+        fail(err, err_len, "uploading the expert failed");
+    }
+    if (ok) {
+        ok = (!xs || hipMemcpy(xs, dxn, H * 4, hipMemcpyDeviceToHost) == hipSuccess) &&
+             (!act || hipMemcpy(act, dact, I * 4, hipMemcpyDeviceToHost) == hipSuccess) &&
+             (!y || hipMemcpy(y, dy, H * 4, hipMemcpyDeviceToHost) == hipSuccess);
+        if (!ok) fail(err, err_len, "copying the expert's results back");
+    }
+    for (void* p : mem) hipFree(p);
+    return ok;
+}
+
+/* ---- extensions --------------------------------------------------------- */
+
+static hipError_t enqueue_step_body(vitna_cuda_model* g) {
+    hipError_t e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
+    for (int l = 0; e == hipSuccess && l < g->NL; l++) {
+        e = enqueue_attention(g, l, 1, false);
+        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, true, 1, g->x);
+        if (e == hipSuccess) e = enqueue_experts(g, l, g->x, 1);
+    }
+    if (e == hipSuccess) e = enqueue_head(g);
+    return e;
+}
+
+static bool ensure_graph(vitna_cuda_model* g, char* err, size_t err_len) {
+    if (g->graph_ready) return true;
+    HIP_TRY(hipStreamSynchronize(g->stream), "before capturing the step");
+    HIP_TRY(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "capturing the step");
+    const hipError_t e = enqueue_step_body(g);
+    hipGraph_t graph = nullptr;
+    const hipError_t e2 = hipStreamEndCapture(g->stream, &graph);
+    if (e != hipSuccess) { if (graph) hipGraphDestroy(graph); return check_launch(g, e, "capturing the step", err, err_len); }
+    HIP_TRY(e2, "ending the capture of the step");
+    const hipError_t e3 = hipGraphInstantiate(&g->step_graph, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    HIP_TRY(e3, "instantiating the step's graph");
+    g->graph_ready = true;
+    return true;
+}
+
+extern "C" bool vitna_hip_moe_step_async(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!g->attention) return fail(err, err_len, "this model has no attention; use vitna_hip_moe_ffn");
+    if (!ensure_graph(g, err, err_len)) return false;
+    if (!set_row(g, seq, token, pos, err, err_len)) return false;
+    HIP_TRY(hipGraphLaunch(g->step_graph, g->stream), "launching the step");
+    return true;
+}
+
+extern "C" bool vitna_hip_moe_step(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, float* logits, char* err,
+                                   size_t err_len) {
+    if (!vitna_hip_moe_step_async(g, seq, token, pos, err, err_len)) return false;
+    if (logits) HIP_TRY(hipMemcpyAsync(logits, g->vocab, (size_t)g->V * 4, hipMemcpyDeviceToHost, g->stream), "copying the logits");
+    HIP_TRY(hipStreamSynchronize(g->stream), "running the step");
+    return true;
+}
+
+extern "C" bool vitna_hip_moe_ffn(struct vitna_cuda_model* g, size_t layer, char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    hipError_t e = enqueue_route(g, (int)layer, g->rlogits, true, 1, g->x);
+    if (e == hipSuccess) e = enqueue_experts(g, (int)layer, g->x, 1);
+    return check_launch(g, e, "the mixture of experts", err, err_len);
+}
+
+extern "C" bool vitna_hip_residual(struct vitna_cuda_model* g, size_t row, float* host, bool to_device, char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no model");
+    if (row >= ROWS_MAX) return fail(err, err_len, "row %zu: at most %d", row, ROWS_MAX);
+    float* d = g->x + row * g->H;
+    HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
+    HIP_TRY(to_device ? hipMemcpy(d, host, g->H * 4, hipMemcpyHostToDevice) : hipMemcpy(host, d, g->H * 4, hipMemcpyDeviceToHost),
+            "copying the residual");
+    return true;
+}
+
+extern "C" bool vitna_hip_routing(struct vitna_cuda_model* g, size_t row, float* logits, int32_t* chosen, int32_t* ids, float* weights,
+                                  char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no model");
+    if (row >= ROWS_MAX) return fail(err, err_len, "row %zu: at most %d", row, ROWS_MAX);
+    HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
+    route_out r;
+    HIP_TRY(hipMemcpy(&r, g->rt + row, sizeof(r), hipMemcpyDeviceToHost), "copying the routing");
+    if (logits) HIP_TRY(hipMemcpy(logits, g->rlogits + row * g->E, g->E * 4, hipMemcpyDeviceToHost), "copying the router's logits");
+    for (int k = 0; k < g->K; k++) {
+        if (chosen) chosen[k] = r.chosen[k];
+        if (ids) ids[k] = r.ids[k];
+        if (weights) weights[k] = r.weights[k];
+    }
+    return true;
+}
+
+extern "C" bool vitna_hip_kv(struct vitna_cuda_model* g, size_t seq, size_t layer, size_t pos0, size_t n, float* k, float* v, bool write,
+                             char* err, size_t err_len) {
+    if (!g || !g->attention) return fail(err, err_len, "no key-value cache");
+    if (seq >= (size_t)g->seqs || layer >= (size_t)g->NL || pos0 + n > (size_t)g->ctx) return fail(err, err_len, "outside the cache");
+    const size_t kd = (size_t)g->nkv * g->hd;
+    const size_t off = ((size_t)seq * g->NL + layer) * g->layer_kv + pos0 * kd;
+    HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
+    const hipMemcpyKind kind = write ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+    if (k) HIP_TRY(write ? hipMemcpy(g->k_cache + off, k, n * kd * 4, kind) : hipMemcpy(k, g->k_cache + off, n * kd * 4, kind), "copying keys");
+    if (v) HIP_TRY(write ? hipMemcpy(g->v_cache + off, v, n * kd * 4, kind) : hipMemcpy(v, g->v_cache + off, n * kd * 4, kind), "copying values");
+    return true;
+}
+
+extern "C" bool vitna_hip_kv_fill(struct vitna_cuda_model* g, uint64_t seed, const size_t* n_pos, char* err, size_t err_len) {
+    if (!g || !g->attention) return fail(err, err_len, "no key-value cache");
+    const size_t kd = (size_t)g->nkv * g->hd;
+    for (int s = 0; s < g->seqs; s++) {
+        const size_t n = std::min(n_pos[s], (size_t)g->ctx);
+        for (int l = 0; l < g->NL; l++) {
+            const size_t off = ((size_t)s * g->NL + l) * g->layer_kv;
+            const uint64_t tag = (seed * 1000003ull + (uint64_t)s) * 1000003ull + (uint64_t)l;
+            HIP_TRY(launch_fill_normal(g->k_cache + off, n * kd, 2 * tag + 1, g->stream), "filling keys");
+            HIP_TRY(launch_fill_normal(g->v_cache + off, n * kd, 2 * tag + 2, g->stream), "filling values");
+        }
+    }
+    HIP_TRY(hipStreamSynchronize(g->stream), "filling the cache");
+    return true;
+}
+
+extern "C" bool vitna_hip_sync(struct vitna_cuda_model* g, char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no model");
+    HIP_TRY(hipStreamSynchronize(g->stream), "the device");
+    return true;
+}
+
+extern "C" void* vitna_hip_stream(struct vitna_cuda_model* g) { return g ? (void*)g->stream : nullptr; }
+extern "C" const float* vitna_hip_logits_device(struct vitna_cuda_model* g) { return g ? g->vocab : nullptr; }
+
+static double qmat_bytes(const qmat& q) {
+    double b = 0;
+    for (int i = 0; i < 4; i++) b += (double)plane_bytes(q.dtype, i, q.rows, q.cols);
+    return b;
+}
+
+extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int reps, int warmup, double* avg_us, double* bytes, char* err,
+                                      size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if ((which >= 3 && !g->attention) || which < 0 || which > 6) return fail(err, err_len, "no such kernel (%d) in this model", which);
+    hipEvent_t t0, t1;
+    HIP_TRY(hipEventCreate(&t0), "events");
+    HIP_TRY(hipEventCreate(&t1), "events");
+    double b = 0;
+    const int H = g->H, K = g->K;
+    auto one = [&](int i) -> hipError_t {
+        const int l = i % g->NL;
+        const dlayer& d = g->L[l];
+        switch (which) {
+            case 0: {
+                experts_in_args ai;
+                ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.act = g->act; ai.K = K;
+                b = 2.0 * K * qmat_bytes(d.gate) + H * 4.0 + K * (double)g->I * 4;
+                return launch_experts_in(ai, g->stream);
+            }
+            case 1: {
+                experts_down_args ad;
+                ad.down = d.down; ad.act = g->act; ad.rt = g->rt; ad.y = g->ypart; ad.K = K; ad.add = 0;
+                b = K * qmat_bytes(d.down) + K * (double)g->I * 4 + H * 4.0;
+                return launch_experts_down(ad, g->stream);
+            }
+            case 2:
+                b = (double)g->E * H * 4 + H * 8.0 + g->E * 4.0;
+                return enqueue_route(g, l, g->rlogits, true, 1, g->x);
+            case 3: {
+                gemv_args ga;
+                memset(&ga, 0, sizeof(ga));
+                ga.w[0] = d.q; ga.w[1] = d.k; ga.w[2] = d.v; ga.y[0] = g->q; ga.y[1] = g->k; ga.y[2] = g->v; ga.n = 3;
+                ga.x = g->x; ga.norm_w = d.attn_norm; ga.eps = g->eps;
+                b = qmat_bytes(d.q) + qmat_bytes(d.k) + qmat_bytes(d.v) + H * 8.0;
+                return launch_gemv(ga, g->stream);
+            }
+            case 4: {
+                attn_args a;
+                memset(&a, 0, sizeof(a));
+                a.q_raw = g->q; a.k_raw = g->k; a.v_raw = g->v; a.q_norm = d.q_norm; a.k_norm = d.k_norm;
+                a.cos_tab = g->cos_tab; a.sin_tab = g->sin_tab;
+                a.k_cache = g->k_cache + (size_t)l * g->layer_kv; a.v_cache = g->v_cache + (size_t)l * g->layer_kv;
+                a.seq_stride = (size_t)g->NL * g->layer_kv; a.rows = g->rows_dev; a.n_rows = 1; a.partial = g->partial;
+                a.counter = g->attn_ctr; a.att = g->att; a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx;
+                a.splits_max = g->splits_max; a.eps = g->eps;
+                b = 0; /* set by the caller from the position */
+                return launch_attention(a, g->stream);
+            }
+            case 5: {
+                gemv_args go;
+                memset(&go, 0, sizeof(go));
+                go.w[0] = d.o; go.y[0] = g->ypart; go.n = 1; go.x = g->att;
+                b = qmat_bytes(d.o) + (double)g->nh * g->hd * 4 + H * 4.0;
+                return launch_gemv(go, g->stream);
+            }
+            default:
+                b = qmat_bytes(g->head) + H * 8.0 + (double)g->V * 4;
+                return enqueue_head(g);
+        }
+    };
+    for (int i = 0; i < warmup; i++)
+        if (!check_launch(g, one(i), "timing", err, err_len)) return false;
+    HIP_TRY(hipEventRecord(t0, g->stream), "events");
+    for (int i = 0; i < reps; i++)
+        if (!check_launch(g, one(warmup + i), "timing", err, err_len)) return false;
+    HIP_TRY(hipEventRecord(t1, g->stream), "events");
+    HIP_TRY(hipEventSynchronize(t1), "timing");
+    float ms = 0;
+    HIP_TRY(hipEventElapsedTime(&ms, t0, t1), "events");
+    hipEventDestroy(t0);
+    hipEventDestroy(t1);
+    if (avg_us) *avg_us = 1000.0 * ms / reps;
+    if (bytes) *bytes = b;
+    return true;
+}
+
+/* Rows and prefill: kernels_rows.hip. */
+
+extern "C" size_t vitna_cuda_moe_rows_max(const struct vitna_cuda_model* g) { return g ? ROWS_MAX : 0; }
+
+extern "C" bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, size_t layer, float* logits,
+                                          float* next, char* err, size_t err_len) {
+    (void)g; (void)rows; (void)n; (void)layer; (void)logits; (void)next;
+    return fail(err, err_len, "rows are not yet served");
+}
+
+extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t layer, size_t n, const int32_t* ids, const float* weights,
+                                            size_t k, const int32_t* guess, char* err, size_t err_len) {
+    (void)g; (void)layer; (void)n; (void)ids; (void)weights; (void)k; (void)guess;
+    return fail(err, err_len, "rows are not yet served");
+}
+
+extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, float* const* logits, char* err, size_t err_len) {
+    (void)g; (void)n; (void)logits;
+    return fail(err, err_len, "rows are not yet served");
+}
+
+extern "C" bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, char* err, size_t err_len) {
+    (void)g; (void)layer; (void)x; (void)n;
+    return fail(err, err_len, "prefill is not yet served");
+}

@@ -1,0 +1,267 @@
+/**
+ * kernels_attn.hip - Decode attention over the float32 key-value cache, for
+ * one or many rows (tokens of possibly different sequences at their own
+ * positions), with Qwen3's per-head QK RMSNorm and the half-split RoPE.
+ *
+ * Reference counterparts: qk_head_norm_rope_kernel model_cuda.cu:1514 and
+ * attention_kernel model_cuda.cu:942 (split-K, last block merges); the CPU
+ * arithmetic it is checked against is engine/src/model.c:909-957.
+ *
+ * Layout: the cache of a layer holds, for every sequence, ctx positions of
+ * n_kv * hd floats (one position's heads back to back), as the reference's
+ * [seq][layer][ctx][kv_dim]. A block takes ATTN_CHUNK positions of one kv
+ * head of one row: four waves of 16 positions, four lanes a position in the
+ * scores (hd / 4 dimensions a lane), a lane per dimension in the weighted sum
+ * of values. Each of the G = n_heads / n_kv query heads sharing the kv head
+ * is served by the same reads of the cache.
+ */
+
+#include "vitna_kernels.h"
+
+#define GMAX 8
+
+/* RMSNorm and RoPE of NV vectors of HD in LDS (v[i] at vecs + i * HD): the
+   reference's per-head norm (engine/src/model.c:916-921) and vitna_rope_half
+   (engine/src/ops.c:273-281). */
+template <int HD>
+__device__ void norm_rope(float* vecs, int nv, const float* wq, const float* wk, int k_from, float eps, const float* c,
+                          const float* s, float* inv_s) {
+    const int tid = threadIdx.x;
+    if (wq) {
+        if (tid < nv) {
+            const float* v = vecs + tid * HD;
+            float ss = 0.f;
+            for (int d = 0; d < HD; d++) ss = fmaf(v[d], v[d], ss);
+            inv_s[tid] = 1.0f / sqrtf(ss / (float)HD + eps);
+        }
+        __syncthreads();
+        for (int i = tid; i < nv * HD; i += blockDim.x) {
+            const int g = i / HD, d = i % HD;
+            const float* w = g >= k_from ? wk : wq;
+            vecs[i] = (vecs[i] * inv_s[g]) * w[d];
+        }
+        __syncthreads();
+    }
+    constexpr int HALF = HD / 2;
+    for (int i = tid; i < nv * HALF; i += blockDim.x) {
+        const int g = i / HALF, j = i % HALF;
+        float* v = vecs + g * HD;
+        const float a = v[j], b = v[j + HALF];
+        const float ac = a * c[j], bs = b * s[j], bc = b * c[j], as = a * s[j];
+        v[j] = ac - bs;
+        v[j + HALF] = bc + as;
+    }
+    __syncthreads();
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
+    constexpr int DPL = HD / 4;        /* dimensions a lane in the scores */
+    constexpr int VPL = HD / 64;       /* dimensions a lane in the values */
+    const int split = blockIdx.x, h = blockIdx.y, row = blockIdx.z;
+    const row_rec rr = a.rows[row];
+    const int pos = rr.pos, seq = rr.seq;
+    const int n_act = pos / ATTN_CHUNK + 1;
+    if (split >= n_act) return;
+    const int G = a.n_heads / a.n_kv, kv_dim = a.n_kv * HD, half = HD / 2;
+    float* kc = a.k_cache + (size_t)seq * a.seq_stride;
+    float* vc = a.v_cache + (size_t)seq * a.seq_stride;
+    __shared__ float sq[(GMAX + 1) * HD]; /* G query heads, then the new key */
+    __shared__ float nv[HD];
+    __shared__ float inv_s[GMAX + 1];
+    __shared__ float sp[4][16][GMAX];
+    __shared__ float wm[4][GMAX], wl[4][GMAX];
+    __shared__ float wacc[4][GMAX][HD];
+    __shared__ int last_s;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    float* nk = sq + G * HD;
+
+    if (a.prepared) {
+        for (int i = tid; i < G * HD; i += 256) sq[i] = a.q_raw[(size_t)row * a.n_heads * HD + (size_t)h * G * HD + i];
+        __syncthreads();
+    } else {
+        for (int i = tid; i < G * HD; i += 256) sq[i] = a.q_raw[(size_t)row * a.n_heads * HD + (size_t)h * G * HD + i];
+        if (tid < HD) {
+            nk[tid] = a.k_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
+            nv[tid] = a.v_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
+        }
+        __syncthreads();
+        norm_rope<HD>(sq, G + 1, a.q_norm, a.k_norm, G, a.eps, a.cos_tab + (size_t)pos * half, a.sin_tab + (size_t)pos * half, inv_s);
+        if (split == n_act - 1 && tid < HD) {
+            kc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = nk[tid];
+            vc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = nv[tid];
+        }
+    }
+
+    /* scores: four lanes a position, sixteen positions a wave */
+    const int p = lane >> 2, qd = lane & 3;
+    const int t = split * ATTN_CHUNK + wave * 16 + p;
+    const bool valid = t <= pos;
+    const bool fresh = !a.prepared && t == pos; /* this row's own key, not yet readable from the cache by other blocks */
+    float kr[DPL];
+    if (valid) {
+        if (fresh) {
+#pragma unroll
+            for (int i = 0; i < DPL; i++) kr[i] = nk[qd * DPL + i];
+        } else {
+            const float4* src = reinterpret_cast<const float4*>(kc + (size_t)t * kv_dim + (size_t)h * HD + qd * DPL);
+#pragma unroll
+            for (int i = 0; i < DPL / 4; i++) {
+                const float4 u = src[i];
+                kr[4 * i] = u.x; kr[4 * i + 1] = u.y; kr[4 * i + 2] = u.z; kr[4 * i + 3] = u.w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < DPL; i++) kr[i] = 0.f;
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+    float mw[GMAX], lw[GMAX], pe[GMAX];
+#pragma unroll
+    for (int g = 0; g < GMAX; g++) {
+        if (g >= G) break;
+        const float* qg = sq + g * HD + qd * DPL;
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; i++) s = fmaf(qg[i], kr[i], s);
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s *= scale;
+        float m = valid ? s : -INFINITY;
+#pragma unroll
+        for (int o = 4; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float e = valid ? expf(s - m) : 0.0f;
+        float l = e;
+#pragma unroll
+        for (int o = 4; o < 64; o <<= 1) l += __shfl_xor(l, o, 64);
+        mw[g] = m;
+        lw[g] = l;
+        pe[g] = e;
+    }
+    if (qd == 0) {
+#pragma unroll
+        for (int g = 0; g < GMAX; g++)
+            if (g < G) sp[wave][p][g] = pe[g];
+    }
+    __syncthreads();
+
+    /* values: a lane per dimension, the wave's sixteen positions */
+    float acc[GMAX][VPL];
+#pragma unroll
+    for (int g = 0; g < GMAX; g++)
+#pragma unroll
+        for (int i = 0; i < VPL; i++) acc[g][i] = 0.f;
+    const int t0 = split * ATTN_CHUNK + wave * 16;
+    for (int pp = 0; pp < 16; pp++) {
+        const int tt = t0 + pp;
+        if (tt > pos) break;
+        const bool fr = !a.prepared && tt == pos;
+        const float* vrow = fr ? nv : vc + (size_t)tt * kv_dim + (size_t)h * HD;
+        float vv[VPL];
+#pragma unroll
+        for (int i = 0; i < VPL; i++) vv[i] = vrow[lane + 64 * i];
+#pragma unroll
+        for (int g = 0; g < GMAX; g++) {
+            if (g >= G) break;
+            const float w = sp[wave][pp][g];
+#pragma unroll
+            for (int i = 0; i < VPL; i++) acc[g][i] = fmaf(w, vv[i], acc[g][i]);
+        }
+    }
+    if (lane == 0) {
+        for (int g = 0; g < G; g++) { wm[wave][g] = mw[g]; wl[wave][g] = lw[g]; }
+    }
+#pragma unroll
+    for (int g = 0; g < GMAX; g++) {
+        if (g >= G) break;
+#pragma unroll
+        for (int i = 0; i < VPL; i++) wacc[wave][g][lane + 64 * i] = acc[g][i];
+    }
+    __syncthreads();
+
+    /* this chunk's partial: the four waves merged */
+    float* part = a.partial + (((size_t)row * a.n_kv + h) * a.splits_max + split) * G * (HD + 2);
+    for (int i = tid; i < G * HD; i += 256) {
+        const int g = i / HD, d = i % HD;
+        float M = -INFINITY;
+        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
+        float L = 0.f, o = 0.f;
+        for (int w = 0; w < 4; w++) {
+            const float f = wm[w][g] == -INFINITY ? 0.0f : expf(wm[w][g] - M);
+            L = fmaf(wl[w][g], f, L);
+            o = fmaf(wacc[w][g][d], f, o);
+        }
+        part[g * (HD + 2) + d] = o;
+        if (d == 0) {
+            part[g * (HD + 2) + HD] = M;
+            part[g * (HD + 2) + HD + 1] = L;
+        }
+    }
+
+    /* the last chunk of this (row, kv head) to finish merges every chunk */
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    unsigned* ctr = a.counter + (size_t)row * a.n_kv + h;
+    if (tid == 0) last_s = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(n_act - 1);
+    __syncthreads();
+    if (!last_s) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const float* base = a.partial + ((size_t)row * a.n_kv + h) * a.splits_max * G * (HD + 2);
+    for (int i = tid; i < G * HD; i += 256) {
+        const int g = i / HD, d = i % HD;
+        float M = -INFINITY;
+        for (int s = 0; s < n_act; s++) M = fmaxf(M, base[((size_t)s * G + g) * (HD + 2) + HD]);
+        float L = 0.f, o = 0.f;
+        for (int s = 0; s < n_act; s++) {
+            const float* ps = base + ((size_t)s * G + g) * (HD + 2);
+            const float f = expf(ps[HD] - M);
+            L = fmaf(ps[HD + 1], f, L);
+            o = fmaf(ps[d], f, o);
+        }
+        a.att[(size_t)row * a.n_heads * HD + ((size_t)h * G + g) * HD + d] = o / L;
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* The prepare pass: one block a (row, kv head), its G query heads and its key. */
+template <int HD>
+__global__ __launch_bounds__(256) void attention_prepare_kernel(attn_args a) {
+    const int h = blockIdx.x, row = blockIdx.y;
+    const row_rec rr = a.rows[row];
+    const int pos = rr.pos, seq = rr.seq;
+    const int G = a.n_heads / a.n_kv, kv_dim = a.n_kv * HD, half = HD / 2;
+    __shared__ float sq[(GMAX + 1) * HD];
+    __shared__ float inv_s[GMAX + 1];
+    const int tid = threadIdx.x;
+    float* nk = sq + G * HD;
+    for (int i = tid; i < G * HD; i += 256) sq[i] = a.q_raw[(size_t)row * a.n_heads * HD + (size_t)h * G * HD + i];
+    if (tid < HD) nk[tid] = a.k_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
+    __syncthreads();
+    norm_rope<HD>(sq, G + 1, a.q_norm, a.k_norm, G, a.eps, a.cos_tab + (size_t)pos * half, a.sin_tab + (size_t)pos * half, inv_s);
+    for (int i = tid; i < G * HD; i += 256) a.q_out[(size_t)row * a.n_heads * HD + (size_t)h * G * HD + i] = sq[i];
+    if (tid < HD) {
+        float* kc = a.k_cache + (size_t)seq * a.seq_stride;
+        float* vc = a.v_cache + (size_t)seq * a.seq_stride;
+        kc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = nk[tid];
+        vc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = a.v_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
+    }
+}
+
+hipError_t launch_attention(const attn_args& a, hipStream_t s) {
+    if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > GMAX || a.n_rows < 1) return hipErrorInvalidValue;
+    if (a.splits_max * ATTN_CHUNK < a.ctx) return hipErrorInvalidValue;
+    const dim3 grid(a.splits_max, a.n_kv, a.n_rows);
+    if (a.hd == 128) attention_kernel<128><<<grid, 256, 0, s>>>(a);
+    else if (a.hd == 64) attention_kernel<64><<<grid, 256, 0, s>>>(a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_prepare(const attn_args& a, hipStream_t s) {
+    if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > GMAX || a.n_rows < 1 || !a.q_out) return hipErrorInvalidValue;
+    const dim3 grid(a.n_kv, a.n_rows);
+    if (a.hd == 128) attention_prepare_kernel<128><<<grid, 256, 0, s>>>(a);
+    else if (a.hd == 64) attention_prepare_kernel<64><<<grid, 256, 0, s>>>(a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}

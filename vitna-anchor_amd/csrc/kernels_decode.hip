@@ -1,0 +1,644 @@
+/**
+ * kernels_decode.hip - The batch-1 decode kernels of the quantized
+ * mixture-of-experts path on gfx950: upload (GGUF blocks to planes), the
+ * exact widening checker, the exact RMSNorm + router + top-k, the expert
+ * GEMVs (gate/up with SiLU, down with the weighted sum and the residual add),
+ * the dense projections and the embedding.
+ *
+ * Reference counterparts (engine/src/model_cuda.cu unless noted):
+ *   route_kernel       router_kernel :1544 + model.c route :667-703 (on the device)
+ *   experts_in_kernel  experts_in_kernel :1566
+ *   experts_down_kernel experts_down_kernel :1591 (+ the residual add)
+ *   gemv_kernel        attn_in_kernel :870 (norm + q/k/v), matvec_add_kernel :1430,
+ *                      head_kernel :1459
+ *   embed_kernel       embed_kernel :854
+ *   widen kernels      vitna_cuda_widen :5441 (widen_rows_kernel :5419)
+ */
+
+#include "vitna_kernels.h"
+
+/* ------------------------------------------------------------------ */
+/* Upload: GGUF blocks into planes                                     */
+/* ------------------------------------------------------------------ */
+
+__global__ void repack_kernel(const uint8_t* __restrict__ src, qmat m, size_t n_blocks) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_blocks) return;
+    uint8_t* P0 = const_cast<uint8_t*>(m.p[0]);
+    uint8_t* P1 = const_cast<uint8_t*>(m.p[1]);
+    uint8_t* P2 = const_cast<uint8_t*>(m.p[2]);
+    uint8_t* P3 = const_cast<uint8_t*>(m.p[3]);
+    if (m.dtype == VITNA_DTYPE_Q8_0) {
+        const uint8_t* b = src + i * 34;
+        P1[i * 2] = b[0];
+        P1[i * 2 + 1] = b[1];
+        for (int j = 0; j < 32; j++) P0[i * 32 + j] = b[2 + j];
+    } else if (m.dtype == VITNA_DTYPE_Q4_K) {
+        const uint8_t* b = src + i * 144;
+        for (int j = 0; j < 16; j++) P1[i * 16 + j] = b[j];
+        for (int j = 0; j < 128; j++) P0[i * 128 + j] = b[16 + j];
+    } else if (m.dtype == VITNA_DTYPE_Q6_K) {
+        const uint8_t* b = src + i * 210;
+        for (int j = 0; j < 128; j++) P0[i * 128 + j] = b[j];
+        for (int j = 0; j < 64; j++) P1[i * 64 + j] = b[128 + j];
+        for (int j = 0; j < 16; j++) P2[i * 16 + j] = b[192 + j];
+        P3[i * 2] = b[208];
+        P3[i * 2 + 1] = b[209];
+    }
+}
+
+hipError_t launch_repack(const uint8_t* src, const qmat& dst, hipStream_t s) {
+    if (dst.dtype != VITNA_DTYPE_Q8_0 && dst.dtype != VITNA_DTYPE_Q4_K && dst.dtype != VITNA_DTYPE_Q6_K) return hipErrorInvalidValue;
+    const size_t n = (size_t)dst.rows * dst.nb;
+    if (n == 0) return hipSuccess;
+    repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(src, dst, n);
+    return hipGetLastError();
+}
+
+__global__ void widen_planes_kernel(qmat m, int e, float* __restrict__ out) {
+    const size_t n = (size_t)m.rows * m.cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = widen_one(m, e, (int)(i / m.cols), (int)(i % m.cols));
+}
+
+hipError_t launch_widen_planes(const qmat& m, int e, float* out, hipStream_t s) {
+    const size_t n = (size_t)m.rows * m.cols;
+    if (n == 0) return hipSuccess;
+    const unsigned g = (unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
+    widen_planes_kernel<<<g, 256, 0, s>>>(m, e, out);
+    return hipGetLastError();
+}
+
+/* The same weights straight from the GGUF blocks, by a second reading of the
+   formats, so the checker compares two independent ways of reading. */
+__device__ __forceinline__ float half_at(const uint8_t* p) { return f16_bits_to_f32((uint32_t)p[0] | ((uint32_t)p[1] << 8)); }
+
+__global__ void widen_blocks_kernel(const uint8_t* __restrict__ src, int dtype, size_t rows, size_t cols, float* __restrict__ out) {
+    const size_t n = rows * cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t row = i / cols, col = i % cols;
+        float w = 0.0f;
+        if (dtype == VITNA_DTYPE_F32) {
+            w = reinterpret_cast<const float*>(src)[i];
+        } else if (dtype == VITNA_DTYPE_Q8_0) {
+            const uint8_t* b = src + (row * (cols / 32) + col / 32) * 34;
+            w = (float)(int8_t)b[2 + col % 32] * half_at(b);
+        } else if (dtype == VITNA_DTYPE_Q4_K) {
+            const uint8_t* b = src + (row * (cols / 256) + col / 256) * 144;
+            const int k = (int)(col % 256), g = k / 32, l = k % 32;
+            const uint8_t* s = b + 4;
+            const int sc = g < 4 ? (s[g] & 63) : ((s[g + 4] & 15) | ((s[g - 4] >> 6) << 4));
+            const int mn = g < 4 ? (s[g + 4] & 63) : ((s[g + 4] >> 4) | ((s[g] >> 6) << 4));
+            const int q = (b[16 + 32 * (g / 2) + l] >> (4 * (g & 1))) & 15;
+            const float d1 = half_at(b) * (float)sc, m1 = half_at(b + 2) * (float)mn;
+            const float p = d1 * (float)q;
+            w = p - m1;
+        } else if (dtype == VITNA_DTYPE_Q6_K) {
+            const uint8_t* b = src + (row * (cols / 256) + col / 256) * 210;
+            const int k = (int)(col % 256), h = k / 128, r = (k % 128) / 32, l = k % 32;
+            const int lo = (b[64 * h + 32 * (r & 1) + l] >> (4 * (r >> 1))) & 15;
+            const int hi = (b[128 + 32 * h + l] >> (2 * r)) & 3;
+            const float ds = half_at(b + 208) * (float)(int8_t)b[192 + k / 16];
+            w = ds * (float)((lo | (hi << 4)) - 32);
+        }
+        out[i] = w;
+    }
+}
+
+hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_t cols, float* out, hipStream_t s) {
+    const size_t n = rows * cols;
+    if (n == 0) return hipSuccess;
+    const unsigned g = (unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
+    widen_blocks_kernel<<<g, 256, 0, s>>>(src, dtype, rows, cols, out);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------------ */
+/* RMSNorm + router + top-k, in the reference CPU's order              */
+/* ------------------------------------------------------------------ */
+
+/* Sixteen lanes (j = 0..15) of a row hold the sixteen FMA chains of
+   engine/src/ops.c:196-209 (chain j: elements 16m + j in order of m). Fold
+   them as the AVX2 path does: v_j = a_j + a_{j+8}, s_j = v_j + v_{j+4},
+   then (s0 + s2) + (s1 + s3). Lane j = 0 of the row gets the result. */
+__device__ __forceinline__ float fold16_lanes(float a) {
+    const float v = a + __shfl_down(a, 8, 16);
+    const float s = v + __shfl_down(v, 4, 16);
+    const float u = s + __shfl_down(s, 2, 16);
+    return u + __shfl_down(u, 1, 16);
+}
+
+/* One wave a block, four router rows a block (sixteen lanes a row). */
+template <int NCH>
+__global__ __launch_bounds__(64) void route_kernel(route_args a) {
+    extern __shared__ float sh[];
+    float* sx = sh;             /* H: x */
+    float* sxn = sh + a.H;      /* H: normalized */
+    __shared__ float chains[16];
+    __shared__ float inv_s;
+    __shared__ int last_s;
+    const int lane = threadIdx.x, j = lane & 15, rrow = blockIdx.x * 4 + (lane >> 4);
+    const int tok = blockIdx.y;
+    const float* x = a.x + (size_t)tok * a.H;
+    /* this lane's chain of router weights, loaded before the norm is known */
+    float w[NCH];
+    const bool has_row = rrow < a.E;
+    const float* wr = a.router + (size_t)(has_row ? rrow : 0) * a.H + j;
+#pragma unroll
+    for (int m = 0; m < NCH; m++) w[m] = wr[16 * m];
+    for (int i = lane; i < a.H; i += 64) sx[i] = x[i];
+    __syncthreads();
+    if (lane < 16) {
+        /* engine/src/kernels.c:115-140: sixteen chains of squares (H a multiple of 16) */
+        float acc = 0.0f;
+        for (int m = 0; m < NCH; m++) acc = fmaf(sx[16 * m + lane], sx[16 * m + lane], acc);
+        chains[lane] = acc;
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float v[8];
+        for (int q = 0; q < 8; q++) v[q] = chains[q] + chains[q + 8];
+        const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
+        const float ss = (s0 + s2) + (s1 + s3);
+        /* kernels.c:146: 1 / sqrtf(ss / n + eps), each step correctly rounded */
+        inv_s = 1.0f / sqrtf(ss / (float)a.H + a.eps);
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int i = lane; i < a.H; i += 64) {
+        const float t = sx[i] * inv;
+        sxn[i] = t * a.norm_w[i];
+    }
+    __syncthreads();
+    if (a.xn_out && blockIdx.x == 0)
+        for (int i = lane; i < a.H; i += 64) a.xn_out[(size_t)tok * a.H + i] = sxn[i];
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NCH; m++) acc = fmaf(w[m], sxn[16 * m + j], acc);
+    const float logit = fold16_lanes(acc);
+    if (has_row && j == 0) a.logits[(size_t)tok * a.E + rrow] = logit;
+    if (!a.topk) return;
+
+    /* The last block of this row to finish routes it (engine/src/model.c:626-703). */
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (lane == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(a.counter + tok, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last_s = prev == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last_s) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const int E = a.E, K = a.K;
+    const float* lg_g = a.logits + (size_t)tok * E;
+    float lg[ROUTE_E_MAX / 64];
+    unsigned taken = 0;
+#pragma unroll
+    for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+        const int e = lane + 64 * i;
+        lg[i] = e < E ? __builtin_nontemporal_load(lg_g + e) : 0.0f;
+    }
+    const float l0 = __shfl(lg[0], 0, 64);
+    __shared__ int chosen_s[ROUTE_K_MAX];
+    for (int k = 0; k < K; k++) {
+        /* the first expert not yet taken, and the largest non-NaN logit among
+           those not taken, the lowest index between equals */
+        int first = 0x7fffffff, bi = 0x7fffffff;
+        float bv = 0.0f;
+#pragma unroll
+        for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+            const int e = lane + 64 * i;
+            if (e < E && !(taken >> i & 1)) {
+                first = min(first, e);
+                const float v = lg[i];
+                if (v == v && (bi == 0x7fffffff || v > bv)) { bv = v; bi = e; }
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            const int of = __shfl_xor(first, o, 64), oi = __shfl_xor(bi, o, 64);
+            const float ov = __shfl_xor(bv, o, 64);
+            first = min(first, of);
+            const bool take = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
+            if (take) { bv = ov; bi = oi; }
+        }
+        /* A NaN where the scan starts is never displaced (x > NaN is false). */
+        const float fv = __shfl(lg[first >> 6 < ROUTE_E_MAX / 64 ? first >> 6 : 0], first & 63, 64);
+        const int pick = (fv != fv || bi == 0x7fffffff) ? first : bi;
+        if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
+        if (lane == 0) chosen_s[k] = pick;
+    }
+    /* softmax over every expert: max as the CPU scans it, the sum of exp(l - max) */
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
+        if (lane + 64 * i < E) mx = fmaxf(mx, lg[i]);
+    mx = wave_max(mx);
+    if (l0 != l0) mx = l0;
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
+        if (lane + 64 * i < E) sum += expf(lg[i] - mx);
+    sum = wave_sum(sum);
+    __syncthreads();
+    if (lane == 0) {
+        route_out* o = a.out + tok;
+        int order[ROUTE_K_MAX];
+        for (int k = 0; k < K; k++) {
+            o->chosen[k] = chosen_s[k];
+            const int e = chosen_s[k];
+            int q = k;
+            while (q > 0 && order[q - 1] > e) { order[q] = order[q - 1]; q--; }
+            order[q] = e;
+        }
+        float wts[ROUTE_K_MAX], share[ROUTE_K_MAX];
+        for (int k = 0; k < K; k++) {
+            const float l = __builtin_nontemporal_load(lg_g + order[k]);
+            wts[k] = expf(l - mx) / sum;
+        }
+        if (a.renorm) {
+            for (int k = 0; k < K; k++) {
+                const float sv = wts[k];
+                int q = k;
+                while (q > 0 && share[q - 1] < sv) { share[q] = share[q - 1]; q--; }
+                share[q] = sv;
+            }
+            float total = 0.0f;
+            for (int k = 0; k < K; k++) total += share[k];
+            for (int k = 0; k < K; k++) wts[k] /= total;
+        }
+        for (int k = 0; k < K; k++) {
+            o->ids[k] = order[k];
+            o->weights[k] = wts[k];
+        }
+        __hip_atomic_store(a.counter + tok, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+hipError_t launch_route(const route_args& a, hipStream_t s) {
+    if (a.H % 16 || a.E < 1 || a.E > ROUTE_E_MAX || a.n_rows < 1 || (a.topk && (a.K < 1 || a.K > ROUTE_K_MAX || a.K > a.E)))
+        return hipErrorInvalidValue;
+    const dim3 grid((a.E + 3) / 4, a.n_rows);
+    const size_t lds = 2 * (size_t)a.H * sizeof(float);
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    switch (a.H / 16) {
+        case 16: route_kernel<16><<<grid, 64, lds, s>>>(a); break;
+        case 32: route_kernel<32><<<grid, 64, lds, s>>>(a); break;
+        case 64: route_kernel<64><<<grid, 64, lds, s>>>(a); break;
+        case 128: route_kernel<128><<<grid, 64, lds, s>>>(a); break;
+        case 256: route_kernel<256><<<grid, 64, lds, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------------ */
+/* Experts, one token                                                  */
+/* ------------------------------------------------------------------ */
+
+/* Slices of one row split among LPR lanes, SPL slices a lane; 64 / LPR rows
+   a wave at once. */
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    /* engine/src/ops.c:283-288: (g / (1 + exp(-g))) * u */
+    const float den = 1.0f + expf(-g);
+    return (g / den) * u;
+}
+
+template <int DT, int LPR, int SPL>
+__global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
+    constexpr int RPW = WAVE / LPR;
+    const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
+    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
+    const int I = a.gate.rows;
+    xslice xs[SPL];
+#pragma unroll
+    for (int j = 0; j < SPL; j++) load_xslice(DT, al + LPR * j, a.xn, xs[j]);
+    const int units = a.K * I;
+    for (int u0 = wave * 2 * RPW; u0 < units; u0 += nwaves * 2 * RPW) {
+        int u[2], e[2], r[2];
+        qraw g[2][SPL], v[2][SPL];
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            u[q] = u0 + q * RPW + sub;
+            const int uu = u[q] < units ? u[q] : units - 1;
+            const int k = uu / I;
+            r[q] = uu - k * I;
+            e[q] = a.rt->ids[k];
+#pragma unroll
+            for (int j = 0; j < SPL; j++) {
+                slice_load<DT>(a.gate, e[q], r[q], al + LPR * j, g[q][j]);
+                slice_load<DT>(a.up, e[q], r[q], al + LPR * j, v[q][j]);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            float pg = 0.f, pu = 0.f;
+#pragma unroll
+            for (int j = 0; j < SPL; j++) {
+                pg += slice_dot<DT>(g[q][j], al + LPR * j, xs[j]);
+                pu += slice_dot<DT>(v[q][j], al + LPR * j, xs[j]);
+            }
+            pg = row_sum<LPR>(pg);
+            pu = row_sum<LPR>(pu);
+            if (al == 0 && u[q] < units) a.act[u[q]] = silu_mul(pg, pu);
+        }
+    }
+}
+
+template <int DT, int LPR, int SPL>
+static hipError_t ein_launch(const experts_in_args& a, hipStream_t s) {
+    constexpr int RPW = WAVE / LPR;
+    const int units = a.K * a.gate.rows;
+    const int waves = (units + 2 * RPW - 1) / (2 * RPW);
+    const int blocks = (waves + 3) / 4;
+    experts_in_kernel<DT, LPR, SPL><<<blocks, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t ein_dispatch(const experts_in_args& a, hipStream_t s) {
+    switch (a.gate.cols / 32) {
+        case 4: return ein_launch<DT, 4, 1>(a, s);
+        case 8: return ein_launch<DT, 8, 1>(a, s);
+        case 16: return ein_launch<DT, 16, 1>(a, s);
+        case 32: return ein_launch<DT, 32, 1>(a, s);
+        case 64: return ein_launch<DT, 64, 1>(a, s);
+        case 128: return ein_launch<DT, 64, 2>(a, s);
+        case 256: return ein_launch<DT, 64, 4>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s) {
+    if (a.gate.dtype != a.up.dtype || a.gate.rows != a.up.rows || a.gate.cols != a.up.cols || a.K < 1 || a.K > ROUTE_K_MAX)
+        return hipErrorInvalidValue;
+    switch (a.gate.dtype) {
+        case VITNA_DTYPE_Q8_0: return ein_dispatch<VITNA_DTYPE_Q8_0>(a, s);
+        case VITNA_DTYPE_Q4_K: return ein_dispatch<VITNA_DTYPE_Q4_K>(a, s);
+        case VITNA_DTYPE_Q6_K: return ein_dispatch<VITNA_DTYPE_Q6_K>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+/* One output row a wave: every (expert, slice) item of the row among the 64
+   lanes, IPL items a lane, each lane's items fixed for every row, so its
+   activations stay in registers. The weighted sum over experts is reduced
+   across the wave. */
+template <int DT, int IPL>
+__global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
+    const int H = a.down.rows, I = a.down.cols, S = I / 32, N = a.K * S;
+    xslice xs[IPL];
+    float wk[IPL];
+    int ek[IPL], tk[IPL];
+#pragma unroll
+    for (int j = 0; j < IPL; j++) {
+        const int i = lane + 64 * j;
+        const bool ok = i < N;
+        const int k = ok ? i / S : 0;
+        tk[j] = ok ? i - k * S : 0;
+        ek[j] = a.rt->ids[k];
+        wk[j] = ok ? a.rt->weights[k] : 0.0f;
+        load_xslice(DT, tk[j], a.act + (size_t)k * I, xs[j]);
+    }
+    for (int r0 = wave * 2; r0 < H; r0 += nwaves * 2) {
+        qraw q[2][IPL];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int r = r0 + h < H ? r0 + h : H - 1;
+#pragma unroll
+            for (int j = 0; j < IPL; j++) slice_load<DT>(a.down, ek[j], r, tk[j], q[h][j]);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float p = 0.f;
+#pragma unroll
+            for (int j = 0; j < IPL; j++) p = fmaf(wk[j], slice_dot<DT>(q[h][j], tk[j], xs[j]), p);
+            p = wave_sum(p);
+            const int r = r0 + h;
+            if (lane == 0 && r < H) a.y[r] = a.add ? a.y[r] + p : p;
+        }
+    }
+}
+
+template <int DT, int IPL>
+static hipError_t edn_launch(const experts_down_args& a, hipStream_t s) {
+    const int waves = (a.down.rows + 1) / 2;
+    experts_down_kernel<DT, IPL><<<(waves + 3) / 4, 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t edn_dispatch(const experts_down_args& a, hipStream_t s) {
+    const int N = a.K * (a.down.cols / 32), ipl = (N + 63) / 64;
+    switch (ipl) {
+        case 1: return edn_launch<DT, 1>(a, s);
+        case 2: return edn_launch<DT, 2>(a, s);
+        case 3: return edn_launch<DT, 3>(a, s);
+        case 4: return edn_launch<DT, 4>(a, s);
+        case 5: return edn_launch<DT, 5>(a, s);
+        case 6: return edn_launch<DT, 6>(a, s);
+        case 8: return edn_launch<DT, 8>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s) {
+    if (a.K < 1 || a.K > ROUTE_K_MAX || a.down.cols % 32) return hipErrorInvalidValue;
+    switch (a.down.dtype) {
+        case VITNA_DTYPE_Q8_0: return edn_dispatch<VITNA_DTYPE_Q8_0>(a, s);
+        case VITNA_DTYPE_Q4_K: return edn_dispatch<VITNA_DTYPE_Q4_K>(a, s);
+        case VITNA_DTYPE_Q6_K: return edn_dispatch<VITNA_DTYPE_Q6_K>(a, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+/* ------------------------------------------------------------------ */
+/* Dense projections                                                   */
+/* ------------------------------------------------------------------ */
+
+template <int DT, int LPR, int SPL>
+__device__ __forceinline__ void gemv_rows(const qmat& w, float* __restrict__ y, int add, const xslice* xs, int unit0, int ustep,
+                                          int lane) {
+    constexpr int RPW = WAVE / LPR;
+    const int sub = lane / LPR, al = lane % LPR;
+    const int units = (w.rows + RPW - 1) / RPW;
+    for (int u = unit0; u < units; u += 2 * ustep) {
+        qraw q[2][SPL];
+        int r[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            r[h] = (u + h * ustep) * RPW + sub;
+            const int rr = r[h] < w.rows ? r[h] : w.rows - 1;
+#pragma unroll
+            for (int j = 0; j < SPL; j++) {
+                if (DT == VITNA_DTYPE_F32) continue;
+                slice_load<DT>(w, 0, rr, al + LPR * j, q[h][j]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int rr = r[h] < w.rows ? r[h] : w.rows - 1;
+            float p = 0.f;
+#pragma unroll
+            for (int j = 0; j < SPL; j++) {
+                if (DT == VITNA_DTYPE_F32)
+                    p += slice_dot_f32(reinterpret_cast<const float*>(w.p[0]) + (size_t)rr * w.cols, al + LPR * j, xs[j]);
+                else
+                    p += slice_dot<DT>(q[h][j], al + LPR * j, xs[j]);
+            }
+            p = row_sum<LPR>(p);
+            if (al == 0 && r[h] < w.rows && (u + h * ustep) < units) y[r[h]] = add ? y[r[h]] + p : p;
+        }
+    }
+}
+
+template <int D0, int D1, int D2, int LPR, int SPL, bool NORM>
+__global__ __launch_bounds__(256) void gemv_kernel(gemv_args a) {
+    extern __shared__ float sh[];
+    const int lane = threadIdx.x & 63;
+    const int H = a.w[0].cols;
+    const float* xin = a.x;
+    if (NORM) {
+        __shared__ float red[4];
+        float ss = 0.f;
+        for (int i = threadIdx.x; i < H; i += blockDim.x) ss = fmaf(a.x[i], a.x[i], ss);
+        ss = wave_sum(ss);
+        if (lane == 0) red[threadIdx.x / WAVE] = ss;
+        __syncthreads();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        const float inv = 1.0f / sqrtf(ss / (float)H + a.eps);
+        for (int i = threadIdx.x; i < H; i += blockDim.x) sh[i] = (a.x[i] * inv) * a.norm_w[i];
+        __syncthreads();
+        xin = sh;
+    }
+    xslice xs[SPL];
+    /* all matrices share a width, and so the lane's slices */
+#pragma unroll
+    for (int j = 0; j < SPL; j++) load_xslice(D0, lane % LPR + LPR * j, xin, xs[j]);
+    /* matrices with another slice layout reload below */
+    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
+    constexpr int RPW = WAVE / LPR;
+    /* the waves are shared among the matrices in proportion to their rows */
+    int total = 0, units[3] = {0, 0, 0};
+    for (int i = 0; i < a.n; i++) { units[i] = (a.w[i].rows + RPW - 1) / RPW; total += units[i]; }
+    /* wave w takes units w, w + nwaves, ... of the concatenated list */
+    int base = 0;
+    for (int i = 0; i < a.n; i++) {
+        const int u0 = wave - base;
+        /* first unit of matrix i this wave takes: smallest u >= 0 with (base + u - wave) % nwaves == 0 */
+        int first = u0 % nwaves;
+        if (first < 0) first += nwaves;
+        if (first < units[i]) {
+            if (i == 0) {
+                gemv_rows<D0, LPR, SPL>(a.w[0], a.y[0], a.add, xs, first, nwaves, lane);
+            } else if (i == 1) {
+                if (D1 != D0) {
+#pragma unroll
+                    for (int j = 0; j < SPL; j++) load_xslice(D1, lane % LPR + LPR * j, xin, xs[j]);
+                }
+                gemv_rows<D1, LPR, SPL>(a.w[1], a.y[1], a.add, xs, first, nwaves, lane);
+            } else {
+#pragma unroll
+                for (int j = 0; j < SPL; j++) load_xslice(D2, lane % LPR + LPR * j, xin, xs[j]);
+                gemv_rows<D2, LPR, SPL>(a.w[2], a.y[2], a.add, xs, first, nwaves, lane);
+            }
+        }
+        base += units[i];
+    }
+    (void)total;
+}
+
+template <int D0, int D1, int D2, bool NORM>
+static hipError_t gemv_by_width(const gemv_args& a, hipStream_t s) {
+    const int S = a.w[0].cols / 32;
+    int units = 0;
+    const int lpr = S < 64 ? S : 64, rpw = WAVE / lpr;
+    for (int i = 0; i < a.n; i++) units += (a.w[i].rows + rpw - 1) / rpw;
+    int waves = (units + 1) / 2;
+    int blocks = (waves + 3) / 4;
+    if (blocks < 1) blocks = 1;
+    const size_t lds = NORM ? (size_t)a.w[0].cols * sizeof(float) : 0;
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    switch (S) {
+        case 4: gemv_kernel<D0, D1, D2, 4, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
+        case 8: gemv_kernel<D0, D1, D2, 8, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
+        case 16: gemv_kernel<D0, D1, D2, 16, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
+        case 32: gemv_kernel<D0, D1, D2, 32, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
+        case 64: gemv_kernel<D0, D1, D2, 64, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
+        case 128: gemv_kernel<D0, D1, D2, 64, 2, NORM><<<blocks, 256, lds, s>>>(a); break;
+        case 256: gemv_kernel<D0, D1, D2, 64, 4, NORM><<<blocks, 256, lds, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int D0, int D1, int D2>
+static hipError_t gemv_norm(const gemv_args& a, hipStream_t s) {
+    return a.norm_w ? gemv_by_width<D0, D1, D2, true>(a, s) : gemv_by_width<D0, D1, D2, false>(a, s);
+}
+
+hipError_t launch_gemv(const gemv_args& a, hipStream_t s) {
+    if (a.n < 1 || a.n > 3) return hipErrorInvalidValue;
+    for (int i = 1; i < a.n; i++)
+        if (a.w[i].cols != a.w[0].cols) return hipErrorInvalidValue;
+    const int d0 = a.w[0].dtype, d1 = a.n > 1 ? a.w[1].dtype : d0, d2 = a.n > 2 ? a.w[2].dtype : d1;
+    constexpr int Q8 = VITNA_DTYPE_Q8_0, Q4 = VITNA_DTYPE_Q4_K, Q6 = VITNA_DTYPE_Q6_K, F = VITNA_DTYPE_F32;
+#define GEMV_CASE(A, B, C) \
+    if (d0 == A && d1 == B && d2 == C) return gemv_norm<A, B, C>(a, s);
+    GEMV_CASE(Q4, Q4, Q6)
+    GEMV_CASE(Q4, Q4, Q4)
+    GEMV_CASE(Q8, Q8, Q8)
+    GEMV_CASE(Q6, Q6, Q6)
+    GEMV_CASE(Q4, Q6, Q6)
+    GEMV_CASE(Q6, Q6, Q4)
+    GEMV_CASE(F, F, F)
+#undef GEMV_CASE
+    return hipErrorInvalidValue;
+}
+
+/* ------------------------------------------------------------------ */
+/* Embedding                                                           */
+/* ------------------------------------------------------------------ */
+
+__global__ void embed_kernel(qmat m, const int32_t* token_dev, int token, float* __restrict__ x) {
+    const int t = token_dev ? *token_dev : token;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < m.cols; c += gridDim.x * blockDim.x) x[c] = widen_one(m, 0, t, c);
+}
+
+hipError_t launch_embed(const qmat& embed, const int32_t* token_dev, int token, float* x, hipStream_t s) {
+    embed_kernel<<<(embed.cols + 255) / 256, 256, 0, s>>>(embed, token_dev, token, x);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------------ */
+/* Seeded N(0,1) fill (keys and values of a synthetic cache)           */
+/* ------------------------------------------------------------------ */
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+__global__ void fill_normal_kernel(float* __restrict__ out, size_t n, uint64_t seed) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const uint64_t h = mix64(seed * 0x9e3779b97f4a7c15ull + i);
+        const float u1 = ((float)(uint32_t)(h >> 40) + 1.0f) * (1.0f / 16777217.0f);
+        const float u2 = (float)(uint32_t)(h & 0xffffff) * (1.0f / 16777216.0f);
+        out[i] = sqrtf(-2.0f * logf(u1)) * cosf(6.28318530718f * u2);
+    }
+}
+
+hipError_t launch_fill_normal(float* out, size_t n, uint64_t seed, hipStream_t s) {
+    if (!n) return hipSuccess;
+    fill_normal_kernel<<<4096, 256, 0, s>>>(out, n, seed);
+    return hipGetLastError();
+}

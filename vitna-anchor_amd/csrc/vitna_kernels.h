@@ -1,0 +1,147 @@
+/**
+ * vitna_kernels.h - Host-side launchers of libvitna_hip's kernels, shared by
+ * the translation units (kernels_*.hip) and the engine (engine.hip). Every
+ * launcher checks on the host that the shapes it is given are the shapes its
+ * kernel assumes, and returns hipErrorInvalidValue otherwise, before anything
+ * is launched.
+ */
+
+#ifndef VITNA_KERNELS_H
+#define VITNA_KERNELS_H
+
+#include "vitna_hip_internal.h"
+
+#define ROUTE_K_MAX 16
+#define ROUTE_E_MAX 512
+
+/* A layer's routing on the device: the experts in order of id (ids), their
+   weights, and the router's choice largest first (chosen). */
+struct route_out {
+    int32_t ids[ROUTE_K_MAX];
+    float weights[ROUTE_K_MAX];
+    int32_t chosen[ROUTE_K_MAX];
+};
+
+/* ---- upload and checking ---- */
+
+/* Split n_blocks GGUF blocks of dtype (AoS, as stored) at src into planes
+   dst (plane pointers of one matrix, rows x nb). */
+hipError_t launch_repack(const uint8_t* src, const qmat& dst, hipStream_t s);
+/* Widen matrix m (expert e) into out, rows x cols, exactly: from the planes
+   (way 0) or from the GGUF blocks at src (way 1). */
+hipError_t launch_widen_planes(const qmat& m, int e, float* out, hipStream_t s);
+hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_t cols, float* out, hipStream_t s);
+
+/* ---- routing ---- */
+
+/* RMSNorm of x (n_rows rows of H, row stride H) with norm_w, in the
+   reference CPU's order, written to xn_out when it is not NULL; the router's
+   logits for each row (E of them, the router F32 [E x H]) in the reference
+   CPU's order into logits (row stride E); and, when topk, each row's routing
+   into out[row] (K of E, renormalized or not). counter: n_rows zeroed
+   unsigned ints the kernel leaves zeroed. */
+struct route_args {
+    const float* x;
+    const float* norm_w;
+    const float* router;
+    float* xn_out;
+    float* logits;
+    route_out* out;
+    unsigned* counter;
+    int H, E, K, renorm, topk, n_rows;
+    float eps;
+};
+hipError_t launch_route(const route_args& a, hipStream_t s);
+
+/* ---- experts, one token ---- */
+
+/* act[k * I + r] = silu(gate_e[r] . xn) * (up_e[r] . xn) for e = ids[k]. */
+struct experts_in_args {
+    qmat gate, up;
+    const float* xn;
+    const route_out* rt;
+    float* act;
+    int K;
+};
+hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s);
+
+/* y[r] (+)= sum_k w_k (down_{ids[k]}[r] . act_k), into y or, with add,
+   onto it. */
+struct experts_down_args {
+    qmat down;
+    const float* act;
+    const route_out* rt;
+    float* y;
+    int K, add;
+};
+hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s);
+
+/* ---- dense projections ---- */
+
+/* Up to three matrices of the same width multiplied by one vector:
+   y_i = W_i . xin, where xin = RMSNorm(x, norm_w) when norm_w is set (each
+   block computes it) and x otherwise; with add, y_i += W_i . xin. */
+struct gemv_args {
+    qmat w[3];
+    float* y[3];
+    int n;          /* matrices */
+    const float* x;
+    const float* norm_w;
+    float eps;
+    int add;
+};
+hipError_t launch_gemv(const gemv_args& a, hipStream_t s);
+
+/* x = the embedding row of token (read from the device word *token when
+   token_dev is set, else token), widened exactly. */
+hipError_t launch_embed(const qmat& embed, const int32_t* token_dev, int token, float* x, hipStream_t s);
+
+/* ---- attention (kernels_attn.hip) ---- */
+
+/* A row of a pass: the token, its position, and the sequence whose cache it
+   reads and writes (engine/include/model_cuda.h:21, vitna_cuda_row_t). */
+struct row_rec {
+    int32_t token, pos, seq;
+};
+
+/* Decode attention for n_rows rows, one layer: each row's q and k through the
+   per-head RMSNorm (when q_norm is set) and the half-split RoPE at its
+   position, its k and v written into its sequence's cache at that position,
+   and softmax(q k^T / sqrt(hd)) v over positions 0..pos into att. Positions
+   are split into chunks of ATTN_CHUNK; the last chunk of a (row, kv head) to
+   finish merges them. */
+#define ATTN_CHUNK 64
+struct attn_args {
+    const float* q_raw;    /* [n_rows][n_heads * hd] */
+    const float* k_raw;    /* [n_rows][n_kv * hd] */
+    const float* v_raw;
+    const float* q_norm;   /* hd, or NULL */
+    const float* k_norm;
+    const float* cos_tab;  /* [ctx][hd/2] */
+    const float* sin_tab;
+    float* k_cache;        /* sequence 0 of this layer: [ctx][n_kv * hd] */
+    float* v_cache;
+    size_t seq_stride;     /* floats from one sequence's cache of this layer to the next's */
+    const row_rec* rows;   /* device, n_rows */
+    int n_rows;
+    float* partial;        /* [n_rows][n_kv][splits_max][G][hd + 2] */
+    unsigned* counter;     /* [n_rows][n_kv], zeroed, left zeroed */
+    float* att;            /* [n_rows][n_heads * hd] */
+    int n_heads, n_kv, hd, ctx, splits_max;
+    float eps;
+    /* 0: this kernel normalizes and rotates q and k and stores k and v at
+       each row's position itself (rows of distinct sequences). 1: q_raw holds
+       the prepared queries and the cache already holds every row's k and v
+       (launch_attention_prepare ran first: rows may share a sequence). */
+    int prepared;
+    float* q_out;          /* prepare: where the prepared queries go */
+};
+hipError_t launch_attention(const attn_args& a, hipStream_t s);
+/* The prepare pass of prepared = 1: q normalized and rotated into q_out, k
+   normalized and rotated and v stored into the cache at each row's position. */
+hipError_t launch_attention_prepare(const attn_args& a, hipStream_t s);
+
+/* ---- helpers ---- */
+hipError_t launch_fill_normal(float* out, size_t n, uint64_t seed, hipStream_t s);
+
+#endif
