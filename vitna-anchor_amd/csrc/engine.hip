@@ -107,14 +107,16 @@ static bool width_ok(size_t cols) {
     return cols % 32 == 0 && (s == 4 || s == 8 || s == 16 || s == 32 || s == 64 || s == 128 || s == 256);
 }
 
-static bool matrix_ok(const vitna_matrix_t* w, size_t rows, size_t cols, const char* what, char* err, size_t err_len) {
+static bool matrix_ok(const vitna_matrix_t* w, size_t rows, size_t cols, const char* what, char* err, size_t err_len,
+                      bool row_gemv = true) {
     if (!w->data) return fail(err, err_len, "%s has no data", what);
     if (w->rows != rows || w->cols != cols)
         return fail(err, err_len, "%s is %zu x %zu where %zu x %zu is needed", what, w->rows, w->cols, rows, cols);
     if (!quant_ok(w->dtype))
         return fail(err, err_len, "%s is %s; this device path reads Q8_0, Q4_K and Q6_K", what, dtype_name(w->dtype));
     if (!vitna_matrix_row_bytes(w->dtype, cols)) return fail(err, err_len, "%s: %zu columns are not whole %s blocks", what, cols, dtype_name(w->dtype));
-    if (!width_ok(cols)) return fail(err, err_len, "%s: width %zu is not one the kernels take (32 x 4 .. 256, powers of two)", what, cols);
+    if (row_gemv && !width_ok(cols))
+        return fail(err, err_len, "%s: width %zu is not one the kernels take (32 x 4 .. 256, powers of two)", what, cols);
     return true;
 }
 
@@ -146,7 +148,7 @@ static bool check_shapes(const vitna_llama_t* m, char* err, size_t err_len) {
             snprintf(what, sizeof(what), "layer %zu expert %zu up", l, e);
             if (!matrix_ok(&x->up, c->intermediate, c->hidden, what, err, err_len)) return false;
             snprintf(what, sizeof(what), "layer %zu expert %zu down", l, e);
-            if (!matrix_ok(&x->down, c->hidden, c->intermediate, what, err, err_len)) return false;
+            if (!matrix_ok(&x->down, c->hidden, c->intermediate, what, err, err_len, false)) return false;
             if (x->gate.dtype != gdt || x->up.dtype != gdt || x->down.dtype != ddt)
                 return fail(err, err_len, "layer %zu: every expert's gate and up, and every expert's down, must share a dtype", l);
         }
@@ -687,7 +689,7 @@ extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_
     if (!gate || !up || !down || !norm_w || !x) return fail(err, err_len, "missing arguments");
     const size_t H = gate->cols, I = gate->rows;
     if (!matrix_ok(gate, I, H, "gate", err, err_len) || !matrix_ok(up, I, H, "up", err, err_len) ||
-        !matrix_ok(down, H, I, "down", err, err_len))
+        !matrix_ok(down, H, I, "down", err, err_len, false))
         return false;
     if (gate->dtype != up->dtype) return fail(err, err_len, "gate and up must share a dtype");
     if (H % 16 || H > 8192) return fail(err, err_len, "width %zu", H);
