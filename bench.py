@@ -75,23 +75,15 @@ def main():
         dev.kv(0, l, 0, pos, kc[l, :pos], vc[l, :pos])
     log("uploaded to %s in %.1f s" % (dev.device_name(), time.time() - t0))
 
-    import torch
-    stream = torch.cuda.ExternalStream(dev.lib.vitna_hip_stream(dev.g))
+    # The library links the image's HIP runtime; torch bundles another, so torch is not loaded in this process.
+    # dev.sync() is the barrier (hipStreamSynchronize on the only stream the model uses).
     for _ in range(args.warmup):
         dev.step_async(0, token, pos)
     dev.sync()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record(stream)
     t_wall = time.perf_counter()
-    for _ in range(args.steps):
-        dev.step_async(0, token, pos)
-    ev1.record(stream)
+    ms = dev.time_steps(0, token, pos, args.steps)  # HIP events on the model's stream around the K steps
     dev.sync()
-    torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t_wall) * 1000.0 / args.steps
-    ms = ev0.elapsed_time(ev1) / args.steps
     tok_s = 1000.0 / ms
     log("step: %.3f ms (events), %.3f ms (wall), %.1f tok/s" % (ms, wall_ms, tok_s))
 

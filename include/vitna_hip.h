@@ -178,6 +178,19 @@ bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, s
 bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int reps, int warmup, double* avg_us, double* bytes, char* err,
                            size_t err_len);
 
+/** steps device-resident decode steps (as vitna_hip_moe_step_async, the
+    same token and position each time) timed with HIP events on the model's
+    stream: the average milliseconds a step. */
+bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, int steps, double* ms_per_step, char* err,
+                          size_t err_len);
+
+/** For checking: the device's routing rule (the one every expert kernel
+    applies to a token's router logits) on n_experts given logits: the choice
+    largest first, the chosen in order of id and their weights, as
+    engine/src/model.c:626-703 routes. */
+bool vitna_hip_route_check(const float* logits, int n_experts, int k, bool renormalize, int32_t* chosen, int32_t* ids, float* weights,
+                           char* err, size_t err_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -115,9 +115,8 @@ def test_create_refuses_bad_shapes_before_touching_a_device():
 
 
 def test_probe_without_gpu_says_why():
-    import torch
-    if torch.cuda.device_count() > 0:
-        pytest.skip("a GPU is present")
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU driver is present")
     lib = va.hip()
     err = C.create_string_buffer(256)
     assert not lib.vitna_cuda_probe(err, 256)

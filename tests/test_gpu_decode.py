@@ -203,3 +203,46 @@ def test_device_step_matches_cpu(name, pos, token):
     finally:
         dev.close()
         model.free()
+
+
+def routing_cases():
+    rng = np.random.default_rng(11)
+    cases = []
+    for E, K in ((128, 8), (64, 8), (16, 4), (512, 16), (8, 8)):
+        cases.append(("random E%d K%d" % (E, K), rng.normal(0, 1, E).astype(np.float32), K))
+    ties = np.zeros(128, np.float32)
+    ties[[3, 9, 17, 40, 41, 100]] = 2.0
+    ties[[5, 6]] = 1.5
+    cases.append(("ties", ties, 8))
+    cases.append(("all equal", np.full(64, 0.25, np.float32), 8))
+    q = np.round(rng.normal(0, 1, 128) * 4).astype(np.float32) / 4  # many exact duplicates
+    cases.append(("quantized", q, 8))
+    inf = rng.normal(0, 1, 128).astype(np.float32)
+    inf[[7, 70]] = np.inf
+    inf[[1, 2]] = -np.inf
+    cases.append(("infinities", inf, 8))
+    nan0 = rng.normal(0, 1, 128).astype(np.float32)
+    nan0[0] = np.nan
+    cases.append(("NaN first", nan0, 8))
+    nanl = rng.normal(0, 1, 128).astype(np.float32)
+    nanl[[5, 77]] = np.nan
+    cases.append(("NaN later", nanl, 8))
+    big = (rng.normal(0, 1, 128) * 40).astype(np.float32)
+    cases.append(("wide range", big, 8))
+    return cases
+
+
+@pytest.mark.parametrize("renorm", [False, True])
+def test_device_routing_rule(renorm):
+    """The device's top-k / softmax / renormalization against the reference's rule (oracle.route), on crafted
+    logits: ties (lower index first), duplicates, infinities, NaN where a pass starts and later. Choice and order
+    identical; weights within 2 ulp-ish (the device's expf and sum order)."""
+    for name, lg, K in routing_cases():
+        say("routing", name, renorm)
+        ch, ids, w = va.route_check(lg, K, renorm)
+        rch, rorder, rw = oracle.route(lg, K, renorm)
+        assert np.array_equal(ch, rch), (name, ch, rch)
+        assert np.array_equal(ids, rorder), (name, ids, rorder)
+        fin = np.isfinite(rw)
+        assert np.array_equal(fin, np.isfinite(w)), name
+        assert np.allclose(w[fin], rw[fin], rtol=3e-6, atol=0), (name, w, rw)

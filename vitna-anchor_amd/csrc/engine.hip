@@ -52,7 +52,6 @@ struct vitna_cuda_model {
     /* scratch, ROWS_MAX rows */
     float *x, *xn, *q, *k, *v, *qp, *att, *act, *ypart, *rlogits, *vocab, *partial;
     route_out* rt;
-    unsigned *route_ctr, *attn_ctr;
     row_rec* rows_dev;
     row_rec* rows_host; /* pinned */
     hipEvent_t rows_copied;
@@ -124,7 +123,8 @@ static bool matrix_ok(const vitna_matrix_t* w, size_t rows, size_t cols, const c
 static bool check_shapes(const vitna_llama_t* m, char* err, size_t err_len) {
     const vitna_llama_config_t* c = &m->cfg;
     if (!c->n_experts) return fail(err, err_len, "this device path serves a mixture of experts, and the model is dense");
-    if (c->n_experts > ROUTE_E_MAX) return fail(err, err_len, "%zu experts; at most %d are routed on the device", c->n_experts, ROUTE_E_MAX);
+    if (c->n_experts > ROUTE_E_MAX || c->n_experts % 4)
+        return fail(err, err_len, "%zu experts; a multiple of 4, at most %d, are routed on the device", c->n_experts, ROUTE_E_MAX);
     if (c->n_experts_used < 1 || c->n_experts_used > ROUTE_K_MAX || c->n_experts_used > c->n_experts)
         return fail(err, err_len, "%zu experts a token; 1 to %d, and no more than the experts, are supported", c->n_experts_used, ROUTE_K_MAX);
     if (c->hidden % 256 || c->hidden > 8192) return fail(err, err_len, "hidden width %zu: a multiple of 256, at most 8192, is needed", c->hidden);
@@ -391,20 +391,18 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
          dalloc(g, &g->act, R * K * c->intermediate * 4, "scratch", err, err_len) &&
          dalloc(g, &g->ypart, R * K * H * 4, "scratch", err, err_len) &&
          dalloc(g, &g->rlogits, 2 * R * E * 4, "scratch", err, err_len) && dalloc(g, &g->rt, R * sizeof(route_out), "scratch", err, err_len) &&
-         dalloc(g, &g->route_ctr, R * 4, "scratch", err, err_len) && dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len);
+         dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len);
     if (ok && g->attention) {
         ok = dalloc(g, &g->q, R * qd * 4, "scratch", err, err_len) && dalloc(g, &g->qp, R * qd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->k, R * kd * 4, "scratch", err, err_len) && dalloc(g, &g->v, R * kd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->att, R * qd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->vocab, R * c->vocab * 4, "the logits", err, err_len) &&
              dalloc(g, &g->partial, (size_t)R * c->n_kv_heads * g->splits_max * G * (c->head_dim + 2) * 4, "attention partials", err, err_len) &&
-             dalloc(g, &g->attn_ctr, R * c->n_kv_heads * 4, "scratch", err, err_len) &&
              dalloc(g, &g->k_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the key cache", err, err_len) &&
              dalloc(g, &g->v_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the value cache", err, err_len);
     }
     if (!ok) return bail();
-    if (hipMemset(g->route_ctr, 0, R * 4) != hipSuccess || (g->attn_ctr && hipMemset(g->attn_ctr, 0, R * c->n_kv_heads * 4) != hipSuccess) ||
-        hipMemset(g->x, 0, R * H * 4) != hipSuccess || hipMemset(g->rt, 0, R * sizeof(route_out)) != hipSuccess) {
+    if (hipMemset(g->x, 0, R * H * 4) != hipSuccess || hipMemset(g->rt, 0, R * sizeof(route_out)) != hipSuccess) {
         fail(err, err_len, "clearing device scratch failed");
         return bail();
     }
@@ -443,12 +441,12 @@ static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, 
     a.rows = g->rows_dev;
     a.n_rows = 1;
     a.partial = g->partial;
-    a.counter = g->attn_ctr;
     a.att = g->att;
     a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx; a.splits_max = g->splits_max;
     a.eps = g->eps;
     a.prepared = prepared ? 1 : 0;
     e = launch_attention(a, g->stream);
+    if (e == hipSuccess) e = launch_attention_merge(a, g->stream);
     if (e != hipSuccess) return e;
     gemv_args go;
     memset(&go, 0, sizeof(go));
@@ -460,26 +458,27 @@ static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, 
     return launch_gemv(go, g->stream);
 }
 
-static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, bool topk, int n_rows, const float* x) {
+static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, int n_rows, const float* x, float* xn_out) {
     const dlayer& d = g->L[layer];
     route_args r;
     memset(&r, 0, sizeof(r));
     r.x = x;
     r.norm_w = d.mlp_norm;
     r.router = d.router;
-    r.xn_out = g->xn;
+    r.xn_out = xn_out;
     r.logits = logits;
-    r.out = g->rt;
-    r.counter = g->route_ctr;
-    r.H = g->H; r.E = g->E; r.K = g->K; r.renorm = g->renorm; r.topk = topk ? 1 : 0; r.n_rows = n_rows;
+    r.H = g->H; r.E = g->E; r.n_rows = n_rows;
     r.eps = g->eps;
     return launch_route(r, g->stream);
 }
 
-static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, float* y, int add) {
+/* The experts of one token: routed on the device from logits when they are
+   given, else as g->rt holds it. */
+static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, const float* logits, float* y, int add) {
     const dlayer& d = g->L[layer];
     experts_in_args ai;
-    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.act = g->act; ai.K = g->K;
+    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.logits = logits; ai.E = g->E; ai.renorm = g->renorm;
+    ai.act = g->act; ai.K = g->K;
     hipError_t e = launch_experts_in(ai, g->stream);
     if (e != hipSuccess) return e;
     experts_down_args ad;
@@ -529,17 +528,10 @@ extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int
     hipError_t e = hipSuccess;
     if (layer == 0) e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
     if (e == hipSuccess) e = enqueue_attention(g, (int)layer, 1, false);
-    if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, false, 1, g->x);
+    if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn);
     const bool nx = next && layer + 1 < (size_t)g->NL;
-    if (e == hipSuccess && nx) {
-        /* the next layer's router on the same residual; its norm must not replace this layer's */
-        const dlayer& d = g->L[layer + 1];
-        route_args r;
-        memset(&r, 0, sizeof(r));
-        r.x = g->x; r.norm_w = d.mlp_norm; r.router = d.router; r.xn_out = nullptr; r.logits = g->rlogits + g->E;
-        r.out = g->rt; r.counter = g->route_ctr; r.H = g->H; r.E = g->E; r.K = g->K; r.topk = 0; r.n_rows = 1; r.eps = g->eps;
-        e = launch_route(r, g->stream);
-    }
+    /* the next layer's router on the same residual; its norm must not replace this layer's */
+    if (e == hipSuccess && nx) e = enqueue_route(g, (int)layer + 1, g->rlogits + g->E, 1, g->x, nullptr);
     if (!check_launch(g, e, "the layer up to its router", err, err_len)) return false;
     HIP_TRY(hipMemcpyAsync(g->h_logits, g->rlogits, (nx ? 2 : 1) * g->E * 4, hipMemcpyDeviceToHost, g->stream), "copying the router's logits");
     HIP_TRY(hipStreamSynchronize(g->stream), "running the layer up to its router");
@@ -575,7 +567,7 @@ extern "C" bool vitna_cuda_moe_experts(struct vitna_cuda_model* g, size_t layer,
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (!put_routing(g, 1, ids, weights, k, err, err_len)) return false;
-    return check_launch(g, enqueue_experts(g, (int)layer, g->x, 1), "the experts", err, err_len);
+    return check_launch(g, enqueue_experts(g, (int)layer, nullptr, g->x, 1), "the experts", err, err_len);
 }
 
 extern "C" bool vitna_cuda_moe_head(struct vitna_cuda_model* g, float* logits, char* err, size_t err_len) {
@@ -730,10 +722,10 @@ extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_
         /* the norm a step uses (the router kernel's, with a one-row router) */
         route_args ra;
         memset(&ra, 0, sizeof(ra));
-        ra.x = dx; ra.norm_w = dw; ra.router = drouter; ra.xn_out = dxn; ra.logits = dl; ra.out = drt; ra.counter = dctr;
-        ra.H = (int)H; ra.E = 1; ra.K = 1; ra.topk = 0; ra.n_rows = 1; ra.eps = eps;
+        ra.x = dx; ra.norm_w = dw; ra.router = drouter; ra.xn_out = dxn; ra.logits = dl;
+        ra.H = (int)H; ra.E = 1; ra.n_rows = 1; ra.eps = eps;
         experts_in_args ai;
-        ai.gate = qg; ai.up = qu; ai.xn = dxn; ai.rt = drt; ai.act = dact; ai.K = 1;
+        ai.gate = qg; ai.up = qu; ai.xn = dxn; ai.rt = drt; ai.logits = nullptr; ai.E = 1; ai.renorm = 0; ai.act = dact; ai.K = 1;
         experts_down_args ad;
         ad.down = qd; ad.act = dact; ad.rt = drt; ad.y = dy; ad.K = 1; ad.add = 0;
         ok = launch_route(ra, s) == hipSuccess && launch_experts_in(ai, s) == hipSuccess && launch_experts_down(ad, s) == hipSuccess &&
@@ -758,8 +750,8 @@ static hipError_t enqueue_step_body(vitna_cuda_model* g) {
     hipError_t e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
     for (int l = 0; e == hipSuccess && l < g->NL; l++) {
         e = enqueue_attention(g, l, 1, false);
-        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, true, 1, g->x);
-        if (e == hipSuccess) e = enqueue_experts(g, l, g->x, 1);
+        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, 1, g->x, g->xn);
+        if (e == hipSuccess) e = enqueue_experts(g, l, g->rlogits, g->x, 1);
     }
     if (e == hipSuccess) e = enqueue_head(g);
     return e;
@@ -801,8 +793,8 @@ extern "C" bool vitna_hip_moe_step(struct vitna_cuda_model* g, size_t seq, int32
 extern "C" bool vitna_hip_moe_ffn(struct vitna_cuda_model* g, size_t layer, char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
-    hipError_t e = enqueue_route(g, (int)layer, g->rlogits, true, 1, g->x);
-    if (e == hipSuccess) e = enqueue_experts(g, (int)layer, g->x, 1);
+    hipError_t e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn);
+    if (e == hipSuccess) e = enqueue_experts(g, (int)layer, g->rlogits, g->x, 1);
     return check_launch(g, e, "the mixture of experts", err, err_len);
 }
 
@@ -891,8 +883,9 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
         switch (which) {
             case 0: {
                 experts_in_args ai;
-                ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.act = g->act; ai.K = K;
-                b = 2.0 * K * qmat_bytes(d.gate) + H * 4.0 + K * (double)g->I * 4;
+                ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.logits = g->rlogits; ai.E = g->E;
+                ai.renorm = g->renorm; ai.act = g->act; ai.K = K;
+                b = 2.0 * K * qmat_bytes(d.gate) + H * 4.0 + K * (double)g->I * 4 + g->E * 4.0;
                 return launch_experts_in(ai, g->stream);
             }
             case 1: {
@@ -903,7 +896,7 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
             }
             case 2:
                 b = (double)g->E * H * 4 + H * 8.0 + g->E * 4.0;
-                return enqueue_route(g, l, g->rlogits, true, 1, g->x);
+                return enqueue_route(g, l, g->rlogits, 1, g->x, g->xn);
             case 3: {
                 gemv_args ga;
                 memset(&ga, 0, sizeof(ga));
@@ -919,10 +912,11 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
                 a.cos_tab = g->cos_tab; a.sin_tab = g->sin_tab;
                 a.k_cache = g->k_cache + (size_t)l * g->layer_kv; a.v_cache = g->v_cache + (size_t)l * g->layer_kv;
                 a.seq_stride = (size_t)g->NL * g->layer_kv; a.rows = g->rows_dev; a.n_rows = 1; a.partial = g->partial;
-                a.counter = g->attn_ctr; a.att = g->att; a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx;
+                a.att = g->att; a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx;
                 a.splits_max = g->splits_max; a.eps = g->eps;
                 b = 0; /* set by the caller from the position */
-                return launch_attention(a, g->stream);
+                const hipError_t e = launch_attention(a, g->stream);
+                return e == hipSuccess ? launch_attention_merge(a, g->stream) : e;
             }
             case 5: {
                 gemv_args go;
@@ -976,4 +970,52 @@ extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, f
 extern "C" bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, char* err, size_t err_len) {
     (void)g; (void)layer; (void)x; (void)n;
     return fail(err, err_len, "prefill is not yet served");
+}
+
+extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, int steps, double* ms_per_step,
+                                     char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (steps < 1) return fail(err, err_len, "at least one step");
+    if (!ensure_graph(g, err, err_len)) return false;
+    if (!set_row(g, seq, token, pos, err, err_len)) return false;
+    hipEvent_t t0, t1;
+    HIP_TRY(hipEventCreate(&t0), "events");
+    HIP_TRY(hipEventCreate(&t1), "events");
+    HIP_TRY(hipStreamSynchronize(g->stream), "before timing");
+    HIP_TRY(hipEventRecord(t0, g->stream), "events");
+    for (int i = 0; i < steps; i++) {
+        if (!set_row(g, seq, token, pos, err, err_len)) return false;
+        HIP_TRY(hipGraphLaunch(g->step_graph, g->stream), "launching the step");
+    }
+    HIP_TRY(hipEventRecord(t1, g->stream), "events");
+    HIP_TRY(hipEventSynchronize(t1), "timing the steps");
+    float ms = 0;
+    HIP_TRY(hipEventElapsedTime(&ms, t0, t1), "events");
+    hipEventDestroy(t0);
+    hipEventDestroy(t1);
+    *ms_per_step = (double)ms / steps;
+    return true;
+}
+
+extern "C" bool vitna_hip_route_check(const float* logits, int n_experts, int k, bool renormalize, int32_t* chosen, int32_t* ids,
+                                      float* weights, char* err, size_t err_len) {
+    if (!logits || n_experts < 1 || n_experts > ROUTE_E_MAX || n_experts % 4 || k < 1 || k > ROUTE_K_MAX || k > n_experts)
+        return fail(err, err_len, "%d experts, %d a token: 1 to %d experts, a multiple of 4, and 1 to %d a token", n_experts, k,
+                    ROUTE_E_MAX, ROUTE_K_MAX);
+    float* dl = nullptr;
+    route_out* dro = nullptr;
+    bool ok = hipMalloc(&dl, n_experts * 4) == hipSuccess && hipMalloc(&dro, sizeof(route_out)) == hipSuccess;
+    route_out r;
+    ok = ok && hipMemcpy(dl, logits, n_experts * 4, hipMemcpyHostToDevice) == hipSuccess &&
+         launch_route_check(dl, n_experts, k, renormalize ? 1 : 0, dro, 0) == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
+         hipMemcpy(&r, dro, sizeof(r), hipMemcpyDeviceToHost) == hipSuccess;
+    hipFree(dl);
+    hipFree(dro);
+    if (!ok) return fail(err, err_len, "the device routing failed");
+    for (int i = 0; i < k; i++) {
+        if (chosen) chosen[i] = r.chosen[i];
+        if (ids) ids[i] = r.ids[i];
+        if (weights) weights[i] = r.weights[i];
+    }
+    return true;
 }

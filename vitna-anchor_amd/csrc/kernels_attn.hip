@@ -13,7 +13,9 @@
  * head of one row: four waves of 16 positions, four lanes a position in the
  * scores (hd / 4 dimensions a lane), a lane per dimension in the weighted sum
  * of values. Each of the G = n_heads / n_kv query heads sharing the kv head
- * is served by the same reads of the cache.
+ * is served by the same reads of the cache. Each block leaves its chunk's
+ * (max, sum, weighted values) per query head; attention_merge_kernel, one
+ * block per (row, query head), combines the chunks.
  */
 
 #include "vitna_kernels.h"
@@ -26,13 +28,19 @@
 template <int HD>
 __device__ void norm_rope(float* vecs, int nv, const float* wq, const float* wk, int k_from, float eps, const float* c,
                           const float* s, float* inv_s) {
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    constexpr int PL = HD / 64; /* elements a lane */
     if (wq) {
-        if (tid < nv) {
-            const float* v = vecs + tid * HD;
+        /* a wave a vector: the sum of squares across the wave */
+        for (int v = wave; v < nv; v += 4) {
             float ss = 0.f;
-            for (int d = 0; d < HD; d++) ss = fmaf(v[d], v[d], ss);
-            inv_s[tid] = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+            for (int i = 0; i < PL; i++) {
+                const float e = vecs[v * HD + lane + 64 * i];
+                ss = fmaf(e, e, ss);
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) inv_s[v] = 1.0f / sqrtf(ss / (float)HD + eps);
         }
         __syncthreads();
         for (int i = tid; i < nv * HD; i += blockDim.x) {
@@ -72,15 +80,17 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     __shared__ float sp[4][16][GMAX];
     __shared__ float wm[4][GMAX], wl[4][GMAX];
     __shared__ float wacc[4][GMAX][HD];
-    __shared__ int last_s;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     float* nk = sq + G * HD;
 
+    {
+        /* the G query heads: G * HD / 4 <= 256 float4, one a thread */
+        const float4* q4 = reinterpret_cast<const float4*>(a.q_raw + (size_t)row * a.n_heads * HD + (size_t)h * G * HD);
+        if (tid < G * HD / 4) reinterpret_cast<float4*>(sq)[tid] = q4[tid];
+    }
     if (a.prepared) {
-        for (int i = tid; i < G * HD; i += 256) sq[i] = a.q_raw[(size_t)row * a.n_heads * HD + (size_t)h * G * HD + i];
         __syncthreads();
     } else {
-        for (int i = tid; i < G * HD; i += 256) sq[i] = a.q_raw[(size_t)row * a.n_heads * HD + (size_t)h * G * HD + i];
         if (tid < HD) {
             nk[tid] = a.k_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
             nv[tid] = a.v_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
@@ -145,27 +155,31 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     }
     __syncthreads();
 
-    /* values: a lane per dimension, the wave's sixteen positions */
+    /* values: a lane per dimension, the wave's sixteen positions, every row
+       loaded before any is used */
     float acc[GMAX][VPL];
 #pragma unroll
     for (int g = 0; g < GMAX; g++)
 #pragma unroll
         for (int i = 0; i < VPL; i++) acc[g][i] = 0.f;
     const int t0 = split * ATTN_CHUNK + wave * 16;
+    float vv[16][VPL];
+#pragma unroll
     for (int pp = 0; pp < 16; pp++) {
         const int tt = t0 + pp;
-        if (tt > pos) break;
         const bool fr = !a.prepared && tt == pos;
-        const float* vrow = fr ? nv : vc + (size_t)tt * kv_dim + (size_t)h * HD;
-        float vv[VPL];
+        const float* vrow = fr ? nv : vc + (size_t)(tt <= pos ? tt : 0) * kv_dim + (size_t)h * HD;
 #pragma unroll
-        for (int i = 0; i < VPL; i++) vv[i] = vrow[lane + 64 * i];
+        for (int i = 0; i < VPL; i++) vv[pp][i] = tt <= pos ? vrow[lane + 64 * i] : 0.0f;
+    }
+#pragma unroll
+    for (int pp = 0; pp < 16; pp++) {
 #pragma unroll
         for (int g = 0; g < GMAX; g++) {
             if (g >= G) break;
             const float w = sp[wave][pp][g];
 #pragma unroll
-            for (int i = 0; i < VPL; i++) acc[g][i] = fmaf(w, vv[i], acc[g][i]);
+            for (int i = 0; i < VPL; i++) acc[g][i] = fmaf(w, vv[pp][i], acc[g][i]);
         }
     }
     if (lane == 0) {
@@ -198,29 +212,6 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
         }
     }
 
-    /* the last chunk of this (row, kv head) to finish merges every chunk */
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    unsigned* ctr = a.counter + (size_t)row * a.n_kv + h;
-    if (tid == 0) last_s = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(n_act - 1);
-    __syncthreads();
-    if (!last_s) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const float* base = a.partial + ((size_t)row * a.n_kv + h) * a.splits_max * G * (HD + 2);
-    for (int i = tid; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
-        float M = -INFINITY;
-        for (int s = 0; s < n_act; s++) M = fmaxf(M, base[((size_t)s * G + g) * (HD + 2) + HD]);
-        float L = 0.f, o = 0.f;
-        for (int s = 0; s < n_act; s++) {
-            const float* ps = base + ((size_t)s * G + g) * (HD + 2);
-            const float f = expf(ps[HD] - M);
-            L = fmaf(ps[HD + 1], f, L);
-            o = fmaf(ps[d], f, o);
-        }
-        a.att[(size_t)row * a.n_heads * HD + ((size_t)h * G + g) * HD + d] = o / L;
-    }
-    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* The prepare pass: one block a (row, kv head), its G query heads and its key. */
@@ -254,6 +245,58 @@ hipError_t launch_attention(const attn_args& a, hipStream_t s) {
     if (a.hd == 128) attention_kernel<128><<<grid, 256, 0, s>>>(a);
     else if (a.hd == 64) attention_kernel<64><<<grid, 256, 0, s>>>(a);
     else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+/* One block per (query head, row), a thread per dimension: the chunks'
+   maxima and sums read in parallel, each chunk's scale exp(m_s - M) computed
+   once, then each dimension's weighted values summed, eight chunks' loads in
+   flight at a time. */
+#define MERGE_MAX 256
+__global__ void attention_merge_kernel(attn_args a) {
+    const int hq = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
+    const int G = a.n_heads / a.n_kv, h = hq / G, g = hq % G, HD = a.hd;
+    const int n_act = a.rows[row].pos / ATTN_CHUNK + 1;
+    const float* base = a.partial + (((size_t)row * a.n_kv + h) * a.splits_max * G + g) * (HD + 2);
+    const size_t stride = (size_t)G * (HD + 2);
+    __shared__ float fm[MERGE_MAX], fl[MERGE_MAX];
+    __shared__ float red[4];
+    float m = -INFINITY;
+    for (int s = d; s < n_act; s += blockDim.x) {
+        fm[s] = base[s * stride + HD];
+        fl[s] = base[s * stride + HD + 1];
+        m = fmaxf(m, fm[s]);
+    }
+    m = wave_max(m);
+    if ((d & 63) == 0) red[d >> 6] = m;
+    __syncthreads();
+    float M = red[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) M = fmaxf(M, red[w]);
+    for (int s = d; s < n_act; s += blockDim.x) fm[s] = expf(fm[s] - M);
+    __syncthreads();
+    float L = 0.f, o = 0.f;
+    int s = 0;
+    for (; s + 8 <= n_act; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = base[(s + i) * stride + d];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            L = fmaf(fl[s + i], fm[s + i], L);
+            o = fmaf(v[i], fm[s + i], o);
+        }
+    }
+    for (; s < n_act; s++) {
+        L = fmaf(fl[s], fm[s], L);
+        o = fmaf(base[s * stride + d], fm[s], o);
+    }
+    a.att[(size_t)row * a.n_heads * HD + (size_t)hq * HD + d] = o / L;
+}
+
+hipError_t launch_attention_merge(const attn_args& a, hipStream_t s) {
+    if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_rows < 1 || (a.hd != 64 && a.hd != 128) || a.splits_max > MERGE_MAX)
+        return hipErrorInvalidValue;
+    attention_merge_kernel<<<dim3(a.n_heads, a.n_rows), a.hd, 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -114,7 +114,7 @@ hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_
 }
 
 /* ------------------------------------------------------------------ */
-/* RMSNorm + router + top-k, in the reference CPU's order              */
+/* RMSNorm + router, in the reference CPU's order                      */
 /* ------------------------------------------------------------------ */
 
 /* Sixteen lanes (j = 0..15) of a row hold the sixteen FMA chains of
@@ -136,7 +136,6 @@ __global__ __launch_bounds__(64) void route_kernel(route_args a) {
     float* sxn = sh + a.H;      /* H: normalized */
     __shared__ float chains[16];
     __shared__ float inv_s;
-    __shared__ int last_s;
     const int lane = threadIdx.x, j = lane & 15, rrow = blockIdx.x * 4 + (lane >> 4);
     const int tok = blockIdx.y;
     const float* x = a.x + (size_t)tok * a.H;
@@ -146,11 +145,20 @@ __global__ __launch_bounds__(64) void route_kernel(route_args a) {
     const float* wr = a.router + (size_t)(has_row ? rrow : 0) * a.H + j;
 #pragma unroll
     for (int m = 0; m < NCH; m++) w[m] = wr[16 * m];
-    for (int i = lane; i < a.H; i += 64) sx[i] = x[i];
+    {
+        /* x into LDS: H / 256 = NCH / 16 float4 a lane, all loads issued before any store */
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        float4 xv[NCH / 16];
+#pragma unroll
+        for (int i = 0; i < NCH / 16; i++) xv[i] = x4[lane + 64 * i];
+#pragma unroll
+        for (int i = 0; i < NCH / 16; i++) reinterpret_cast<float4*>(sx)[lane + 64 * i] = xv[i];
+    }
     __syncthreads();
     if (lane < 16) {
         /* engine/src/kernels.c:115-140: sixteen chains of squares (H a multiple of 16) */
         float acc = 0.0f;
+#pragma unroll 16
         for (int m = 0; m < NCH; m++) acc = fmaf(sx[16 * m + lane], sx[16 * m + lane], acc);
         chains[lane] = acc;
     }
@@ -165,118 +173,31 @@ __global__ __launch_bounds__(64) void route_kernel(route_args a) {
     }
     __syncthreads();
     const float inv = inv_s;
-    for (int i = lane; i < a.H; i += 64) {
-        const float t = sx[i] * inv;
-        sxn[i] = t * a.norm_w[i];
+    {
+        const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+        float4 nw[NCH / 16];
+#pragma unroll
+        for (int i = 0; i < NCH / 16; i++) nw[i] = w4[lane + 64 * i];
+#pragma unroll
+        for (int i = 0; i < NCH / 16; i++) {
+            const float4 xv = reinterpret_cast<const float4*>(sx)[lane + 64 * i];
+            float4 o;
+            o.x = (xv.x * inv) * nw[i].x; o.y = (xv.y * inv) * nw[i].y;
+            o.z = (xv.z * inv) * nw[i].z; o.w = (xv.w * inv) * nw[i].w;
+            reinterpret_cast<float4*>(sxn)[lane + 64 * i] = o;
+            if (a.xn_out && blockIdx.x == 0) reinterpret_cast<float4*>(a.xn_out + (size_t)tok * a.H)[lane + 64 * i] = o;
+        }
     }
     __syncthreads();
-    if (a.xn_out && blockIdx.x == 0)
-        for (int i = lane; i < a.H; i += 64) a.xn_out[(size_t)tok * a.H + i] = sxn[i];
     float acc = 0.0f;
 #pragma unroll
     for (int m = 0; m < NCH; m++) acc = fmaf(w[m], sxn[16 * m + j], acc);
     const float logit = fold16_lanes(acc);
     if (has_row && j == 0) a.logits[(size_t)tok * a.E + rrow] = logit;
-    if (!a.topk) return;
-
-    /* The last block of this row to finish routes it (engine/src/model.c:626-703). */
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (lane == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counter + tok, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last_s = prev == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!last_s) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const int E = a.E, K = a.K;
-    const float* lg_g = a.logits + (size_t)tok * E;
-    float lg[ROUTE_E_MAX / 64];
-    unsigned taken = 0;
-#pragma unroll
-    for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
-        const int e = lane + 64 * i;
-        lg[i] = e < E ? __builtin_nontemporal_load(lg_g + e) : 0.0f;
-    }
-    const float l0 = __shfl(lg[0], 0, 64);
-    __shared__ int chosen_s[ROUTE_K_MAX];
-    for (int k = 0; k < K; k++) {
-        /* the first expert not yet taken, and the largest non-NaN logit among
-           those not taken, the lowest index between equals */
-        int first = 0x7fffffff, bi = 0x7fffffff;
-        float bv = 0.0f;
-#pragma unroll
-        for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
-            const int e = lane + 64 * i;
-            if (e < E && !(taken >> i & 1)) {
-                first = min(first, e);
-                const float v = lg[i];
-                if (v == v && (bi == 0x7fffffff || v > bv)) { bv = v; bi = e; }
-            }
-        }
-        for (int o = 32; o > 0; o >>= 1) {
-            const int of = __shfl_xor(first, o, 64), oi = __shfl_xor(bi, o, 64);
-            const float ov = __shfl_xor(bv, o, 64);
-            first = min(first, of);
-            const bool take = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-            if (take) { bv = ov; bi = oi; }
-        }
-        /* A NaN where the scan starts is never displaced (x > NaN is false). */
-        const float fv = __shfl(lg[first >> 6 < ROUTE_E_MAX / 64 ? first >> 6 : 0], first & 63, 64);
-        const int pick = (fv != fv || bi == 0x7fffffff) ? first : bi;
-        if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
-        if (lane == 0) chosen_s[k] = pick;
-    }
-    /* softmax over every expert: max as the CPU scans it, the sum of exp(l - max) */
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
-        if (lane + 64 * i < E) mx = fmaxf(mx, lg[i]);
-    mx = wave_max(mx);
-    if (l0 != l0) mx = l0;
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
-        if (lane + 64 * i < E) sum += expf(lg[i] - mx);
-    sum = wave_sum(sum);
-    __syncthreads();
-    if (lane == 0) {
-        route_out* o = a.out + tok;
-        int order[ROUTE_K_MAX];
-        for (int k = 0; k < K; k++) {
-            o->chosen[k] = chosen_s[k];
-            const int e = chosen_s[k];
-            int q = k;
-            while (q > 0 && order[q - 1] > e) { order[q] = order[q - 1]; q--; }
-            order[q] = e;
-        }
-        float wts[ROUTE_K_MAX], share[ROUTE_K_MAX];
-        for (int k = 0; k < K; k++) {
-            const float l = __builtin_nontemporal_load(lg_g + order[k]);
-            wts[k] = expf(l - mx) / sum;
-        }
-        if (a.renorm) {
-            for (int k = 0; k < K; k++) {
-                const float sv = wts[k];
-                int q = k;
-                while (q > 0 && share[q - 1] < sv) { share[q] = share[q - 1]; q--; }
-                share[q] = sv;
-            }
-            float total = 0.0f;
-            for (int k = 0; k < K; k++) total += share[k];
-            for (int k = 0; k < K; k++) wts[k] /= total;
-        }
-        for (int k = 0; k < K; k++) {
-            o->ids[k] = order[k];
-            o->weights[k] = wts[k];
-        }
-        __hip_atomic_store(a.counter + tok, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
 }
 
 hipError_t launch_route(const route_args& a, hipStream_t s) {
-    if (a.H % 16 || a.E < 1 || a.E > ROUTE_E_MAX || a.n_rows < 1 || (a.topk && (a.K < 1 || a.K > ROUTE_K_MAX || a.K > a.E)))
-        return hipErrorInvalidValue;
+    if (a.H % 256 || a.E < 1 || a.E > ROUTE_E_MAX || a.n_rows < 1) return hipErrorInvalidValue;
     const dim3 grid((a.E + 3) / 4, a.n_rows);
     const size_t lds = 2 * (size_t)a.H * sizeof(float);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
@@ -288,6 +209,132 @@ hipError_t launch_route(const route_args& a, hipStream_t s) {
         case 256: route_kernel<256><<<grid, 64, lds, s>>>(a); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+/* The reference's routing (engine/src/model.c:626-703) of one token by one
+   wave: the K largest of E logits, largest first, the lower index first
+   between equals; the chosen sorted by id; softmax weights over every
+   expert; renormalized over the chosen, summed largest first, when renorm.
+   Lane 0 writes *o. slg: E floats of LDS.
+
+   Without NaNs the K passes of argmax equal a ranking: expert e is chosen
+   k-th where k is the number of experts better than it (a larger logit, or
+   an equal one at a lower index), so every lane ranks its own experts against
+   all E at once. With a NaN among the logits the passes are run as the
+   reference runs them (a NaN where a pass starts is kept, since x > NaN is
+   false; a later one never wins). */
+__device__ void wave_route(const float* __restrict__ lg_in, int E, int K, int renorm, route_out* o, float* slg) {
+    const int lane = threadIdx.x & 63;
+    __shared__ int chosen_s[ROUTE_K_MAX];
+    __shared__ float share_s[ROUTE_K_MAX];
+    float lg[ROUTE_E_MAX / 64];
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+        const int e = lane + 64 * i;
+        lg[i] = e < E ? lg_in[e] : -INFINITY;
+        if (e < E) {
+            slg[e] = lg[i];
+            nan |= lg[i] != lg[i];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const float l0 = slg[0];
+    if (__any(nan)) {
+        unsigned taken = 0;
+        for (int k = 0; k < K; k++) {
+            int first = 0x7fffffff, bi = 0x7fffffff;
+            float bv = 0.0f;
+#pragma unroll
+            for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+                const int e = lane + 64 * i;
+                if (e < E && !(taken >> i & 1)) {
+                    first = min(first, e);
+                    const float v = lg[i];
+                    if (v == v && (bi == 0x7fffffff || v > bv)) { bv = v; bi = e; }
+                }
+            }
+            for (int off = 32; off > 0; off >>= 1) {
+                const int of = __shfl_xor(first, off, 64), oi = __shfl_xor(bi, off, 64);
+                const float ov = __shfl_xor(bv, off, 64);
+                first = min(first, of);
+                const bool take = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
+                if (take) { bv = ov; bi = oi; }
+            }
+            const float fv = slg[first];
+            const int pick = (fv != fv || bi == 0x7fffffff) ? first : bi;
+            if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
+            if (lane == 0) chosen_s[k] = pick;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+            const int e = lane + 64 * i;
+            if (e >= E) continue;
+            const float v = lg[i];
+            int rank = 0;
+            for (int q = 0; q < E; q += 4) {
+                const float4 u = *reinterpret_cast<const float4*>(slg + q);
+                rank += (u.x > v) | ((u.x == v) & (q < e));
+                rank += (u.y > v) | ((u.y == v) & (q + 1 < e));
+                rank += (u.z > v) | ((u.z == v) & (q + 2 < e));
+                rank += (u.w > v) | ((u.w == v) & (q + 3 < e));
+            }
+            if (rank < K) chosen_s[rank] = e;
+        }
+    }
+    /* softmax over every expert: the max as the CPU scans it (a NaN first stays), the sum of exp(l - max) */
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
+        if (lane + 64 * i < E) mx = fmaxf(mx, lg[i]);
+    mx = wave_max(mx);
+    if (l0 != l0) mx = l0;
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
+        if (lane + 64 * i < E) sum += expf(lg[i] - mx);
+    sum = wave_sum(sum);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (lane < K) share_s[lane] = expf(slg[chosen_s[lane]] - mx) / sum;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (lane == 0) {
+        /* the chosen are largest first, so their shares are too: the total in that order */
+        float total = 0.0f;
+        for (int k = 0; k < K; k++) total += share_s[k];
+        int order[ROUTE_K_MAX];
+        float wts[ROUTE_K_MAX];
+        for (int k = 0; k < K; k++) {
+            const int e = chosen_s[k];
+            const float w = renorm ? share_s[k] / total : share_s[k];
+            o->chosen[k] = e;
+            int q = k;
+            while (q > 0 && order[q - 1] > e) { order[q] = order[q - 1]; wts[q] = wts[q - 1]; q--; }
+            order[q] = e;
+            wts[q] = w;
+        }
+        for (int k = 0; k < K; k++) {
+            o->ids[k] = order[k];
+            o->weights[k] = wts[k];
+        }
+    }
+}
+
+__global__ void route_check_kernel(const float* __restrict__ logits, int E, int K, int renorm, route_out* out) {
+    __shared__ float slg[ROUTE_E_MAX];
+    __shared__ route_out o;
+    wave_route(logits, E, K, renorm, &o, slg);
+    __syncthreads();
+    if (threadIdx.x < 3 * ROUTE_K_MAX) reinterpret_cast<int32_t*>(out)[threadIdx.x] = reinterpret_cast<const int32_t*>(&o)[threadIdx.x];
+}
+
+hipError_t launch_route_check(const float* logits, int E, int K, int renorm, route_out* out, hipStream_t s) {
+    if (E < 1 || E > ROUTE_E_MAX || E % 4 || K < 1 || K > ROUTE_K_MAX || K > E) return hipErrorInvalidValue;
+    route_check_kernel<<<1, 64, 0, s>>>(logits, E, K, renorm, out);
     return hipGetLastError();
 }
 
@@ -310,30 +357,46 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / den) * u;
 }
 
+/* The routing of this token into LDS: computed from the logits by wave 0
+   (block 0 also publishing it to rt), or read from rt. */
+__device__ __forceinline__ void block_routing(const experts_in_args& a, route_out* srt) {
+    if (a.logits) {
+        __shared__ float slg[ROUTE_E_MAX];
+        if (threadIdx.x < 64) wave_route(a.logits, a.E, a.K, a.renorm, srt, slg);
+        __syncthreads();
+        if (blockIdx.x == 0 && threadIdx.x < 3 * ROUTE_K_MAX)
+            reinterpret_cast<int32_t*>(a.rt)[threadIdx.x] = reinterpret_cast<const int32_t*>(srt)[threadIdx.x];
+    } else {
+        if (threadIdx.x < 3 * ROUTE_K_MAX)
+            reinterpret_cast<int32_t*>(srt)[threadIdx.x] = reinterpret_cast<const int32_t*>(a.rt)[threadIdx.x];
+        __syncthreads();
+    }
+}
+
 template <int DT, int LPR, int SPL>
 __global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
     constexpr int RPW = WAVE / LPR;
+    __shared__ route_out srt;
     const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
     const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
     const int I = a.gate.rows;
     xslice xs[SPL];
 #pragma unroll
     for (int j = 0; j < SPL; j++) load_xslice(DT, al + LPR * j, a.xn, xs[j]);
+    block_routing(a, &srt);
     const int units = a.K * I;
-    for (int u0 = wave * 2 * RPW; u0 < units; u0 += nwaves * 2 * RPW) {
-        int u[2], e[2], r[2];
+    for (int u0 = wave * RPW; u0 < units; u0 += 2 * nwaves * RPW) {
+        int u[2];
         qraw g[2][SPL], v[2][SPL];
 #pragma unroll
         for (int q = 0; q < 2; q++) {
-            u[q] = u0 + q * RPW + sub;
+            u[q] = u0 + q * nwaves * RPW + sub;
             const int uu = u[q] < units ? u[q] : units - 1;
-            const int k = uu / I;
-            r[q] = uu - k * I;
-            e[q] = a.rt->ids[k];
+            const int k = uu / I, r = uu - k * I, e = srt.ids[k];
 #pragma unroll
             for (int j = 0; j < SPL; j++) {
-                slice_load<DT>(a.gate, e[q], r[q], al + LPR * j, g[q][j]);
-                slice_load<DT>(a.up, e[q], r[q], al + LPR * j, v[q][j]);
+                slice_load<DT>(a.gate, e, r, al + LPR * j, g[q][j]);
+                slice_load<DT>(a.up, e, r, al + LPR * j, v[q][j]);
             }
         }
 #pragma unroll
@@ -378,6 +441,7 @@ static hipError_t ein_dispatch(const experts_in_args& a, hipStream_t s) {
 hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s) {
     if (a.gate.dtype != a.up.dtype || a.gate.rows != a.up.rows || a.gate.cols != a.up.cols || a.K < 1 || a.K > ROUTE_K_MAX)
         return hipErrorInvalidValue;
+    if (a.logits && (a.E < a.K || a.E > ROUTE_E_MAX || a.E % 4)) return hipErrorInvalidValue;
     switch (a.gate.dtype) {
         case VITNA_DTYPE_Q8_0: return ein_dispatch<VITNA_DTYPE_Q8_0>(a, s);
         case VITNA_DTYPE_Q4_K: return ein_dispatch<VITNA_DTYPE_Q4_K>(a, s);
@@ -408,11 +472,11 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
         wk[j] = ok ? a.rt->weights[k] : 0.0f;
         load_xslice(DT, tk[j], a.act + (size_t)k * I, xs[j]);
     }
-    for (int r0 = wave * 2; r0 < H; r0 += nwaves * 2) {
+    for (int r0 = wave; r0 < H; r0 += 2 * nwaves) {
         qraw q[2][IPL];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const int r = r0 + h < H ? r0 + h : H - 1;
+            const int r = r0 + h * nwaves < H ? r0 + h * nwaves : H - 1;
 #pragma unroll
             for (int j = 0; j < IPL; j++) slice_load<DT>(a.down, ek[j], r, tk[j], q[h][j]);
         }
@@ -422,7 +486,7 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
 #pragma unroll
             for (int j = 0; j < IPL; j++) p = fmaf(wk[j], slice_dot<DT>(q[h][j], tk[j], xs[j]), p);
             p = wave_sum(p);
-            const int r = r0 + h;
+            const int r = r0 + h * nwaves;
             if (lane == 0 && r < H) a.y[r] = a.add ? a.y[r] + p : p;
         }
     }
@@ -464,17 +528,19 @@ hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s) {
 /* Dense projections                                                   */
 /* ------------------------------------------------------------------ */
 
-template <int DT, int LPR, int SPL>
+/* Units of RPW rows, U units in flight a wave: their loads all issued before
+   any of their arithmetic. */
+template <int DT, int LPR, int SPL, int U>
 __device__ __forceinline__ void gemv_rows(const qmat& w, float* __restrict__ y, int add, const xslice* xs, int unit0, int ustep,
                                           int lane) {
     constexpr int RPW = WAVE / LPR;
     const int sub = lane / LPR, al = lane % LPR;
     const int units = (w.rows + RPW - 1) / RPW;
-    for (int u = unit0; u < units; u += 2 * ustep) {
-        qraw q[2][SPL];
-        int r[2];
+    for (int u = unit0; u < units; u += U * ustep) {
+        qraw q[U][SPL];
+        int r[U];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < U; h++) {
             r[h] = (u + h * ustep) * RPW + sub;
             const int rr = r[h] < w.rows ? r[h] : w.rows - 1;
 #pragma unroll
@@ -484,7 +550,7 @@ __device__ __forceinline__ void gemv_rows(const qmat& w, float* __restrict__ y, 
             }
         }
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < U; h++) {
             const int rr = r[h] < w.rows ? r[h] : w.rows - 1;
             float p = 0.f;
 #pragma unroll
@@ -495,10 +561,12 @@ __device__ __forceinline__ void gemv_rows(const qmat& w, float* __restrict__ y, 
                     p += slice_dot<DT>(q[h][j], al + LPR * j, xs[j]);
             }
             p = row_sum<LPR>(p);
-            if (al == 0 && r[h] < w.rows && (u + h * ustep) < units) y[r[h]] = add ? y[r[h]] + p : p;
+            if (al == 0 && r[h] < w.rows) y[r[h]] = add ? y[r[h]] + p : p;
         }
     }
 }
+
+#define GEMV_U 4
 
 template <int D0, int D1, int D2, int LPR, int SPL, bool NORM>
 __global__ __launch_bounds__(256) void gemv_kernel(gemv_args a) {
@@ -507,53 +575,74 @@ __global__ __launch_bounds__(256) void gemv_kernel(gemv_args a) {
     const int H = a.w[0].cols;
     const float* xin = a.x;
     if (NORM) {
+        /* up to eight float4 of x and of the weights a thread (H at most 8192, launch_gemv checks) */
         __shared__ float red[4];
+        const int n4 = H / 4;
+        float4 xv[8], wv[8];
+        const float4* x4 = reinterpret_cast<const float4*>(a.x);
+        const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if ((int)threadIdx.x + 256 * i < n4) { xv[i] = x4[threadIdx.x + 256 * i]; wv[i] = w4[threadIdx.x + 256 * i]; }
         float ss = 0.f;
-        for (int i = threadIdx.x; i < H; i += blockDim.x) ss = fmaf(a.x[i], a.x[i], ss);
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if ((int)threadIdx.x + 256 * i < n4) {
+                ss = fmaf(xv[i].x, xv[i].x, ss); ss = fmaf(xv[i].y, xv[i].y, ss);
+                ss = fmaf(xv[i].z, xv[i].z, ss); ss = fmaf(xv[i].w, xv[i].w, ss);
+            }
         ss = wave_sum(ss);
         if (lane == 0) red[threadIdx.x / WAVE] = ss;
         __syncthreads();
         ss = (red[0] + red[1]) + (red[2] + red[3]);
         const float inv = 1.0f / sqrtf(ss / (float)H + a.eps);
-        for (int i = threadIdx.x; i < H; i += blockDim.x) sh[i] = (a.x[i] * inv) * a.norm_w[i];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if ((int)threadIdx.x + 256 * i < n4) {
+                float4 o;
+                o.x = (xv[i].x * inv) * wv[i].x; o.y = (xv[i].y * inv) * wv[i].y;
+                o.z = (xv[i].z * inv) * wv[i].z; o.w = (xv[i].w * inv) * wv[i].w;
+                reinterpret_cast<float4*>(sh)[threadIdx.x + 256 * i] = o;
+            }
         __syncthreads();
         xin = sh;
     }
     xslice xs[SPL];
-    /* all matrices share a width, and so the lane's slices */
-#pragma unroll
-    for (int j = 0; j < SPL; j++) load_xslice(D0, lane % LPR + LPR * j, xin, xs[j]);
-    /* matrices with another slice layout reload below */
     const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
     constexpr int RPW = WAVE / LPR;
-    /* the waves are shared among the matrices in proportion to their rows */
-    int total = 0, units[3] = {0, 0, 0};
-    for (int i = 0; i < a.n; i++) { units[i] = (a.w[i].rows + RPW - 1) / RPW; total += units[i]; }
-    /* wave w takes units w, w + nwaves, ... of the concatenated list */
+    /* the matrices' units concatenated; wave w takes units w, w + nwaves, ... */
     int base = 0;
     for (int i = 0; i < a.n; i++) {
-        const int u0 = wave - base;
-        /* first unit of matrix i this wave takes: smallest u >= 0 with (base + u - wave) % nwaves == 0 */
-        int first = u0 % nwaves;
+        const int units = (a.w[i].rows + RPW - 1) / RPW;
+        int first = (wave - base) % nwaves;
         if (first < 0) first += nwaves;
-        if (first < units[i]) {
+        if (first < units) {
             if (i == 0) {
-                gemv_rows<D0, LPR, SPL>(a.w[0], a.y[0], a.add, xs, first, nwaves, lane);
-            } else if (i == 1) {
-                if (D1 != D0) {
 #pragma unroll
-                    for (int j = 0; j < SPL; j++) load_xslice(D1, lane % LPR + LPR * j, xin, xs[j]);
-                }
-                gemv_rows<D1, LPR, SPL>(a.w[1], a.y[1], a.add, xs, first, nwaves, lane);
+                for (int j = 0; j < SPL; j++) load_xslice(D0, lane % LPR + LPR * j, xin, xs[j]);
+                gemv_rows<D0, LPR, SPL, GEMV_U>(a.w[0], a.y[0], a.add, xs, first, nwaves, lane);
+            } else if (i == 1) {
+#pragma unroll
+                for (int j = 0; j < SPL; j++) load_xslice(D1, lane % LPR + LPR * j, xin, xs[j]);
+                gemv_rows<D1, LPR, SPL, GEMV_U>(a.w[1], a.y[1], a.add, xs, first, nwaves, lane);
             } else {
 #pragma unroll
                 for (int j = 0; j < SPL; j++) load_xslice(D2, lane % LPR + LPR * j, xin, xs[j]);
-                gemv_rows<D2, LPR, SPL>(a.w[2], a.y[2], a.add, xs, first, nwaves, lane);
+                gemv_rows<D2, LPR, SPL, GEMV_U>(a.w[2], a.y[2], a.add, xs, first, nwaves, lane);
             }
         }
-        base += units[i];
+        base += units;
     }
-    (void)total;
+}
+
+static int g_cus = 0;
+static int device_cus() {
+    if (!g_cus) {
+        int dev = 0;
+        hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || g_cus < 1) g_cus = 256;
+    }
+    return g_cus;
 }
 
 template <int D0, int D1, int D2, bool NORM>
@@ -562,11 +651,12 @@ static hipError_t gemv_by_width(const gemv_args& a, hipStream_t s) {
     int units = 0;
     const int lpr = S < 64 ? S : 64, rpw = WAVE / lpr;
     for (int i = 0; i < a.n; i++) units += (a.w[i].rows + rpw - 1) / rpw;
-    int waves = (units + 1) / 2;
-    int blocks = (waves + 3) / 4;
+    /* enough waves to cover the units GEMV_U at a time, at most four blocks a CU (the loop covers the rest) */
+    int blocks = (units + 4 * GEMV_U - 1) / (4 * GEMV_U);
+    blocks = blocks < 4 * device_cus() ? blocks : 4 * device_cus();
     if (blocks < 1) blocks = 1;
     const size_t lds = NORM ? (size_t)a.w[0].cols * sizeof(float) : 0;
-    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    if (lds > 64 * 1024 || (NORM && a.w[0].cols > 8192)) return hipErrorInvalidValue;
     switch (S) {
         case 4: gemv_kernel<D0, D1, D2, 4, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
         case 8: gemv_kernel<D0, D1, D2, 8, 1, NORM><<<blocks, 256, lds, s>>>(a); break;

@@ -35,31 +35,36 @@ hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_
 /* ---- routing ---- */
 
 /* RMSNorm of x (n_rows rows of H, row stride H) with norm_w, in the
-   reference CPU's order, written to xn_out when it is not NULL; the router's
-   logits for each row (E of them, the router F32 [E x H]) in the reference
-   CPU's order into logits (row stride E); and, when topk, each row's routing
-   into out[row] (K of E, renormalized or not). counter: n_rows zeroed
-   unsigned ints the kernel leaves zeroed. */
+   reference CPU's order, written to xn_out when it is not NULL, and the
+   router's logits for each row (E of them, the router F32 [E x H]) in the
+   reference CPU's order into logits (row stride E). */
 struct route_args {
     const float* x;
     const float* norm_w;
     const float* router;
     float* xn_out;
     float* logits;
-    route_out* out;
-    unsigned* counter;
-    int H, E, K, renorm, topk, n_rows;
+    int H, E, n_rows;
     float eps;
 };
 hipError_t launch_route(const route_args& a, hipStream_t s);
 
+/* The device routing of one token's E logits (the rule every expert kernel
+   applies), into *out: for checking it against the reference's rule. */
+hipError_t launch_route_check(const float* logits, int E, int K, int renorm, route_out* out, hipStream_t s);
+
 /* ---- experts, one token ---- */
 
-/* act[k * I + r] = silu(gate_e[r] . xn) * (up_e[r] . xn) for e = ids[k]. */
+/* act[k * I + r] = silu(gate_e[r] . xn) * (up_e[r] . xn) for e = ids[k].
+   With logits set, every block first routes (engine/src/model.c:626-703:
+   top-k of the E logits, softmax weights, renormalized when renorm) and
+   block 0 writes the routing to rt; otherwise rt holds it already. */
 struct experts_in_args {
     qmat gate, up;
     const float* xn;
-    const route_out* rt;
+    route_out* rt;
+    const float* logits;
+    int E, renorm;
     float* act;
     int K;
 };
@@ -107,9 +112,10 @@ struct row_rec {
 /* Decode attention for n_rows rows, one layer: each row's q and k through the
    per-head RMSNorm (when q_norm is set) and the half-split RoPE at its
    position, its k and v written into its sequence's cache at that position,
-   and softmax(q k^T / sqrt(hd)) v over positions 0..pos into att. Positions
-   are split into chunks of ATTN_CHUNK; the last chunk of a (row, kv head) to
-   finish merges them. */
+   and softmax(q k^T / sqrt(hd)) v over positions 0..pos. Positions are split
+   into chunks of ATTN_CHUNK, each block leaving its chunk's partial (max,
+   sum, weighted values) in partial; launch_attention_merge combines them into
+   att. */
 #define ATTN_CHUNK 64
 struct attn_args {
     const float* q_raw;    /* [n_rows][n_heads * hd] */
@@ -125,7 +131,6 @@ struct attn_args {
     const row_rec* rows;   /* device, n_rows */
     int n_rows;
     float* partial;        /* [n_rows][n_kv][splits_max][G][hd + 2] */
-    unsigned* counter;     /* [n_rows][n_kv], zeroed, left zeroed */
     float* att;            /* [n_rows][n_heads * hd] */
     int n_heads, n_kv, hd, ctx, splits_max;
     float eps;
@@ -137,6 +142,8 @@ struct attn_args {
     float* q_out;          /* prepare: where the prepared queries go */
 };
 hipError_t launch_attention(const attn_args& a, hipStream_t s);
+/* The chunks' partials of every (row, query head) combined into att. */
+hipError_t launch_attention_merge(const attn_args& a, hipStream_t s);
 /* The prepare pass of prepared = 1: q normalized and rotated into q_out, k
    normalized and rotated and v stored into the cache at each row's position. */
 hipError_t launch_attention_prepare(const attn_args& a, hipStream_t s);

@@ -240,6 +240,9 @@ def _hip():
         "vitna_hip_sync": (C.c_bool, [P, *E]),
         "vitna_hip_stream": (P, [P]),
         "vitna_hip_moe_prefill": (C.c_bool, [P, C.c_size_t, _FP, C.c_size_t, *E]),
+"vitna_hip_route_check": (C.c_bool, [_FP, C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
+                                             _FP, *E]),
+        "vitna_hip_time_steps": (C.c_bool, [P, C.c_size_t, C.c_int32, C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_kernel": (C.c_bool, [P, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double),
                                              C.POINTER(C.c_double), *E]),
     }
@@ -369,6 +372,11 @@ class Device:
         self._ok(self.lib.vitna_hip_time_kernel(self.g, which, reps, warmup, C.byref(us), C.byref(b), self.err, 512))
         return us.value, b.value
 
+    def time_steps(self, seq, token, pos, steps):
+        ms = C.c_double()
+        self._ok(self.lib.vitna_hip_time_steps(self.g, seq, token, pos, steps, C.byref(ms), self.err, 512))
+        return ms.value
+
     def device_name(self):
         return self.lib.vitna_cuda_device_name(self.g).decode()
 
@@ -396,6 +404,19 @@ def expert_check(gate, up, down, norm_w, x, eps):
                                        fptr(act), fptr(y), err, 512):
         raise VitnaError(err.value.decode())
     return xs, act, y
+
+
+def route_check(logits, k, renormalize):
+    """vitna_hip_route_check: the device's routing of the given logits -> (chosen, ids, weights)."""
+    lib = hip()
+    lg = np.ascontiguousarray(logits, np.float32)
+    ch = np.empty(k, np.int32)
+    ids = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    err = C.create_string_buffer(512)
+    if not lib.vitna_hip_route_check(fptr(lg), lg.size, k, renormalize, _i32(ch), _i32(ids), fptr(w), err, 512):
+        raise VitnaError(err.value.decode())
+    return ch, ids, w
 
 
 def matrix_from_bytes(buf, dtype, rows, cols):
