@@ -33,7 +33,8 @@ import numpy as np  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 METRIC = "Qwen3-30B-A3B Q4_K_M decode tok/s @1 GPU; expert GEMV HBM GB/s (% of peak)"
 KERNELS = {0: "experts_in (gate/up + SiLU)", 1: "experts_down (+ weighted sum)", 2: "route (norm + router + top-k)",
-           3: "q/k/v projections", 4: "attention", 5: "o-projection", 6: "LM head"}
+           3: "q/k/v projections", 4: "attention (+ merge)", 5: "o-projection", 6: "LM head",
+           7: "route without top-k", 8: "routing rule alone (1 block)", 9: "tiny launch (floor)"}
 
 
 def log(*a):
@@ -89,7 +90,7 @@ def main():
 
     # algorithmic bytes of one step (weights and cache read once, logits written)
     per_kernel = {}
-    for which in range(7):
+    for which in range(10):
         us, b = dev.time_kernel(which, reps=4 * L if which != 6 else 20, warmup=L)
         if which == 4:
             b = 2.0 * (pos + 1) * kd * 4 + cfg.n_heads * cfg.head_dim * 8.0

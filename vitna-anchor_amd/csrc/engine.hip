@@ -458,7 +458,7 @@ static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, 
     return launch_gemv(go, g->stream);
 }
 
-static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, int n_rows, const float* x, float* xn_out) {
+static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, int n_rows, const float* x, float* xn_out, bool topk) {
     const dlayer& d = g->L[layer];
     route_args r;
     memset(&r, 0, sizeof(r));
@@ -469,16 +469,16 @@ static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, i
     r.logits = logits;
     r.H = g->H; r.E = g->E; r.n_rows = n_rows;
     r.eps = g->eps;
-    return launch_route(r, g->stream);
+    hipError_t e = launch_route(r, g->stream);
+    if (e == hipSuccess && topk) e = launch_topk(logits, n_rows, g->E, g->K, g->renorm, g->rt, g->stream);
+    return e;
 }
 
-/* The experts of one token: routed on the device from logits when they are
-   given, else as g->rt holds it. */
-static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, const float* logits, float* y, int add) {
+/* The experts of one token, routed as g->rt holds it. */
+static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, float* y, int add) {
     const dlayer& d = g->L[layer];
     experts_in_args ai;
-    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.logits = logits; ai.E = g->E; ai.renorm = g->renorm;
-    ai.act = g->act; ai.K = g->K;
+    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.act = g->act; ai.K = g->K;
     hipError_t e = launch_experts_in(ai, g->stream);
     if (e != hipSuccess) return e;
     experts_down_args ad;
@@ -528,10 +528,10 @@ extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int
     hipError_t e = hipSuccess;
     if (layer == 0) e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
     if (e == hipSuccess) e = enqueue_attention(g, (int)layer, 1, false);
-    if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn);
+    if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn, false);
     const bool nx = next && layer + 1 < (size_t)g->NL;
     /* the next layer's router on the same residual; its norm must not replace this layer's */
-    if (e == hipSuccess && nx) e = enqueue_route(g, (int)layer + 1, g->rlogits + g->E, 1, g->x, nullptr);
+    if (e == hipSuccess && nx) e = enqueue_route(g, (int)layer + 1, g->rlogits + g->E, 1, g->x, nullptr, false);
     if (!check_launch(g, e, "the layer up to its router", err, err_len)) return false;
     HIP_TRY(hipMemcpyAsync(g->h_logits, g->rlogits, (nx ? 2 : 1) * g->E * 4, hipMemcpyDeviceToHost, g->stream), "copying the router's logits");
     HIP_TRY(hipStreamSynchronize(g->stream), "running the layer up to its router");
@@ -567,7 +567,7 @@ extern "C" bool vitna_cuda_moe_experts(struct vitna_cuda_model* g, size_t layer,
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (!put_routing(g, 1, ids, weights, k, err, err_len)) return false;
-    return check_launch(g, enqueue_experts(g, (int)layer, nullptr, g->x, 1), "the experts", err, err_len);
+    return check_launch(g, enqueue_experts(g, (int)layer, g->x, 1), "the experts", err, err_len);
 }
 
 extern "C" bool vitna_cuda_moe_head(struct vitna_cuda_model* g, float* logits, char* err, size_t err_len) {
@@ -725,7 +725,7 @@ extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_
         ra.x = dx; ra.norm_w = dw; ra.router = drouter; ra.xn_out = dxn; ra.logits = dl;
         ra.H = (int)H; ra.E = 1; ra.n_rows = 1; ra.eps = eps;
         experts_in_args ai;
-        ai.gate = qg; ai.up = qu; ai.xn = dxn; ai.rt = drt; ai.logits = nullptr; ai.E = 1; ai.renorm = 0; ai.act = dact; ai.K = 1;
+        ai.gate = qg; ai.up = qu; ai.xn = dxn; ai.rt = drt; ai.act = dact; ai.K = 1;
         experts_down_args ad;
         ad.down = qd; ad.act = dact; ad.rt = drt; ad.y = dy; ad.K = 1; ad.add = 0;
         ok = launch_route(ra, s) == hipSuccess && launch_experts_in(ai, s) == hipSuccess && launch_experts_down(ad, s) == hipSuccess &&
@@ -750,8 +750,8 @@ static hipError_t enqueue_step_body(vitna_cuda_model* g) {
     hipError_t e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
     for (int l = 0; e == hipSuccess && l < g->NL; l++) {
         e = enqueue_attention(g, l, 1, false);
-        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, 1, g->x, g->xn);
-        if (e == hipSuccess) e = enqueue_experts(g, l, g->rlogits, g->x, 1);
+        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, 1, g->x, g->xn, true);
+        if (e == hipSuccess) e = enqueue_experts(g, l, g->x, 1);
     }
     if (e == hipSuccess) e = enqueue_head(g);
     return e;
@@ -793,8 +793,8 @@ extern "C" bool vitna_hip_moe_step(struct vitna_cuda_model* g, size_t seq, int32
 extern "C" bool vitna_hip_moe_ffn(struct vitna_cuda_model* g, size_t layer, char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
-    hipError_t e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn);
-    if (e == hipSuccess) e = enqueue_experts(g, (int)layer, g->rlogits, g->x, 1);
+    hipError_t e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn, true);
+    if (e == hipSuccess) e = enqueue_experts(g, (int)layer, g->x, 1);
     return check_launch(g, e, "the mixture of experts", err, err_len);
 }
 
@@ -871,7 +871,8 @@ static double qmat_bytes(const qmat& q) {
 extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int reps, int warmup, double* avg_us, double* bytes, char* err,
                                       size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
-    if ((which >= 3 && !g->attention) || which < 0 || which > 6) return fail(err, err_len, "no such kernel (%d) in this model", which);
+    if ((which >= 3 && which <= 6 && !g->attention) || which < 0 || which > 9)
+        return fail(err, err_len, "no such kernel (%d) in this model", which);
     hipEvent_t t0, t1;
     HIP_TRY(hipEventCreate(&t0), "events");
     HIP_TRY(hipEventCreate(&t1), "events");
@@ -883,11 +884,23 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
         switch (which) {
             case 0: {
                 experts_in_args ai;
-                ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.logits = g->rlogits; ai.E = g->E;
-                ai.renorm = g->renorm; ai.act = g->act; ai.K = K;
-                b = 2.0 * K * qmat_bytes(d.gate) + H * 4.0 + K * (double)g->I * 4 + g->E * 4.0;
+                ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.act = g->act; ai.K = K;
+                b = 2.0 * K * qmat_bytes(d.gate) + H * 4.0 + K * (double)g->I * 4;
                 return launch_experts_in(ai, g->stream);
             }
+            case 8:
+                /* the routing rule alone, one block */
+                b = g->E * 4.0;
+                return launch_route_check(g->rlogits, g->E, g->K, g->renorm, g->rt, g->stream);
+            case 9:
+                /* an empty launch: the floor of any kernel */
+                b = 0;
+                return launch_fill_normal(g->ypart, 0, 0, g->stream) == hipSuccess ? launch_route_check(g->rlogits, 4, 1, 0, g->rt + 1, g->stream)
+                                                                                   : hipErrorInvalidValue;
+            case 7:
+                /* the router without the top-k */
+                b = (double)g->E * H * 4 + H * 8.0 + g->E * 4.0;
+                return enqueue_route(g, l, g->rlogits, 1, g->x, g->xn, false);
             case 1: {
                 experts_down_args ad;
                 ad.down = d.down; ad.act = g->act; ad.rt = g->rt; ad.y = g->ypart; ad.K = K; ad.add = 0;
@@ -896,7 +909,7 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
             }
             case 2:
                 b = (double)g->E * H * 4 + H * 8.0 + g->E * 4.0;
-                return enqueue_route(g, l, g->rlogits, 1, g->x, g->xn);
+                return enqueue_route(g, l, g->rlogits, 1, g->x, g->xn, true);
             case 3: {
                 gemv_args ga;
                 memset(&ga, 0, sizeof(ga));

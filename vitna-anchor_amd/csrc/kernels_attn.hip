@@ -83,6 +83,35 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     float* nk = sq + G * HD;
 
+    /* the chunk's keys and values, requested before anything waits on them: four lanes a position (hd / 4 keys
+       a lane) and a lane a dimension across the wave's sixteen positions */
+    const int p = lane >> 2, qd = lane & 3;
+    const int t = split * ATTN_CHUNK + wave * 16 + p;
+    const bool valid = t <= pos;
+    const bool fresh = !a.prepared && t == pos; /* this row's own key: in LDS once normalized, not in the cache yet */
+    float kr[DPL];
+    if (valid && !fresh) {
+        const float4* src = reinterpret_cast<const float4*>(kc + (size_t)t * kv_dim + (size_t)h * HD + qd * DPL);
+#pragma unroll
+        for (int i = 0; i < DPL / 4; i++) {
+            const float4 u = src[i];
+            kr[4 * i] = u.x; kr[4 * i + 1] = u.y; kr[4 * i + 2] = u.z; kr[4 * i + 3] = u.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < DPL; i++) kr[i] = 0.f;
+    }
+    const int t0 = split * ATTN_CHUNK + wave * 16;
+    float vv[16][VPL];
+#pragma unroll
+    for (int pp = 0; pp < 16; pp++) {
+        const int tt = t0 + pp;
+        const bool ok = tt <= pos && !(!a.prepared && tt == pos);
+        const float* vrow = vc + (size_t)(ok ? tt : 0) * kv_dim + (size_t)h * HD;
+#pragma unroll
+        for (int i = 0; i < VPL; i++) vv[pp][i] = ok ? vrow[lane + 64 * i] : 0.0f;
+    }
+
     {
         /* the G query heads: G * HD / 4 <= 256 float4, one a thread */
         const float4* q4 = reinterpret_cast<const float4*>(a.q_raw + (size_t)row * a.n_heads * HD + (size_t)h * G * HD);
@@ -101,30 +130,19 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
             kc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = nk[tid];
             vc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = nv[tid];
         }
-    }
-
-    /* scores: four lanes a position, sixteen positions a wave */
-    const int p = lane >> 2, qd = lane & 3;
-    const int t = split * ATTN_CHUNK + wave * 16 + p;
-    const bool valid = t <= pos;
-    const bool fresh = !a.prepared && t == pos; /* this row's own key, not yet readable from the cache by other blocks */
-    float kr[DPL];
-    if (valid) {
         if (fresh) {
 #pragma unroll
             for (int i = 0; i < DPL; i++) kr[i] = nk[qd * DPL + i];
-        } else {
-            const float4* src = reinterpret_cast<const float4*>(kc + (size_t)t * kv_dim + (size_t)h * HD + qd * DPL);
-#pragma unroll
-            for (int i = 0; i < DPL / 4; i++) {
-                const float4 u = src[i];
-                kr[4 * i] = u.x; kr[4 * i + 1] = u.y; kr[4 * i + 2] = u.z; kr[4 * i + 3] = u.w;
-            }
         }
-    } else {
 #pragma unroll
-        for (int i = 0; i < DPL; i++) kr[i] = 0.f;
+        for (int pp = 0; pp < 16; pp++)
+            if (t0 + pp == pos) {
+#pragma unroll
+                for (int i = 0; i < VPL; i++) vv[pp][i] = nv[lane + 64 * i];
+            }
     }
+
+    /* scores, and each head's max and sum over the wave's positions */
     const float scale = 1.0f / sqrtf((float)HD);
     float mw[GMAX], lw[GMAX], pe[GMAX];
 #pragma unroll
@@ -155,23 +173,12 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     }
     __syncthreads();
 
-    /* values: a lane per dimension, the wave's sixteen positions, every row
-       loaded before any is used */
+    /* values: a lane per dimension */
     float acc[GMAX][VPL];
 #pragma unroll
     for (int g = 0; g < GMAX; g++)
 #pragma unroll
         for (int i = 0; i < VPL; i++) acc[g][i] = 0.f;
-    const int t0 = split * ATTN_CHUNK + wave * 16;
-    float vv[16][VPL];
-#pragma unroll
-    for (int pp = 0; pp < 16; pp++) {
-        const int tt = t0 + pp;
-        const bool fr = !a.prepared && tt == pos;
-        const float* vrow = fr ? nv : vc + (size_t)(tt <= pos ? tt : 0) * kv_dim + (size_t)h * HD;
-#pragma unroll
-        for (int i = 0; i < VPL; i++) vv[pp][i] = tt <= pos ? vrow[lane + 64 * i] : 0.0f;
-    }
 #pragma unroll
     for (int pp = 0; pp < 16; pp++) {
 #pragma unroll
@@ -211,7 +218,6 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
             part[g * (HD + 2) + HD + 1] = L;
         }
     }
-
 }
 
 /* The prepare pass: one block a (row, kv head), its G query heads and its key. */
@@ -238,6 +244,7 @@ __global__ __launch_bounds__(256) void attention_prepare_kernel(attn_args a) {
     }
 }
 
+
 hipError_t launch_attention(const attn_args& a, hipStream_t s) {
     if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > GMAX || a.n_rows < 1) return hipErrorInvalidValue;
     if (a.splits_max * ATTN_CHUNK < a.ctx) return hipErrorInvalidValue;
@@ -247,6 +254,7 @@ hipError_t launch_attention(const attn_args& a, hipStream_t s) {
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
+
 
 /* One block per (query head, row), a thread per dimension: the chunks'
    maxima and sums read in parallel, each chunk's scale exp(m_s - M) computed

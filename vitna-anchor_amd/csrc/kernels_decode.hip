@@ -128,6 +128,136 @@ __device__ __forceinline__ float fold16_lanes(float a) {
     return u + __shfl_down(u, 1, 16);
 }
 
+/* The reference's routing (engine/src/model.c:626-703) of one token by one
+   wave: the K largest of E logits, largest first, the lower index first
+   between equals; the chosen sorted by id; softmax weights over every
+   expert; renormalized over the chosen, summed largest first, when renorm.
+   Lane 0 writes *o. slg: E floats of LDS.
+
+   Without NaNs the K passes of argmax equal a ranking: expert e is chosen
+   k-th where k is the number of experts better than it (a larger logit, or
+   an equal one at a lower index), so every lane ranks its own experts against
+   all E at once. With a NaN among the logits the passes are run as the
+   reference runs them (a NaN where a pass starts is kept, since x > NaN is
+   false; a later one never wins). */
+__device__ __forceinline__ void wave_route(const float* __restrict__ lg_in, int E, int K, int renorm, route_out* o, float* slg) {
+    const int lane = threadIdx.x & 63;
+    __shared__ int chosen_s[ROUTE_K_MAX];
+    __shared__ float share_s[ROUTE_K_MAX];
+    float lg[ROUTE_E_MAX / 64];
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+        const int e = lane + 64 * i;
+        lg[i] = e < E ? lg_in[e] : -INFINITY;
+        if (e < E) {
+            slg[e] = lg[i];
+            nan |= lg[i] != lg[i];
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const float l0 = slg[0];
+    if (__any(nan)) {
+        unsigned taken = 0;
+        for (int k = 0; k < K; k++) {
+            int first = 0x7fffffff, bi = 0x7fffffff;
+            float bv = 0.0f;
+#pragma unroll
+            for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+                const int e = lane + 64 * i;
+                if (e < E && !(taken >> i & 1)) {
+                    first = min(first, e);
+                    const float v = lg[i];
+                    if (v == v && (bi == 0x7fffffff || v > bv)) { bv = v; bi = e; }
+                }
+            }
+            for (int off = 32; off > 0; off >>= 1) {
+                const int of = __shfl_xor(first, off, 64), oi = __shfl_xor(bi, off, 64);
+                const float ov = __shfl_xor(bv, off, 64);
+                first = min(first, of);
+                const bool take = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
+                if (take) { bv = ov; bi = oi; }
+            }
+            const float fv = slg[first];
+            const int pick = (fv != fv || bi == 0x7fffffff) ? first : bi;
+            if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
+            if (lane == 0) chosen_s[k] = pick;
+        }
+    } else if (E <= 128) {
+        /* ranks against all E logits read four at a time, the loop unrolled over the largest E it serves */
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int e = lane + 64 * i;
+            const float v = lg[i];
+            int rank = 0;
+#pragma unroll
+            for (int q = 0; q < 128; q += 4) {
+                if (q < E) {
+                    const float4 u = *reinterpret_cast<const float4*>(slg + q);
+                    rank += (u.x > v) | ((u.x == v) & (q < e));
+                    rank += (u.y > v) | ((u.y == v) & (q + 1 < e));
+                    rank += (u.z > v) | ((u.z == v) & (q + 2 < e));
+                    rank += (u.w > v) | ((u.w == v) & (q + 3 < e));
+                }
+            }
+            if (e < E && rank < K) chosen_s[rank] = e;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+            const int e = lane + 64 * i;
+            if (e >= E) continue;
+            const float v = lg[i];
+            int rank = 0;
+            for (int q = 0; q < E; q += 4) {
+                const float4 u = *reinterpret_cast<const float4*>(slg + q);
+                rank += (u.x > v) | ((u.x == v) & (q < e));
+                rank += (u.y > v) | ((u.y == v) & (q + 1 < e));
+                rank += (u.z > v) | ((u.z == v) & (q + 2 < e));
+                rank += (u.w > v) | ((u.w == v) & (q + 3 < e));
+            }
+            if (rank < K) chosen_s[rank] = e;
+        }
+    }
+    /* softmax over every expert: the max as the CPU scans it (a NaN first stays), the sum of exp(l - max) */
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
+        if (lane + 64 * i < E) mx = fmaxf(mx, lg[i]);
+    mx = wave_max(mx);
+    if (l0 != l0) mx = l0;
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
+        if (lane + 64 * i < E) sum += expf(lg[i] - mx);
+    sum = wave_sum(sum);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    /* lane k < K: the k-th chosen, its share, and where it falls in order of id */
+    int e_k = 0, at = 0;
+    float share = 0.0f;
+    if (lane < K) {
+        e_k = chosen_s[lane];
+        share = expf(slg[e_k] - mx) / sum;
+        share_s[lane] = share;
+        for (int j = 0; j < K; j++) at += chosen_s[j] < e_k;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (lane < K) {
+        float total = 1.0f;
+        if (renorm) {
+            /* the chosen are largest first, so their shares are too: the total in that order */
+            total = 0.0f;
+            for (int j = 0; j < K; j++) total += share_s[j];
+        }
+        o->chosen[lane] = e_k;
+        o->ids[at] = e_k;
+        o->weights[at] = renorm ? share / total : share;
+    }
+}
+
 /* One wave a block, four router rows a block (sixteen lanes a row). */
 template <int NCH>
 __global__ __launch_bounds__(64) void route_kernel(route_args a) {
@@ -212,124 +342,24 @@ hipError_t launch_route(const route_args& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-/* The reference's routing (engine/src/model.c:626-703) of one token by one
-   wave: the K largest of E logits, largest first, the lower index first
-   between equals; the chosen sorted by id; softmax weights over every
-   expert; renormalized over the chosen, summed largest first, when renorm.
-   Lane 0 writes *o. slg: E floats of LDS.
-
-   Without NaNs the K passes of argmax equal a ranking: expert e is chosen
-   k-th where k is the number of experts better than it (a larger logit, or
-   an equal one at a lower index), so every lane ranks its own experts against
-   all E at once. With a NaN among the logits the passes are run as the
-   reference runs them (a NaN where a pass starts is kept, since x > NaN is
-   false; a later one never wins). */
-__device__ void wave_route(const float* __restrict__ lg_in, int E, int K, int renorm, route_out* o, float* slg) {
-    const int lane = threadIdx.x & 63;
-    __shared__ int chosen_s[ROUTE_K_MAX];
-    __shared__ float share_s[ROUTE_K_MAX];
-    float lg[ROUTE_E_MAX / 64];
-    bool nan = false;
-#pragma unroll
-    for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
-        const int e = lane + 64 * i;
-        lg[i] = e < E ? lg_in[e] : -INFINITY;
-        if (e < E) {
-            slg[e] = lg[i];
-            nan |= lg[i] != lg[i];
-        }
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    const float l0 = slg[0];
-    if (__any(nan)) {
-        unsigned taken = 0;
-        for (int k = 0; k < K; k++) {
-            int first = 0x7fffffff, bi = 0x7fffffff;
-            float bv = 0.0f;
-#pragma unroll
-            for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
-                const int e = lane + 64 * i;
-                if (e < E && !(taken >> i & 1)) {
-                    first = min(first, e);
-                    const float v = lg[i];
-                    if (v == v && (bi == 0x7fffffff || v > bv)) { bv = v; bi = e; }
-                }
-            }
-            for (int off = 32; off > 0; off >>= 1) {
-                const int of = __shfl_xor(first, off, 64), oi = __shfl_xor(bi, off, 64);
-                const float ov = __shfl_xor(bv, off, 64);
-                first = min(first, of);
-                const bool take = oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-                if (take) { bv = ov; bi = oi; }
-            }
-            const float fv = slg[first];
-            const int pick = (fv != fv || bi == 0x7fffffff) ? first : bi;
-            if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
-            if (lane == 0) chosen_s[k] = pick;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
-            const int e = lane + 64 * i;
-            if (e >= E) continue;
-            const float v = lg[i];
-            int rank = 0;
-            for (int q = 0; q < E; q += 4) {
-                const float4 u = *reinterpret_cast<const float4*>(slg + q);
-                rank += (u.x > v) | ((u.x == v) & (q < e));
-                rank += (u.y > v) | ((u.y == v) & (q + 1 < e));
-                rank += (u.z > v) | ((u.z == v) & (q + 2 < e));
-                rank += (u.w > v) | ((u.w == v) & (q + 3 < e));
-            }
-            if (rank < K) chosen_s[rank] = e;
-        }
-    }
-    /* softmax over every expert: the max as the CPU scans it (a NaN first stays), the sum of exp(l - max) */
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
-        if (lane + 64 * i < E) mx = fmaxf(mx, lg[i]);
-    mx = wave_max(mx);
-    if (l0 != l0) mx = l0;
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
-        if (lane + 64 * i < E) sum += expf(lg[i] - mx);
-    sum = wave_sum(sum);
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    if (lane < K) share_s[lane] = expf(slg[chosen_s[lane]] - mx) / sum;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    if (lane == 0) {
-        /* the chosen are largest first, so their shares are too: the total in that order */
-        float total = 0.0f;
-        for (int k = 0; k < K; k++) total += share_s[k];
-        int order[ROUTE_K_MAX];
-        float wts[ROUTE_K_MAX];
-        for (int k = 0; k < K; k++) {
-            const int e = chosen_s[k];
-            const float w = renorm ? share_s[k] / total : share_s[k];
-            o->chosen[k] = e;
-            int q = k;
-            while (q > 0 && order[q - 1] > e) { order[q] = order[q - 1]; wts[q] = wts[q - 1]; q--; }
-            order[q] = e;
-            wts[q] = w;
-        }
-        for (int k = 0; k < K; k++) {
-            o->ids[k] = order[k];
-            o->weights[k] = wts[k];
-        }
-    }
-}
-
 __global__ void route_check_kernel(const float* __restrict__ logits, int E, int K, int renorm, route_out* out) {
     __shared__ float slg[ROUTE_E_MAX];
     __shared__ route_out o;
     wave_route(logits, E, K, renorm, &o, slg);
     __syncthreads();
     if (threadIdx.x < 3 * ROUTE_K_MAX) reinterpret_cast<int32_t*>(out)[threadIdx.x] = reinterpret_cast<const int32_t*>(&o)[threadIdx.x];
+}
+
+/* One wave a row: the routing of n_rows rows of logits (row stride E) into out. */
+__global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ logits, int E, int K, int renorm, route_out* out) {
+    __shared__ float slg[ROUTE_E_MAX];
+    wave_route(logits + (size_t)blockIdx.x * E, E, K, renorm, out + blockIdx.x, slg);
+}
+
+hipError_t launch_topk(const float* logits, int n_rows, int E, int K, int renorm, route_out* out, hipStream_t s) {
+    if (n_rows < 1 || E < 1 || E > ROUTE_E_MAX || E % 4 || K < 1 || K > ROUTE_K_MAX || K > E) return hipErrorInvalidValue;
+    topk_kernel<<<n_rows, 64, 0, s>>>(logits, E, K, renorm, out);
+    return hipGetLastError();
 }
 
 hipError_t launch_route_check(const float* logits, int E, int K, int renorm, route_out* out, hipStream_t s) {
@@ -357,22 +387,6 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / den) * u;
 }
 
-/* The routing of this token into LDS: computed from the logits by wave 0
-   (block 0 also publishing it to rt), or read from rt. */
-__device__ __forceinline__ void block_routing(const experts_in_args& a, route_out* srt) {
-    if (a.logits) {
-        __shared__ float slg[ROUTE_E_MAX];
-        if (threadIdx.x < 64) wave_route(a.logits, a.E, a.K, a.renorm, srt, slg);
-        __syncthreads();
-        if (blockIdx.x == 0 && threadIdx.x < 3 * ROUTE_K_MAX)
-            reinterpret_cast<int32_t*>(a.rt)[threadIdx.x] = reinterpret_cast<const int32_t*>(srt)[threadIdx.x];
-    } else {
-        if (threadIdx.x < 3 * ROUTE_K_MAX)
-            reinterpret_cast<int32_t*>(srt)[threadIdx.x] = reinterpret_cast<const int32_t*>(a.rt)[threadIdx.x];
-        __syncthreads();
-    }
-}
-
 template <int DT, int LPR, int SPL>
 __global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
     constexpr int RPW = WAVE / LPR;
@@ -380,10 +394,11 @@ __global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
     const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
     const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
     const int I = a.gate.rows;
+    if (threadIdx.x < ROUTE_K_MAX) srt.ids[threadIdx.x] = a.rt->ids[threadIdx.x];
     xslice xs[SPL];
 #pragma unroll
     for (int j = 0; j < SPL; j++) load_xslice(DT, al + LPR * j, a.xn, xs[j]);
-    block_routing(a, &srt);
+    __syncthreads();
     const int units = a.K * I;
     for (int u0 = wave * RPW; u0 < units; u0 += 2 * nwaves * RPW) {
         int u[2];
@@ -441,7 +456,6 @@ static hipError_t ein_dispatch(const experts_in_args& a, hipStream_t s) {
 hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s) {
     if (a.gate.dtype != a.up.dtype || a.gate.rows != a.up.rows || a.gate.cols != a.up.cols || a.K < 1 || a.K > ROUTE_K_MAX)
         return hipErrorInvalidValue;
-    if (a.logits && (a.E < a.K || a.E > ROUTE_E_MAX || a.E % 4)) return hipErrorInvalidValue;
     switch (a.gate.dtype) {
         case VITNA_DTYPE_Q8_0: return ein_dispatch<VITNA_DTYPE_Q8_0>(a, s);
         case VITNA_DTYPE_Q4_K: return ein_dispatch<VITNA_DTYPE_Q4_K>(a, s);

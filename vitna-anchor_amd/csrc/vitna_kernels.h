@@ -37,7 +37,8 @@ hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_
 /* RMSNorm of x (n_rows rows of H, row stride H) with norm_w, in the
    reference CPU's order, written to xn_out when it is not NULL, and the
    router's logits for each row (E of them, the router F32 [E x H]) in the
-   reference CPU's order into logits (row stride E). */
+   reference CPU's order into logits (row stride E). The routing itself
+   runs after it (launch_topk). */
 struct route_args {
     const float* x;
     const float* norm_w;
@@ -53,18 +54,16 @@ hipError_t launch_route(const route_args& a, hipStream_t s);
    applies), into *out: for checking it against the reference's rule. */
 hipError_t launch_route_check(const float* logits, int E, int K, int renorm, route_out* out, hipStream_t s);
 
+/* The routing of n_rows rows of logits (row stride E), one wave a row. */
+hipError_t launch_topk(const float* logits, int n_rows, int E, int K, int renorm, route_out* out, hipStream_t s);
+
 /* ---- experts, one token ---- */
 
-/* act[k * I + r] = silu(gate_e[r] . xn) * (up_e[r] . xn) for e = ids[k].
-   With logits set, every block first routes (engine/src/model.c:626-703:
-   top-k of the E logits, softmax weights, renormalized when renorm) and
-   block 0 writes the routing to rt; otherwise rt holds it already. */
+/* act[k * I + r] = silu(gate_e[r] . xn) * (up_e[r] . xn) for e = rt->ids[k]. */
 struct experts_in_args {
     qmat gate, up;
     const float* xn;
-    route_out* rt;
-    const float* logits;
-    int E, renorm;
+    const route_out* rt;
     float* act;
     int K;
 };
