@@ -101,6 +101,12 @@ def main():
     step_bytes = L * sum(per_kernel[w][1] for w in range(6)) + per_kernel[6][1]
     log("algorithmic bytes a step: %.3f GB -> %.1f GB/s over the whole step" % (step_bytes / 1e9, step_bytes / ms / 1e6))
 
+    # the yardstick: a plain device copy of 256 MiB (reads + writes), what streaming reaches on this box
+    copy_bytes = 256 << 20
+    copy_us = va.copy_probe(copy_bytes, reps=10)
+    copy_gbs = 2.0 * copy_bytes / copy_us / 1e3
+    log("copy probe: %d MiB in %.1f us -> %.1f GB/s (read + write)" % (copy_bytes >> 20, copy_us, copy_gbs))
+
     cpu = None
     if not args.no_cpu:
         import oracle
@@ -128,6 +134,7 @@ def main():
                      "bytes_per_launch": b0, "avg_us": round(us0, 3)},
         "kernels_us": {KERNELS[w]: round(per_kernel[w][0], 3) for w in per_kernel},
         "step_algorithmic_GBps": round(step_bytes / ms / 1e6, 1),
+        "copy_probe_GBps": round(copy_gbs, 1),
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

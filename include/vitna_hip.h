@@ -191,6 +191,11 @@ bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int32_t token,
 bool vitna_hip_route_check(const float* logits, int n_experts, int k, bool renormalize, int32_t* chosen, int32_t* ids, float* weights,
                            char* err, size_t err_len);
 
+/** A plain device copy of bytes (a multiple of 16), reps times, on a buffer
+    of its own: the average microseconds a copy. Its hardware counters of
+    bytes fetched and written are the yardstick for the other kernels'. */
+bool vitna_hip_copy_probe(size_t bytes, int reps, double* avg_us, char* err, size_t err_len);
+
 #ifdef __cplusplus
 }
 #endif

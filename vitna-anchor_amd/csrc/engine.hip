@@ -56,6 +56,7 @@ struct vitna_cuda_model {
     row_rec* rows_host; /* pinned */
     hipEvent_t rows_copied;
     float* h_logits;    /* pinned, 2 * ROWS_MAX * E */
+    hipGraph_t step_graph_src; /* kept until free: graph tools may refer to its nodes */
     hipGraphExec_t step_graph;
     bool graph_ready;
     bool lost;
@@ -280,7 +281,10 @@ extern "C" void vitna_cuda_free(struct vitna_cuda_model* g) {
     if (!g) return;
     hipSetDevice(g->device);
     if (g->stream) hipStreamSynchronize(g->stream);
-    if (g->graph_ready) hipGraphExecDestroy(g->step_graph);
+    if (g->graph_ready) {
+        hipGraphExecDestroy(g->step_graph);
+        hipGraphDestroy(g->step_graph_src);
+    }
     for (void* p : g->allocs) hipFree(p);
     if (g->rows_host) hipHostFree(g->rows_host);
     if (g->h_logits) hipHostFree(g->h_logits);
@@ -470,15 +474,17 @@ static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, i
     r.H = g->H; r.E = g->E; r.n_rows = n_rows;
     r.eps = g->eps;
     hipError_t e = launch_route(r, g->stream);
-    if (e == hipSuccess && topk) e = launch_topk(logits, n_rows, g->E, g->K, g->renorm, g->rt, g->stream);
+    /* one token's top-k runs in the experts' prologue (enqueue_experts); several rows' in a kernel of its own */
+    if (e == hipSuccess && topk && n_rows > 1) e = launch_topk(logits, n_rows, g->E, g->K, g->renorm, g->rt, g->stream);
     return e;
 }
 
-/* The experts of one token, routed as g->rt holds it. */
-static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, float* y, int add) {
+/* The experts of one token: routed from logits in the kernel's prologue when they are given, else as g->rt holds it. */
+static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, const float* logits, float* y, int add) {
     const dlayer& d = g->L[layer];
     experts_in_args ai;
-    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.act = g->act; ai.K = g->K;
+    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.logits = logits; ai.E = g->E; ai.renorm = g->renorm;
+    ai.act = g->act; ai.K = g->K;
     hipError_t e = launch_experts_in(ai, g->stream);
     if (e != hipSuccess) return e;
     experts_down_args ad;
@@ -567,7 +573,7 @@ extern "C" bool vitna_cuda_moe_experts(struct vitna_cuda_model* g, size_t layer,
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (!put_routing(g, 1, ids, weights, k, err, err_len)) return false;
-    return check_launch(g, enqueue_experts(g, (int)layer, g->x, 1), "the experts", err, err_len);
+    return check_launch(g, enqueue_experts(g, (int)layer, nullptr, g->x, 1), "the experts", err, err_len);
 }
 
 extern "C" bool vitna_cuda_moe_head(struct vitna_cuda_model* g, float* logits, char* err, size_t err_len) {
@@ -725,7 +731,7 @@ extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_
         ra.x = dx; ra.norm_w = dw; ra.router = drouter; ra.xn_out = dxn; ra.logits = dl;
         ra.H = (int)H; ra.E = 1; ra.n_rows = 1; ra.eps = eps;
         experts_in_args ai;
-        ai.gate = qg; ai.up = qu; ai.xn = dxn; ai.rt = drt; ai.act = dact; ai.K = 1;
+        ai.gate = qg; ai.up = qu; ai.xn = dxn; ai.rt = drt; ai.logits = nullptr; ai.E = 1; ai.renorm = 0; ai.act = dact; ai.K = 1;
         experts_down_args ad;
         ad.down = qd; ad.act = dact; ad.rt = drt; ad.y = dy; ad.K = 1; ad.add = 0;
         ok = launch_route(ra, s) == hipSuccess && launch_experts_in(ai, s) == hipSuccess && launch_experts_down(ad, s) == hipSuccess &&
@@ -751,7 +757,7 @@ static hipError_t enqueue_step_body(vitna_cuda_model* g) {
     for (int l = 0; e == hipSuccess && l < g->NL; l++) {
         e = enqueue_attention(g, l, 1, false);
         if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, 1, g->x, g->xn, true);
-        if (e == hipSuccess) e = enqueue_experts(g, l, g->x, 1);
+        if (e == hipSuccess) e = enqueue_experts(g, l, g->rlogits, g->x, 1);
     }
     if (e == hipSuccess) e = enqueue_head(g);
     return e;
@@ -767,8 +773,9 @@ static bool ensure_graph(vitna_cuda_model* g, char* err, size_t err_len) {
     if (e != hipSuccess) { if (graph) hipGraphDestroy(graph); return check_launch(g, e, "capturing the step", err, err_len); }
     HIP_TRY(e2, "ending the capture of the step");
     const hipError_t e3 = hipGraphInstantiate(&g->step_graph, graph, nullptr, nullptr, 0);
-    hipGraphDestroy(graph);
+    if (e3 != hipSuccess) hipGraphDestroy(graph);
     HIP_TRY(e3, "instantiating the step's graph");
+    g->step_graph_src = graph;
     g->graph_ready = true;
     return true;
 }
@@ -794,7 +801,7 @@ extern "C" bool vitna_hip_moe_ffn(struct vitna_cuda_model* g, size_t layer, char
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     hipError_t e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn, true);
-    if (e == hipSuccess) e = enqueue_experts(g, (int)layer, g->x, 1);
+    if (e == hipSuccess) e = enqueue_experts(g, (int)layer, g->rlogits, g->x, 1);
     return check_launch(g, e, "the mixture of experts", err, err_len);
 }
 
@@ -884,8 +891,9 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
         switch (which) {
             case 0: {
                 experts_in_args ai;
-                ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.act = g->act; ai.K = K;
-                b = 2.0 * K * qmat_bytes(d.gate) + H * 4.0 + K * (double)g->I * 4;
+                ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.logits = g->rlogits; ai.E = g->E;
+                ai.renorm = g->renorm; ai.act = g->act; ai.K = K;
+                b = 2.0 * K * qmat_bytes(d.gate) + H * 4.0 + K * (double)g->I * 4 + g->E * 4.0;
                 return launch_experts_in(ai, g->stream);
             }
             case 8:
@@ -1030,5 +1038,24 @@ extern "C" bool vitna_hip_route_check(const float* logits, int n_experts, int k,
         if (ids) ids[i] = r.ids[i];
         if (weights) weights[i] = r.weights[i];
     }
+    return true;
+}
+
+extern "C" bool vitna_hip_copy_probe(size_t bytes, int reps, double* avg_us, char* err, size_t err_len) {
+    if (bytes % 16 || bytes == 0 || reps < 1) return fail(err, err_len, "a positive multiple of 16 bytes, at least one repetition");
+    void *a = nullptr, *b = nullptr;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    bool ok = hipMalloc(&a, bytes) == hipSuccess && hipMalloc(&b, bytes) == hipSuccess && hipMemset(a, 0, bytes) == hipSuccess &&
+              hipEventCreate(&t0) == hipSuccess && hipEventCreate(&t1) == hipSuccess && launch_copy_probe(a, b, bytes, 0) == hipSuccess &&
+              hipEventRecord(t0, 0) == hipSuccess;
+    for (int i = 0; ok && i < reps; i++) ok = launch_copy_probe(a, b, bytes, 0) == hipSuccess;
+    float ms = 0;
+    ok = ok && hipEventRecord(t1, 0) == hipSuccess && hipEventSynchronize(t1) == hipSuccess && hipEventElapsedTime(&ms, t0, t1) == hipSuccess;
+    if (t0) hipEventDestroy(t0);
+    if (t1) hipEventDestroy(t1);
+    hipFree(a);
+    hipFree(b);
+    if (!ok) return fail(err, err_len, "the copy probe failed");
+    if (avg_us) *avg_us = 1000.0 * ms / reps;
     return true;
 }

@@ -132,22 +132,36 @@ __device__ __forceinline__ float fold16_lanes(float a) {
    wave: the K largest of E logits, largest first, the lower index first
    between equals; the chosen sorted by id; softmax weights over every
    expert; renormalized over the chosen, summed largest first, when renorm.
-   Lane 0 writes *o. slg: E floats of LDS.
+   Lanes write *o. slg: ROUTE_E_MAX floats of LDS.
 
-   Without NaNs the K passes of argmax equal a ranking: expert e is chosen
-   k-th where k is the number of experts better than it (a larger logit, or
-   an equal one at a lower index), so every lane ranks its own experts against
-   all E at once. With a NaN among the logits the passes are run as the
+   Without NaNs the K passes of argmax equal a selection by value: every
+   logit becomes an order-preserving 32-bit key (-0 keyed as +0, since the
+   passes compare with >), the K-th largest key is found a bit at a time from
+   the top (ballots and popcounts), the keys above it are chosen and then the
+   lowest indices among those equal to it, and the chosen are ranked among
+   themselves. With a NaN among the logits the passes are run as the
    reference runs them (a NaN where a pass starts is kept, since x > NaN is
    false; a later one never wins). */
+#define RPL (ROUTE_E_MAX / 64) /* logits a lane */
+
+__device__ __forceinline__ uint32_t order_key(float v) {
+    uint32_t u = __float_as_uint(v);
+    if (u == 0x80000000u) u = 0; /* -0 == +0 */
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ int popc64(uint64_t b) { return __popcll(b); }
+
 __device__ __forceinline__ void wave_route(const float* __restrict__ lg_in, int E, int K, int renorm, route_out* o, float* slg) {
     const int lane = threadIdx.x & 63;
     __shared__ int chosen_s[ROUTE_K_MAX];
+    __shared__ int cand_e[ROUTE_K_MAX];
+    __shared__ uint32_t cand_k[ROUTE_K_MAX];
     __shared__ float share_s[ROUTE_K_MAX];
-    float lg[ROUTE_E_MAX / 64];
+    float lg[RPL];
     bool nan = false;
 #pragma unroll
-    for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+    for (int i = 0; i < RPL; i++) {
         const int e = lane + 64 * i;
         lg[i] = e < E ? lg_in[e] : -INFINITY;
         if (e < E) {
@@ -164,7 +178,7 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ lg_in, int 
             int first = 0x7fffffff, bi = 0x7fffffff;
             float bv = 0.0f;
 #pragma unroll
-            for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
+            for (int i = 0; i < RPL; i++) {
                 const int e = lane + 64 * i;
                 if (e < E && !(taken >> i & 1)) {
                     first = min(first, e);
@@ -184,52 +198,72 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ lg_in, int 
             if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
             if (lane == 0) chosen_s[k] = pick;
         }
-    } else if (E <= 128) {
-        /* ranks against all E logits read four at a time, the loop unrolled over the largest E it serves */
+    } else {
+        uint32_t key[RPL];
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < RPL; i++) key[i] = lane + 64 * i < E ? order_key(lg[i]) : 0u;
+        /* the K-th largest key: the largest t with #{key >= t} >= K (keys of absent experts are 0, below every logit's) */
+        uint32_t thr = 0;
+        for (int bit = 31; bit >= 0; bit--) {
+            const uint32_t cand = thr | (1u << bit);
+            int cnt = 0;
+#pragma unroll
+            for (int i = 0; i < RPL; i++)
+                if (64 * i < E) cnt += popc64(__ballot(key[i] >= cand));
+            if (cnt >= K) thr = cand;
+        }
+        /* chosen: every key above thr, then the lowest indices with key == thr */
+        int above = 0;
+#pragma unroll
+        for (int i = 0; i < RPL; i++)
+            if (64 * i < E) above += popc64(__ballot(key[i] > thr && lane + 64 * i < E));
+        int slot_gt = 0, slot_eq = above;
+#pragma unroll
+        for (int i = 0; i < RPL; i++) {
+            if (64 * i >= E) continue;
             const int e = lane + 64 * i;
-            const float v = lg[i];
-            int rank = 0;
-#pragma unroll
-            for (int q = 0; q < 128; q += 4) {
-                if (q < E) {
-                    const float4 u = *reinterpret_cast<const float4*>(slg + q);
-                    rank += (u.x > v) | ((u.x == v) & (q < e));
-                    rank += (u.y > v) | ((u.y == v) & (q + 1 < e));
-                    rank += (u.z > v) | ((u.z == v) & (q + 2 < e));
-                    rank += (u.w > v) | ((u.w == v) & (q + 3 < e));
+            const bool gt = key[i] > thr && e < E, eq = key[i] == thr && e < E;
+            const uint64_t bgt = __ballot(gt), beq = __ballot(eq);
+            const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+            if (gt) {
+                const int at = slot_gt + popc64(bgt & below);
+                cand_e[at] = e;
+                cand_k[at] = key[i];
+            }
+            if (eq) {
+                const int at = slot_eq + popc64(beq & below);
+                if (at < K) {
+                    cand_e[at] = e;
+                    cand_k[at] = key[i];
                 }
             }
-            if (e < E && rank < K) chosen_s[rank] = e;
+            slot_gt += popc64(bgt);
+            slot_eq += popc64(beq);
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < ROUTE_E_MAX / 64; i++) {
-            const int e = lane + 64 * i;
-            if (e >= E) continue;
-            const float v = lg[i];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        /* rank the K candidates: a larger key, or an equal one at a lower index, comes first */
+        if (lane < K) {
+            const int e = cand_e[lane];
+            const uint32_t kk = cand_k[lane];
             int rank = 0;
-            for (int q = 0; q < E; q += 4) {
-                const float4 u = *reinterpret_cast<const float4*>(slg + q);
-                rank += (u.x > v) | ((u.x == v) & (q < e));
-                rank += (u.y > v) | ((u.y == v) & (q + 1 < e));
-                rank += (u.z > v) | ((u.z == v) & (q + 2 < e));
-                rank += (u.w > v) | ((u.w == v) & (q + 3 < e));
+            for (int j = 0; j < K; j++) {
+                const uint32_t kj = cand_k[j];
+                rank += (kj > kk) | ((kj == kk) & (cand_e[j] < e));
             }
-            if (rank < K) chosen_s[rank] = e;
+            chosen_s[rank] = e;
         }
     }
     /* softmax over every expert: the max as the CPU scans it (a NaN first stays), the sum of exp(l - max) */
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
+    for (int i = 0; i < RPL; i++)
         if (lane + 64 * i < E) mx = fmaxf(mx, lg[i]);
     mx = wave_max(mx);
     if (l0 != l0) mx = l0;
     float sum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < ROUTE_E_MAX / 64; i++)
+    for (int i = 0; i < RPL; i++)
         if (lane + 64 * i < E) sum += expf(lg[i] - mx);
     sum = wave_sum(sum);
     __builtin_amdgcn_wave_barrier();
@@ -394,11 +428,19 @@ __global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
     const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
     const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
     const int I = a.gate.rows;
-    if (threadIdx.x < ROUTE_K_MAX) srt.ids[threadIdx.x] = a.rt->ids[threadIdx.x];
     xslice xs[SPL];
 #pragma unroll
     for (int j = 0; j < SPL; j++) load_xslice(DT, al + LPR * j, a.xn, xs[j]);
-    __syncthreads();
+    if (a.logits) {
+        __shared__ float slg[ROUTE_E_MAX];
+        if (threadIdx.x < 64) wave_route(a.logits, a.E, a.K, a.renorm, &srt, slg);
+        __syncthreads();
+        if (blockIdx.x == 0 && threadIdx.x < 3 * ROUTE_K_MAX)
+            reinterpret_cast<int32_t*>(a.rt)[threadIdx.x] = reinterpret_cast<const int32_t*>(&srt)[threadIdx.x];
+    } else {
+        if (threadIdx.x < ROUTE_K_MAX) srt.ids[threadIdx.x] = a.rt->ids[threadIdx.x];
+        __syncthreads();
+    }
     const int units = a.K * I;
     for (int u0 = wave * RPW; u0 < units; u0 += 2 * nwaves * RPW) {
         int u[2];
@@ -456,6 +498,7 @@ static hipError_t ein_dispatch(const experts_in_args& a, hipStream_t s) {
 hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s) {
     if (a.gate.dtype != a.up.dtype || a.gate.rows != a.up.rows || a.gate.cols != a.up.cols || a.K < 1 || a.K > ROUTE_K_MAX)
         return hipErrorInvalidValue;
+    if (a.logits && (a.E < a.K || a.E > ROUTE_E_MAX || a.E % 4)) return hipErrorInvalidValue;
     switch (a.gate.dtype) {
         case VITNA_DTYPE_Q8_0: return ein_dispatch<VITNA_DTYPE_Q8_0>(a, s);
         case VITNA_DTYPE_Q4_K: return ein_dispatch<VITNA_DTYPE_Q4_K>(a, s);
@@ -744,5 +787,20 @@ __global__ void fill_normal_kernel(float* __restrict__ out, size_t n, uint64_t s
 hipError_t launch_fill_normal(float* out, size_t n, uint64_t seed, hipStream_t s) {
     if (!n) return hipSuccess;
     fill_normal_kernel<<<4096, 256, 0, s>>>(out, n, seed);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------------ */
+/* A plain copy of known size: the yardstick hardware counters of bytes  */
+/* read and written are scaled by.                                       */
+/* ------------------------------------------------------------------ */
+
+__global__ void copy_probe_kernel(const float4* __restrict__ src, float4* __restrict__ dst, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) dst[i] = src[i];
+}
+
+hipError_t launch_copy_probe(const void* src, void* dst, size_t bytes, hipStream_t s) {
+    if (bytes % 16) return hipErrorInvalidValue;
+    copy_probe_kernel<<<2048, 256, 0, s>>>(reinterpret_cast<const float4*>(src), reinterpret_cast<float4*>(dst), bytes / 16);
     return hipGetLastError();
 }

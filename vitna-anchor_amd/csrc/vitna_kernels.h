@@ -59,11 +59,16 @@ hipError_t launch_topk(const float* logits, int n_rows, int E, int K, int renorm
 
 /* ---- experts, one token ---- */
 
-/* act[k * I + r] = silu(gate_e[r] . xn) * (up_e[r] . xn) for e = rt->ids[k]. */
+/* act[k * I + r] = silu(gate_e[r] . xn) * (up_e[r] . xn) for e = ids[k].
+   With logits set, every block first routes the token (the rule of
+   engine/src/model.c:626-703 on its E router logits) and block 0 publishes
+   the routing to rt; otherwise rt holds it already. */
 struct experts_in_args {
     qmat gate, up;
     const float* xn;
-    const route_out* rt;
+    route_out* rt;
+    const float* logits;
+    int E, renorm;
     float* act;
     int K;
 };
@@ -148,6 +153,7 @@ hipError_t launch_attention_merge(const attn_args& a, hipStream_t s);
 hipError_t launch_attention_prepare(const attn_args& a, hipStream_t s);
 
 /* ---- helpers ---- */
+hipError_t launch_copy_probe(const void* src, void* dst, size_t bytes, hipStream_t s);
 hipError_t launch_fill_normal(float* out, size_t n, uint64_t seed, hipStream_t s);
 
 #endif

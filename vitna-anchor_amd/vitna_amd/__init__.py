@@ -242,6 +242,7 @@ def _hip():
         "vitna_hip_moe_prefill": (C.c_bool, [P, C.c_size_t, _FP, C.c_size_t, *E]),
 "vitna_hip_route_check": (C.c_bool, [_FP, C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                              _FP, *E]),
+        "vitna_hip_copy_probe": (C.c_bool, [C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_steps": (C.c_bool, [P, C.c_size_t, C.c_int32, C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_kernel": (C.c_bool, [P, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double),
                                              C.POINTER(C.c_double), *E]),
@@ -404,6 +405,15 @@ def expert_check(gate, up, down, norm_w, x, eps):
                                        fptr(act), fptr(y), err, 512):
         raise VitnaError(err.value.decode())
     return xs, act, y
+
+
+def copy_probe(nbytes, reps=10):
+    """vitna_hip_copy_probe: average microseconds of a plain device copy of nbytes."""
+    us = C.c_double()
+    err = C.create_string_buffer(512)
+    if not hip().vitna_hip_copy_probe(nbytes, reps, C.byref(us), err, 512):
+        raise VitnaError(err.value.decode())
+    return us.value
 
 
 def route_check(logits, k, renormalize):
