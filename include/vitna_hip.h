@@ -131,6 +131,16 @@ bool vitna_hip_moe_step(struct vitna_cuda_model* g, size_t seq, int32_t token, s
     throughput measurement. */
 bool vitna_hip_moe_step_async(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, char* err, size_t err_len);
 
+/** A whole decode step of n rows (tokens of any sequences at their own
+    positions, as vitna_cuda_moe_rows_route takes them) on the device:
+    attention over each row's cache, the router and top-k of every row on the
+    device, the rows grouped by expert so each selected expert's weights are
+    read once for all the rows routed to it, the head. logits[i] receives row
+    i's vocab logits where logits and it are not NULL; with logits NULL the
+    step is only enqueued. Captured into a HIP graph per row count. */
+bool vitna_hip_moe_rows_step(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, float* const* logits, char* err,
+                             size_t err_len);
+
 /** The mixture-of-experts half of layer (RMSNorm, router, top-k on the
     device, experts, weighted sum) on residual row 0, in place, enqueued. */
 bool vitna_hip_moe_ffn(struct vitna_cuda_model* g, size_t layer, char* err, size_t err_len);

@@ -1,0 +1,97 @@
+"""Several rows a layer at a time (BASELINE config 3's ragged decode, and the
+ABI's vitna_cuda_moe_rows_*), against the CPU checker run a step at a time.
+
+Each row must give what its own step would: identical expert choice every
+layer, logits within 1e-3 of max |cpu| (fp32 accumulation in another order).
+Rows of one sequence at consecutive positions see each other's keys, as
+consecutive steps would.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import vitna_amd as va
+from test_gpu_decode import SMALL, rel, say
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-3
+
+
+def model_with_cache(name, seed, prefill, seqs):
+    spec = dict(SMALL[name], seqs=seqs)
+    model = va.Model(va.shape(**spec), seed)
+    cfg = model.cfg
+    kd = cfg.n_kv_heads * cfg.head_dim
+    L, ctx = cfg.n_layers, model.m.ctx
+    kc = np.ctypeslib.as_array(model.m.k_cache, shape=(seqs, L, ctx, kd))
+    vc = np.ctypeslib.as_array(model.m.v_cache, shape=(seqs, L, ctx, kd))
+    kc[:] = va.normal(seed, 101, kc.size).reshape(kc.shape)
+    vc[:] = va.normal(seed, 102, vc.size).reshape(vc.shape)
+    dev = va.Device(model)
+    for s in range(seqs):
+        for l in range(L):
+            dev.kv(s, l, 0, prefill[s], kc[s, l, :prefill[s]], vc[s, l, :prefill[s]])
+    return model, dev
+
+
+def cpu_rows(model, rows):
+    """The CPU checker a step at a time, in the rows' order: (logits, chosen per layer) per row."""
+    out = []
+    for tok, pos, seq in rows:
+        lg, _, tc, _ = oracle.step(model, seq, tok, pos)
+        out.append((lg, tc))
+    return out
+
+
+@pytest.mark.parametrize("name", ["q8", "q4km"])
+def test_rows_abi_layer_by_layer(name):
+    """model.c's moe_rows_on_gpu played by the test: rows up to the router on the device, the host routes each
+    row, the device runs the grouped experts. Two rows share sequence 1 at consecutive positions."""
+    say("rows abi", name)
+    prefill = [40, 17, 60]
+    model, dev = model_with_cache(name, 777, prefill, 3)
+    try:
+        cfg = model.cfg
+        K = cfg.n_experts_used
+        rows = [(5, prefill[0], 0), (9, prefill[1], 1), (13, prefill[2], 2), (21, prefill[1] + 1, 1)]
+        ref = cpu_rows(model, rows)
+        for l in range(cfg.n_layers):
+            lg = dev.rows_route(rows, l)
+            ids, ws = [], []
+            for i in range(len(rows)):
+                ch, order, w = oracle.route(lg[i], K, bool(cfg.renormalize))
+                assert np.array_equal(ch, ref[i][1][l]), ("row", i, "layer", l)
+                ids.append(order)
+                ws.append(w)
+            dev.rows_experts(l, np.array(ids), np.array(ws))
+        logits = dev.rows_head(len(rows))
+        for i in range(len(rows)):
+            r = rel(logits[i], ref[i][0])
+            say("  row", i, "logits rel err", r)
+            assert r <= REL
+    finally:
+        dev.close()
+        model.free()
+
+
+@pytest.mark.parametrize("name", ["q8", "q4km"])
+def test_rows_step_device_routed(name):
+    """vitna_hip_moe_rows_step: ragged rows of distinct sequences (config 3's shape, scaled down), routed and
+    grouped on the device, replayed twice through one graph (the second pass one position on)."""
+    say("rows step", name)
+    seqs = 6
+    prefill = [3, 70, 12, 45, 1, 66]
+    model, dev = model_with_cache(name, 888, [p + 1 for p in prefill], seqs)
+    try:
+        for shift in (0, 1):
+            rows = [(11 * s + 3, prefill[s] - 1 + shift, s) for s in range(seqs)]
+            ref = cpu_rows(model, rows)
+            logits = dev.rows_step(rows)
+            for i in range(seqs):
+                r = rel(logits[i], ref[i][0])
+                assert r <= REL, ("row", i, r)
+            say("  pass", shift, "max rel err", max(rel(logits[i], ref[i][0]) for i in range(seqs)))
+    finally:
+        dev.close()
+        model.free()

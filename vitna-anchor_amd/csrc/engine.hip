@@ -57,6 +57,12 @@ struct vitna_cuda_model {
     hipEvent_t rows_copied;
     float* h_logits;    /* pinned, 2 * ROWS_MAX * E */
     hipGraph_t step_graph_src; /* kept until free: graph tools may refer to its nodes */
+    int *grp_count, *grp_pairs; /* expert grouping of a pass of rows: [E], [E][ROWS_MAX] */
+    bool rows_shared_seq;       /* the pass's rows include two of one sequence (attention prepares first) */
+    hipGraph_t rows_graph_src;
+    hipGraphExec_t rows_graph;
+    int rows_graph_n;           /* the pass the rows graph was captured for: rows, or 0 for none */
+    bool rows_graph_shared;
     hipGraphExec_t step_graph;
     bool graph_ready;
     bool lost;
@@ -285,6 +291,10 @@ extern "C" void vitna_cuda_free(struct vitna_cuda_model* g) {
         hipGraphExecDestroy(g->step_graph);
         hipGraphDestroy(g->step_graph_src);
     }
+    if (g->rows_graph_n) {
+        hipGraphExecDestroy(g->rows_graph);
+        hipGraphDestroy(g->rows_graph_src);
+    }
     for (void* p : g->allocs) hipFree(p);
     if (g->rows_host) hipHostFree(g->rows_host);
     if (g->h_logits) hipHostFree(g->h_logits);
@@ -395,7 +405,9 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
          dalloc(g, &g->act, R * K * c->intermediate * 4, "scratch", err, err_len) &&
          dalloc(g, &g->ypart, R * K * H * 4, "scratch", err, err_len) &&
          dalloc(g, &g->rlogits, 2 * R * E * 4, "scratch", err, err_len) && dalloc(g, &g->rt, R * sizeof(route_out), "scratch", err, err_len) &&
-         dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len);
+         dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len) &&
+         dalloc(g, &g->grp_count, E * sizeof(int), "scratch", err, err_len) &&
+         dalloc(g, &g->grp_pairs, E * R * sizeof(int), "scratch", err, err_len);
     if (ok && g->attention) {
         ok = dalloc(g, &g->q, R * qd * 4, "scratch", err, err_len) && dalloc(g, &g->qp, R * qd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->k, R * kd * 4, "scratch", err, err_len) && dalloc(g, &g->v, R * kd * 4, "scratch", err, err_len) &&
@@ -969,25 +981,6 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
 
 /* Rows and prefill: kernels_rows.hip. */
 
-extern "C" size_t vitna_cuda_moe_rows_max(const struct vitna_cuda_model* g) { return g ? ROWS_MAX : 0; }
-
-extern "C" bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, size_t layer, float* logits,
-                                          float* next, char* err, size_t err_len) {
-    (void)g; (void)rows; (void)n; (void)layer; (void)logits; (void)next;
-    return fail(err, err_len, "rows are not yet served");
-}
-
-extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t layer, size_t n, const int32_t* ids, const float* weights,
-                                            size_t k, const int32_t* guess, char* err, size_t err_len) {
-    (void)g; (void)layer; (void)n; (void)ids; (void)weights; (void)k; (void)guess;
-    return fail(err, err_len, "rows are not yet served");
-}
-
-extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, float* const* logits, char* err, size_t err_len) {
-    (void)g; (void)n; (void)logits;
-    return fail(err, err_len, "rows are not yet served");
-}
-
 extern "C" bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, char* err, size_t err_len) {
     (void)g; (void)layer; (void)x; (void)n;
     return fail(err, err_len, "prefill is not yet served");
@@ -1057,5 +1050,198 @@ extern "C" bool vitna_hip_copy_probe(size_t bytes, int reps, double* avg_us, cha
     hipFree(b);
     if (!ok) return fail(err, err_len, "the copy probe failed");
     if (avg_us) *avg_us = 1000.0 * ms / reps;
+    return true;
+}
+
+/* ---- several rows a layer at a time (model_cuda.h:124-161) -------------- */
+
+extern "C" size_t vitna_cuda_moe_rows_max(const struct vitna_cuda_model* g) { return g ? ROWS_MAX : 0; }
+
+static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n) {
+    const dlayer& d = g->L[layer];
+    hipError_t e = launch_norm_rows(g->x, d.attn_norm, g->xn, n, g->H, g->eps, g->stream);
+    if (e != hipSuccess) return e;
+    gemv_multi_args ga;
+    memset(&ga, 0, sizeof(ga));
+    ga.w[0] = d.q; ga.w[1] = d.k; ga.w[2] = d.v;
+    ga.y[0] = g->q; ga.y[1] = g->k; ga.y[2] = g->v;
+    ga.nm = 3; ga.x = g->xn; ga.n = n; ga.xstride = g->H;
+    e = launch_gemv_multi(ga, g->stream);
+    if (e != hipSuccess) return e;
+    attn_args a;
+    memset(&a, 0, sizeof(a));
+    a.q_raw = g->q; a.k_raw = g->k; a.v_raw = g->v;
+    a.q_norm = d.q_norm; a.k_norm = d.k_norm;
+    a.cos_tab = g->cos_tab; a.sin_tab = g->sin_tab;
+    a.k_cache = g->k_cache + (size_t)layer * g->layer_kv;
+    a.v_cache = g->v_cache + (size_t)layer * g->layer_kv;
+    a.seq_stride = (size_t)g->NL * g->layer_kv;
+    a.rows = g->rows_dev;
+    a.n_rows = n;
+    a.partial = g->partial;
+    a.att = g->att;
+    a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx; a.splits_max = g->splits_max;
+    a.eps = g->eps;
+    if (g->rows_shared_seq) {
+        /* rows of one sequence see each other's keys: all of them stored before any attention reads */
+        a.q_out = g->qp;
+        e = launch_attention_prepare(a, g->stream);
+        if (e != hipSuccess) return e;
+        a.q_raw = g->qp;
+        a.prepared = 1;
+    }
+    e = launch_attention(a, g->stream);
+    if (e == hipSuccess) e = launch_attention_merge(a, g->stream);
+    if (e != hipSuccess) return e;
+    gemv_multi_args go;
+    memset(&go, 0, sizeof(go));
+    go.w[0] = d.o; go.y[0] = g->x; go.nm = 1; go.x = g->att; go.n = n; go.xstride = g->nh * g->hd; go.add = 1;
+    return launch_gemv_multi(go, g->stream);
+}
+
+/* The grouped experts of the pass's n rows, routed as g->rt[0..n) holds it, added onto the residual rows. */
+static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n) {
+    const dlayer& d = g->L[layer];
+    hipError_t e = launch_group(g->rt, n, g->E, g->K, ROWS_MAX, g->grp_count, g->grp_pairs, g->stream);
+    if (e != hipSuccess) return e;
+    grouped_args a;
+    a.gate = d.gate; a.up = d.up; a.down = d.down;
+    a.xn = g->xn; a.rt = g->rt; a.count = g->grp_count; a.pairs = g->grp_pairs;
+    a.E = g->E; a.K = g->K; a.cap = ROWS_MAX; a.act = g->act; a.ypart = g->ypart;
+    e = launch_grouped_in(a, g->stream);
+    if (e == hipSuccess) e = launch_grouped_down(a, g->stream);
+    if (e == hipSuccess) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
+    return e;
+}
+
+static hipError_t enqueue_rows_head(vitna_cuda_model* g, int n) {
+    hipError_t e = launch_norm_rows(g->x, g->final_norm, g->xn, n, g->H, g->eps, g->stream);
+    if (e != hipSuccess) return e;
+    gemv_multi_args gh;
+    memset(&gh, 0, sizeof(gh));
+    gh.w[0] = g->head; gh.y[0] = g->vocab; gh.nm = 1; gh.x = g->xn; gh.n = n; gh.xstride = g->H;
+    return launch_gemv_multi(gh, g->stream);
+}
+
+/* The pass's rows to the device, checked as a step checks its token (model.c:1190-1200). */
+static bool set_rows(vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, char* err, size_t err_len) {
+    if (n < 1 || n > ROWS_MAX) return fail(err, err_len, "%zu rows: 1 to %d a pass", n, ROWS_MAX);
+    bool shared = false;
+    for (size_t i = 0; i < n; i++) {
+        const vitna_cuda_row_t r = rows[i];
+        if (r.seq < 0 || r.seq >= g->seqs) return fail(err, err_len, "row %zu: sequence %d, the cache holds %d", i, r.seq, g->seqs);
+        if (r.pos < 0 || r.pos >= g->ctx) return fail(err, err_len, "row %zu: position %d, the cache holds %d", i, r.pos, g->ctx);
+        if (r.token < 0 || r.token >= g->V) return fail(err, err_len, "row %zu: token %d outside the vocabulary of %d", i, r.token, g->V);
+        for (size_t j = 0; j < i; j++) shared |= rows[j].seq == r.seq;
+    }
+    HIP_TRY(hipEventSynchronize(g->rows_copied), "waiting for the previous row copy");
+    for (size_t i = 0; i < n; i++) g->rows_host[i] = {rows[i].token, rows[i].pos, rows[i].seq};
+    HIP_TRY(hipMemcpyAsync(g->rows_dev, g->rows_host, n * sizeof(row_rec), hipMemcpyHostToDevice, g->stream), "copying the rows");
+    HIP_TRY(hipEventRecord(g->rows_copied, g->stream), "recording the row copy");
+    g->rows_n = (int)n;
+    g->rows_shared_seq = shared;
+    return true;
+}
+
+extern "C" bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, size_t layer, float* logits,
+                                          float* next, char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!g->attention) return fail(err, err_len, "this model has no attention");
+    if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    if (layer == 0) {
+        if (!set_rows(g, rows, n, err, err_len)) return false;
+        if (!check_launch(g, launch_embed_rows(g->embed, g->rows_dev, (int)n, g->x, g->stream), "the embeddings", err, err_len)) return false;
+    } else if (n != (size_t)g->rows_n) {
+        return fail(err, err_len, "%zu rows at layer %zu; the pass took %d at layer 0", n, layer, g->rows_n);
+    }
+    hipError_t e = enqueue_rows_attention(g, (int)layer, (int)n);
+    if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, (int)n, g->x, g->xn, false);
+    const bool nx = next && layer + 1 < (size_t)g->NL;
+    if (e == hipSuccess && nx) {
+        const dlayer& d = g->L[layer + 1];
+        route_args r;
+        memset(&r, 0, sizeof(r));
+        r.x = g->x; r.norm_w = d.mlp_norm; r.router = d.router; r.logits = g->rlogits + (size_t)ROWS_MAX * g->E;
+        r.H = g->H; r.E = g->E; r.n_rows = (int)n; r.eps = g->eps;
+        e = launch_route(r, g->stream);
+    }
+    if (!check_launch(g, e, "the rows up to their router", err, err_len)) return false;
+    const size_t bytes = n * g->E * 4;
+    HIP_TRY(hipMemcpyAsync(logits, g->rlogits, bytes, hipMemcpyDeviceToHost, g->stream), "copying the router's logits");
+    if (nx) HIP_TRY(hipMemcpyAsync(next, g->rlogits + (size_t)ROWS_MAX * g->E, bytes, hipMemcpyDeviceToHost, g->stream), "copying the guess");
+    HIP_TRY(hipStreamSynchronize(g->stream), "running the rows up to their router");
+    return true;
+}
+
+extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t layer, size_t n, const int32_t* ids, const float* weights,
+                                            size_t k, const int32_t* guess, char* err, size_t err_len) {
+    (void)guess;
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
+    if (!put_routing(g, n, ids, weights, k, err, err_len)) return false;
+    return check_launch(g, enqueue_rows_experts(g, (int)layer, (int)n), "the rows' experts", err, err_len);
+}
+
+extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, float* const* logits, char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!g->attention) return fail(err, err_len, "this model has no output projection");
+    if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
+    if (!check_launch(g, enqueue_rows_head(g, (int)n), "the head", err, err_len)) return false;
+    for (size_t i = 0; i < n; i++)
+        if (logits && logits[i])
+            HIP_TRY(hipMemcpyAsync(logits[i], g->vocab + i * g->V, (size_t)g->V * 4, hipMemcpyDeviceToHost, g->stream), "copying logits");
+    HIP_TRY(hipStreamSynchronize(g->stream), "running the head");
+    return true;
+}
+
+/* A whole decode step of n rows on the device, routing included. */
+static hipError_t enqueue_rows_step_body(vitna_cuda_model* g, int n) {
+    hipError_t e = launch_embed_rows(g->embed, g->rows_dev, n, g->x, g->stream);
+    for (int l = 0; e == hipSuccess && l < g->NL; l++) {
+        e = enqueue_rows_attention(g, l, n);
+        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, n, g->x, g->xn, true);
+        if (e == hipSuccess && n == 1) e = launch_topk(g->rlogits, 1, g->E, g->K, g->renorm, g->rt, g->stream);
+        if (e == hipSuccess) e = enqueue_rows_experts(g, l, n);
+    }
+    if (e == hipSuccess) e = enqueue_rows_head(g, n);
+    return e;
+}
+
+static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_len) {
+    if (g->rows_graph_n == n && g->rows_graph_shared == g->rows_shared_seq) return true;
+    if (g->rows_graph_n) {
+        HIP_TRY(hipStreamSynchronize(g->stream), "before recapturing the rows step");
+        hipGraphExecDestroy(g->rows_graph);
+        hipGraphDestroy(g->rows_graph_src);
+        g->rows_graph_n = 0;
+    }
+    HIP_TRY(hipStreamSynchronize(g->stream), "before capturing the rows step");
+    HIP_TRY(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "capturing the rows step");
+    const hipError_t e = enqueue_rows_step_body(g, n);
+    hipGraph_t graph = nullptr;
+    const hipError_t e2 = hipStreamEndCapture(g->stream, &graph);
+    if (e != hipSuccess) { if (graph) hipGraphDestroy(graph); return check_launch(g, e, "capturing the rows step", err, err_len); }
+    HIP_TRY(e2, "ending the capture of the rows step");
+    const hipError_t e3 = hipGraphInstantiate(&g->rows_graph, graph, nullptr, nullptr, 0);
+    if (e3 != hipSuccess) hipGraphDestroy(graph);
+    HIP_TRY(e3, "instantiating the rows step's graph");
+    g->rows_graph_src = graph;
+    g->rows_graph_n = n;
+    g->rows_graph_shared = g->rows_shared_seq;
+    return true;
+}
+
+extern "C" bool vitna_hip_moe_rows_step(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, float* const* logits, char* err,
+                                        size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!g->attention) return fail(err, err_len, "this model has no attention");
+    if (!set_rows(g, rows, n, err, err_len)) return false;
+    if (!ensure_rows_graph(g, (int)n, err, err_len)) return false;
+    HIP_TRY(hipGraphLaunch(g->rows_graph, g->stream), "launching the rows step");
+    for (size_t i = 0; i < n; i++)
+        if (logits && logits[i])
+            HIP_TRY(hipMemcpyAsync(logits[i], g->vocab + i * g->V, (size_t)g->V * 4, hipMemcpyDeviceToHost, g->stream), "copying logits");
+    if (logits) HIP_TRY(hipStreamSynchronize(g->stream), "running the rows step");
     return true;
 }

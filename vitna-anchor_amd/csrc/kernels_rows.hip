@@ -1,0 +1,358 @@
+/**
+ * kernels_rows.hip - Several rows at once (tokens of possibly different
+ * sequences, each at its own position): the dense projections applied to
+ * every row with one read of the weights, and the per-token expert grouping
+ * that turns a ragged batch into grouped expert work, each selected expert's
+ * weights read once for all the rows routed to it.
+ *
+ * Reference counterparts (engine/src/model_cuda.cu): the host counting sort
+ * of (row, expert) pairs :5151-5176, gather_rows_kernel :2059,
+ * experts_in_rows_kernel :2071, experts_down_rows_kernel :2101,
+ * add_rows_kernel :2120, norm_rows_kernel :2020, embed_multi_kernel :1858,
+ * the *_multi kernels :1872-2006.
+ *
+ * The grouping is built on the device (group_kernel): one block per expert
+ * scans every row's routing and lists the (row, slot) pairs routed to it in
+ * order of row, at a fixed capacity of ROWS_CAP pairs an expert, so no prefix
+ * sum over experts is needed. Each pair's output is kept apart (ypart, one
+ * hidden-wide row per pair) and reduce_rows_kernel adds a row's K outputs in
+ * order of expert id, then onto the residual: the order the reference sums
+ * in (engine/src/model.c:757-760).
+ */
+
+#include "vitna_kernels.h"
+
+template <int LPR>
+__device__ __forceinline__ float rsum(float v) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+/* ---- embedding and norms ---------------------------------------------- */
+
+__global__ void embed_rows_kernel(qmat m, const row_rec* __restrict__ rows, float* __restrict__ x, int H) {
+    const int r = blockIdx.y;
+    const int t = rows[r].token;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < H; c += gridDim.x * blockDim.x) x[(size_t)r * H + c] = widen_one(m, 0, t, c);
+}
+
+hipError_t launch_embed_rows(const qmat& embed, const row_rec* rows, int n, float* x, hipStream_t s) {
+    if (n < 1) return hipErrorInvalidValue;
+    embed_rows_kernel<<<dim3((embed.cols + 255) / 256, n), 256, 0, s>>>(embed, rows, x, embed.cols);
+    return hipGetLastError();
+}
+
+/* RMSNorm of each row (block per row), y = (x * inv) * w. */
+__global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y, int H,
+                                                        float eps) {
+    const int r = blockIdx.x;
+    const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)r * H);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 xv[8], wv[8];
+    const int n4 = H / 4;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        if ((int)threadIdx.x + 256 * i < n4) { xv[i] = x4[threadIdx.x + 256 * i]; wv[i] = w4[threadIdx.x + 256 * i]; }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        if ((int)threadIdx.x + 256 * i < n4) {
+            ss = fmaf(xv[i].x, xv[i].x, ss); ss = fmaf(xv[i].y, xv[i].y, ss);
+            ss = fmaf(xv[i].z, xv[i].z, ss); ss = fmaf(xv[i].w, xv[i].w, ss);
+        }
+    __shared__ float red[4];
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    float4* y4 = reinterpret_cast<float4*>(y + (size_t)r * H);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        if ((int)threadIdx.x + 256 * i < n4) {
+            float4 o;
+            o.x = (xv[i].x * inv) * wv[i].x; o.y = (xv[i].y * inv) * wv[i].y;
+            o.z = (xv[i].z * inv) * wv[i].z; o.w = (xv[i].w * inv) * wv[i].w;
+            y4[threadIdx.x + 256 * i] = o;
+        }
+}
+
+hipError_t launch_norm_rows(const float* x, const float* w, float* y, int n, int H, float eps, hipStream_t s) {
+    if (n < 1 || H % 4 || H > 8192) return hipErrorInvalidValue;
+    norm_rows_kernel<<<n, 256, 0, s>>>(x, w, y, H, eps);
+    return hipGetLastError();
+}
+
+/* ---- dense projections of several rows -------------------------------- */
+
+/* y_i[row][r] (+)= W_i[r] . x[row], row < n: a wave's slices of a weight row
+   are read once and applied to every row's activations (x rows L2-resident). */
+template <int DT, int LPR, int SPL>
+__device__ __forceinline__ void gemv_multi_rows(const qmat& w, float* __restrict__ y, int add, const float* __restrict__ x, int n, int xstride,
+                                                int unit0, int ustep, int lane) {
+    constexpr int RPW = WAVE / LPR;
+    const int sub = lane / LPR, al = lane % LPR;
+    const int units = (w.rows + RPW - 1) / RPW;
+    for (int u = unit0; u < units; u += ustep) {
+        const int r = u * RPW + sub, rr = r < w.rows ? r : w.rows - 1;
+        qraw q[SPL];
+#pragma unroll
+        for (int j = 0; j < SPL; j++) slice_load<DT>(w, 0, rr, al + LPR * j, q[j]);
+        for (int t = 0; t < n; t++) {
+            float p = 0.f;
+#pragma unroll
+            for (int j = 0; j < SPL; j++) {
+                xslice xs;
+                load_xslice(DT, al + LPR * j, x + (size_t)t * xstride, xs);
+                p += slice_dot<DT>(q[j], al + LPR * j, xs);
+            }
+            p = rsum<LPR>(p);
+            if (al == 0 && r < w.rows) {
+                float* o = y + (size_t)t * w.rows + r;
+                *o = add ? *o + p : p;
+            }
+        }
+    }
+}
+
+template <int D0, int D1, int D2, int LPR, int SPL>
+__global__ __launch_bounds__(256) void gemv_multi_kernel(gemv_multi_args a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
+    constexpr int RPW = WAVE / LPR;
+    int base = 0;
+    for (int i = 0; i < a.nm; i++) {
+        const int units = (a.w[i].rows + RPW - 1) / RPW;
+        int first = (wave - base) % nwaves;
+        if (first < 0) first += nwaves;
+        if (first < units) {
+            if (i == 0) gemv_multi_rows<D0, LPR, SPL>(a.w[0], a.y[0], a.add, a.x, a.n, a.xstride, first, nwaves, lane);
+            else if (i == 1) gemv_multi_rows<D1, LPR, SPL>(a.w[1], a.y[1], a.add, a.x, a.n, a.xstride, first, nwaves, lane);
+            else gemv_multi_rows<D2, LPR, SPL>(a.w[2], a.y[2], a.add, a.x, a.n, a.xstride, first, nwaves, lane);
+        }
+        base += units;
+    }
+}
+
+template <int D0, int D1, int D2>
+static hipError_t gemv_multi_width(const gemv_multi_args& a, hipStream_t s) {
+    const int S = a.w[0].cols / 32;
+    const int lpr = S < 64 ? S : 64, rpw = WAVE / lpr;
+    int units = 0;
+    for (int i = 0; i < a.nm; i++) units += (a.w[i].rows + rpw - 1) / rpw;
+    int blocks = (units + 3) / 4;
+    if (blocks > 2048) blocks = 2048;
+    switch (S) {
+        case 4: gemv_multi_kernel<D0, D1, D2, 4, 1><<<blocks, 256, 0, s>>>(a); break;
+        case 8: gemv_multi_kernel<D0, D1, D2, 8, 1><<<blocks, 256, 0, s>>>(a); break;
+        case 16: gemv_multi_kernel<D0, D1, D2, 16, 1><<<blocks, 256, 0, s>>>(a); break;
+        case 32: gemv_multi_kernel<D0, D1, D2, 32, 1><<<blocks, 256, 0, s>>>(a); break;
+        case 64: gemv_multi_kernel<D0, D1, D2, 64, 1><<<blocks, 256, 0, s>>>(a); break;
+        case 128: gemv_multi_kernel<D0, D1, D2, 64, 2><<<blocks, 256, 0, s>>>(a); break;
+        case 256: gemv_multi_kernel<D0, D1, D2, 64, 4><<<blocks, 256, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_multi(const gemv_multi_args& a, hipStream_t s) {
+    if (a.nm < 1 || a.nm > 3 || a.n < 1) return hipErrorInvalidValue;
+    for (int i = 1; i < a.nm; i++)
+        if (a.w[i].cols != a.w[0].cols) return hipErrorInvalidValue;
+    const int d0 = a.w[0].dtype, d1 = a.nm > 1 ? a.w[1].dtype : d0, d2 = a.nm > 2 ? a.w[2].dtype : d1;
+    constexpr int Q8 = VITNA_DTYPE_Q8_0, Q4 = VITNA_DTYPE_Q4_K, Q6 = VITNA_DTYPE_Q6_K;
+#define GM_CASE(A, B, C) \
+    if (d0 == A && d1 == B && d2 == C) return gemv_multi_width<A, B, C>(a, s);
+    GM_CASE(Q4, Q4, Q6)
+    GM_CASE(Q4, Q4, Q4)
+    GM_CASE(Q8, Q8, Q8)
+    GM_CASE(Q6, Q6, Q6)
+    GM_CASE(Q4, Q6, Q6)
+    GM_CASE(Q6, Q6, Q4)
+#undef GM_CASE
+    return hipErrorInvalidValue;
+}
+
+/* ---- grouping --------------------------------------------------------- */
+
+/* Block e lists the (row, slot) pairs whose routing names expert e, in order
+   of row: pairs[e * cap + i] = row * ROUTE_K_MAX + slot, count[e] = how many. */
+__global__ __launch_bounds__(256) void group_kernel(const route_out* __restrict__ rt, int n, int K, int cap, int* __restrict__ count,
+                                                    int* __restrict__ pairs) {
+    const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ int wave_n[4];
+    int base = 0;
+    for (int r0 = 0; r0 < n; r0 += 256) {
+        const int r = r0 + tid;
+        int slot = -1;
+        if (r < n)
+            for (int k = 0; k < K; k++)
+                if (rt[r].ids[k] == e) slot = k;
+        const uint64_t b = __ballot(slot >= 0);
+        const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+        if (lane == 0) wave_n[wave] = __popcll(b);
+        __syncthreads();
+        int before = base;
+        for (int w = 0; w < wave; w++) before += wave_n[w];
+        if (slot >= 0) {
+            const int at = before + __popcll(b & below);
+            if (at < cap) pairs[(size_t)e * cap + at] = r * ROUTE_K_MAX + slot;
+        }
+        base += wave_n[0] + wave_n[1] + wave_n[2] + wave_n[3];
+        __syncthreads();
+    }
+    if (tid == 0) count[e] = base < cap ? base : cap;
+}
+
+hipError_t launch_group(const route_out* rt, int n, int E, int K, int cap, int* count, int* pairs, hipStream_t s) {
+    if (n < 1 || n > cap || E < 1 || K < 1 || K > ROUTE_K_MAX) return hipErrorInvalidValue;
+    group_kernel<<<E, 256, 0, s>>>(rt, n, K, cap, count, pairs);
+    return hipGetLastError();
+}
+
+/* ---- grouped experts -------------------------------------------------- */
+
+/* Units (expert, weight row); a wave takes a unit's gate and up slices once
+   and applies them to every row routed to the expert:
+   act[row * K + slot][r] = silu(gate_e[r] . xn[row]) * (up_e[r] . xn[row]). */
+template <int DT, int LPR, int SPL>
+__global__ __launch_bounds__(256) void grouped_in_kernel(grouped_args a) {
+    constexpr int RPW = WAVE / LPR;
+    const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
+    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
+    const int I = a.gate.rows, H = a.gate.cols;
+    const int upe = (I + RPW - 1) / RPW; /* units an expert */
+    for (int u = wave; u < a.E * upe; u += nwaves) {
+        const int e = u / upe, r = (u - e * upe) * RPW + sub;
+        const int c = a.count[e];
+        if (c == 0) continue;
+        const int rr = r < I ? r : I - 1;
+        qraw g[SPL], v[SPL];
+#pragma unroll
+        for (int j = 0; j < SPL; j++) {
+            slice_load<DT>(a.gate, e, rr, al + LPR * j, g[j]);
+            slice_load<DT>(a.up, e, rr, al + LPR * j, v[j]);
+        }
+        for (int i = 0; i < c; i++) {
+            const int pr = a.pairs[(size_t)e * a.cap + i], row = pr / ROUTE_K_MAX, slot = pr % ROUTE_K_MAX;
+            float pg = 0.f, pu = 0.f;
+#pragma unroll
+            for (int j = 0; j < SPL; j++) {
+                xslice xs;
+                load_xslice(DT, al + LPR * j, a.xn + (size_t)row * H, xs);
+                pg += slice_dot<DT>(g[j], al + LPR * j, xs);
+                pu += slice_dot<DT>(v[j], al + LPR * j, xs);
+            }
+            pg = rsum<LPR>(pg);
+            pu = rsum<LPR>(pu);
+            if (al == 0 && r < I) {
+                const float den = 1.0f + expf(-pg);
+                a.act[((size_t)row * a.K + slot) * I + r] = (pg / den) * pu;
+            }
+        }
+    }
+}
+
+/* Units (expert, output row); the down row's slices (S = I / 32 of them,
+   among LPR lanes) read once for every row routed to the expert:
+   ypart[row * K + slot][r] = w_slot * (down_e[r] . act[row * K + slot]). */
+template <int DT, int LPR, int SPL>
+__global__ __launch_bounds__(256) void grouped_down_kernel(grouped_args a) {
+    constexpr int RPW = WAVE / LPR;
+    const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
+    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
+    const int H = a.down.rows, I = a.down.cols, S = I / 32;
+    const int upe = (H + RPW - 1) / RPW;
+    for (int u = wave; u < a.E * upe; u += nwaves) {
+        const int e = u / upe, r = (u - e * upe) * RPW + sub;
+        const int c = a.count[e];
+        if (c == 0) continue;
+        const int rr = r < H ? r : H - 1;
+        qraw q[SPL];
+        bool on[SPL];
+#pragma unroll
+        for (int j = 0; j < SPL; j++) {
+            const int t = al + LPR * j;
+            on[j] = t < S;
+            slice_load<DT>(a.down, e, rr, on[j] ? t : 0, q[j]);
+        }
+        for (int i = 0; i < c; i++) {
+            const int pr = a.pairs[(size_t)e * a.cap + i], row = pr / ROUTE_K_MAX, slot = pr % ROUTE_K_MAX;
+            const float* act = a.act + ((size_t)row * a.K + slot) * I;
+            float p = 0.f;
+#pragma unroll
+            for (int j = 0; j < SPL; j++) {
+                if (!on[j]) continue;
+                xslice xs;
+                load_xslice(DT, al + LPR * j, act, xs);
+                p += slice_dot<DT>(q[j], al + LPR * j, xs);
+            }
+            p = rsum<LPR>(p);
+            if (al == 0 && r < H) a.ypart[((size_t)row * a.K + slot) * H + r] = a.rt[row].weights[slot] * p;
+        }
+    }
+}
+
+template <int DT>
+static hipError_t grouped_dispatch(const grouped_args& a, bool down, hipStream_t s) {
+    const int cols = down ? a.down.cols : a.gate.cols;
+    const int rows = down ? a.down.rows : a.gate.rows;
+    const int S = cols / 32;
+    /* lanes a row: the smallest power of two holding the row's slices, at most 64 */
+    int lpr = 4;
+    while (lpr < S && lpr < 64) lpr *= 2;
+    const int rpw = WAVE / lpr;
+    const long units = (long)a.E * ((rows + rpw - 1) / rpw);
+    int blocks = (int)((units + 3) / 4);
+    if (blocks > 4096) blocks = 4096;
+    const int spl = (S + lpr - 1) / lpr;
+#define GD(L, P)                                                                             \
+    if (lpr == L && spl == P) {                                                              \
+        if (down) grouped_down_kernel<DT, L, P><<<blocks, 256, 0, s>>>(a);                   \
+        else grouped_in_kernel<DT, L, P><<<blocks, 256, 0, s>>>(a);                          \
+        return hipGetLastError();                                                            \
+    }
+    GD(4, 1) GD(8, 1) GD(16, 1) GD(32, 1) GD(64, 1) GD(64, 2) GD(64, 3) GD(64, 4)
+#undef GD
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_grouped_in(const grouped_args& a, hipStream_t s) {
+    if (a.gate.dtype != a.up.dtype || a.gate.cols % 32 || a.gate.cols / 32 > 256 || a.K < 1 || a.K > ROUTE_K_MAX) return hipErrorInvalidValue;
+    /* the gate/up slices of a row must fill the lanes: a power-of-two width */
+    const int S = a.gate.cols / 32;
+    if (S & (S - 1)) return hipErrorInvalidValue;
+    switch (a.gate.dtype) {
+        case VITNA_DTYPE_Q8_0: return grouped_dispatch<VITNA_DTYPE_Q8_0>(a, false, s);
+        case VITNA_DTYPE_Q4_K: return grouped_dispatch<VITNA_DTYPE_Q4_K>(a, false, s);
+        case VITNA_DTYPE_Q6_K: return grouped_dispatch<VITNA_DTYPE_Q6_K>(a, false, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_grouped_down(const grouped_args& a, hipStream_t s) {
+    if (a.down.cols % 32 || a.K < 1 || a.K > ROUTE_K_MAX) return hipErrorInvalidValue;
+    switch (a.down.dtype) {
+        case VITNA_DTYPE_Q8_0: return grouped_dispatch<VITNA_DTYPE_Q8_0>(a, true, s);
+        case VITNA_DTYPE_Q4_K: return grouped_dispatch<VITNA_DTYPE_Q4_K>(a, true, s);
+        case VITNA_DTYPE_Q6_K: return grouped_dispatch<VITNA_DTYPE_Q6_K>(a, true, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+/* x[row][r] = x[row][r] + sum over slots k (in order) of ypart[row * K + k][r]. */
+__global__ void reduce_rows_kernel(const float* __restrict__ ypart, float* __restrict__ x, int n, int K, int H) {
+    const int row = blockIdx.y;
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < H; r += gridDim.x * blockDim.x) {
+        float sum = 0.0f;
+        for (int k = 0; k < K; k++) sum = sum + ypart[((size_t)row * K + k) * H + r];
+        x[(size_t)row * H + r] = x[(size_t)row * H + r] + sum;
+    }
+}
+
+hipError_t launch_reduce_rows(const float* ypart, float* x, int n, int K, int H, hipStream_t s) {
+    if (n < 1 || K < 1) return hipErrorInvalidValue;
+    reduce_rows_kernel<<<dim3((H + 255) / 256, n), 256, 0, s>>>(ypart, x, n, K, H);
+    return hipGetLastError();
+}

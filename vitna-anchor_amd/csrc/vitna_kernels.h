@@ -152,6 +152,40 @@ hipError_t launch_attention_merge(const attn_args& a, hipStream_t s);
    normalized and rotated and v stored into the cache at each row's position. */
 hipError_t launch_attention_prepare(const attn_args& a, hipStream_t s);
 
+/* ---- several rows (kernels_rows.hip) ---- */
+
+hipError_t launch_embed_rows(const qmat& embed, const row_rec* rows, int n, float* x, hipStream_t s);
+hipError_t launch_norm_rows(const float* x, const float* w, float* y, int n, int H, float eps, hipStream_t s);
+
+/* y_i[row][r] (+)= W_i[r] . x[row] for n rows of x (row stride xstride); up to three matrices of one width. */
+struct gemv_multi_args {
+    qmat w[3];
+    float* y[3];
+    int nm;
+    const float* x;
+    int n, xstride, add;
+};
+hipError_t launch_gemv_multi(const gemv_multi_args& a, hipStream_t s);
+
+/* The per-expert lists of (row, slot) pairs of n rows' routing: count[E],
+   pairs[E][cap] = row * ROUTE_K_MAX + slot, in order of row. */
+hipError_t launch_group(const route_out* rt, int n, int E, int K, int cap, int* count, int* pairs, hipStream_t s);
+
+struct grouped_args {
+    qmat gate, up, down;
+    const float* xn;       /* [n][H] */
+    const route_out* rt;   /* [n] */
+    const int* count;      /* [E] */
+    const int* pairs;      /* [E][cap] */
+    int E, K, cap;
+    float* act;            /* [n][K][I] */
+    float* ypart;          /* [n][K][H] */
+};
+hipError_t launch_grouped_in(const grouped_args& a, hipStream_t s);
+hipError_t launch_grouped_down(const grouped_args& a, hipStream_t s);
+/* x[row] += the row's K outputs in ypart, added in slot order. */
+hipError_t launch_reduce_rows(const float* ypart, float* x, int n, int K, int H, hipStream_t s);
+
 /* ---- helpers ---- */
 hipError_t launch_copy_probe(const void* src, void* dst, size_t bytes, hipStream_t s);
 hipError_t launch_fill_normal(float* out, size_t n, uint64_t seed, hipStream_t s);

@@ -233,6 +233,7 @@ def _hip():
         "vitna_hip_moe_step": (C.c_bool, [P, C.c_size_t, C.c_int32, C.c_size_t, _FP, *E]),
         "vitna_hip_moe_step_async": (C.c_bool, [P, C.c_size_t, C.c_int32, C.c_size_t, *E]),
         "vitna_hip_moe_ffn": (C.c_bool, [P, C.c_size_t, *E]),
+        "vitna_hip_moe_rows_step": (C.c_bool, [P, C.POINTER(RowT), C.c_size_t, C.POINTER(_FP), *E]),
         "vitna_hip_residual": (C.c_bool, [P, C.c_size_t, _FP, C.c_bool, *E]),
         "vitna_hip_routing": (C.c_bool, [P, C.c_size_t, _FP, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _FP, *E]),
         "vitna_hip_kv": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, _FP, _FP, C.c_bool, *E]),
@@ -317,6 +318,43 @@ class Device:
     def step(self, seq, token, pos, logits=True):
         out = np.empty(self.model.cfg.vocab, np.float32) if logits else None
         self._ok(self.lib.vitna_hip_moe_step(self.g, seq, token, pos, fptr(out) if logits else None, self.err, 512))
+        return out
+
+    # --- several rows a layer at a time (the ABI's rows_*) ---
+    @staticmethod
+    def _rows(rows):
+        arr = (RowT * len(rows))()
+        for i, (tok, pos, seq) in enumerate(rows):
+            arr[i].token, arr[i].pos, arr[i].seq = tok, pos, seq
+        return arr
+
+    def rows_route(self, rows, layer, want_next=False):
+        E = self.model.cfg.n_experts
+        n = len(rows)
+        lg = np.empty((n, E), np.float32)
+        nx = np.empty((n, E), np.float32) if want_next else None
+        self._ok(self.lib.vitna_cuda_moe_rows_route(self.g, self._rows(rows), n, layer, fptr(lg),
+                                                    fptr(nx) if want_next else None, self.err, 512))
+        return (lg, nx) if want_next else lg
+
+    def rows_experts(self, layer, ids, weights):
+        ids = np.ascontiguousarray(ids, np.int32)
+        w = np.ascontiguousarray(weights, np.float32)
+        n, k = ids.shape
+        self._ok(self.lib.vitna_cuda_moe_rows_experts(self.g, layer, n, _i32(ids), fptr(w), k, None, self.err, 512))
+
+    def rows_head(self, n):
+        V = self.model.cfg.vocab
+        out = np.empty((n, V), np.float32)
+        ptrs = (_FP * n)(*[out[i].ctypes.data_as(_FP) for i in range(n)])
+        self._ok(self.lib.vitna_cuda_moe_rows_head(self.g, n, ptrs, self.err, 512))
+        return out
+
+    def rows_step(self, rows, logits=True):
+        n = len(rows)
+        out = np.empty((n, self.model.cfg.vocab), np.float32) if logits else None
+        ptrs = (_FP * n)(*[out[i].ctypes.data_as(_FP) for i in range(n)]) if logits else None
+        self._ok(self.lib.vitna_hip_moe_rows_step(self.g, self._rows(rows), n, ptrs, self.err, 512))
         return out
 
     def step_async(self, seq, token, pos):
