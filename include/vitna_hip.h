@@ -175,8 +175,22 @@ const float* vitna_hip_logits_device(struct vitna_cuda_model* g);
 /** Prefill of n tokens through the mixture-of-experts half of layer: x is
     n x hidden on the host; each row is normalized, routed (bit-exact expert
     choice), run through its experts as a grouped bf16 MFMA GEMM with fp32
-    accumulation, and its weighted sum added to it in place. */
-bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, char* err, size_t err_len);
+    accumulation, and its weighted sum added to it in place. chosen (n x K,
+    or NULL) receives each row's experts, largest first. The reference's
+    prefill grouping: model_cuda.cu:5151-5176, :2288-2343. Q8_0 experts. */
+bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, int32_t* chosen, char* err, size_t err_len);
+
+/** A prefill of n rows drawn N(0,1) on the device (seed), timed with HIP
+    events over reps runs after a warm-up: us_total, and us_phase[5] = norm +
+    router, routing + grouping, gate/up GEMM, down GEMM, ordered sum. The
+    rows stay on the device for vitna_hip_prefill_rows. */
+bool vitna_hip_time_prefill(struct vitna_cuda_model* g, size_t layer, size_t n, uint64_t seed, int reps, double* us_total,
+                            double* us_phase, char* err, size_t err_len);
+
+/** The input rows, output rows and experts chosen (any may be NULL) of the
+    first n rows of the last prefill on the device. */
+bool vitna_hip_prefill_rows(struct vitna_cuda_model* g, size_t n, float* x_in, float* x_out, int32_t* chosen, char* err,
+                            size_t err_len);
 
 /** Average duration in microseconds of one launch of a kernel of the decode
     path, timed with HIP events on the model's stream over reps launches

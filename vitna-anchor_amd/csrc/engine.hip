@@ -25,6 +25,7 @@
 #include <string.h>
 #include <vector>
 #include <algorithm>
+#include <type_traits>
 
 #define ROWS_MAX 256
 
@@ -68,6 +69,13 @@ struct vitna_cuda_model {
     bool lost;
     size_t fast_rows, long_from;
     int rows_n;         /* rows of the pass in flight (vitna_cuda_moe_rows_*) */
+    /* prefill through one MoE layer: buffers for pf_cap rows, allocated on first use */
+    size_t pf_cap;
+    std::vector<void*> pf_allocs;
+    float *pf_x, *pf_x0, *pf_xn, *pf_logits, *pf_ypart;
+    uint16_t *pf_xb, *pf_act;
+    route_out* pf_rt;
+    int *pf_count, *pf_pairs, *pf_off, *pf_tiles, *pf_ntiles;
 };
 
 static bool fail(char* err, size_t len, const char* fmt, ...) {
@@ -296,6 +304,7 @@ extern "C" void vitna_cuda_free(struct vitna_cuda_model* g) {
         hipGraphDestroy(g->rows_graph_src);
     }
     for (void* p : g->allocs) hipFree(p);
+    for (void* p : g->pf_allocs) hipFree(p);
     if (g->rows_host) hipHostFree(g->rows_host);
     if (g->h_logits) hipHostFree(g->h_logits);
     if (g->rows_copied) hipEventDestroy(g->rows_copied);
@@ -981,9 +990,142 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
 
 /* Rows and prefill: kernels_rows.hip. */
 
-extern "C" bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, char* err, size_t err_len) {
-    (void)g; (void)layer; (void)x; (void)n;
-    return fail(err, err_len, "prefill is not yet served");
+/* ---- prefill through one MoE layer: kernels_prefill.hip ---- */
+
+static bool sync_stream(vitna_cuda_model* g, const char* what, char* err, size_t err_len) {
+    HIP_TRY(hipStreamSynchronize(g->stream), what);
+    return true;
+}
+
+static bool prefill_reserve(vitna_cuda_model* g, size_t n, char* err, size_t err_len) {
+    if (n <= g->pf_cap) return true;
+    HIP_TRY(hipStreamSynchronize(g->stream), "waiting before the prefill buffers grow");
+    for (void* p : g->pf_allocs) hipFree(p);
+    g->pf_allocs.clear();
+    g->pf_cap = 0;
+    const size_t H = g->H, E = g->E, K = g->K, I = g->I;
+    const size_t tiles = (size_t)prefill_max_tiles((int)n, (int)K, (int)E) + 1;
+    auto get = [&](auto** ptr, size_t bytes) -> bool {
+        void* p = nullptr;
+        const hipError_t e = hipMalloc(&p, bytes ? bytes : 256);
+        if (e != hipSuccess) return fail(err, err_len, "device memory for a prefill of %zu rows (%zu bytes): %s", n, bytes, hipGetErrorString(e));
+        g->pf_allocs.push_back(p);
+        *ptr = static_cast<std::remove_reference_t<decltype(*ptr)>>(p);
+        return true;
+    };
+    if (!(get(&g->pf_x, n * H * 4) && get(&g->pf_x0, n * H * 4) && get(&g->pf_xn, n * H * 4) && get(&g->pf_xb, n * H * 2) &&
+          get(&g->pf_logits, n * E * 4) && get(&g->pf_rt, n * sizeof(route_out)) && get(&g->pf_count, E * 4) &&
+          get(&g->pf_pairs, E * n * 4) && get(&g->pf_off, E * 4) && get(&g->pf_tiles, tiles * 4) && get(&g->pf_ntiles, 4) &&
+          get(&g->pf_act, n * K * I * 2) && get(&g->pf_ypart, n * K * H * 4)))
+        return false;
+    g->pf_cap = n;
+    return true;
+}
+
+/* The phases of a prefill of n rows held in pf_x, in place; ev (6 events or NULL) marks their boundaries:
+   norm + router | routing + grouping + plan | gate/up GEMM | down GEMM | ordered sum. */
+static hipError_t enqueue_prefill(vitna_cuda_model* g, int layer, int n, hipEvent_t* ev) {
+    const dlayer& d = g->L[layer];
+    hipStream_t s = g->stream;
+    hipError_t e = hipSuccess;
+    auto mark = [&](int i) { if (ev && e == hipSuccess) e = hipEventRecord(ev[i], s); };
+    mark(0);
+    if (e == hipSuccess) e = launch_prefill_norm(g->pf_x, d.mlp_norm, g->pf_xn, g->pf_xb, n, g->H, g->eps, s);
+    if (e == hipSuccess) e = launch_prefill_router(g->pf_xn, d.router, g->pf_logits, n, g->E, g->H, s);
+    mark(1);
+    if (e == hipSuccess) e = launch_topk(g->pf_logits, n, g->E, g->K, g->renorm, g->pf_rt, s);
+    if (e == hipSuccess) e = launch_group(g->pf_rt, n, g->E, g->K, n, g->pf_count, g->pf_pairs, s);
+    if (e == hipSuccess) e = launch_prefill_plan(g->pf_count, g->E, g->pf_off, g->pf_tiles, g->pf_ntiles, s);
+    mark(2);
+    prefill_args a;
+    a.gate = d.gate; a.up = d.up; a.down = d.down;
+    a.xb = g->pf_xb; a.rt = g->pf_rt; a.count = g->pf_count; a.pairs = g->pf_pairs; a.off = g->pf_off;
+    a.tiles = g->pf_tiles; a.n_tiles = g->pf_ntiles; a.act = g->pf_act; a.ypart = g->pf_ypart;
+    a.E = g->E; a.K = g->K; a.cap = n; a.n = n;
+    if (e == hipSuccess) e = launch_prefill_gemm(a, true, s);
+    mark(3);
+    if (e == hipSuccess) e = launch_prefill_gemm(a, false, s);
+    mark(4);
+    if (e == hipSuccess) e = launch_reduce_rows(g->pf_ypart, g->pf_x, n, g->K, g->H, s);
+    mark(5);
+    return e;
+}
+
+static bool prefill_check(vitna_cuda_model* g, size_t layer, size_t n, char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no model");
+    if (g->lost) return fail(err, err_len, "the device was lost earlier");
+    if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    if (n < 1 || n > 65536) return fail(err, err_len, "%zu rows: a prefill takes 1 to 65536", n);
+    const dlayer& d = g->L[layer];
+    if (d.gate.dtype != VITNA_DTYPE_Q8_0 || d.up.dtype != VITNA_DTYPE_Q8_0 || d.down.dtype != VITNA_DTYPE_Q8_0)
+        return fail(err, err_len, "layer %zu: the prefill GEMM serves Q8_0 experts; these are %s/%s/%s", layer, dtype_name(d.gate.dtype),
+                    dtype_name(d.up.dtype), dtype_name(d.down.dtype));
+    if (g->H % 128 || g->I % 64) return fail(err, err_len, "the prefill GEMM needs hidden %% 128 == 0 and expert width %% 64 == 0 (%d, %d)", g->H, g->I);
+    return true;
+}
+
+extern "C" bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, int32_t* chosen, char* err,
+                                      size_t err_len) {
+    if (!prefill_check(g, layer, n, err, err_len)) return false;
+    if (!x) return fail(err, err_len, "no rows");
+    hipSetDevice(g->device);
+    if (!prefill_reserve(g, n, err, err_len)) return false;
+    HIP_TRY(hipMemcpyAsync(g->pf_x, x, n * g->H * 4, hipMemcpyHostToDevice, g->stream), "copying the rows to the device");
+    if (!check_launch(g, enqueue_prefill(g, (int)layer, (int)n, nullptr), "the prefill", err, err_len)) return false;
+    HIP_TRY(hipMemcpyAsync(x, g->pf_x, n * g->H * 4, hipMemcpyDeviceToHost, g->stream), "copying the rows back");
+    if (chosen) {
+        std::vector<route_out> rt(n);
+        HIP_TRY(hipMemcpyAsync(rt.data(), g->pf_rt, n * sizeof(route_out), hipMemcpyDeviceToHost, g->stream), "copying the routing");
+        if (!sync_stream(g, "the prefill", err, err_len)) return false;
+        for (size_t i = 0; i < n; i++)
+            for (int k = 0; k < g->K; k++) chosen[i * g->K + k] = rt[i].chosen[k];
+        return true;
+    }
+    return sync_stream(g, "the prefill", err, err_len);
+}
+
+extern "C" bool vitna_hip_time_prefill(struct vitna_cuda_model* g, size_t layer, size_t n, uint64_t seed, int reps, double* us_total,
+                                       double* us_phase, char* err, size_t err_len) {
+    if (!prefill_check(g, layer, n, err, err_len)) return false;
+    if (reps < 1) return fail(err, err_len, "reps must be positive");
+    hipSetDevice(g->device);
+    if (!prefill_reserve(g, n, err, err_len)) return false;
+    HIP_TRY(launch_fill_normal(g->pf_x0, n * g->H, seed, g->stream), "filling the rows");
+    hipEvent_t ev[6];
+    for (int i = 0; i < 6; i++) HIP_TRY(hipEventCreate(&ev[i]), "creating an event");
+    double ph[5] = {0, 0, 0, 0, 0};
+    bool ok = true;
+    for (int r = -1; r < reps && ok; r++) { /* r = -1: warm-up */
+        hipError_t e = hipMemcpyAsync(g->pf_x, g->pf_x0, n * g->H * 4, hipMemcpyDeviceToDevice, g->stream);
+        if (e == hipSuccess) e = enqueue_prefill(g, (int)layer, (int)n, ev);
+        if (e == hipSuccess) e = hipEventSynchronize(ev[5]);
+        if (e != hipSuccess) { ok = fail_hip(err, err_len, "the timed prefill", e); break; }
+        for (int i = 0; r >= 0 && i < 5; i++) {
+            float ms = 0;
+            hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+            ph[i] += ms * 1000.0 / reps;
+        }
+    }
+    for (int i = 0; i < 6; i++) hipEventDestroy(ev[i]);
+    if (!ok) return false;
+    if (us_total) *us_total = ph[0] + ph[1] + ph[2] + ph[3] + ph[4];
+    for (int i = 0; us_phase && i < 5; i++) us_phase[i] = ph[i];
+    return true;
+}
+
+/* The prefill's routing and output rows of the last timed or served prefill, to the host. */
+extern "C" bool vitna_hip_prefill_rows(struct vitna_cuda_model* g, size_t n, float* x_in, float* x_out, int32_t* chosen, char* err,
+                                       size_t err_len) {
+    if (!g || n > g->pf_cap) return fail(err, err_len, "%zu rows: the last prefill held %zu", n, g ? g->pf_cap : 0);
+    hipSetDevice(g->device);
+    if (x_in) HIP_TRY(hipMemcpyAsync(x_in, g->pf_x0, n * g->H * 4, hipMemcpyDeviceToHost, g->stream), "copying the input rows");
+    if (x_out) HIP_TRY(hipMemcpyAsync(x_out, g->pf_x, n * g->H * 4, hipMemcpyDeviceToHost, g->stream), "copying the output rows");
+    std::vector<route_out> rt(chosen ? n : 0);
+    if (chosen) HIP_TRY(hipMemcpyAsync(rt.data(), g->pf_rt, n * sizeof(route_out), hipMemcpyDeviceToHost, g->stream), "copying the routing");
+    if (!sync_stream(g, "copying the prefill", err, err_len)) return false;
+    for (size_t i = 0; chosen && i < n; i++)
+        for (int k = 0; k < g->K; k++) chosen[i * g->K + k] = rt[i].chosen[k];
+    return true;
 }
 
 extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, int steps, double* ms_per_step,

@@ -117,16 +117,6 @@ hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_
 /* RMSNorm + router, in the reference CPU's order                      */
 /* ------------------------------------------------------------------ */
 
-/* Sixteen lanes (j = 0..15) of a row hold the sixteen FMA chains of
-   engine/src/ops.c:196-209 (chain j: elements 16m + j in order of m). Fold
-   them as the AVX2 path does: v_j = a_j + a_{j+8}, s_j = v_j + v_{j+4},
-   then (s0 + s2) + (s1 + s3). Lane j = 0 of the row gets the result. */
-__device__ __forceinline__ float fold16_lanes(float a) {
-    const float v = a + __shfl_down(a, 8, 16);
-    const float s = v + __shfl_down(v, 4, 16);
-    const float u = s + __shfl_down(s, 2, 16);
-    return u + __shfl_down(u, 1, 16);
-}
 
 /* The reference's routing (engine/src/model.c:626-703) of one token by one
    wave: the K largest of E logits, largest first, the lower index first

@@ -76,6 +76,17 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
+/* The AVX2 horizontal tree over sixteen chain sums held by lanes j = 0..15 of
+   a 16-lane group (engine/src/ops.c:165-170, kernels.c:140-146):
+   v_j = a_j + a_{j+8}, then ((v0 + v4) + (v2 + v6)) + ((v1 + v5) + (v3 + v7)).
+   Valid in lane j = 0 of the group. */
+__device__ __forceinline__ float fold16_lanes(float a) {
+    const float v = a + __shfl_down(a, 8, 16);
+    const float s = v + __shfl_down(v, 4, 16);
+    const float u = s + __shfl_down(s, 2, 16);
+    return u + __shfl_down(u, 1, 16);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);

@@ -190,4 +190,25 @@ hipError_t launch_reduce_rows(const float* ypart, float* x, int n, int K, int H,
 hipError_t launch_copy_probe(const void* src, void* dst, size_t bytes, hipStream_t s);
 hipError_t launch_fill_normal(float* out, size_t n, uint64_t seed, hipStream_t s);
 
+
+/* ---- prefill through one MoE layer (kernels_prefill.hip) ---- */
+struct prefill_args {
+    qmat gate, up, down;    /* Q8_0 experts of the layer */
+    const uint16_t* xb;     /* bf16 normalized rows [n][H] */
+    const route_out* rt;    /* [n] */
+    const int* count;       /* [E] pairs of each expert */
+    const int* pairs;       /* [E][cap] row * ROUTE_K_MAX + slot, rows ascending */
+    const int* off;         /* [E] first pair of each expert in act */
+    const int* tiles;       /* (expert << 16) | tile of 128 pairs */
+    const int* n_tiles;
+    uint16_t* act;          /* bf16 [n * K][I], pairs in expert order */
+    float* ypart;           /* [n * K][H], row * K + slot */
+    int E, K, cap, n;
+};
+hipError_t launch_prefill_norm(const float* x, const float* w, float* xn, uint16_t* xb, int n, int H, float eps, hipStream_t s);
+hipError_t launch_prefill_router(const float* xn, const float* R, float* logits, int n, int E, int H, hipStream_t s);
+hipError_t launch_prefill_plan(const int* count, int E, int* off, int* tiles, int* n_tiles, hipStream_t s);
+int prefill_max_tiles(int n, int K, int E);
+hipError_t launch_prefill_gemm(const prefill_args& a, bool gate_up, hipStream_t s);
+
 #endif

@@ -240,7 +240,10 @@ def _hip():
         "vitna_hip_kv_fill": (C.c_bool, [P, C.c_uint64, C.POINTER(C.c_size_t), *E]),
         "vitna_hip_sync": (C.c_bool, [P, *E]),
         "vitna_hip_stream": (P, [P]),
-        "vitna_hip_moe_prefill": (C.c_bool, [P, C.c_size_t, _FP, C.c_size_t, *E]),
+        "vitna_hip_moe_prefill": (C.c_bool, [P, C.c_size_t, _FP, C.c_size_t, C.POINTER(C.c_int32), *E]),
+        "vitna_hip_time_prefill": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.c_uint64, C.c_int, C.POINTER(C.c_double),
+                                              C.POINTER(C.c_double), *E]),
+        "vitna_hip_prefill_rows": (C.c_bool, [P, C.c_size_t, _FP, _FP, C.POINTER(C.c_int32), *E]),
 "vitna_hip_route_check": (C.c_bool, [_FP, C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                              _FP, *E]),
         "vitna_hip_copy_probe": (C.c_bool, [C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
@@ -401,9 +404,27 @@ class Device:
         self._ok(self.lib.vitna_hip_sync(self.g, self.err, 512))
 
     def prefill(self, layer, x):
-        x = np.ascontiguousarray(x, np.float32)
-        self._ok(self.lib.vitna_hip_moe_prefill(self.g, layer, fptr(x), x.shape[0], self.err, 512))
-        return x
+        """x (n x hidden) through the MoE half of layer on the device: (x + moe(x), experts chosen n x K)."""
+        x = np.array(x, np.float32, order="C", copy=True)
+        ch = np.empty((x.shape[0], self.model.cfg.n_experts_used), np.int32)
+        self._ok(self.lib.vitna_hip_moe_prefill(self.g, layer, fptr(x), x.shape[0], _i32(ch), self.err, 512))
+        return x, ch
+
+    def time_prefill(self, layer, n, seed=1, reps=10):
+        """(total us, [norm + router, routing + grouping, gate/up, down, ordered sum] us) of a prefill of n rows."""
+        tot = C.c_double()
+        ph = (C.c_double * 5)()
+        self._ok(self.lib.vitna_hip_time_prefill(self.g, layer, n, seed, reps, C.byref(tot), ph, self.err, 512))
+        return tot.value, list(ph)
+
+    def prefill_rows(self, n):
+        """(input rows, output rows, chosen) of the first n rows of the last prefill on the device."""
+        H, K = self.model.cfg.hidden, self.model.cfg.n_experts_used
+        xi = np.empty((n, H), np.float32)
+        xo = np.empty((n, H), np.float32)
+        ch = np.empty((n, K), np.int32)
+        self._ok(self.lib.vitna_hip_prefill_rows(self.g, n, fptr(xi), fptr(xo), _i32(ch), self.err, 512))
+        return xi, xo, ch
 
     def time_kernel(self, which, reps, warmup=3):
         us = C.c_double()
