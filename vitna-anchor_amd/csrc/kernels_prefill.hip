@@ -12,10 +12,9 @@
  * sixteen-chain order (engine/src/kernels.c:115-146, ops.c:212-229), so every
  * row chooses the experts the CPU chooses, with the same weights.
  *
- * The experts: Q8_0 quants (|q| <= 127) are exact in bf16, so they enter the
- * MFMA unscaled; each 32-weight block's fp32 scale d multiplies that block's
- * fp32 partial product on the accumulators. The only rounding beyond fp32 is
- * that of the activations (normed rows, then the SwiGLU output) to bf16.
+ * The experts: each Q8_0 weight q * d (exact in fp32) is rounded to bf16 as
+ * its fragment is read from LDS; the normed rows and the SwiGLU output are
+ * rounded to bf16 too; products accumulate in fp32 on the matrix cores.
  *
  * Pipeline, one stream:
  *   prefill_norm_kernel     exact RMSNorm; fp32 rows for the router, bf16 for the GEMM
@@ -27,9 +26,9 @@
  *   prefill_gemm_kernel<0>  ypart[row * K + slot] = w * (act_e D_e^T)
  *   reduce_rows_kernel      x += the K parts of a row in slot order (kernels_rows.hip)
  *
- * GEMM tiling: a 256-thread workgroup owns 128 pairs x 128 weight rows (for
- * gate/up: 64 gate rows and the 64 up rows of the same columns, so SwiGLU is
- * local to a lane). Each wave owns 64 x 64 as 2 x 2 tiles of
+ * GEMM tiling: a 512-thread workgroup owns 256 pairs x 256 weight rows (for
+ * gate/up: 128 gate rows and the 128 up rows of the same columns, so SwiGLU is
+ * local to a lane). Each wave owns 64 x 128 as 2 x 4 tiles of
  * v_mfma_f32_32x32x16_bf16. K advances 64 a stage (two Q8_0 blocks) through
  * a three-stage LDS ring filled by global-to-LDS loads, two stages ahead. Work items (tile, column block) are split into eight
  * contiguous ranges, one per XCD (workgroup i runs on XCD i mod 8), so the
@@ -41,18 +40,14 @@
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-#define PF_BM 128 /* pairs a tile */
-#define PF_BN 128 /* weight rows a workgroup */
+#define PF_BM 256 /* pairs a tile */
+#define PF_BN 256 /* weight rows a workgroup */
+#define PF_THREADS 512
 #define PF_BK 64  /* contraction a stage: two Q8_0 blocks */
 
 __device__ __forceinline__ uint32_t bf16_rne(float f) {
     const uint32_t b = __float_as_uint(f);
     return (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
-}
-
-/* two small integers (exact in bf16: the top half of the float) packed low, high */
-__device__ __forceinline__ uint32_t pack_int_bf16(int lo, int hi) {
-    return (__float_as_uint((float)lo) >> 16) | (__float_as_uint((float)hi) & 0xffff0000u);
 }
 
 /* ---- exact RMSNorm of every row --------------------------------------- */
@@ -165,39 +160,46 @@ __global__ __launch_bounds__(256) void prefill_plan_kernel(const int* __restrict
 typedef __attribute__((address_space(3))) void* lds_void;
 typedef __attribute__((address_space(1))) void* glb_void;
 
-/* LDS ring of PF_STAGES stages; a stage holds K = 64 of the tile:
-     A  128 rows x 128 B (bf16), 16-byte chunk c of row r at position c ^ (r & 7)
-     B  128 rows x  64 B (int8 quants), chunk c of row n at position c ^ ((n >> 2) & 3)
-     D  128 rows x 2 f16 scales, each in the low half of a dword (a 2-byte
-        global-to-LDS load fills 4 bytes of LDS a lane)
-   The swizzles keep the fragment reads (eight or sixteen consecutive rows at
-   one chunk) on distinct banks. Global-to-LDS loads (global_load_lds) fill
-   them without passing through registers; each wave issues the same seven
-   loads a stage, so "stage s has landed" is vmcnt <= 7 x (stages in flight
-   after s), followed by a barrier for the other waves' parts. */
-#define PF_STAGES 3
-#define PF_A_BYTES (PF_BM * 128)
-#define PF_B_BYTES (PF_BN * 64)
-#define PF_D_BYTES (PF_BN * 8)
-#define PF_STAGE_BYTES (PF_A_BYTES + PF_B_BYTES + PF_D_BYTES)
+/* LDS of a workgroup (160 KiB, gfx950's limit):
+     A ring, 3 stages of 256 rows x 128 B (bf16, K = 64), filled by
+       global-to-LDS loads two stages ahead of use;
+     B pair, 2 stages of 256 rows x 128 B (bf16), written by the workgroup's
+       own threads: each thread loads 32 quants and their scale of the stage
+       two ahead into registers, and one stage ahead dequantizes them (q * d in
+       fp32, rounded to bf16) into the B stage. Every weight is dequantized
+       once a workgroup.
+   Rows of both hold 16-byte chunk c at position c ^ ((row >> 1) & 7): the
+   fragment reads (sixteen consecutive rows at one chunk) then cover all 64
+   banks without conflict. Each thread issues the same seven loads a stage
+   (three for B, then four for A), so the vmcnt waits count stages. */
+#define PF_A_STAGES 3
+#define PF_TILE_BYTES (PF_BM * 128)
 
-/* 8 int8 quants (two dwords) as 8 bf16 */
-__device__ __forceinline__ bf16x8 widen_q8(uint32_t w0, uint32_t w1) {
-    u32x4 o;
-    o[0] = pack_int_bf16((int)(int8_t)(w0 & 0xff), (int)(int8_t)((w0 >> 8) & 0xff));
-    o[1] = pack_int_bf16((int)(int8_t)((w0 >> 16) & 0xff), (int)(int8_t)(w0 >> 24));
-    o[2] = pack_int_bf16((int)(int8_t)(w1 & 0xff), (int)(int8_t)((w1 >> 8) & 0xff));
-    o[3] = pack_int_bf16((int)(int8_t)((w1 >> 16) & 0xff), (int)(int8_t)(w1 >> 24));
-    return __builtin_bit_cast(bf16x8, o);
+__device__ __forceinline__ int chunk_pos(int row, int c) { return c ^ ((row >> 1) & 7); }
+
+/* 16 int8 quants (four dwords) times d, rounded to bf16, as two 16-byte chunks */
+__device__ __forceinline__ void dequant16(const u32x4 q, float d, u32x4& lo, u32x4& hi) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    uint32_t o[8];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t v = q[w];
+        const bf16x2 p0 = {(__bf16)((float)(int8_t)(v & 0xff) * d), (__bf16)((float)(int8_t)((v >> 8) & 0xff) * d)};
+        const bf16x2 p1 = {(__bf16)((float)(int8_t)((v >> 16) & 0xff) * d), (__bf16)((float)(int8_t)(v >> 24) * d)};
+        o[2 * w] = __builtin_bit_cast(uint32_t, p0);
+        o[2 * w + 1] = __builtin_bit_cast(uint32_t, p1);
+    }
+    lo = u32x4{o[0], o[1], o[2], o[3]};
+    hi = u32x4{o[4], o[5], o[6], o[7]};
 }
 
 template <bool GU>
-__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(prefill_args a) {
-    __shared__ __attribute__((aligned(1024))) uint8_t ring[PF_STAGES * PF_STAGE_BYTES];
+__global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[(PF_A_STAGES + 2) * PF_TILE_BYTES];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int H = a.gate.cols, I = a.gate.rows;
-    const int NT = GU ? I / 64 : H / PF_BN; /* column blocks a tile */
-    const int KD = GU ? H : I;              /* contraction length */
+    const int NT = GU ? I / (PF_BN / 2) : H / PF_BN; /* column blocks a tile */
+    const int KD = GU ? H : I;                       /* contraction length */
     const int nwork = *a.n_tiles * NT;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = (nwork + 7) >> 3;
     const int w = xcd * per + slot;
@@ -208,110 +210,113 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(prefill_args a) {
     const int pbase = a.off[e];
     const int nb = KD / 32;
 
-    /* global sources of this lane's seven loads a stage (advanced by the stage) */
+    /* A: this lane's four 16-byte global-to-LDS loads a stage */
     const uint8_t* asrc[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int sl = (wv * 4 + i) * 64 + lane, r = sl >> 3, c = (sl & 7) ^ (r & 7);
+        const int sl = (wv * 4 + i) * 64 + lane, r = sl >> 3, c = chunk_pos(r, sl & 7);
         const int pa = min(m0 + r, cnt - 1);
         const uint16_t* row = GU ? a.xb + (size_t)(a.pairs[(size_t)e * a.cap + pa] / ROUTE_K_MAX) * H : a.act + (size_t)(pbase + pa) * I;
         asrc[i] = reinterpret_cast<const uint8_t*>(row) + 16 * c;
     }
-    const uint8_t* bsrc[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int sl = (wv * 2 + i) * 64 + lane, n = sl >> 2, c = (sl & 3) ^ ((n >> 2) & 3);
-        const qmat& wm = GU ? (n < 64 ? a.gate : a.up) : a.down;
-        const int wrow = GU ? nt * 64 + (n & 63) : nt * PF_BN + n;
-        bsrc[i] = wm.p[0] + (size_t)e * wm.estride[0] + (size_t)wrow * nb * 32 + 16 * c;
-    }
-    const uint8_t* dsrc;
-    {
-        const int sl = wv * 64 + lane, n = sl >> 1, blk = sl & 1;
-        const qmat& wm = GU ? (n < 64 ? a.gate : a.up) : a.down;
-        const int wrow = GU ? nt * 64 + (n & 63) : nt * PF_BN + n;
-        dsrc = wm.p[1] + (size_t)e * wm.estride[1] + ((size_t)wrow * nb + blk) * 2;
-    }
-    auto issue = [&](int s, int buf) {
-        uint8_t* base = ring + buf * PF_STAGE_BYTES;
+    /* B: this thread's weight row bn and block bh of the stage (32 quants, one scale) */
+    const int bn = tid >> 1, bh = tid & 1;
+    const qmat& wmat = GU ? (bn < PF_BN / 2 ? a.gate : a.up) : a.down;
+    const int wrow = GU ? nt * (PF_BN / 2) + (bn % (PF_BN / 2)) : nt * PF_BN + bn;
+    const u32x4* bsrc = reinterpret_cast<const u32x4*>(wmat.p[0] + (size_t)e * wmat.estride[0] + ((size_t)wrow * nb + bh) * 32);
+    const uint16_t* dsrc = reinterpret_cast<const uint16_t*>(wmat.p[1] + (size_t)e * wmat.estride[1]) + (size_t)wrow * nb + bh;
+
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+    const uint32_t bstage0 = lds0 + PF_A_STAGES * PF_TILE_BYTES;
+    auto issue_a = [&](int s) {
+        uint8_t* base = lds + (s % PF_A_STAGES) * PF_TILE_BYTES;
 #pragma unroll
         for (int i = 0; i < 4; i++)
             __builtin_amdgcn_global_load_lds((glb_void)(asrc[i] + (size_t)s * 128), (lds_void)(base + (wv * 4 + i) * 1024), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            __builtin_amdgcn_global_load_lds((glb_void)(bsrc[i] + (size_t)s * 64), (lds_void)(base + PF_A_BYTES + (wv * 2 + i) * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((glb_void)(dsrc + (size_t)s * 4), (lds_void)(base + PF_A_BYTES + PF_B_BYTES + wv * 256), 2, 0, 0);
+    };
+    u32x4 bq0, bq1;
+    uint32_t bd;
+    auto load_b = [&](int s) {
+        bq0 = bsrc[4 * s];
+        bq1 = bsrc[4 * s + 1];
+        bd = dsrc[2 * s];
+    };
+    /* dequantize the loaded stage into B stage buffer s & 1: row bn, chunks 4 bh .. 4 bh + 3 */
+    auto store_b = [&](int s) {
+        const float d = f16_bits_to_f32(bd);
+        u32x4 c0, c1, c2, c3;
+        dequant16(bq0, d, c0, c1);
+        dequant16(bq1, d, c2, c3);
+        const uint32_t rowb = bstage0 + (s & 1) * PF_TILE_BYTES + bn * 128;
+        asm volatile("ds_write_b128 %0, %1" ::"v"(rowb + (chunk_pos(bn, 4 * bh) << 4)), "v"(c0) : "memory");
+        asm volatile("ds_write_b128 %0, %1" ::"v"(rowb + (chunk_pos(bn, 4 * bh + 1) << 4)), "v"(c1) : "memory");
+        asm volatile("ds_write_b128 %0, %1" ::"v"(rowb + (chunk_pos(bn, 4 * bh + 2) << 4)), "v"(c2) : "memory");
+        asm volatile("ds_write_b128 %0, %1" ::"v"(rowb + (chunk_pos(bn, 4 * bh + 3) << 4)), "v"(c3) : "memory");
     };
 
-    /* this wave's 64 x 64: A rows wmi * 64 + 32 i + lane % 32, B rows brow[k]; the lane's k-octet kq */
+    /* this wave's 64 x 128: A rows wmi * 64 + 32 i + lane % 32; B rows brow[k] (for gate/up: k = 0, 1 gate
+       columns, k = 2, 3 the up rows of the same columns); the lane's k-octet kq */
     const int wmi = wv >> 1, wni = wv & 1, l32 = lane & 31, kq = lane >> 5;
-    int aoff[2], boff[2], brow[2];
+    uint32_t aoff[2], boff[4];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int r = wmi * 64 + i * 32 + l32;
-        aoff[i] = r * 128;
-        brow[i] = GU ? i * 64 + wni * 32 + l32 : wni * 64 + i * 32 + l32;
-        boff[i] = brow[i] * 64 ;
-    }
-    const int aswz[2] = {(wmi * 64 + l32) & 7, (wmi * 64 + 32 + l32) & 7};
-    const int bswz[2] = {(brow[0] >> 2) & 3, (brow[1] >> 2) & 3};
+    for (int i = 0; i < 2; i++) aoff[i] = (wmi * 64 + i * 32 + l32) * 128;
+#pragma unroll
+    for (int k = 0; k < 4; k++) boff[k] = (GU ? (k >> 1) * (PF_BN / 2) + wni * 64 + (k & 1) * 32 + l32 : wni * 128 + k * 32 + l32) * 128;
+    /* (row >> 1) & 7 of every fragment row this lane reads: the rows differ by multiples of 32 */
+    const int swz = (l32 >> 1) & 7;
+    /* 32-row subtiles past the expert's last pair do no MFMA work */
+    const bool live0 = m0 + wmi * 64 < cnt, live1 = m0 + wmi * 64 + 32 < cnt;
 
-    f32x16 acc[2][2];
+    f32x16 acc[2][4];
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int k = 0; k < 2; k++)
+        for (int k = 0; k < 4; k++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][k][r] = 0.0f;
-    const f32x16 zero = {};
 
-    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;
     const int S = KD / PF_BK;
-    issue(0, 0);
-    if (S > 1) issue(1, 1);
+    /* prologue: B of stage 0 dequantized, B of stage 1 in registers, A of stages 0 and 1 in flight */
+    load_b(0);
+    issue_a(0);
+    store_b(0);
+    if (S > 1) { load_b(1); issue_a(1); }
     for (int s = 0; s < S; s++) {
-        if (s + 1 < S) asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        /* A of stage s landed (the seven loads of stage s + 1 may be in flight); this thread's B writes done */
+        if (s + 1 < S) asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
-        if (s + 2 < S) issue(s + 2, (s + 2) % PF_STAGES);
-        /* Fragment reads are issued as ds_read instructions of our own: the compiler would otherwise wait for
-           every global-to-LDS load in flight (vmcnt(0)) before any LDS read, the stage being filled included. */
-        const uint32_t base = ring_lds + (s % PF_STAGES) * PF_STAGE_BYTES;
+        if (s + 1 < S) store_b(s + 1);
+        if (s + 2 < S) { load_b(s + 2); issue_a(s + 2); }
+        if (!live0) continue;
+        /* Fragment reads are ds_read instructions of our own: the compiler would otherwise wait for every
+           global-to-LDS load in flight (vmcnt(0)) before any LDS read. */
+        const uint32_t abase = lds0 + (s % PF_A_STAGES) * PF_TILE_BYTES, bbase = bstage0 + (s & 1) * PF_TILE_BYTES;
 #pragma unroll
         for (int b = 0; b < 2; b++) {
-            u32x4 af[2][2];
-            uint2 bq[2][2];
-            uint32_t dr[2];
+            u32x4 af[2][2], bf[4][2];
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int h = 0; h < 2; h++) {
+                const int c = 4 * b + 2 * h + kq; /* chunk of k = 32 b + 16 h + 8 kq */
+                const uint32_t cp = (uint32_t)((c ^ swz) << 4);
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const int c = 4 * b + 2 * h + kq; /* A chunk: k = 32 b + 16 h + 8 kq */
-                    asm volatile("ds_read_b128 %0, %1" : "=v"(af[i][h]) : "v"(base + aoff[i] + ((c ^ aswz[i]) << 4)));
-                    const int cb = 2 * b + h; /* B chunk: the same k, 16 quants a chunk */
-                    asm volatile("ds_read_b64 %0, %1" : "=v"(bq[i][h]) : "v"(base + PF_A_BYTES + boff[i] + ((cb ^ bswz[i]) << 4) + 8 * kq));
-                }
+                for (int i = 0; i < 2; i++) asm volatile("ds_read_b128 %0, %1" : "=v"(af[i][h]) : "v"(abase + aoff[i] + cp));
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-                asm volatile("ds_read_u16 %0, %1" : "=v"(dr[i]) : "v"(base + PF_A_BYTES + PF_B_BYTES + (brow[i] * 2 + b) * 4));
+                for (int k = 0; k < 4; k++) asm volatile("ds_read_b128 %0, %1" : "=v"(bf[k][h]) : "v"(bbase + boff[k] + cp));
+            }
             asm volatile("s_waitcnt lgkmcnt(0)"
-                         : "+v"(af[0][0]), "+v"(af[0][1]), "+v"(af[1][0]), "+v"(af[1][1]), "+v"(bq[0][0]), "+v"(bq[0][1]), "+v"(bq[1][0]),
-                           "+v"(bq[1][1]), "+v"(dr[0]), "+v"(dr[1]));
-            bf16x8 bfr[2][2];
+                         : "+v"(af[0][0]), "+v"(af[0][1]), "+v"(af[1][0]), "+v"(af[1][1]), "+v"(bf[0][0]), "+v"(bf[0][1]), "+v"(bf[1][0]),
+                           "+v"(bf[1][1]), "+v"(bf[2][0]), "+v"(bf[2][1]), "+v"(bf[3][0]), "+v"(bf[3][1]));
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int h = 0; h < 2; h++) bfr[i][h] = widen_q8(bq[i][h].x, bq[i][h].y);
-            const float dd[2] = {f16_bits_to_f32(dr[0] & 0xffff), f16_bits_to_f32(dr[1] & 0xffff)};
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int k = 0; k < 2; k++) {
-                    f32x16 t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[i][0]), bfr[k][0], zero, 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[i][1]), bfr[k][1], t, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; r++) acc[i][k][r] = fmaf(dd[k], t[r], acc[i][k][r]);
+            for (int k = 0; k < 4; k++) {
+                const bf16x8 b0 = __builtin_bit_cast(bf16x8, bf[k][0]), b1 = __builtin_bit_cast(bf16x8, bf[k][1]);
+                acc[0][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[0][0]), b0, acc[0][k], 0, 0, 0);
+                acc[0][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[0][1]), b1, acc[0][k], 0, 0, 0);
+                if (live1) {
+                    acc[1][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[1][0]), b0, acc[1][k], 0, 0, 0);
+                    acc[1][k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af[1][1]), b1, acc[1][k], 0, 0, 0);
                 }
+            }
         }
     }
 
@@ -323,15 +328,18 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(prefill_args a) {
             const int p = m0 + wmi * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (p >= cnt) continue;
             if (GU) {
-                const float gt = acc[i][0][r], up = acc[i][1][r];
-                const float v = gt / (1.0f + __expf(-gt)) * up;
-                a.act[(size_t)(pbase + p) * I + nt * 64 + wni * 32 + l32] = (uint16_t)bf16_rne(v);
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const float gt = acc[i][k][r], up = acc[i][k + 2][r];
+                    const float v = gt / (1.0f + __expf(-gt)) * up;
+                    a.act[(size_t)(pbase + p) * I + nt * (PF_BN / 2) + wni * 64 + k * 32 + l32] = (uint16_t)bf16_rne(v);
+                }
             } else {
                 const int pr = a.pairs[(size_t)e * a.cap + p], row = pr / ROUTE_K_MAX, sl = pr % ROUTE_K_MAX;
                 const float wt = a.rt[row].weights[sl];
-                float* y = a.ypart + ((size_t)row * a.K + sl) * H + nt * PF_BN + wni * 64 + l32;
-                y[0] = acc[i][0][r] * wt;
-                y[32] = acc[i][1][r] * wt;
+                float* y = a.ypart + ((size_t)row * a.K + sl) * H + nt * PF_BN + wni * 128 + l32;
+#pragma unroll
+                for (int k = 0; k < 4; k++) y[32 * k] = acc[i][k][r] * wt;
             }
         }
 }
@@ -364,12 +372,12 @@ hipError_t launch_prefill_gemm(const prefill_args& a, bool gate_up, hipStream_t 
     const qmat* parts[3] = {&a.gate, &a.up, &a.down};
     for (const qmat* q : parts)
         if (q->dtype != VITNA_DTYPE_Q8_0) return hipErrorInvalidValue;
-    if (H % PF_BN || I % PF_BK || a.up.rows != I || a.up.cols != H || a.down.rows != H || a.down.cols != I) return hipErrorInvalidValue;
+    if (H % PF_BN || I % (PF_BN / 2) || a.up.rows != I || a.up.cols != H || a.down.rows != H || a.down.cols != I) return hipErrorInvalidValue;
     if (a.K < 1 || a.K > ROUTE_K_MAX || a.cap > 65536 * PF_BM || a.E > ROUTE_E_MAX) return hipErrorInvalidValue;
-    const int NT = gate_up ? I / 64 : H / PF_BN;
+    const int NT = gate_up ? I / (PF_BN / 2) : H / PF_BN;
     const size_t blocks = ((size_t)NT * prefill_max_tiles(a.n, a.K, a.E) + 7) / 8 * 8;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    if (gate_up) prefill_gemm_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(a);
-    else prefill_gemm_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(a);
+    if (gate_up) prefill_gemm_kernel<true><<<(unsigned)blocks, PF_THREADS, 0, s>>>(a);
+    else prefill_gemm_kernel<false><<<(unsigned)blocks, PF_THREADS, 0, s>>>(a);
     return hipGetLastError();
 }
