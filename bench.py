@@ -1,6 +1,6 @@
 """Benchmark: Qwen3-30B-A3B-shaped Q4_K_M batch-1 decode on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
 
 Workload: a full 48-layer Qwen3-30B-A3B-shaped model
 with seeded random weights (Q4_K gate/up/q/k/o, Q6_K down/v/LM head, Q4_K
@@ -16,7 +16,13 @@ Prints one JSON line. Besides the step throughput it carries:
             achieved GB/s against the 8 TB/s HBM peak;
   cpu_baseline: the CPU checker's decode step (the reference's CPU arithmetic
             restated, oracle/) on this host, single-threaded, over a bounded
-            number of tokens.
+            number of tokens;
+  configs:  the other BASELINE workloads measured on the same device (unless
+            --no-extra): configs[3], 32 sequences of one new token each at
+            key-value lengths drawn from U{128..8192}, one rows step (device
+            routing, experts grouped so each chosen expert is read once a
+            layer); configs[4], a prefill of 4096 rows through one
+            Qwen3-shaped MoE layer with Q8_0 experts (bf16 MFMA grouped GEMM).
 """
 import argparse
 import json
@@ -32,6 +38,10 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "Qwen3-30B-A3B Q4_K_M decode tok/s @1 GPU; expert GEMV HBM GB/s (% of peak)"
+# HBM bytes a launch of experts_in_kernel<Q4_K> moves at this workload, from two rocprofv3 --pmc passes
+# (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, each factor calibrated on copy_probe_kernel):
+# profiles/decode_step_qwen3_hbm_traffic.md
+EXPERTS_IN_TRAFFIC = 14445631 + 49344
 KERNELS = {0: "experts_in (gate/up + SiLU)", 1: "experts_down (+ weighted sum)", 2: "route (norm + router + top-k)",
            3: "q/k/v projections", 4: "attention (+ merge)", 5: "o-projection", 6: "LM head",
            7: "route without top-k", 8: "routing rule alone (1 block)", 9: "tiny launch (floor)"}
@@ -49,6 +59,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--layers", type=int, default=48)
+    ap.add_argument("--no-extra", action="store_true", help="measure configs[2] only")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU). "
@@ -59,19 +70,28 @@ def main():
 
     pos, token = 2048, 1234
     t0 = time.time()
-    shp = va.shape(n_layers=args.layers, ctx=pos + 1, seqs=1, kv_host=1)
+    # 32 sequences of up to 8193 positions serve configs[3]; configs[2] uses sequence 0 (the host cache is
+    # allocated lazily: only what is written is committed)
+    shp = va.shape(n_layers=args.layers, ctx=8193, seqs=32, kv_host=1)
     model = va.Model(shp, 20260101, threads=16)
     cfg = model.cfg
     kd = cfg.n_kv_heads * cfg.head_dim
     L = cfg.n_layers
-    kc = np.ctypeslib.as_array(model.m.k_cache, shape=(L, model.m.ctx, kd))
+    kc = np.ctypeslib.as_array(model.m.k_cache, shape=(L, model.m.ctx, kd))  # sequence 0
     vc = np.ctypeslib.as_array(model.m.v_cache, shape=(L, model.m.ctx, kd))
     for l in range(L):
         kc[l, :pos] = va.normal(7, 2 * l, pos * kd).reshape(pos, kd)
         vc[l, :pos] = va.normal(7, 2 * l + 1, pos * kd).reshape(pos, kd)
     log("synthetic model generated in %.1f s" % (time.time() - t0))
     t0 = time.time()
-    dev = va.Device(model)
+    # configs[2]'s device model holds one sequence of pos + 1 positions (the attention grid is sized by the
+    # cache); the host model keeps its layout for the CPU baseline
+    saved = (model.m.ctx, model.m.seqs)
+    model.m.ctx, model.m.seqs = pos + 1, 1
+    try:
+        dev = va.Device(model)
+    finally:
+        model.m.ctx, model.m.seqs = saved
     for l in range(L):
         dev.kv(0, l, 0, pos, kc[l, :pos], vc[l, :pos])
     log("uploaded to %s in %.1f s" % (dev.device_name(), time.time() - t0))
@@ -121,6 +141,16 @@ def main():
                          "the reference's CPU arithmetic (AVX2 order) restated in oracle/vitna_oracle.c" % n}
         log("cpu baseline: %d steps in %.1f s -> %.3f tok/s" % (n, t_cpu, n / t_cpu))
 
+    dev.close()
+    extra = None
+    if not args.no_extra:
+        t0 = time.time()
+        dev = va.Device(model)
+        log("uploaded for 32 sequences of 8193 positions in %.1f s" % (time.time() - t0))
+        extra = {"3": bench_ragged(va, model, dev, args.steps)}
+        dev.close()
+        extra["4"] = bench_prefill(va)
+
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
@@ -129,17 +159,66 @@ def main():
                                "48 layers, KV 2048 positions fp32, LM head Q6_K 151936x2048",
                    "layers": L, "position": pos, "global_batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": EXPERTS_IN_TRAFFIC,
                      "kernel": "experts_in_kernel<Q4_K> (8 experts x (gate + up) 768 x 2048)",
                      "bytes_per_launch": b0, "avg_us": round(us0, 3)},
         "kernels_us": {KERNELS[w]: round(per_kernel[w][0], 3) for w in per_kernel},
         "step_algorithmic_GBps": round(step_bytes / ms / 1e6, 1),
         "copy_probe_GBps": round(copy_gbs, 1),
         "cpu_baseline": cpu,
+        "configs": extra,
     }
     print(json.dumps(out), flush=True)
-    dev.close()
     model.free()
+
+
+def bench_ragged(va, model, dev, steps):
+    """32 sequences, one new token each, key-value lengths U{128..8192} (seeded), values N(0,1)."""
+    cfg = model.cfg
+    rng = np.random.RandomState(20260103)
+    lengths = rng.randint(128, 8193, size=32)
+    t0 = time.time()
+    dev.kv_fill(3, [int(n) for n in lengths])
+    rows = [(int(rng.randint(0, cfg.vocab)), int(lengths[s]), s) for s in range(32)]
+    ms = dev.time_rows(rows, max(steps // 5, 5))
+    L, kd = cfg.n_layers, cfg.n_kv_heads * cfg.head_dim
+    kv_bytes = float(np.sum(lengths + 1)) * kd * 4 * 2 * L
+    # expected distinct experts a layer when 32 tokens each choose 8 of 128 (uniform routing)
+    E, K = cfg.n_experts, cfg.n_experts_used
+    uniq = E * (1.0 - (1.0 - K / E) ** 32)
+    expert_bytes = L * uniq * (2 * 884736 + 1290240)
+    log("configs[3]: %d rows, %.3f ms a step, %.1f tok/s (cache filled in %.1f s)" % (len(rows), ms, 32e3 / ms, time.time() - t0))
+    return {"workload": "BASELINE configs[3]: 32 sequences, one new token each, key-value lengths U{128..8192}, "
+                        "Qwen3-30B-A3B-shaped Q4_K_M, 48 layers",
+            "value": round(32e3 / ms, 1), "unit": "tok/s", "ms_per_step": round(ms, 4),
+            "kv_positions": int(np.sum(lengths)),
+            "est_GBps": round((kv_bytes + expert_bytes + 5.2258e8 + 5.0332e7 + 2.5525e8) / ms / 1e6, 1),
+            "est_note": "key-value bytes exact; expert bytes for the expected %.1f distinct experts a layer" % uniq}
+
+
+def bench_prefill(va):
+    """4096 rows N(0,1) through one Qwen3-shaped MoE layer, Q8_0 experts, top-8 of 128."""
+    model = va.Model(va.shape(**va.CONFIGS[4]), 20260104, threads=16)
+    dev = va.Device(model)
+    try:
+        n = 4096
+        tot, ph = dev.time_prefill(0, n, seed=11, reps=10)
+        cfg = model.cfg
+        flops = 2.0 * n * cfg.n_experts_used * 3 * cfg.intermediate * cfg.hidden
+        gemm_us = ph[2] + ph[3]
+        log("configs[4]: prefill of %d rows %.1f us (norm+router %.1f, routing %.1f, gate/up %.1f, down %.1f, sum %.1f)"
+            % (n, tot, *ph))
+        return {"workload": "BASELINE configs[4]: prefill of 4096 rows through one Qwen3-shaped MoE layer, Q8_0 experts, "
+                            "bf16 MFMA grouped GEMM", "value": round(n / tot * 1e6, 1), "unit": "tok/s",
+                "us": round(tot, 1), "phases_us": {k: round(v, 1) for k, v in zip(
+                    ["norm+router", "routing+grouping", "gate/up GEMM", "down GEMM", "ordered sum"], ph)},
+                "roofline": {"bound": "mfma", "achieved": round(flops / gemm_us / 1e6, 1), "peak": 2500.0,
+                             "unit": "TFLOP/s", "frac": round(flops / gemm_us / 1e6 / 2500.0, 4),
+                             "note": "both GEMMs: 2 n K (3 I H) flops over their summed duration"},
+                "tflops_whole": round(flops / tot / 1e6, 1)}
+    finally:
+        dev.close()
+        model.free()
 
 
 if __name__ == "__main__":

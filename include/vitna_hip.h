@@ -187,6 +187,12 @@ bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, s
 bool vitna_hip_time_prefill(struct vitna_cuda_model* g, size_t layer, size_t n, uint64_t seed, int reps, double* us_total,
                             double* us_phase, char* err, size_t err_len);
 
+/** The rows step (vitna_hip_moe_rows_step, logits left on the device) for
+    the same rows replayed steps times after one warm-up, timed with HIP
+    events on the model's stream: milliseconds a step. */
+bool vitna_hip_time_rows(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, int steps, double* ms_per_step, char* err,
+                         size_t err_len);
+
 /** The input rows, output rows and experts chosen (any may be NULL) of the
     first n rows of the last prefill on the device. */
 bool vitna_hip_prefill_rows(struct vitna_cuda_model* g, size_t n, float* x_in, float* x_out, int32_t* chosen, char* err,

@@ -1387,3 +1387,27 @@ extern "C" bool vitna_hip_moe_rows_step(struct vitna_cuda_model* g, const vitna_
     if (logits) HIP_TRY(hipStreamSynchronize(g->stream), "running the rows step");
     return true;
 }
+
+extern "C" bool vitna_hip_time_rows(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, int steps, double* ms_per_step,
+                                    char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!g->attention) return fail(err, err_len, "this model has no attention");
+    if (steps < 1) return fail(err, err_len, "at least one step");
+    if (!set_rows(g, rows, n, err, err_len)) return false;
+    if (!ensure_rows_graph(g, (int)n, err, err_len)) return false;
+    hipEvent_t t0, t1;
+    HIP_TRY(hipEventCreate(&t0), "events");
+    HIP_TRY(hipEventCreate(&t1), "events");
+    HIP_TRY(hipGraphLaunch(g->rows_graph, g->stream), "launching the rows step"); /* warm-up */
+    HIP_TRY(hipStreamSynchronize(g->stream), "before timing");
+    HIP_TRY(hipEventRecord(t0, g->stream), "events");
+    for (int i = 0; i < steps; i++) HIP_TRY(hipGraphLaunch(g->rows_graph, g->stream), "launching the rows step");
+    HIP_TRY(hipEventRecord(t1, g->stream), "events");
+    HIP_TRY(hipEventSynchronize(t1), "timing the rows steps");
+    float ms = 0;
+    HIP_TRY(hipEventElapsedTime(&ms, t0, t1), "events");
+    hipEventDestroy(t0);
+    hipEventDestroy(t1);
+    *ms_per_step = (double)ms / steps;
+    return true;
+}

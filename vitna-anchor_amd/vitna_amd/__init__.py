@@ -243,6 +243,7 @@ def _hip():
         "vitna_hip_moe_prefill": (C.c_bool, [P, C.c_size_t, _FP, C.c_size_t, C.POINTER(C.c_int32), *E]),
         "vitna_hip_time_prefill": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.c_uint64, C.c_int, C.POINTER(C.c_double),
                                               C.POINTER(C.c_double), *E]),
+        "vitna_hip_time_rows": (C.c_bool, [P, C.POINTER(RowT), C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_prefill_rows": (C.c_bool, [P, C.c_size_t, _FP, _FP, C.POINTER(C.c_int32), *E]),
 "vitna_hip_route_check": (C.c_bool, [_FP, C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                              _FP, *E]),
@@ -435,6 +436,12 @@ class Device:
     def time_steps(self, seq, token, pos, steps):
         ms = C.c_double()
         self._ok(self.lib.vitna_hip_time_steps(self.g, seq, token, pos, steps, C.byref(ms), self.err, 512))
+        return ms.value
+
+    def time_rows(self, rows, steps):
+        """Milliseconds a rows step (device routing and grouping, logits left in HBM) of these rows."""
+        ms = C.c_double()
+        self._ok(self.lib.vitna_hip_time_rows(self.g, self._rows(rows), len(rows), steps, C.byref(ms), self.err, 512))
         return ms.value
 
     def device_name(self):
