@@ -422,7 +422,7 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
              dalloc(g, &g->k, R * kd * 4, "scratch", err, err_len) && dalloc(g, &g->v, R * kd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->att, R * qd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->vocab, R * c->vocab * 4, "the logits", err, err_len) &&
-             dalloc(g, &g->partial, (size_t)R * c->n_kv_heads * g->splits_max * G * (c->head_dim + 2) * 4, "attention partials", err, err_len) &&
+             dalloc(g, &g->partial, (size_t)R * c->n_kv_heads * g->splits_max * G * (c->head_dim + 4) * 4, "attention partials", err, err_len) &&
              dalloc(g, &g->k_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the key cache", err, err_len) &&
              dalloc(g, &g->v_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the value cache", err, err_len);
     }

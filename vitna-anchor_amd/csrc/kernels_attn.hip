@@ -62,10 +62,71 @@ __device__ void norm_rope(float* vecs, int nv, const float* wq, const float* wk,
     __syncthreads();
 }
 
+/* Sum over the lanes of one head's float4 group (HD / 4 consecutive lanes: a
+   32-lane half for HD 128, a 16-lane row for HD 64), in every lane of it. */
+template <int HD>
+__device__ __forceinline__ float head_sum(float v) {
+    if constexpr (HD == 128) {
+        return half_sum_dpp(v);
+    } else {
+        v = row_scan_sum(v);
+        const int r = (threadIdx.x >> 4) & 3;
+        const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
+        const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+        const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 47));
+        const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+        return r == 0 ? r0 : r == 1 ? r1 : r == 2 ? r2 : r3;
+    }
+}
+
+/* The float4 of the RoPE partner (dimensions +- HD / 2) of this lane's float4. */
+template <int HD>
+__device__ __forceinline__ float4 rope_partner(float4 v) {
+    float4 o;
+    if constexpr (HD == 128) {
+        o.x = swap16(v.x); o.y = swap16(v.y); o.z = swap16(v.z); o.w = swap16(v.w);
+    } else { /* row_ror:8 within a 16-lane row swaps its halves */
+        o.x = dpp_f<0x128, 0xf, 0xf>(v.x, 0.0f); o.y = dpp_f<0x128, 0xf, 0xf>(v.y, 0.0f);
+        o.z = dpp_f<0x128, 0xf, 0xf>(v.z, 0.0f); o.w = dpp_f<0x128, 0xf, 0xf>(v.w, 0.0f);
+    }
+    return o;
+}
+
+/* The reference's per-head RMSNorm (engine/src/model.c:916-921) and
+   vitna_rope_half (engine/src/ops.c:273-281) of one head's vector, held as
+   float4 j of the head by HD / 4 consecutive lanes; every lane of the wave
+   takes part (lanes outside a head pass zeros). */
+template <int HD>
+__device__ __forceinline__ float4 head_norm_rope(float4 v, int j, const float* w, float eps, const float* c, const float* s) {
+    constexpr int QF4 = HD / 4, HALF = HD / 2;
+    float ss = 0.0f;
+    ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+    ss = head_sum<HD>(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)HD + eps);
+    const float4 wv = reinterpret_cast<const float4*>(w)[j];
+    v.x = (v.x * inv) * wv.x; v.y = (v.y * inv) * wv.y; v.z = (v.z * inv) * wv.z; v.w = (v.w * inv) * wv.w;
+    const float4 pv = rope_partner<HD>(v);
+    const bool first = j < QF4 / 2;
+    const int d0 = 4 * (first ? j : j - QF4 / 2);
+    const float4 cv = reinterpret_cast<const float4*>(c + d0)[0], sv = reinterpret_cast<const float4*>(s + d0)[0];
+    (void)HALF;
+    float4 o;
+    if (first) { /* a = own, b = partner: a c - b s */
+        o.x = v.x * cv.x - pv.x * sv.x; o.y = v.y * cv.y - pv.y * sv.y;
+        o.z = v.z * cv.z - pv.z * sv.z; o.w = v.w * cv.w - pv.w * sv.w;
+    } else { /* b = own, a = partner: b c + a s */
+        o.x = v.x * cv.x + pv.x * sv.x; o.y = v.y * cv.y + pv.y * sv.y;
+        o.z = v.z * cv.z + pv.z * sv.z; o.w = v.w * cv.w + pv.w * sv.w;
+    }
+    return o;
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
-    constexpr int DPL = HD / 4;        /* dimensions a lane in the scores */
-    constexpr int VPL = HD / 64;       /* dimensions a lane in the values */
+    constexpr int DPL = HD / 4;  /* dimensions a lane in the scores */
+    constexpr int VPL = HD / 64; /* dimensions a lane in the values */
+    constexpr int QF4 = HD / 4;  /* float4 of a head */
+    constexpr int PS = HD + 4;   /* floats of a (chunk, query head) partial */
     const int split = blockIdx.x, h = blockIdx.y, row = blockIdx.z;
     const row_rec rr = a.rows[row];
     const int pos = rr.pos, seq = rr.seq;
@@ -74,21 +135,21 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     const int G = a.n_heads / a.n_kv, kv_dim = a.n_kv * HD, half = HD / 2;
     float* kc = a.k_cache + (size_t)seq * a.seq_stride;
     float* vc = a.v_cache + (size_t)seq * a.seq_stride;
-    __shared__ float sq[(GMAX + 1) * HD]; /* G query heads, then the new key */
-    __shared__ float nv[HD];
-    __shared__ float inv_s[GMAX + 1];
-    __shared__ float sp[4][16][GMAX];
+    __shared__ __attribute__((aligned(16))) float sq[GMAX * HD]; /* the G query heads, normalized */
+    __shared__ __attribute__((aligned(16))) float nk[HD];        /* this row's own key, normalized */
+    __shared__ __attribute__((aligned(16))) float nvs[HD];       /* and value */
+    __shared__ __attribute__((aligned(16))) float sp[4][16][GMAX];
     __shared__ float wm[4][GMAX], wl[4][GMAX];
-    __shared__ float wacc[4][GMAX][HD];
+    __shared__ __attribute__((aligned(16))) float wacc[4][GMAX][HD];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    float* nk = sq + G * HD;
+    const bool fresh_block = !a.prepared && split == n_act - 1; /* holds the row's own position */
 
     /* the chunk's keys and values, requested before anything waits on them: four lanes a position (hd / 4 keys
        a lane) and a lane a dimension across the wave's sixteen positions */
     const int p = lane >> 2, qd = lane & 3;
     const int t = split * ATTN_CHUNK + wave * 16 + p;
     const bool valid = t <= pos;
-    const bool fresh = !a.prepared && t == pos; /* this row's own key: in LDS once normalized, not in the cache yet */
+    const bool fresh = fresh_block && t == pos; /* this row's own key: in LDS once normalized, not in the cache yet */
     float kr[DPL];
     if (valid && !fresh) {
         const float4* src = reinterpret_cast<const float4*>(kc + (size_t)t * kv_dim + (size_t)h * HD + qd * DPL);
@@ -106,39 +167,49 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
 #pragma unroll
     for (int pp = 0; pp < 16; pp++) {
         const int tt = t0 + pp;
-        const bool ok = tt <= pos && !(!a.prepared && tt == pos);
+        const bool ok = tt <= pos && !(fresh_block && tt == pos);
         const float* vrow = vc + (size_t)(ok ? tt : 0) * kv_dim + (size_t)h * HD;
 #pragma unroll
         for (int i = 0; i < VPL; i++) vv[pp][i] = ok ? vrow[lane + 64 * i] : 0.0f;
     }
 
+    /* the G query heads: thread tid holds float4 j of head g */
     {
-        /* the G query heads: G * HD / 4 <= 256 float4, one a thread */
-        const float4* q4 = reinterpret_cast<const float4*>(a.q_raw + (size_t)row * a.n_heads * HD + (size_t)h * G * HD);
-        if (tid < G * HD / 4) reinterpret_cast<float4*>(sq)[tid] = q4[tid];
+        const int g = tid / QF4, j = tid % QF4;
+        const bool qt = g < G;
+        float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (qt) qv = reinterpret_cast<const float4*>(a.q_raw + (size_t)row * a.n_heads * HD + (size_t)(h * G + g) * HD)[j];
+        if (!a.prepared) {
+            const float* cs = a.cos_tab + (size_t)pos * half;
+            const float* sn = a.sin_tab + (size_t)pos * half;
+            if (g < GMAX) qv = head_norm_rope<HD>(qv, j, a.q_norm, a.eps, cs, sn);
+            /* this row's own key and value, in the block that holds its position */
+            if (fresh_block && wave == 0) {
+                float4 kv4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (lane < QF4) kv4 = reinterpret_cast<const float4*>(a.k_raw + (size_t)row * kv_dim + (size_t)h * HD)[lane];
+                kv4 = head_norm_rope<HD>(kv4, lane % QF4, a.k_norm, a.eps, cs, sn);
+                if (lane < QF4) {
+                    const float4 vn = reinterpret_cast<const float4*>(a.v_raw + (size_t)row * kv_dim + (size_t)h * HD)[lane];
+                    reinterpret_cast<float4*>(nk)[lane] = kv4;
+                    reinterpret_cast<float4*>(nvs)[lane] = vn;
+                    reinterpret_cast<float4*>(kc + (size_t)pos * kv_dim + (size_t)h * HD)[lane] = kv4;
+                    reinterpret_cast<float4*>(vc + (size_t)pos * kv_dim + (size_t)h * HD)[lane] = vn;
+                }
+            }
+        }
+        if (qt) reinterpret_cast<float4*>(sq)[tid] = qv;
     }
-    if (a.prepared) {
-        __syncthreads();
-    } else {
-        if (tid < HD) {
-            nk[tid] = a.k_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
-            nv[tid] = a.v_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
-        }
-        __syncthreads();
-        norm_rope<HD>(sq, G + 1, a.q_norm, a.k_norm, G, a.eps, a.cos_tab + (size_t)pos * half, a.sin_tab + (size_t)pos * half, inv_s);
-        if (split == n_act - 1 && tid < HD) {
-            kc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = nk[tid];
-            vc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = nv[tid];
-        }
-        if (fresh) {
+    __syncthreads();
+    if (fresh) {
 #pragma unroll
-            for (int i = 0; i < DPL; i++) kr[i] = nk[qd * DPL + i];
-        }
+        for (int i = 0; i < DPL; i++) kr[i] = nk[qd * DPL + i];
+    }
+    if (fresh_block) {
 #pragma unroll
         for (int pp = 0; pp < 16; pp++)
             if (t0 + pp == pos) {
 #pragma unroll
-                for (int i = 0; i < VPL; i++) vv[pp][i] = nv[lane + 64 * i];
+                for (int i = 0; i < VPL; i++) vv[pp][i] = nvs[lane + 64 * i];
             }
     }
 
@@ -148,22 +219,21 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
 #pragma unroll
     for (int g = 0; g < GMAX; g++) {
         if (g >= G) break;
-        const float* qg = sq + g * HD + qd * DPL;
+        const float4* qg = reinterpret_cast<const float4*>(sq + g * HD + qd * DPL);
         float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < DPL; i++) s = fmaf(qg[i], kr[i], s);
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s *= scale;
-        float m = valid ? s : -INFINITY;
-#pragma unroll
-        for (int o = 4; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        for (int i = 0; i < DPL / 4; i++) {
+            const float4 q4 = qg[i];
+            s = fmaf(q4.x, kr[4 * i], s);
+            s = fmaf(q4.y, kr[4 * i + 1], s);
+            s = fmaf(q4.z, kr[4 * i + 2], s);
+            s = fmaf(q4.w, kr[4 * i + 3], s);
+        }
+        s = quad_sum(s) * scale;
+        const float m = wave_max_dpp(valid ? s : -INFINITY);
         const float e = valid ? expf(s - m) : 0.0f;
-        float l = e;
-#pragma unroll
-        for (int o = 4; o < 64; o <<= 1) l += __shfl_xor(l, o, 64);
         mw[g] = m;
-        lw[g] = l;
+        lw[g] = wave_sum_dpp(qd == 0 ? e : 0.0f);
         pe[g] = e;
     }
     if (qd == 0) {
@@ -171,7 +241,9 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
         for (int g = 0; g < GMAX; g++)
             if (g < G) sp[wave][p][g] = pe[g];
     }
-    __syncthreads();
+    /* sp[wave] is this wave's own: LDS operations of one wave complete in order */
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 
     /* values: a lane per dimension */
     float acc[GMAX][VPL];
@@ -181,16 +253,20 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
         for (int i = 0; i < VPL; i++) acc[g][i] = 0.f;
 #pragma unroll
     for (int pp = 0; pp < 16; pp++) {
+        const float4 w0 = *reinterpret_cast<const float4*>(&sp[wave][pp][0]);
+        const float4 w1 = *reinterpret_cast<const float4*>(&sp[wave][pp][4]);
+        const float w[GMAX] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
         for (int g = 0; g < GMAX; g++) {
             if (g >= G) break;
-            const float w = sp[wave][pp][g];
 #pragma unroll
-            for (int i = 0; i < VPL; i++) acc[g][i] = fmaf(w, vv[pp][i], acc[g][i]);
+            for (int i = 0; i < VPL; i++) acc[g][i] = fmaf(w[g], vv[pp][i], acc[g][i]);
         }
     }
     if (lane == 0) {
-        for (int g = 0; g < G; g++) { wm[wave][g] = mw[g]; wl[wave][g] = lw[g]; }
+#pragma unroll
+        for (int g = 0; g < GMAX; g++)
+            if (g < G) { wm[wave][g] = mw[g]; wl[wave][g] = lw[g]; }
     }
 #pragma unroll
     for (int g = 0; g < GMAX; g++) {
@@ -200,22 +276,28 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     }
     __syncthreads();
 
-    /* this chunk's partial: the four waves merged */
-    float* part = a.partial + (((size_t)row * a.n_kv + h) * a.splits_max + split) * G * (HD + 2);
-    for (int i = tid; i < G * HD; i += 256) {
-        const int g = i / HD, d = i % HD;
-        float M = -INFINITY;
-        for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
-        float L = 0.f, o = 0.f;
-        for (int w = 0; w < 4; w++) {
-            const float f = wm[w][g] == -INFINITY ? 0.0f : expf(wm[w][g] - M);
-            L = fmaf(wl[w][g], f, L);
-            o = fmaf(wacc[w][g][d], f, o);
-        }
-        part[g * (HD + 2) + d] = o;
-        if (d == 0) {
-            part[g * (HD + 2) + HD] = M;
-            part[g * (HD + 2) + HD + 1] = L;
+    /* this chunk's partial: the four waves merged, a float4 of one head a thread */
+    {
+        const int g = tid / QF4, j = tid % QF4;
+        if (g < G) {
+            float* part = a.partial + (((size_t)row * a.n_kv + h) * a.splits_max + split) * G * PS + (size_t)g * PS;
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
+            float L = 0.f;
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float f = wm[w][g] == -INFINITY ? 0.0f : expf(wm[w][g] - M);
+                const float4 x = reinterpret_cast<const float4*>(&wacc[w][g][0])[j];
+                L = fmaf(wl[w][g], f, L);
+                o.x = fmaf(x.x, f, o.x); o.y = fmaf(x.y, f, o.y); o.z = fmaf(x.z, f, o.z); o.w = fmaf(x.w, f, o.w);
+            }
+            reinterpret_cast<float4*>(part)[j] = o;
+            if (j == 0) {
+                part[HD] = M;
+                part[HD + 1] = L;
+            }
         }
     }
 }
@@ -265,8 +347,8 @@ __global__ void attention_merge_kernel(attn_args a) {
     const int hq = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
     const int G = a.n_heads / a.n_kv, h = hq / G, g = hq % G, HD = a.hd;
     const int n_act = a.rows[row].pos / ATTN_CHUNK + 1;
-    const float* base = a.partial + (((size_t)row * a.n_kv + h) * a.splits_max * G + g) * (HD + 2);
-    const size_t stride = (size_t)G * (HD + 2);
+    const float* base = a.partial + (((size_t)row * a.n_kv + h) * a.splits_max * G + g) * (HD + 4);
+    const size_t stride = (size_t)G * (HD + 4);
     __shared__ float fm[MERGE_MAX], fl[MERGE_MAX];
     __shared__ float red[4];
     float m = -INFINITY;

@@ -124,12 +124,9 @@ hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_
    expert; renormalized over the chosen, summed largest first, when renorm.
    Lanes write *o. slg: ROUTE_E_MAX floats of LDS.
 
-   Without NaNs the K passes of argmax equal a selection by value: every
-   logit becomes an order-preserving 32-bit key (-0 keyed as +0, since the
-   passes compare with >), the K-th largest key is found a bit at a time from
-   the top (ballots and popcounts), the keys above it are chosen and then the
-   lowest indices among those equal to it, and the chosen are ranked among
-   themselves. With a NaN among the logits the passes are run as the
+   Without NaNs each pass of argmax is a wave-wide maximum of order-preserving
+   32-bit keys (-0 keyed as +0, since the passes compare with >) followed by
+   the lowest index holding it. With a NaN among the logits the passes are run as the
    reference runs them (a NaN where a pass starts is kept, since x > NaN is
    false; a later one never wins). */
 #define RPL (ROUTE_E_MAX / 64) /* logits a lane */
@@ -140,13 +137,20 @@ __device__ __forceinline__ uint32_t order_key(float v) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ int popc64(uint64_t b) { return __popcll(b); }
+/* The largest of the wave's values, in every lane: row shifts then row broadcasts (DPP), read from lane 63. */
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false)); /* row_shr:1 */
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false)); /* row_shr:2 */
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false)); /* row_shr:4 */
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false)); /* row_shr:8 */
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xa, 0xf, false)); /* row_bcast:15 */
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xc, 0xf, false)); /* row_bcast:31 */
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
 
 __device__ __forceinline__ void wave_route(const float* __restrict__ lg_in, int E, int K, int renorm, route_out* o, float* slg) {
     const int lane = threadIdx.x & 63;
     __shared__ int chosen_s[ROUTE_K_MAX];
-    __shared__ int cand_e[ROUTE_K_MAX];
-    __shared__ uint32_t cand_k[ROUTE_K_MAX];
     __shared__ float share_s[ROUTE_K_MAX];
     float lg[RPL];
     bool nan = false;
@@ -189,59 +193,29 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ lg_in, int 
             if (lane == 0) chosen_s[k] = pick;
         }
     } else {
+        /* K rounds: the largest remaining key over the wave, then the lowest index holding it, which is
+           the pass's argmax (strict >: the first of equals wins). Keys of absent or taken experts are 0,
+           below every logit's key (order_key(-inf) > 0). */
         uint32_t key[RPL];
 #pragma unroll
         for (int i = 0; i < RPL; i++) key[i] = lane + 64 * i < E ? order_key(lg[i]) : 0u;
-        /* the K-th largest key: the largest t with #{key >= t} >= K (keys of absent experts are 0, below every logit's) */
-        uint32_t thr = 0;
-        for (int bit = 31; bit >= 0; bit--) {
-            const uint32_t cand = thr | (1u << bit);
-            int cnt = 0;
+        for (int k = 0; k < K; k++) {
+            uint32_t m = 0;
 #pragma unroll
             for (int i = 0; i < RPL; i++)
-                if (64 * i < E) cnt += popc64(__ballot(key[i] >= cand));
-            if (cnt >= K) thr = cand;
-        }
-        /* chosen: every key above thr, then the lowest indices with key == thr */
-        int above = 0;
+                if (64 * i < E) m = max(m, key[i]);
+            m = wave_max_u32(m);
+            int pick = -1;
 #pragma unroll
-        for (int i = 0; i < RPL; i++)
-            if (64 * i < E) above += popc64(__ballot(key[i] > thr && lane + 64 * i < E));
-        int slot_gt = 0, slot_eq = above;
+            for (int i = 0; i < RPL; i++) {
+                if (64 * i >= E) continue;
+                const uint64_t b = __ballot(key[i] == m);
+                if (pick < 0 && b) pick = 64 * i + (int)__builtin_ctzll(b);
+            }
 #pragma unroll
-        for (int i = 0; i < RPL; i++) {
-            if (64 * i >= E) continue;
-            const int e = lane + 64 * i;
-            const bool gt = key[i] > thr && e < E, eq = key[i] == thr && e < E;
-            const uint64_t bgt = __ballot(gt), beq = __ballot(eq);
-            const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-            if (gt) {
-                const int at = slot_gt + popc64(bgt & below);
-                cand_e[at] = e;
-                cand_k[at] = key[i];
-            }
-            if (eq) {
-                const int at = slot_eq + popc64(beq & below);
-                if (at < K) {
-                    cand_e[at] = e;
-                    cand_k[at] = key[i];
-                }
-            }
-            slot_gt += popc64(bgt);
-            slot_eq += popc64(beq);
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-        /* rank the K candidates: a larger key, or an equal one at a lower index, comes first */
-        if (lane < K) {
-            const int e = cand_e[lane];
-            const uint32_t kk = cand_k[lane];
-            int rank = 0;
-            for (int j = 0; j < K; j++) {
-                const uint32_t kj = cand_k[j];
-                rank += (kj > kk) | ((kj == kk) & (cand_e[j] < e));
-            }
-            chosen_s[rank] = e;
+            for (int i = 0; i < RPL; i++)
+                if (pick == lane + 64 * i) key[i] = 0u;
+            if (lane == 0) chosen_s[k] = pick;
         }
     }
     /* softmax over every expert: the max as the CPU scans it (a NaN first stays), the sum of exp(l - max) */

@@ -106,6 +106,67 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+/* ---- cross-lane reductions on the DPP paths (no LDS traffic) ----
+   A lane whose DPP source falls outside its row, or whose row or bank is
+   masked off, reads `old`: the identity of the reduction. */
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v, float old) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+}
+#define DPP_ROW_SHR(n) (0x110 + (n))
+#define DPP_ROW_BCAST15 0x142
+#define DPP_ROW_BCAST31 0x143
+#define DPP_QUAD_XOR1 0xB1 /* quad_perm [1,0,3,2] */
+#define DPP_QUAD_XOR2 0x4E /* quad_perm [2,3,0,1] */
+
+/* Sum over each group of four lanes, in every lane of the group. */
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_f<DPP_QUAD_XOR1, 0xf, 0xf>(v, 0.0f);
+    return v + dpp_f<DPP_QUAD_XOR2, 0xf, 0xf>(v, 0.0f);
+}
+
+/* Doubling scans within each 16-lane row: lane 15 of a row ends with the row's total. */
+__device__ __forceinline__ float row_scan_sum(float v) {
+    v += dpp_f<DPP_ROW_SHR(1), 0xf, 0xf>(v, 0.0f);
+    v += dpp_f<DPP_ROW_SHR(2), 0xf, 0xf>(v, 0.0f);
+    v += dpp_f<DPP_ROW_SHR(4), 0xf, 0xf>(v, 0.0f);
+    return v + dpp_f<DPP_ROW_SHR(8), 0xf, 0xf>(v, 0.0f);
+}
+__device__ __forceinline__ float row_scan_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_ROW_SHR(1), 0xf, 0xf>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<DPP_ROW_SHR(2), 0xf, 0xf>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<DPP_ROW_SHR(4), 0xf, 0xf>(v, -INFINITY));
+    return fmaxf(v, dpp_f<DPP_ROW_SHR(8), 0xf, 0xf>(v, -INFINITY));
+}
+
+/* Sum of the wave, in every lane (the total gathers in lane 63, then a readlane). */
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v = row_scan_sum(v);
+    v += dpp_f<DPP_ROW_BCAST15, 0xa, 0xf>(v, 0.0f);
+    v += dpp_f<DPP_ROW_BCAST31, 0xc, 0xf>(v, 0.0f);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = row_scan_max(v);
+    v = fmaxf(v, dpp_f<DPP_ROW_BCAST15, 0xa, 0xf>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<DPP_ROW_BCAST31, 0xc, 0xf>(v, -INFINITY));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+/* Sum over each 32-lane half of the wave, in every lane of the half. */
+__device__ __forceinline__ float half_sum_dpp(float v) {
+    v = row_scan_sum(v);
+    v += dpp_f<DPP_ROW_BCAST15, 0xa, 0xf>(v, 0.0f);
+    const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return (threadIdx.x & 32) ? hi : lo;
+}
+
+/* The value of lane (this lane xor 16), within each 32-lane half (ds_swizzle, bit mode). */
+__device__ __forceinline__ float swap16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+
 /* Columns of slice t of a row: two runs of 16, starting at *lo and *hi. */
 __device__ __forceinline__ void slice_cols(int dtype, int t, int* lo, int* hi) {
     if (dtype == VITNA_DTYPE_Q8_0) {

@@ -134,7 +134,7 @@ struct attn_args {
     size_t seq_stride;     /* floats from one sequence's cache of this layer to the next's */
     const row_rec* rows;   /* device, n_rows */
     int n_rows;
-    float* partial;        /* [n_rows][n_kv][splits_max][G][hd + 2] */
+    float* partial;        /* [n_rows][n_kv][splits_max][G][hd + 4]: values, max, sum, padding */
     float* att;            /* [n_rows][n_heads * hd] */
     int n_heads, n_kv, hd, ctx, splits_max;
     float eps;
