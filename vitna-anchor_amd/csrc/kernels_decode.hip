@@ -129,7 +129,6 @@ hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_
    the lowest index holding it. With a NaN among the logits the passes are run as the
    reference runs them (a NaN where a pass starts is kept, since x > NaN is
    false; a later one never wins). */
-#define RPL (ROUTE_E_MAX / 64) /* logits a lane */
 
 __device__ __forceinline__ uint32_t order_key(float v) {
     uint32_t u = __float_as_uint(v);
@@ -148,31 +147,37 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-__device__ __forceinline__ void wave_route(const float* __restrict__ lg_in, int E, int K, int renorm, route_out* o, float* slg) {
+/* order_key's inverse (a key from -0 comes back as +0, which exp(l - max) cannot tell apart). */
+__device__ __forceinline__ float key_value(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k); }
+
+/* NS logits a lane (E <= 64 NS). */
+template <int NS>
+__device__ __forceinline__ void wave_route_n(const float* __restrict__ lg_in, int E, int K, int renorm, route_out* o, float* slg) {
     const int lane = threadIdx.x & 63;
-    __shared__ int chosen_s[ROUTE_K_MAX];
-    __shared__ float share_s[ROUTE_K_MAX];
-    float lg[RPL];
+    float lg[NS];
     bool nan = false;
 #pragma unroll
-    for (int i = 0; i < RPL; i++) {
+    for (int i = 0; i < NS; i++) {
         const int e = lane + 64 * i;
         lg[i] = e < E ? lg_in[e] : -INFINITY;
-        if (e < E) {
-            slg[e] = lg[i];
-            nan |= lg[i] != lg[i];
-        }
+        nan |= e < E && lg[i] != lg[i];
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    const float l0 = slg[0];
+    int e_mine = 0;       /* lane k < K: the k-th chosen, largest first */
+    float v_mine = 0.0f;  /* and its logit */
+    float mx;             /* the max as the CPU scans it */
     if (__any(nan)) {
+        __shared__ int chosen_s[ROUTE_K_MAX];
+#pragma unroll
+        for (int i = 0; i < NS; i++)
+            if (lane + 64 * i < E) slg[lane + 64 * i] = lg[i];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         unsigned taken = 0;
         for (int k = 0; k < K; k++) {
             int first = 0x7fffffff, bi = 0x7fffffff;
             float bv = 0.0f;
 #pragma unroll
-            for (int i = 0; i < RPL; i++) {
+            for (int i = 0; i < NS; i++) {
                 const int e = lane + 64 * i;
                 if (e < E && !(taken >> i & 1)) {
                     first = min(first, e);
@@ -192,68 +197,76 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ lg_in, int 
             if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
             if (lane == 0) chosen_s[k] = pick;
         }
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NS; i++)
+            if (lane + 64 * i < E) m = fmaxf(m, lg[i]);
+        mx = wave_max(m);
+        if (slg[0] != slg[0]) mx = slg[0]; /* a NaN first stays the max */
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (lane < K) {
+            e_mine = chosen_s[lane];
+            v_mine = slg[e_mine];
+        }
     } else {
         /* K rounds: the largest remaining key over the wave, then the lowest index holding it, which is
            the pass's argmax (strict >: the first of equals wins). Keys of absent or taken experts are 0,
-           below every logit's key (order_key(-inf) > 0). */
-        uint32_t key[RPL];
+           below every logit's key (order_key(-inf) > 0). The first round's key is the max. */
+        uint32_t key[NS];
 #pragma unroll
-        for (int i = 0; i < RPL; i++) key[i] = lane + 64 * i < E ? order_key(lg[i]) : 0u;
+        for (int i = 0; i < NS; i++) key[i] = lane + 64 * i < E ? order_key(lg[i]) : 0u;
+        mx = 0.0f;
         for (int k = 0; k < K; k++) {
-            uint32_t m = 0;
+            uint32_t m = key[0];
 #pragma unroll
-            for (int i = 0; i < RPL; i++)
-                if (64 * i < E) m = max(m, key[i]);
+            for (int i = 1; i < NS; i++) m = max(m, key[i]);
             m = wave_max_u32(m);
+            if (k == 0) mx = key_value(m);
             int pick = -1;
 #pragma unroll
-            for (int i = 0; i < RPL; i++) {
-                if (64 * i >= E) continue;
+            for (int i = 0; i < NS; i++) {
                 const uint64_t b = __ballot(key[i] == m);
                 if (pick < 0 && b) pick = 64 * i + (int)__builtin_ctzll(b);
             }
+            float sel = lg[0];
 #pragma unroll
-            for (int i = 0; i < RPL; i++)
+            for (int i = 1; i < NS; i++)
+                if ((pick >> 6) == i) sel = lg[i];
+            const float pv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sel), pick & 63));
+            if (lane == k) { e_mine = pick; v_mine = pv; }
+#pragma unroll
+            for (int i = 0; i < NS; i++)
                 if (pick == lane + 64 * i) key[i] = 0u;
-            if (lane == 0) chosen_s[k] = pick;
         }
     }
-    /* softmax over every expert: the max as the CPU scans it (a NaN first stays), the sum of exp(l - max) */
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < RPL; i++)
-        if (lane + 64 * i < E) mx = fmaxf(mx, lg[i]);
-    mx = wave_max(mx);
-    if (l0 != l0) mx = l0;
+    /* softmax over every expert: the sum of exp(l - max) */
     float sum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < RPL; i++)
+    for (int i = 0; i < NS; i++)
         if (lane + 64 * i < E) sum += expf(lg[i] - mx);
-    sum = wave_sum(sum);
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    /* lane k < K: the k-th chosen, its share, and where it falls in order of id */
-    int e_k = 0, at = 0;
-    float share = 0.0f;
-    if (lane < K) {
-        e_k = chosen_s[lane];
-        share = expf(slg[e_k] - mx) / sum;
-        share_s[lane] = share;
-        for (int j = 0; j < K; j++) at += chosen_s[j] < e_k;
+    sum = wave_sum_dpp(sum);
+    const float share = lane < K ? expf(v_mine - mx) / sum : 0.0f;
+    float total = 1.0f;
+    if (renorm) {
+        /* the chosen are largest first, so their shares are too: the total in that order */
+        total = 0.0f;
+        for (int j = 0; j < K; j++) total += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(share), j));
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    int at = 0; /* where the lane's expert falls in order of id */
+    for (int j = 0; j < K; j++) at += __builtin_amdgcn_readlane(e_mine, j) < e_mine;
     if (lane < K) {
-        float total = 1.0f;
-        if (renorm) {
-            /* the chosen are largest first, so their shares are too: the total in that order */
-            total = 0.0f;
-            for (int j = 0; j < K; j++) total += share_s[j];
-        }
-        o->chosen[lane] = e_k;
-        o->ids[at] = e_k;
+        o->chosen[lane] = e_mine;
+        o->ids[at] = e_mine;
         o->weights[at] = renorm ? share / total : share;
     }
+}
+
+__device__ __forceinline__ void wave_route(const float* __restrict__ lg_in, int E, int K, int renorm, route_out* o, float* slg) {
+    if (E <= 64) wave_route_n<1>(lg_in, E, K, renorm, o, slg);
+    else if (E <= 128) wave_route_n<2>(lg_in, E, K, renorm, o, slg);
+    else if (E <= 256) wave_route_n<4>(lg_in, E, K, renorm, o, slg);
+    else wave_route_n<8>(lg_in, E, K, renorm, o, slg);
 }
 
 /* One wave a block, four router rows a block (sixteen lanes a row). */
