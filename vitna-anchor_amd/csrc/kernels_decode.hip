@@ -566,10 +566,10 @@ hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s) {
    any of their arithmetic. */
 template <int DT, int LPR, int SPL, int U>
 __device__ __forceinline__ void gemv_rows(const qmat& w, float* __restrict__ y, int add, const xslice* xs, int unit0, int ustep,
-                                          int lane) {
+                                          int lane, int unit_end = 0x7fffffff) {
     constexpr int RPW = WAVE / LPR;
     const int sub = lane / LPR, al = lane % LPR;
-    const int units = (w.rows + RPW - 1) / RPW;
+    const int units = min((w.rows + RPW - 1) / RPW, unit_end);
     for (int u = unit0; u < units; u += U * ustep) {
         qraw q[U][SPL];
         int r[U];
@@ -644,13 +644,42 @@ __global__ __launch_bounds__(256) void gemv_kernel(gemv_args a) {
     xslice xs[SPL];
     const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
     constexpr int RPW = WAVE / LPR;
-    /* the matrices' units concatenated; wave w takes units w, w + nwaves, ... */
+    int units[3], batches = 0;
+    for (int i = 0; i < 3; i++) {
+        units[i] = i < a.n ? (a.w[i].rows + RPW - 1) / RPW : 0;
+        batches += (units[i] + GEMV_U - 1) / GEMV_U;
+    }
+    if (nwaves >= batches) {
+        /* one pass: wave w takes GEMV_U consecutive units of one matrix, so all its loads go out together */
+        int wb = 0;
+        for (int i = 0; i < a.n; i++) {
+            const int nb = (units[i] + GEMV_U - 1) / GEMV_U;
+            if (wave >= wb && wave < wb + nb) {
+                const int u0 = (wave - wb) * GEMV_U;
+                if (i == 0) {
+#pragma unroll
+                    for (int j = 0; j < SPL; j++) load_xslice(D0, lane % LPR + LPR * j, xin, xs[j]);
+                    gemv_rows<D0, LPR, SPL, GEMV_U>(a.w[0], a.y[0], a.add, xs, u0, 1, lane, u0 + GEMV_U);
+                } else if (i == 1) {
+#pragma unroll
+                    for (int j = 0; j < SPL; j++) load_xslice(D1, lane % LPR + LPR * j, xin, xs[j]);
+                    gemv_rows<D1, LPR, SPL, GEMV_U>(a.w[1], a.y[1], a.add, xs, u0, 1, lane, u0 + GEMV_U);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < SPL; j++) load_xslice(D2, lane % LPR + LPR * j, xin, xs[j]);
+                    gemv_rows<D2, LPR, SPL, GEMV_U>(a.w[2], a.y[2], a.add, xs, u0, 1, lane, u0 + GEMV_U);
+                }
+            }
+            wb += nb;
+        }
+        return;
+    }
+    /* several passes: the matrices' units concatenated; wave w takes units w, w + nwaves, ... */
     int base = 0;
     for (int i = 0; i < a.n; i++) {
-        const int units = (a.w[i].rows + RPW - 1) / RPW;
         int first = (wave - base) % nwaves;
         if (first < 0) first += nwaves;
-        if (first < units) {
+        if (first < units[i]) {
             if (i == 0) {
 #pragma unroll
                 for (int j = 0; j < SPL; j++) load_xslice(D0, lane % LPR + LPR * j, xin, xs[j]);
@@ -665,7 +694,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(gemv_args a) {
                 gemv_rows<D2, LPR, SPL, GEMV_U>(a.w[2], a.y[2], a.add, xs, first, nwaves, lane);
             }
         }
-        base += units;
+        base += units[i];
     }
 }
 
@@ -682,11 +711,11 @@ static int device_cus() {
 template <int D0, int D1, int D2, bool NORM>
 static hipError_t gemv_by_width(const gemv_args& a, hipStream_t s) {
     const int S = a.w[0].cols / 32;
-    int units = 0;
+    int batches = 0;
     const int lpr = S < 64 ? S : 64, rpw = WAVE / lpr;
-    for (int i = 0; i < a.n; i++) units += (a.w[i].rows + rpw - 1) / rpw;
-    /* enough waves to cover the units GEMV_U at a time, at most four blocks a CU (the loop covers the rest) */
-    int blocks = (units + 4 * GEMV_U - 1) / (4 * GEMV_U);
+    for (int i = 0; i < a.n; i++) batches += ((a.w[i].rows + rpw - 1) / rpw + GEMV_U - 1) / GEMV_U;
+    /* a wave a batch of GEMV_U units when that takes at most four blocks a CU; else four blocks a CU loop */
+    int blocks = (batches + 3) / 4;
     blocks = blocks < 4 * device_cus() ? blocks : 4 * device_cus();
     if (blocks < 1) blocks = 1;
     const size_t lds = NORM ? (size_t)a.w[0].cols * sizeof(float) : 0;
