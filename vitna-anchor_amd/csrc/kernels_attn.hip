@@ -342,7 +342,8 @@ hipError_t launch_attention(const attn_args& a, hipStream_t s) {
    maxima and sums read in parallel, each chunk's scale exp(m_s - M) computed
    once, then each dimension's weighted values summed, eight chunks' loads in
    flight at a time. */
-#define MERGE_MAX 256
+#define MERGE_MAX 1024
+#define MERGE_PRE 32 /* chunks whose values are requested with their maxima and sums */
 __global__ void attention_merge_kernel(attn_args a) {
     const int hq = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
     const int G = a.n_heads / a.n_kv, h = hq / G, g = hq % G, HD = a.hd;
@@ -351,13 +352,17 @@ __global__ void attention_merge_kernel(attn_args a) {
     const size_t stride = (size_t)G * (HD + 4);
     __shared__ float fm[MERGE_MAX], fl[MERGE_MAX];
     __shared__ float red[4];
+    /* the first MERGE_PRE chunks' values, loaded alongside the maxima: one round trip for most rows */
+    float v0[MERGE_PRE];
+#pragma unroll
+    for (int i = 0; i < MERGE_PRE; i++) v0[i] = i < n_act ? base[i * stride + d] : 0.0f;
     float m = -INFINITY;
     for (int s = d; s < n_act; s += blockDim.x) {
         fm[s] = base[s * stride + HD];
         fl[s] = base[s * stride + HD + 1];
         m = fmaxf(m, fm[s]);
     }
-    m = wave_max(m);
+    m = wave_max_dpp(m);
     if ((d & 63) == 0) red[d >> 6] = m;
     __syncthreads();
     float M = red[0];
@@ -365,7 +370,13 @@ __global__ void attention_merge_kernel(attn_args a) {
     for (int s = d; s < n_act; s += blockDim.x) fm[s] = expf(fm[s] - M);
     __syncthreads();
     float L = 0.f, o = 0.f;
-    int s = 0;
+#pragma unroll
+    for (int i = 0; i < MERGE_PRE; i++)
+        if (i < n_act) {
+            L = fmaf(fl[i], fm[i], L);
+            o = fmaf(v0[i], fm[i], o);
+        }
+    int s = MERGE_PRE;
     for (; s + 8 <= n_act; s += 8) {
         float v[8];
 #pragma unroll

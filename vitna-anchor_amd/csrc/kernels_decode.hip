@@ -600,9 +600,8 @@ __device__ __forceinline__ void gemv_rows(const qmat& w, float* __restrict__ y, 
     }
 }
 
-#define GEMV_U 4
 
-template <int D0, int D1, int D2, int LPR, int SPL, bool NORM>
+template <int D0, int D1, int D2, int LPR, int SPL, bool NORM, int GEMV_U>
 __global__ __launch_bounds__(256) void gemv_kernel(gemv_args a) {
     extern __shared__ float sh[];
     const int lane = threadIdx.x & 63;
@@ -708,29 +707,40 @@ static int device_cus() {
     return g_cus;
 }
 
-template <int D0, int D1, int D2, bool NORM>
-static hipError_t gemv_by_width(const gemv_args& a, hipStream_t s) {
-    const int S = a.w[0].cols / 32;
-    int batches = 0;
-    const int lpr = S < 64 ? S : 64, rpw = WAVE / lpr;
-    for (int i = 0; i < a.n; i++) batches += ((a.w[i].rows + rpw - 1) / rpw + GEMV_U - 1) / GEMV_U;
-    /* a wave a batch of GEMV_U units when that takes at most four blocks a CU; else four blocks a CU loop */
-    int blocks = (batches + 3) / 4;
-    blocks = blocks < 4 * device_cus() ? blocks : 4 * device_cus();
-    if (blocks < 1) blocks = 1;
-    const size_t lds = NORM ? (size_t)a.w[0].cols * sizeof(float) : 0;
-    if (lds > 64 * 1024 || (NORM && a.w[0].cols > 8192)) return hipErrorInvalidValue;
-    switch (S) {
-        case 4: gemv_kernel<D0, D1, D2, 4, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
-        case 8: gemv_kernel<D0, D1, D2, 8, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
-        case 16: gemv_kernel<D0, D1, D2, 16, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
-        case 32: gemv_kernel<D0, D1, D2, 32, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
-        case 64: gemv_kernel<D0, D1, D2, 64, 1, NORM><<<blocks, 256, lds, s>>>(a); break;
-        case 128: gemv_kernel<D0, D1, D2, 64, 2, NORM><<<blocks, 256, lds, s>>>(a); break;
-        case 256: gemv_kernel<D0, D1, D2, 64, 4, NORM><<<blocks, 256, lds, s>>>(a); break;
+template <int D0, int D1, int D2, bool NORM, int U>
+static hipError_t gemv_launch(const gemv_args& a, int blocks, size_t lds, hipStream_t s) {
+    switch (a.w[0].cols / 32) {
+        case 4: gemv_kernel<D0, D1, D2, 4, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
+        case 8: gemv_kernel<D0, D1, D2, 8, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
+        case 16: gemv_kernel<D0, D1, D2, 16, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
+        case 32: gemv_kernel<D0, D1, D2, 32, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
+        case 64: gemv_kernel<D0, D1, D2, 64, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
+        case 128: gemv_kernel<D0, D1, D2, 64, 2, NORM, U><<<blocks, 256, lds, s>>>(a); break;
+        case 256: gemv_kernel<D0, D1, D2, 64, 4, NORM, U><<<blocks, 256, lds, s>>>(a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+/* Rows a wave takes at a time (U): the most of 4, 2, 1 that still gives two waves a SIMD in one pass; when
+   even U = 4 needs more than four blocks a CU, four blocks a CU loop over the rows. */
+template <int D0, int D1, int D2, bool NORM>
+static hipError_t gemv_by_width(const gemv_args& a, hipStream_t s) {
+    const int S = a.w[0].cols / 32;
+    const int lpr = S < 64 ? S : 64, rpw = WAVE / lpr;
+    int units[3] = {0, 0, 0};
+    for (int i = 0; i < a.n; i++) units[i] = (a.w[i].rows + rpw - 1) / rpw;
+    auto batches = [&](int u) { return (units[0] + u - 1) / u + (units[1] + u - 1) / u + (units[2] + u - 1) / u; };
+    const int cus = device_cus(), want = 8 * cus; /* waves: two a SIMD */
+    const size_t lds = NORM ? (size_t)a.w[0].cols * sizeof(float) : 0;
+    if (lds > 64 * 1024 || (NORM && a.w[0].cols > 8192)) return hipErrorInvalidValue;
+    if (batches(4) >= want) {
+        int blocks = (batches(4) + 3) / 4;
+        blocks = blocks < 4 * cus ? blocks : 4 * cus;
+        return gemv_launch<D0, D1, D2, NORM, 4>(a, blocks, lds, s);
+    }
+    if (batches(2) >= want) return gemv_launch<D0, D1, D2, NORM, 2>(a, (batches(2) + 3) / 4, lds, s);
+    return gemv_launch<D0, D1, D2, NORM, 1>(a, (batches(1) + 3) / 4 > 0 ? (batches(1) + 3) / 4 : 1, lds, s);
 }
 
 template <int D0, int D1, int D2>
