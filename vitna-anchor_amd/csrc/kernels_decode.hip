@@ -15,7 +15,7 @@
  *   widen kernels      vitna_cuda_widen :5441 (widen_rows_kernel :5419)
  */
 
-#include "vitna_kernels.h"
+#include "gemv_impl.h"
 
 /* ------------------------------------------------------------------ */
 /* Upload: GGUF blocks into planes                                     */
@@ -383,14 +383,6 @@ hipError_t launch_route_check(const float* logits, int E, int K, int renorm, rou
 /* Experts, one token                                                  */
 /* ------------------------------------------------------------------ */
 
-/* Slices of one row split among LPR lanes, SPL slices a lane; 64 / LPR rows
-   a wave at once. */
-template <int LPR>
-__device__ __forceinline__ float row_sum(float v) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
-}
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
     /* engine/src/ops.c:283-288: (g / (1 + exp(-g))) * u */
@@ -443,7 +435,7 @@ __global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
             }
             pg = row_sum<LPR>(pg);
             pu = row_sum<LPR>(pu);
-            if (al == 0 && u[q] < units) a.act[u[q]] = silu_mul(pg, pu);
+            if (al == LPR - 1 && u[q] < units) a.act[u[q]] = silu_mul(pg, pu);
         }
     }
 }
@@ -559,193 +551,17 @@ hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s) {
 }
 
 /* ------------------------------------------------------------------ */
-/* Dense projections                                                   */
+/* Dense projections: gemv_impl.h, instantiated in gemv_q4/q6/q8.hip    */
 /* ------------------------------------------------------------------ */
 
-/* Units of RPW rows, U units in flight a wave: their loads all issued before
-   any of their arithmetic. */
-template <int DT, int LPR, int SPL, int U>
-__device__ __forceinline__ void gemv_rows(const qmat& w, float* __restrict__ y, int add, const xslice* xs, int unit0, int ustep,
-                                          int lane, int unit_end = 0x7fffffff) {
-    constexpr int RPW = WAVE / LPR;
-    const int sub = lane / LPR, al = lane % LPR;
-    const int units = min((w.rows + RPW - 1) / RPW, unit_end);
-    for (int u = unit0; u < units; u += U * ustep) {
-        qraw q[U][SPL];
-        int r[U];
-#pragma unroll
-        for (int h = 0; h < U; h++) {
-            r[h] = (u + h * ustep) * RPW + sub;
-            const int rr = r[h] < w.rows ? r[h] : w.rows - 1;
-#pragma unroll
-            for (int j = 0; j < SPL; j++) {
-                if (DT == VITNA_DTYPE_F32) continue;
-                slice_load<DT>(w, 0, rr, al + LPR * j, q[h][j]);
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < U; h++) {
-            const int rr = r[h] < w.rows ? r[h] : w.rows - 1;
-            float p = 0.f;
-#pragma unroll
-            for (int j = 0; j < SPL; j++) {
-                if (DT == VITNA_DTYPE_F32)
-                    p += slice_dot_f32(reinterpret_cast<const float*>(w.p[0]) + (size_t)rr * w.cols, al + LPR * j, xs[j]);
-                else
-                    p += slice_dot<DT>(q[h][j], al + LPR * j, xs[j]);
-            }
-            p = row_sum<LPR>(p);
-            if (al == 0 && r[h] < w.rows) y[r[h]] = add ? y[r[h]] + p : p;
-        }
-    }
-}
-
-
-template <int D0, int D1, int D2, int LPR, int SPL, bool NORM, int GEMV_U>
-__global__ __launch_bounds__(256) void gemv_kernel(gemv_args a) {
-    extern __shared__ float sh[];
-    const int lane = threadIdx.x & 63;
-    const int H = a.w[0].cols;
-    const float* xin = a.x;
-    if (NORM) {
-        /* up to eight float4 of x and of the weights a thread (H at most 8192, launch_gemv checks) */
-        __shared__ float red[4];
-        const int n4 = H / 4;
-        float4 xv[8], wv[8];
-        const float4* x4 = reinterpret_cast<const float4*>(a.x);
-        const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if ((int)threadIdx.x + 256 * i < n4) { xv[i] = x4[threadIdx.x + 256 * i]; wv[i] = w4[threadIdx.x + 256 * i]; }
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if ((int)threadIdx.x + 256 * i < n4) {
-                ss = fmaf(xv[i].x, xv[i].x, ss); ss = fmaf(xv[i].y, xv[i].y, ss);
-                ss = fmaf(xv[i].z, xv[i].z, ss); ss = fmaf(xv[i].w, xv[i].w, ss);
-            }
-        ss = wave_sum(ss);
-        if (lane == 0) red[threadIdx.x / WAVE] = ss;
-        __syncthreads();
-        ss = (red[0] + red[1]) + (red[2] + red[3]);
-        const float inv = 1.0f / sqrtf(ss / (float)H + a.eps);
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if ((int)threadIdx.x + 256 * i < n4) {
-                float4 o;
-                o.x = (xv[i].x * inv) * wv[i].x; o.y = (xv[i].y * inv) * wv[i].y;
-                o.z = (xv[i].z * inv) * wv[i].z; o.w = (xv[i].w * inv) * wv[i].w;
-                reinterpret_cast<float4*>(sh)[threadIdx.x + 256 * i] = o;
-            }
-        __syncthreads();
-        xin = sh;
-    }
-    xslice xs[SPL];
-    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
-    constexpr int RPW = WAVE / LPR;
-    int units[3], batches = 0;
-    for (int i = 0; i < 3; i++) {
-        units[i] = i < a.n ? (a.w[i].rows + RPW - 1) / RPW : 0;
-        batches += (units[i] + GEMV_U - 1) / GEMV_U;
-    }
-    if (nwaves >= batches) {
-        /* one pass: wave w takes GEMV_U consecutive units of one matrix, so all its loads go out together */
-        int wb = 0;
-        for (int i = 0; i < a.n; i++) {
-            const int nb = (units[i] + GEMV_U - 1) / GEMV_U;
-            if (wave >= wb && wave < wb + nb) {
-                const int u0 = (wave - wb) * GEMV_U;
-                if (i == 0) {
-#pragma unroll
-                    for (int j = 0; j < SPL; j++) load_xslice(D0, lane % LPR + LPR * j, xin, xs[j]);
-                    gemv_rows<D0, LPR, SPL, GEMV_U>(a.w[0], a.y[0], a.add, xs, u0, 1, lane, u0 + GEMV_U);
-                } else if (i == 1) {
-#pragma unroll
-                    for (int j = 0; j < SPL; j++) load_xslice(D1, lane % LPR + LPR * j, xin, xs[j]);
-                    gemv_rows<D1, LPR, SPL, GEMV_U>(a.w[1], a.y[1], a.add, xs, u0, 1, lane, u0 + GEMV_U);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < SPL; j++) load_xslice(D2, lane % LPR + LPR * j, xin, xs[j]);
-                    gemv_rows<D2, LPR, SPL, GEMV_U>(a.w[2], a.y[2], a.add, xs, u0, 1, lane, u0 + GEMV_U);
-                }
-            }
-            wb += nb;
-        }
-        return;
-    }
-    /* several passes: the matrices' units concatenated; wave w takes units w, w + nwaves, ... */
-    int base = 0;
-    for (int i = 0; i < a.n; i++) {
-        int first = (wave - base) % nwaves;
-        if (first < 0) first += nwaves;
-        if (first < units[i]) {
-            if (i == 0) {
-#pragma unroll
-                for (int j = 0; j < SPL; j++) load_xslice(D0, lane % LPR + LPR * j, xin, xs[j]);
-                gemv_rows<D0, LPR, SPL, GEMV_U>(a.w[0], a.y[0], a.add, xs, first, nwaves, lane);
-            } else if (i == 1) {
-#pragma unroll
-                for (int j = 0; j < SPL; j++) load_xslice(D1, lane % LPR + LPR * j, xin, xs[j]);
-                gemv_rows<D1, LPR, SPL, GEMV_U>(a.w[1], a.y[1], a.add, xs, first, nwaves, lane);
-            } else {
-#pragma unroll
-                for (int j = 0; j < SPL; j++) load_xslice(D2, lane % LPR + LPR * j, xin, xs[j]);
-                gemv_rows<D2, LPR, SPL, GEMV_U>(a.w[2], a.y[2], a.add, xs, first, nwaves, lane);
-            }
-        }
-        base += units[i];
-    }
-}
-
-static int g_cus = 0;
-static int device_cus() {
-    if (!g_cus) {
+int gemv_device_cus() {
+    static int cus = 0;
+    if (!cus) {
         int dev = 0;
         hipGetDevice(&dev);
-        if (hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || g_cus < 1) g_cus = 256;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
     }
-    return g_cus;
-}
-
-template <int D0, int D1, int D2, bool NORM, int U>
-static hipError_t gemv_launch(const gemv_args& a, int blocks, size_t lds, hipStream_t s) {
-    switch (a.w[0].cols / 32) {
-        case 4: gemv_kernel<D0, D1, D2, 4, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 8: gemv_kernel<D0, D1, D2, 8, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 16: gemv_kernel<D0, D1, D2, 16, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 32: gemv_kernel<D0, D1, D2, 32, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 64: gemv_kernel<D0, D1, D2, 64, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 128: gemv_kernel<D0, D1, D2, 64, 2, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 256: gemv_kernel<D0, D1, D2, 64, 4, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
-/* Rows a wave takes at a time (U): the most of 4, 2, 1 that still gives two waves a SIMD in one pass; when
-   even U = 4 needs more than four blocks a CU, four blocks a CU loop over the rows. */
-template <int D0, int D1, int D2, bool NORM>
-static hipError_t gemv_by_width(const gemv_args& a, hipStream_t s) {
-    const int S = a.w[0].cols / 32;
-    const int lpr = S < 64 ? S : 64, rpw = WAVE / lpr;
-    int units[3] = {0, 0, 0};
-    for (int i = 0; i < a.n; i++) units[i] = (a.w[i].rows + rpw - 1) / rpw;
-    auto batches = [&](int u) { return (units[0] + u - 1) / u + (units[1] + u - 1) / u + (units[2] + u - 1) / u; };
-    const int cus = device_cus(), want = 8 * cus; /* waves: two a SIMD */
-    const size_t lds = NORM ? (size_t)a.w[0].cols * sizeof(float) : 0;
-    if (lds > 64 * 1024 || (NORM && a.w[0].cols > 8192)) return hipErrorInvalidValue;
-    if (batches(4) >= want) {
-        int blocks = (batches(4) + 3) / 4;
-        blocks = blocks < 4 * cus ? blocks : 4 * cus;
-        return gemv_launch<D0, D1, D2, NORM, 4>(a, blocks, lds, s);
-    }
-    if (batches(2) >= want) return gemv_launch<D0, D1, D2, NORM, 2>(a, (batches(2) + 3) / 4, lds, s);
-    return gemv_launch<D0, D1, D2, NORM, 1>(a, (batches(1) + 3) / 4 > 0 ? (batches(1) + 3) / 4 : 1, lds, s);
-}
-
-template <int D0, int D1, int D2>
-static hipError_t gemv_norm(const gemv_args& a, hipStream_t s) {
-    return a.norm_w ? gemv_by_width<D0, D1, D2, true>(a, s) : gemv_by_width<D0, D1, D2, false>(a, s);
+    return cus;
 }
 
 hipError_t launch_gemv(const gemv_args& a, hipStream_t s) {
@@ -753,18 +569,11 @@ hipError_t launch_gemv(const gemv_args& a, hipStream_t s) {
     for (int i = 1; i < a.n; i++)
         if (a.w[i].cols != a.w[0].cols) return hipErrorInvalidValue;
     const int d0 = a.w[0].dtype, d1 = a.n > 1 ? a.w[1].dtype : d0, d2 = a.n > 2 ? a.w[2].dtype : d1;
-    constexpr int Q8 = VITNA_DTYPE_Q8_0, Q4 = VITNA_DTYPE_Q4_K, Q6 = VITNA_DTYPE_Q6_K, F = VITNA_DTYPE_F32;
-#define GEMV_CASE(A, B, C) \
-    if (d0 == A && d1 == B && d2 == C) return gemv_norm<A, B, C>(a, s);
-    GEMV_CASE(Q4, Q4, Q6)
-    GEMV_CASE(Q4, Q4, Q4)
-    GEMV_CASE(Q8, Q8, Q8)
-    GEMV_CASE(Q6, Q6, Q6)
-    GEMV_CASE(Q4, Q6, Q6)
-    GEMV_CASE(Q6, Q6, Q4)
-    GEMV_CASE(F, F, F)
-#undef GEMV_CASE
-    return hipErrorInvalidValue;
+    bool served = false;
+    hipError_t e = gemv_combo_q4(a, d0, d1, d2, s, &served);
+    if (!served) e = gemv_combo_q6(a, d0, d1, d2, s, &served);
+    if (!served) e = gemv_combo_q8(a, d0, d1, d2, s, &served);
+    return served ? e : hipErrorInvalidValue;
 }
 
 /* ------------------------------------------------------------------ */

@@ -153,6 +153,21 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+/* Slices of one row split among LPR lanes: the sum over each group of LPR
+   consecutive lanes, complete in the group's last lane (lane LPR - 1 of the
+   group): doubling scans within 16-lane rows, then row broadcasts for groups
+   of 32 and 64. */
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+    if constexpr (LPR >= 2) v += dpp_f<DPP_ROW_SHR(1), 0xf, 0xf>(v, 0.0f);
+    if constexpr (LPR >= 4) v += dpp_f<DPP_ROW_SHR(2), 0xf, 0xf>(v, 0.0f);
+    if constexpr (LPR >= 8) v += dpp_f<DPP_ROW_SHR(4), 0xf, 0xf>(v, 0.0f);
+    if constexpr (LPR >= 16) v += dpp_f<DPP_ROW_SHR(8), 0xf, 0xf>(v, 0.0f);
+    if constexpr (LPR >= 32) v += dpp_f<DPP_ROW_BCAST15, 0xa, 0xf>(v, 0.0f);
+    if constexpr (LPR >= 64) v += dpp_f<DPP_ROW_BCAST31, 0xc, 0xf>(v, 0.0f);
+    return v;
+}
+
 /* Sum over each 32-lane half of the wave, in every lane of the half. */
 __device__ __forceinline__ float half_sum_dpp(float v) {
     v = row_scan_sum(v);
