@@ -121,7 +121,7 @@ __device__ __forceinline__ float4 head_norm_rope(float4 v, int j, const float* w
     return o;
 }
 
-template <int HD>
+template <int HD, int G>
 __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     constexpr int DPL = HD / 4;  /* dimensions a lane in the scores */
     constexpr int VPL = HD / 64; /* dimensions a lane in the values */
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     const int pos = rr.pos, seq = rr.seq;
     const int n_act = pos / ATTN_CHUNK + 1;
     if (split >= n_act) return;
-    const int G = a.n_heads / a.n_kv, kv_dim = a.n_kv * HD, half = HD / 2;
+    const int kv_dim = a.n_kv * HD, half = HD / 2;
     float* kc = a.k_cache + (size_t)seq * a.seq_stride;
     float* vc = a.v_cache + (size_t)seq * a.seq_stride;
     __shared__ __attribute__((aligned(16))) float sq[GMAX * HD]; /* the G query heads, normalized */
@@ -213,42 +213,44 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
             }
     }
 
-    /* scores, and each head's max and sum over the wave's positions */
+    /* scores, and each head's max and sum over the wave's positions; the G heads side by side, so their
+       cross-lane steps interleave */
     const float scale = 1.0f / sqrtf((float)HD);
-    float mw[GMAX], lw[GMAX], pe[GMAX];
+    float sc[G], mw[G], lw[G], pe[G];
 #pragma unroll
-    for (int g = 0; g < GMAX; g++) {
-        if (g >= G) break;
+    for (int g = 0; g < G; g++) {
         const float4* qg = reinterpret_cast<const float4*>(sq + g * HD + qd * DPL);
-        float s = 0.f;
+        float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < DPL / 4; i++) {
             const float4 q4 = qg[i];
-            s = fmaf(q4.x, kr[4 * i], s);
-            s = fmaf(q4.y, kr[4 * i + 1], s);
-            s = fmaf(q4.z, kr[4 * i + 2], s);
-            s = fmaf(q4.w, kr[4 * i + 3], s);
+            acc = fmaf(q4.x, kr[4 * i], acc);
+            acc = fmaf(q4.y, kr[4 * i + 1], acc);
+            acc = fmaf(q4.z, kr[4 * i + 2], acc);
+            acc = fmaf(q4.w, kr[4 * i + 3], acc);
         }
-        s = quad_sum(s) * scale;
-        const float m = wave_max_dpp(valid ? s : -INFINITY);
-        const float e = valid ? expf(s - m) : 0.0f;
-        mw[g] = m;
-        lw[g] = wave_sum_dpp(qd == 0 ? e : 0.0f);
-        pe[g] = e;
+        sc[g] = acc;
     }
+#pragma unroll
+    for (int g = 0; g < G; g++) sc[g] = quad_sum(sc[g]) * scale;
+#pragma unroll
+    for (int g = 0; g < G; g++) mw[g] = wave_max_dpp(valid ? sc[g] : -INFINITY);
+#pragma unroll
+    for (int g = 0; g < G; g++) pe[g] = valid ? expf(sc[g] - mw[g]) : 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; g++) lw[g] = wave_sum_dpp(qd == 0 ? pe[g] : 0.0f);
     if (qd == 0) {
 #pragma unroll
-        for (int g = 0; g < GMAX; g++)
-            if (g < G) sp[wave][p][g] = pe[g];
+        for (int g = 0; g < G; g++) sp[wave][p][g] = pe[g];
     }
     /* sp[wave] is this wave's own: LDS operations of one wave complete in order */
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 
     /* values: a lane per dimension */
-    float acc[GMAX][VPL];
+    float acc[G][VPL];
 #pragma unroll
-    for (int g = 0; g < GMAX; g++)
+    for (int g = 0; g < G; g++)
 #pragma unroll
         for (int i = 0; i < VPL; i++) acc[g][i] = 0.f;
 #pragma unroll
@@ -257,23 +259,18 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
         const float4 w1 = *reinterpret_cast<const float4*>(&sp[wave][pp][4]);
         const float w[GMAX] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-        for (int g = 0; g < GMAX; g++) {
-            if (g >= G) break;
+        for (int g = 0; g < G; g++)
 #pragma unroll
             for (int i = 0; i < VPL; i++) acc[g][i] = fmaf(w[g], vv[pp][i], acc[g][i]);
-        }
     }
     if (lane == 0) {
 #pragma unroll
-        for (int g = 0; g < GMAX; g++)
-            if (g < G) { wm[wave][g] = mw[g]; wl[wave][g] = lw[g]; }
+        for (int g = 0; g < G; g++) { wm[wave][g] = mw[g]; wl[wave][g] = lw[g]; }
     }
 #pragma unroll
-    for (int g = 0; g < GMAX; g++) {
-        if (g >= G) break;
+    for (int g = 0; g < G; g++)
 #pragma unroll
         for (int i = 0; i < VPL; i++) wacc[wave][g][lane + 64 * i] = acc[g][i];
-    }
     __syncthreads();
 
     /* this chunk's partial: the four waves merged, a float4 of one head a thread */
@@ -331,10 +328,13 @@ hipError_t launch_attention(const attn_args& a, hipStream_t s) {
     if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > GMAX || a.n_rows < 1) return hipErrorInvalidValue;
     if (a.splits_max * ATTN_CHUNK < a.ctx) return hipErrorInvalidValue;
     const dim3 grid(a.splits_max, a.n_kv, a.n_rows);
-    if (a.hd == 128) attention_kernel<128><<<grid, 256, 0, s>>>(a);
-    else if (a.hd == 64) attention_kernel<64><<<grid, 256, 0, s>>>(a);
-    else return hipErrorInvalidValue;
-    return hipGetLastError();
+    const int G = a.n_heads / a.n_kv;
+#define ATTN_CASE(HD, GG) \
+    if (a.hd == HD && G == GG) { attention_kernel<HD, GG><<<grid, 256, 0, s>>>(a); return hipGetLastError(); }
+    ATTN_CASE(128, 8) ATTN_CASE(128, 4) ATTN_CASE(128, 2) ATTN_CASE(128, 1)
+    ATTN_CASE(64, 8) ATTN_CASE(64, 4) ATTN_CASE(64, 2) ATTN_CASE(64, 1)
+#undef ATTN_CASE
+    return hipErrorInvalidValue;
 }
 
 
