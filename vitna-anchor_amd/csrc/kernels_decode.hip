@@ -511,9 +511,9 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
             float p = 0.f;
 #pragma unroll
             for (int j = 0; j < IPL; j++) p = fmaf(wk[j], slice_dot<DT>(q[h][j], tk[j], xs[j]), p);
-            p = wave_sum(p);
+            p = row_sum<64>(p);
             const int r = r0 + h * nwaves;
-            if (lane == 0 && r < H) a.y[r] = a.add ? a.y[r] + p : p;
+            if (lane == 63 && r < H) a.y[r] = a.add ? a.y[r] + p : p;
         }
     }
 }

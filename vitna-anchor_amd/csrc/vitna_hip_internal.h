@@ -80,12 +80,7 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
    a 16-lane group (engine/src/ops.c:165-170, kernels.c:140-146):
    v_j = a_j + a_{j+8}, then ((v0 + v4) + (v2 + v6)) + ((v1 + v5) + (v3 + v7)).
    Valid in lane j = 0 of the group. */
-__device__ __forceinline__ float fold16_lanes(float a) {
-    const float v = a + __shfl_down(a, 8, 16);
-    const float s = v + __shfl_down(v, 4, 16);
-    const float u = s + __shfl_down(s, 2, 16);
-    return u + __shfl_down(u, 1, 16);
-}
+__device__ __forceinline__ float fold16_lanes(float a);
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -166,6 +161,15 @@ __device__ __forceinline__ float row_sum(float v) {
     if constexpr (LPR >= 32) v += dpp_f<DPP_ROW_BCAST15, 0xa, 0xf>(v, 0.0f);
     if constexpr (LPR >= 64) v += dpp_f<DPP_ROW_BCAST31, 0xc, 0xf>(v, 0.0f);
     return v;
+}
+
+#define DPP_ROW_SHL(n) (0x100 + (n))
+__device__ __forceinline__ float fold16_lanes(float a) {
+    /* lane j adds lane j + 8 (row_shl reads the higher lane), then + 4, + 2, + 1 */
+    const float v = a + dpp_f<DPP_ROW_SHL(8), 0xf, 0xf>(a, 0.0f);
+    const float s = v + dpp_f<DPP_ROW_SHL(4), 0xf, 0xf>(v, 0.0f);
+    const float u = s + dpp_f<DPP_ROW_SHL(2), 0xf, 0xf>(s, 0.0f);
+    return u + dpp_f<DPP_ROW_SHL(1), 0xf, 0xf>(u, 0.0f);
 }
 
 /* Sum over each 32-lane half of the wave, in every lane of the half. */
