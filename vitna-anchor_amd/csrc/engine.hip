@@ -59,6 +59,7 @@ struct vitna_cuda_model {
     float* h_logits;    /* pinned, 2 * ROWS_MAX * E */
     hipGraph_t step_graph_src; /* kept until free: graph tools may refer to its nodes */
     int *grp_count, *grp_pairs; /* expert grouping of a pass of rows: [E], [E][ROWS_MAX] */
+    uint16_t *sk_xh, *sk_xl;    /* a pass's activations split into bf16 hi and lo, [ROWS_MAX][widest row] */
     bool rows_shared_seq;       /* the pass's rows include two of one sequence (attention prepares first) */
     hipGraph_t rows_graph_src;
     hipGraphExec_t rows_graph;
@@ -413,6 +414,8 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
     ok = dalloc(g, &g->x, R * H * 4, "the residual", err, err_len) && dalloc(g, &g->xn, R * H * 4, "scratch", err, err_len) &&
          dalloc(g, &g->act, R * K * c->intermediate * 4, "scratch", err, err_len) &&
          dalloc(g, &g->ypart, R * K * H * 4, "scratch", err, err_len) &&
+         dalloc(g, &g->sk_xh, R * std::max<size_t>(H, (size_t)c->n_heads * c->head_dim) * 2, "scratch", err, err_len) &&
+         dalloc(g, &g->sk_xl, R * std::max<size_t>(H, (size_t)c->n_heads * c->head_dim) * 2, "scratch", err, err_len) &&
          dalloc(g, &g->rlogits, 2 * R * E * 4, "scratch", err, err_len) && dalloc(g, &g->rt, R * sizeof(route_out), "scratch", err, err_len) &&
          dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len) &&
          dalloc(g, &g->grp_count, E * sizeof(int), "scratch", err, err_len) &&
@@ -580,6 +583,7 @@ static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const
             ro[t].ids[i] = e;
             ro[t].weights[i] = weights[t * k + i];
             ro[t].chosen[i] = e;
+            ro[t].cw[i] = weights[t * k + i];
         }
     }
     /* pageable source: the copy has taken the bytes when this returns */
@@ -742,6 +746,7 @@ extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_
     route_out r;
     memset(&r, 0, sizeof(r));
     r.weights[0] = 1.0f;
+    r.cw[0] = 1.0f; /* expert 0, the only one: ids[0] = chosen[0] = 0 */
     ok = ok && hipMemcpy(dx, x, H * 4, hipMemcpyHostToDevice) == hipSuccess && hipMemcpy(dw, norm_w, H * 4, hipMemcpyHostToDevice) == hipSuccess &&
          hipMemcpy(drt, &r, sizeof(r), hipMemcpyHostToDevice) == hipSuccess && hipMemset(dctr, 0, 16) == hipSuccess &&
          hipMemset(drouter, 0, H * 4) == hipSuccess;
@@ -1199,6 +1204,23 @@ extern "C" bool vitna_hip_copy_probe(size_t bytes, int reps, double* avg_us, cha
 
 extern "C" size_t vitna_cuda_moe_rows_max(const struct vitna_cuda_model* g) { return g ? ROWS_MAX : 0; }
 
+/* Several rows times up to three matrices: from SKINNY_MIN rows on, on the matrix cores (kernels_skinny.hip),
+   the rows split into bf16 hi and lo first; below, the multi-row GEMV. */
+#define SKINNY_MIN 4
+static hipError_t enqueue_multi(vitna_cuda_model* g, const gemv_multi_args& m) {
+    bool quant = true;
+    for (int i = 0; i < m.nm; i++) quant &= m.w[i].dtype != VITNA_DTYPE_F32;
+    if (m.n < SKINNY_MIN || !quant) return launch_gemv_multi(m, g->stream);
+    const int K = m.w[0].cols;
+    hipError_t e = launch_split_rows(m.x, m.n, K, m.xstride, g->sk_xh, g->sk_xl, g->stream);
+    if (e != hipSuccess) return e;
+    skinny_args a;
+    memset(&a, 0, sizeof(a));
+    for (int i = 0; i < m.nm; i++) { a.w[i] = m.w[i]; a.y[i] = m.y[i]; }
+    a.nm = m.nm; a.xh = g->sk_xh; a.xl = g->sk_xl; a.n = m.n; a.add = m.add;
+    return launch_skinny(a, g->stream);
+}
+
 static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n) {
     const dlayer& d = g->L[layer];
     hipError_t e = launch_norm_rows(g->x, d.attn_norm, g->xn, n, g->H, g->eps, g->stream);
@@ -1208,7 +1230,7 @@ static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n) 
     ga.w[0] = d.q; ga.w[1] = d.k; ga.w[2] = d.v;
     ga.y[0] = g->q; ga.y[1] = g->k; ga.y[2] = g->v;
     ga.nm = 3; ga.x = g->xn; ga.n = n; ga.xstride = g->H;
-    e = launch_gemv_multi(ga, g->stream);
+    e = enqueue_multi(g, ga);
     if (e != hipSuccess) return e;
     attn_args a;
     memset(&a, 0, sizeof(a));
@@ -1238,7 +1260,7 @@ static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n) 
     gemv_multi_args go;
     memset(&go, 0, sizeof(go));
     go.w[0] = d.o; go.y[0] = g->x; go.nm = 1; go.x = g->att; go.n = n; go.xstride = g->nh * g->hd; go.add = 1;
-    return launch_gemv_multi(go, g->stream);
+    return enqueue_multi(g, go);
 }
 
 /* The grouped experts of the pass's n rows, routed as g->rt[0..n) holds it, added onto the residual rows. */
@@ -1262,7 +1284,7 @@ static hipError_t enqueue_rows_head(vitna_cuda_model* g, int n) {
     gemv_multi_args gh;
     memset(&gh, 0, sizeof(gh));
     gh.w[0] = g->head; gh.y[0] = g->vocab; gh.nm = 1; gh.x = g->xn; gh.n = n; gh.xstride = g->H;
-    return launch_gemv_multi(gh, g->stream);
+    return enqueue_multi(g, gh);
 }
 
 /* The pass's rows to the device, checked as a step checks its token (model.c:1190-1200). */

@@ -256,9 +256,11 @@ __device__ __forceinline__ void wave_route_n(const float* __restrict__ lg_in, in
     int at = 0; /* where the lane's expert falls in order of id */
     for (int j = 0; j < K; j++) at += __builtin_amdgcn_readlane(e_mine, j) < e_mine;
     if (lane < K) {
+        const float wt = renorm ? share / total : share;
         o->chosen[lane] = e_mine;
+        o->cw[lane] = wt;
         o->ids[at] = e_mine;
-        o->weights[at] = renorm ? share / total : share;
+        o->weights[at] = wt;
     }
 }
 
@@ -358,7 +360,7 @@ __global__ void route_check_kernel(const float* __restrict__ logits, int E, int 
     __shared__ route_out o;
     wave_route(logits, E, K, renorm, &o, slg);
     __syncthreads();
-    if (threadIdx.x < 3 * ROUTE_K_MAX) reinterpret_cast<int32_t*>(out)[threadIdx.x] = reinterpret_cast<const int32_t*>(&o)[threadIdx.x];
+    if (threadIdx.x < sizeof(route_out) / 4) reinterpret_cast<int32_t*>(out)[threadIdx.x] = reinterpret_cast<const int32_t*>(&o)[threadIdx.x];
 }
 
 /* One wave a row: the routing of n_rows rows of logits (row stride E) into out. */
@@ -390,61 +392,116 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / den) * u;
 }
 
+/* The experts' gate and up rows against the normalized token: units (slot k, row r), k in the order of
+   rt.chosen (largest logit first), act[k * I + r] = silu(gate . xn) * (up . xn). A wave takes 2 RPW
+   consecutive units (one slot, except where a slot ends) and, when it routes the logits itself, runs only the
+   selection rounds up to its slot before its loads go out. */
+template <int DT, int LPR, int SPL, int NS>
+__device__ __forceinline__ void experts_in_body(const experts_in_args& a, const xslice (&xs)[SPL], int wave, int lane) {
+    constexpr int RPW = WAVE / LPR;
+    const int sub = lane / LPR, al = lane % LPR, wib = threadIdx.x / WAVE;
+    const int I = a.gate.rows, units = a.K * I;
+    const int b = wave * 2 * RPW; /* this wave's first unit */
+    __shared__ int wch[4][ROUTE_K_MAX];
+    __shared__ route_out wrt[4];
+    __shared__ float slg[4][NS * 64];
+    int kmax = (min(b + 2 * RPW, units) - 1) / I;
+    if (a.logits) {
+        /* the selection rounds (the reference's passes, engine/src/model.c:626-650) up to slot kmax */
+        float lg[NS];
+        bool nan = false;
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const int e = lane + 64 * i;
+            lg[i] = e < a.E ? a.logits[e] : -INFINITY;
+            nan |= e < a.E && lg[i] != lg[i];
+        }
+        if (__any(nan)) {
+            wave_route_n<NS>(a.logits, a.E, a.K, a.renorm, &wrt[wib], slg[wib]);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            if (lane < a.K) wch[wib][lane] = wrt[wib].chosen[lane];
+        } else {
+            uint32_t key[NS];
+#pragma unroll
+            for (int i = 0; i < NS; i++) key[i] = lane + 64 * i < a.E ? order_key(lg[i]) : 0u;
+            for (int k = 0; k <= kmax; k++) {
+                uint32_t m = key[0];
+#pragma unroll
+                for (int i = 1; i < NS; i++) m = max(m, key[i]);
+                m = wave_max_u32(m);
+                int pick = -1;
+#pragma unroll
+                for (int i = 0; i < NS; i++) {
+                    const uint64_t bb = __ballot(key[i] == m);
+                    if (pick < 0 && bb) pick = 64 * i + (int)__builtin_ctzll(bb);
+                }
+#pragma unroll
+                for (int i = 0; i < NS; i++)
+                    if (pick == lane + 64 * i) key[i] = 0u;
+                if (lane == 0) wch[wib][k] = pick;
+            }
+        }
+    } else if (lane < a.K) {
+        wch[wib][lane] = a.rt->chosen[lane];
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    int u[2];
+    qraw g[2][SPL], v[2][SPL];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        u[q] = b + q * RPW + sub;
+        const int uu = u[q] < units ? u[q] : units - 1;
+        const int k = uu / I, r = uu - k * I, e = wch[wib][k];
+#pragma unroll
+        for (int j = 0; j < SPL; j++) {
+            slice_load<DT>(a.gate, e, r, al + LPR * j, g[q][j]);
+            slice_load<DT>(a.up, e, r, al + LPR * j, v[q][j]);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        float pg = 0.f, pu = 0.f;
+#pragma unroll
+        for (int j = 0; j < SPL; j++) {
+            pg += slice_dot<DT>(g[q][j], al + LPR * j, xs[j]);
+            pu += slice_dot<DT>(v[q][j], al + LPR * j, xs[j]);
+        }
+        pg = row_sum<LPR>(pg);
+        pu = row_sum<LPR>(pu);
+        if (al == LPR - 1 && u[q] < units) a.act[u[q]] = silu_mul(pg, pu);
+    }
+}
+
 template <int DT, int LPR, int SPL>
 __global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
     constexpr int RPW = WAVE / LPR;
-    __shared__ route_out srt;
-    const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
-    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
-    const int I = a.gate.rows;
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    const int uwaves = (a.K * a.gate.rows + 2 * RPW - 1) / (2 * RPW); /* waves with units */
+    if (wave >= uwaves) {
+        /* the wave past the units publishes the whole routing for the down projection */
+        if (wave == uwaves && a.logits) {
+            __shared__ float pslg[ROUTE_E_MAX];
+            wave_route(a.logits, a.E, a.K, a.renorm, a.rt, pslg);
+        }
+        return;
+    }
     xslice xs[SPL];
 #pragma unroll
-    for (int j = 0; j < SPL; j++) load_xslice(DT, al + LPR * j, a.xn, xs[j]);
-    if (a.logits) {
-        __shared__ float slg[ROUTE_E_MAX];
-        if (threadIdx.x < 64) wave_route(a.logits, a.E, a.K, a.renorm, &srt, slg);
-        __syncthreads();
-        if (blockIdx.x == 0 && threadIdx.x < 3 * ROUTE_K_MAX)
-            reinterpret_cast<int32_t*>(a.rt)[threadIdx.x] = reinterpret_cast<const int32_t*>(&srt)[threadIdx.x];
-    } else {
-        if (threadIdx.x < ROUTE_K_MAX) srt.ids[threadIdx.x] = a.rt->ids[threadIdx.x];
-        __syncthreads();
-    }
-    const int units = a.K * I;
-    for (int u0 = wave * RPW; u0 < units; u0 += 2 * nwaves * RPW) {
-        int u[2];
-        qraw g[2][SPL], v[2][SPL];
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            u[q] = u0 + q * nwaves * RPW + sub;
-            const int uu = u[q] < units ? u[q] : units - 1;
-            const int k = uu / I, r = uu - k * I, e = srt.ids[k];
-#pragma unroll
-            for (int j = 0; j < SPL; j++) {
-                slice_load<DT>(a.gate, e, r, al + LPR * j, g[q][j]);
-                slice_load<DT>(a.up, e, r, al + LPR * j, v[q][j]);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            float pg = 0.f, pu = 0.f;
-#pragma unroll
-            for (int j = 0; j < SPL; j++) {
-                pg += slice_dot<DT>(g[q][j], al + LPR * j, xs[j]);
-                pu += slice_dot<DT>(v[q][j], al + LPR * j, xs[j]);
-            }
-            pg = row_sum<LPR>(pg);
-            pu = row_sum<LPR>(pu);
-            if (al == LPR - 1 && u[q] < units) a.act[u[q]] = silu_mul(pg, pu);
-        }
-    }
+    for (int j = 0; j < SPL; j++) load_xslice(DT, lane % LPR + LPR * j, a.xn, xs[j]);
+    if (!a.logits || a.E <= 64) experts_in_body<DT, LPR, SPL, 1>(a, xs, wave, lane);
+    else if (a.E <= 128) experts_in_body<DT, LPR, SPL, 2>(a, xs, wave, lane);
+    else if (a.E <= 256) experts_in_body<DT, LPR, SPL, 4>(a, xs, wave, lane);
+    else experts_in_body<DT, LPR, SPL, 8>(a, xs, wave, lane);
 }
 
 template <int DT, int LPR, int SPL>
 static hipError_t ein_launch(const experts_in_args& a, hipStream_t s) {
     constexpr int RPW = WAVE / LPR;
     const int units = a.K * a.gate.rows;
-    const int waves = (units + 2 * RPW - 1) / (2 * RPW);
+    const int waves = (units + 2 * RPW - 1) / (2 * RPW) + 1; /* the last one publishes the routing */
     const int blocks = (waves + 3) / 4;
     experts_in_kernel<DT, LPR, SPL><<<blocks, 256, 0, s>>>(a);
     return hipGetLastError();
@@ -494,8 +551,8 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
         const bool ok = i < N;
         const int k = ok ? i / S : 0;
         tk[j] = ok ? i - k * S : 0;
-        ek[j] = a.rt->ids[k];
-        wk[j] = ok ? a.rt->weights[k] : 0.0f;
+        ek[j] = a.rt->chosen[k];
+        wk[j] = ok ? a.rt->cw[k] : 0.0f;
         load_xslice(DT, tk[j], a.act + (size_t)k * I, xs[j]);
     }
     for (int r0 = wave; r0 < H; r0 += 2 * nwaves) {

@@ -17,9 +17,10 @@
 /* A layer's routing on the device: the experts in order of id (ids), their
    weights, and the router's choice largest first (chosen). */
 struct route_out {
-    int32_t ids[ROUTE_K_MAX];
-    float weights[ROUTE_K_MAX];
-    int32_t chosen[ROUTE_K_MAX];
+    int32_t ids[ROUTE_K_MAX];     /* the chosen experts, ascending (the order the mixture is summed in) */
+    float weights[ROUTE_K_MAX];   /* their weights, in the order of ids */
+    int32_t chosen[ROUTE_K_MAX];  /* the chosen experts, largest logit first: the decode path's expert slots */
+    float cw[ROUTE_K_MAX];        /* their weights, in the order of chosen */
 };
 
 /* ---- upload and checking ---- */
@@ -166,6 +167,20 @@ struct gemv_multi_args {
     int n, xstride, add;
 };
 hipError_t launch_gemv_multi(const gemv_multi_args& a, hipStream_t s);
+
+/* Multi-row projections on the matrix cores (kernels_skinny.hip): y_i[t][r]
+   (+)= W_i[r] . x[t] for t < n, to fp32 accuracy; x comes split into bf16
+   hi and lo parts ([n][cols] each, launch_split_rows). */
+struct skinny_args {
+    qmat w[3];
+    float* y[3];
+    int nm;
+    const uint16_t* xh;
+    const uint16_t* xl;
+    int n, add;
+};
+hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, hipStream_t s);
+hipError_t launch_skinny(const skinny_args& a, hipStream_t s);
 
 /* The per-expert lists of (row, slot) pairs of n rows' routing: count[E],
    pairs[E][cap] = row * ROUTE_K_MAX + slot, in order of row. */
