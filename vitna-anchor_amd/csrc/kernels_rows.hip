@@ -21,6 +21,7 @@
  */
 
 #include "vitna_kernels.h"
+#include <algorithm>
 
 template <int LPR>
 __device__ __forceinline__ float rsum(float v) {
@@ -254,42 +255,66 @@ __global__ __launch_bounds__(256) void grouped_in_kernel(grouped_args a) {
     }
 }
 
-/* Units (expert, output row); the down row's slices (S = I / 32 of them,
-   among LPR lanes) read once for every row routed to the expert:
-   ypart[row * K + slot][r] = w_slot * (down_e[r] . act[row * K + slot]). */
-template <int DT, int LPR, int SPL>
-__global__ __launch_bounds__(256) void grouped_down_kernel(grouped_args a) {
+/* A down wave takes one expert and up to UMAX of its output rows (units): all of their slices are requested
+   at once, then applied to the rows routed to the expert, GB rows' activations at a time; wpe waves an expert
+   cover its rows. */
+#define GB 2
+
+/* ypart[row * K + slot][r] = w_slot * (down_e[r] . act[row * K + slot]): the down row's slices (S = I / 32 of
+   them, among LPR lanes). */
+template <int DT, int LPR, int SPL, int UMAX>
+__global__ __launch_bounds__(256) void grouped_down_kernel(grouped_args a, int wpe) {
     constexpr int RPW = WAVE / LPR;
     const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
-    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
+    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    const int e = wave / wpe, part = wave % wpe;
+    if (e >= a.E) return;
+    const int c = a.count[e];
+    if (c == 0) return;
     const int H = a.down.rows, I = a.down.cols, S = I / 32;
     const int upe = (H + RPW - 1) / RPW;
-    for (int u = wave; u < a.E * upe; u += nwaves) {
-        const int e = u / upe, r = (u - e * upe) * RPW + sub;
-        const int c = a.count[e];
-        if (c == 0) continue;
-        const int rr = r < H ? r : H - 1;
-        qraw q[SPL];
-        bool on[SPL];
+    const int u0 = part * UMAX, nu = min(UMAX, upe - u0);
+    if (nu <= 0) return;
+    bool on[SPL];
 #pragma unroll
-        for (int j = 0; j < SPL; j++) {
-            const int t = al + LPR * j;
-            on[j] = t < S;
-            slice_load<DT>(a.down, e, rr, on[j] ? t : 0, q[j]);
+    for (int j = 0; j < SPL; j++) on[j] = al + LPR * j < S;
+    qraw q[UMAX][SPL];
+#pragma unroll
+    for (int k = 0; k < UMAX; k++) {
+        if (k >= nu) break;
+        const int r = min((u0 + k) * RPW + sub, H - 1);
+#pragma unroll
+        for (int j = 0; j < SPL; j++) slice_load<DT>(a.down, e, r, on[j] ? al + LPR * j : 0, q[k][j]);
+    }
+    for (int b0 = 0; b0 < c; b0 += GB) {
+        const int nb = min(GB, c - b0);
+        int prow[GB], pslot[GB];
+        float pw[GB];
+        xslice xs[GB][SPL];
+#pragma unroll
+        for (int i = 0; i < GB; i++) {
+            const int pr = a.pairs[(size_t)e * a.cap + b0 + min(i, nb - 1)];
+            prow[i] = pr / ROUTE_K_MAX;
+            pslot[i] = pr % ROUTE_K_MAX;
+            pw[i] = a.rt[prow[i]].weights[pslot[i]];
+            const float* act = a.act + ((size_t)prow[i] * a.K + pslot[i]) * I;
+#pragma unroll
+            for (int j = 0; j < SPL; j++) load_xslice(DT, on[j] ? al + LPR * j : 0, act, xs[i][j]);
         }
-        for (int i = 0; i < c; i++) {
-            const int pr = a.pairs[(size_t)e * a.cap + i], row = pr / ROUTE_K_MAX, slot = pr % ROUTE_K_MAX;
-            const float* act = a.act + ((size_t)row * a.K + slot) * I;
-            float p = 0.f;
 #pragma unroll
-            for (int j = 0; j < SPL; j++) {
-                if (!on[j]) continue;
-                xslice xs;
-                load_xslice(DT, al + LPR * j, act, xs);
-                p += slice_dot<DT>(q[j], al + LPR * j, xs);
+        for (int k = 0; k < UMAX; k++) {
+            if (k >= nu) break;
+            const int r = (u0 + k) * RPW + sub;
+#pragma unroll
+            for (int i = 0; i < GB; i++) {
+                if (i >= nb) break;
+                float p = 0.f;
+#pragma unroll
+                for (int j = 0; j < SPL; j++)
+                    if (on[j]) p += slice_dot<DT>(q[k][j], al + LPR * j, xs[i][j]);
+                p = row_sum<LPR>(p);
+                if (al == LPR - 1 && r < H) a.ypart[((size_t)prow[i] * a.K + pslot[i]) * H + r] = pw[i] * p;
             }
-            p = rsum<LPR>(p);
-            if (al == 0 && r < H) a.ypart[((size_t)row * a.K + slot) * H + r] = a.rt[row].weights[slot] * p;
         }
     }
 }
@@ -302,16 +327,17 @@ static hipError_t grouped_dispatch(const grouped_args& a, bool down, hipStream_t
     /* lanes a row: the smallest power of two holding the row's slices, at most 64 */
     int lpr = 4;
     while (lpr < S && lpr < 64) lpr *= 2;
-    const int rpw = WAVE / lpr;
-    const long units = (long)a.E * ((rows + rpw - 1) / rpw);
-    int blocks = (int)((units + 3) / 4);
-    if (blocks > 4096) blocks = 4096;
-    const int spl = (S + lpr - 1) / lpr;
-#define GD(L, P)                                                                             \
-    if (lpr == L && spl == P) {                                                              \
-        if (down) grouped_down_kernel<DT, L, P><<<blocks, 256, 0, s>>>(a);                   \
-        else grouped_in_kernel<DT, L, P><<<blocks, 256, 0, s>>>(a);                          \
-        return hipGetLastError();                                                            \
+    const int rpw = WAVE / lpr, spl = (S + lpr - 1) / lpr;
+    constexpr int UDN = 8; /* output rows a down wave */
+    const int upe = (rows + rpw - 1) / rpw;
+    const int umax = std::max(1, UDN / spl); /* as the down kernel's UMAX */
+    const int wpe = (upe + umax - 1) / umax;
+    const int blocks = down ? (a.E * wpe + 3) / 4 : (int)std::min<long>(4096, ((long)a.E * upe + 3) / 4);
+#define GD(L, P)                                                                                           \
+    if (lpr == L && spl == P) {                                                                            \
+        if (down) grouped_down_kernel<DT, L, P, (UDN / P > 0 ? UDN / P : 1)><<<blocks, 256, 0, s>>>(a, wpe); \
+        else grouped_in_kernel<DT, L, P><<<blocks, 256, 0, s>>>(a);                                          \
+        return hipGetLastError();                                                                          \
     }
     GD(4, 1) GD(8, 1) GD(16, 1) GD(32, 1) GD(64, 1) GD(64, 2) GD(64, 3) GD(64, 4)
 #undef GD
