@@ -95,3 +95,46 @@ def test_rows_step_device_routed(name):
     finally:
         dev.close()
         model.free()
+
+
+@pytest.mark.parametrize("name", ["q8", "q4km"])
+def test_rows_crowded_experts(name):
+    """The grouped experts alone, 24 rows on 16 (32) experts: about six tokens an expert, so experts take
+    several four-token tiles, and the small models' short rows give the kernels' column split empty and
+    odd-started ranges. Each layer: the device's residual rows before and after vitna_cuda_moe_rows_experts
+    (routed by the host from the device's router logits, as model.c routes), against the CPU checker's
+    mixture of the same rows. Layer by layer, so no error is carried into the next layer's input."""
+    say("rows crowded experts", name)
+    seqs = 24
+    prefill = [1 + (7 * s) % 60 for s in range(seqs)]
+    model, dev = model_with_cache(name, 999, prefill, seqs)
+    try:
+        cfg = model.cfg
+        H, K = cfg.hidden, cfg.n_experts_used
+        rows = [(5 * s + 1, prefill[s], s) for s in range(seqs)]
+        most, worst = 0, 0.0
+        for l in range(cfg.n_layers):
+            norm = np.ctypeslib.as_array(model.m.layers[l].mlp_norm, shape=(H,)).copy()
+            lg = dev.rows_route(rows, l)
+            x0 = np.stack([dev.residual(i) for i in range(seqs)])
+            ids, ws, projs = [], [], []
+            for i in range(seqs):
+                ch, order, w = oracle.route(lg[i], K, bool(cfg.renormalize))
+                _, cch, _, _, proj = oracle.moe(model, l, oracle.rmsnorm(x0[i], norm, cfg.rms_eps))
+                assert np.array_equal(ch, cch), ("row", i, "layer", l)
+                ids.append(order)
+                ws.append(w)
+                projs.append(proj)
+            most = max(most, int(np.bincount(np.concatenate(ids)).max()))
+            dev.rows_experts(l, np.array(ids), np.array(ws))
+            x1 = np.stack([dev.residual(i) for i in range(seqs)])
+            for i in range(seqs):
+                got = x1[i].astype(np.float64) - x0[i]
+                r = float(np.max(np.abs(got - projs[i])) / np.max(np.abs(projs[i])))
+                worst = max(worst, r)
+                assert r <= REL, ("row", i, "layer", l, r)
+        assert most > 4, "no expert took more than one tile"
+        say("  most rows on one expert", most, "worst rel err of the mixture", worst)
+    finally:
+        dev.close()
+        model.free()

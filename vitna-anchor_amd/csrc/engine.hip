@@ -60,6 +60,8 @@ struct vitna_cuda_model {
     hipGraph_t step_graph_src; /* kept until free: graph tools may refer to its nodes */
     int *grp_count, *grp_pairs; /* expert grouping of a pass of rows: [E], [E][ROWS_MAX] */
     uint16_t *sk_xh, *sk_xl;    /* a pass's activations split into bf16 hi and lo, [ROWS_MAX][widest row] */
+    uint16_t *gm_xs, *gm_as;    /* the grouped experts' split activations: [ROWS_MAX][2H], [ROWS_MAX * K][2I] */
+    float *gm_xsum, *gm_asum;   /* and their sums over runs of 16 or more columns */
     bool rows_shared_seq;       /* the pass's rows include two of one sequence (attention prepares first) */
     hipGraph_t rows_graph_src;
     hipGraphExec_t rows_graph;
@@ -416,6 +418,10 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
          dalloc(g, &g->ypart, R * K * H * 4, "scratch", err, err_len) &&
          dalloc(g, &g->sk_xh, R * std::max<size_t>(H, (size_t)c->n_heads * c->head_dim) * 2, "scratch", err, err_len) &&
          dalloc(g, &g->sk_xl, R * std::max<size_t>(H, (size_t)c->n_heads * c->head_dim) * 2, "scratch", err, err_len) &&
+         dalloc(g, &g->gm_xs, R * 2 * H * 2, "scratch", err, err_len) &&
+         dalloc(g, &g->gm_as, R * K * 2 * c->intermediate * 2, "scratch", err, err_len) &&
+         dalloc(g, &g->gm_xsum, R * (H / 16) * 4, "scratch", err, err_len) &&
+         dalloc(g, &g->gm_asum, R * K * (c->intermediate / 16) * 4, "scratch", err, err_len) &&
          dalloc(g, &g->rlogits, 2 * R * E * 4, "scratch", err, err_len) && dalloc(g, &g->rt, R * sizeof(route_out), "scratch", err, err_len) &&
          dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len) &&
          dalloc(g, &g->grp_count, E * sizeof(int), "scratch", err, err_len) &&
@@ -1268,6 +1274,17 @@ static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n) {
     const dlayer& d = g->L[layer];
     hipError_t e = launch_group(g->rt, n, g->E, g->K, ROWS_MAX, g->grp_count, g->grp_pairs, g->stream);
     if (e != hipSuccess) return e;
+    if (gmma_fits(d.gate, d.up, d.down)) {
+        e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
+        gmma_args m;
+        m.gate = d.gate; m.up = d.up; m.down = d.down;
+        m.xs = g->gm_xs; m.xsum = g->gm_xsum; m.as = g->gm_as; m.asum = g->gm_asum; m.rt = g->rt; m.count = g->grp_count; m.pairs = g->grp_pairs;
+        m.E = g->E; m.K = g->K; m.cap = ROWS_MAX; m.ypart = g->ypart;
+        if (e == hipSuccess) e = launch_gmma_in(m, g->stream);
+        if (e == hipSuccess) e = launch_gmma_down(m, g->stream);
+        if (e == hipSuccess) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
+        return e;
+    }
     grouped_args a;
     a.gate = d.gate; a.up = d.up; a.down = d.down;
     a.xn = g->xn; a.rt = g->rt; a.count = g->grp_count; a.pairs = g->grp_pairs;

@@ -198,6 +198,26 @@ struct grouped_args {
 };
 hipError_t launch_grouped_in(const grouped_args& a, hipStream_t s);
 hipError_t launch_grouped_down(const grouped_args& a, hipStream_t s);
+/* The same grouped experts on the bf16 matrix cores (kernels_gmma.hip): activations split into bf16 hi/lo
+   chunks with sums over runs of gmma_gran(dtype) columns (launch_gmma_split), gate/up writing the SwiGLU output
+   split the same way, down into ypart. */
+struct gmma_args {
+    qmat gate, up, down;
+    const uint16_t* xs;    /* the normalized rows, split [n][2H] */
+    const float* xsum;     /* their sums [n][H / gmma_gran(gate)] */
+    uint16_t* as;          /* the SwiGLU output, split [n * K][2I] */
+    float* asum;           /* its sums [n * K][I / gmma_gran(down)] */
+    const route_out* rt;   /* [n] */
+    const int* count;      /* [E] */
+    const int* pairs;      /* [E][cap] */
+    int E, K, cap;
+    float* ypart;          /* [n][K][H] */
+};
+bool gmma_fits(const qmat& gate, const qmat& up, const qmat& down);
+int gmma_gran(int dtype);
+hipError_t launch_gmma_split(const float* x, int n, int K, int xstride, int gran, uint16_t* xs, float* sums, hipStream_t s);
+hipError_t launch_gmma_in(const gmma_args& a, hipStream_t s);
+hipError_t launch_gmma_down(const gmma_args& a, hipStream_t s);
 /* x[row] += the row's K outputs in ypart, added in slot order. */
 hipError_t launch_reduce_rows(const float* ypart, float* x, int n, int K, int H, hipStream_t s);
 

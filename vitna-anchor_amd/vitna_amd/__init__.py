@@ -16,7 +16,7 @@ import numpy as np
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ROOT = os.path.dirname(PKG)
-HIP_LIB = os.path.join(PKG, "libvitna_hip.so")
+HIP_LIB = os.environ.get("VITNA_HIP_LIB") or os.path.join(PKG, "libvitna_hip.so")
 SYNTH_LIB = os.path.join(PKG, "synth", "libvitna_synth.so")
 
 # vitna_dtype_t (include/vitna_model.h; engine/include/safetensors.h:23-45)
