@@ -164,13 +164,21 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     }
     const int t0 = split * ATTN_CHUNK + wave * 16;
     float vv[16][VPL];
+    if (t0 + 15 < pos) { /* the wave's sixteen positions all before the row's own: no checks */
+        const float* vrow = vc + (size_t)t0 * kv_dim + (size_t)h * HD + lane;
 #pragma unroll
-    for (int pp = 0; pp < 16; pp++) {
-        const int tt = t0 + pp;
-        const bool ok = tt <= pos && !(fresh_block && tt == pos);
-        const float* vrow = vc + (size_t)(ok ? tt : 0) * kv_dim + (size_t)h * HD;
+        for (int pp = 0; pp < 16; pp++)
 #pragma unroll
-        for (int i = 0; i < VPL; i++) vv[pp][i] = ok ? vrow[lane + 64 * i] : 0.0f;
+            for (int i = 0; i < VPL; i++) vv[pp][i] = vrow[(size_t)pp * kv_dim + 64 * i];
+    } else {
+#pragma unroll
+        for (int pp = 0; pp < 16; pp++) {
+            const int tt = t0 + pp;
+            const bool ok = tt <= pos && !(fresh_block && tt == pos);
+            const float* vrow = vc + (size_t)(ok ? tt : 0) * kv_dim + (size_t)h * HD;
+#pragma unroll
+            for (int i = 0; i < VPL; i++) vv[pp][i] = ok ? vrow[lane + 64 * i] : 0.0f;
+        }
     }
 
     /* the G query heads: thread tid holds float4 j of head g */
@@ -236,7 +244,7 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
 #pragma unroll
     for (int g = 0; g < G; g++) mw[g] = wave_max_dpp(valid ? sc[g] : -INFINITY);
 #pragma unroll
-    for (int g = 0; g < G; g++) pe[g] = valid ? expf(sc[g] - mw[g]) : 0.0f;
+    for (int g = 0; g < G; g++) pe[g] = valid ? __expf(sc[g] - mw[g]) : 0.0f;
 #pragma unroll
     for (int g = 0; g < G; g++) lw[g] = wave_sum_dpp(qd == 0 ? pe[g] : 0.0f);
     if (qd == 0) {

@@ -127,11 +127,13 @@ __device__ __forceinline__ float row_scan_sum(float v) {
     v += dpp_f<DPP_ROW_SHR(4), 0xf, 0xf>(v, 0.0f);
     return v + dpp_f<DPP_ROW_SHR(8), 0xf, 0xf>(v, 0.0f);
 }
+/* For a maximum a lane with no source reads its own value (max(v, v) = v), which lets the compiler fold
+   the move into v_max_f32_dpp. */
 __device__ __forceinline__ float row_scan_max(float v) {
-    v = fmaxf(v, dpp_f<DPP_ROW_SHR(1), 0xf, 0xf>(v, -INFINITY));
-    v = fmaxf(v, dpp_f<DPP_ROW_SHR(2), 0xf, 0xf>(v, -INFINITY));
-    v = fmaxf(v, dpp_f<DPP_ROW_SHR(4), 0xf, 0xf>(v, -INFINITY));
-    return fmaxf(v, dpp_f<DPP_ROW_SHR(8), 0xf, 0xf>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<DPP_ROW_SHR(1), 0xf, 0xf>(v, v));
+    v = fmaxf(v, dpp_f<DPP_ROW_SHR(2), 0xf, 0xf>(v, v));
+    v = fmaxf(v, dpp_f<DPP_ROW_SHR(4), 0xf, 0xf>(v, v));
+    return fmaxf(v, dpp_f<DPP_ROW_SHR(8), 0xf, 0xf>(v, v));
 }
 
 /* Sum of the wave, in every lane (the total gathers in lane 63, then a readlane). */
@@ -143,8 +145,8 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 }
 __device__ __forceinline__ float wave_max_dpp(float v) {
     v = row_scan_max(v);
-    v = fmaxf(v, dpp_f<DPP_ROW_BCAST15, 0xa, 0xf>(v, -INFINITY));
-    v = fmaxf(v, dpp_f<DPP_ROW_BCAST31, 0xc, 0xf>(v, -INFINITY));
+    v = fmaxf(v, dpp_f<DPP_ROW_BCAST15, 0xa, 0xf>(v, v));
+    v = fmaxf(v, dpp_f<DPP_ROW_BCAST31, 0xc, 0xf>(v, v));
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 

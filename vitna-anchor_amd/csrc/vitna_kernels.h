@@ -222,6 +222,8 @@ hipError_t launch_gmma_down(const gmma_args& a, hipStream_t s);
 hipError_t launch_reduce_rows(const float* ypart, float* x, int n, int K, int H, hipStream_t s);
 
 /* ---- helpers ---- */
+/* compute units of the current device (cached) */
+int gemv_device_cus();
 hipError_t launch_copy_probe(const void* src, void* dst, size_t bytes, hipStream_t s);
 hipError_t launch_fill_normal(float* out, size_t n, uint64_t seed, hipStream_t s);
 
