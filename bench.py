@@ -1,6 +1,7 @@
 """Benchmark: Qwen3-30B-A3B-shaped Q4_K_M batch-1 decode on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+    python bench.py --only 3|4 [--steps K]     one of the other configs alone (profiling)
 
 Workload: a full 48-layer Qwen3-30B-A3B-shaped model
 with seeded random weights (Q4_K gate/up/q/k/o, Q6_K down/v/LM head, Q4_K
@@ -60,6 +61,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-extra", action="store_true", help="measure configs[2] only")
+    ap.add_argument("--only", choices=["3", "4"], help="run one of the other configs alone (profiling) and print its object")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU). "
@@ -67,6 +69,18 @@ def main():
         sys.exit(2)
 
     import vitna_amd as va
+
+    if args.only:
+        if args.only == "4":
+            res = bench_prefill(va)
+        else:
+            model = va.Model(va.shape(n_layers=args.layers, ctx=8193, seqs=32, kv_host=0), 20260101, threads=16)
+            dev = va.Device(model)
+            res = bench_ragged(va, model, dev, args.steps, reps=args.steps)
+            dev.close()
+            model.free()
+        print(json.dumps({"configs": {args.only: res}}), flush=True)
+        return
 
     pos, token = 2048, 1234
     t0 = time.time()
@@ -172,15 +186,16 @@ def main():
     model.free()
 
 
-def bench_ragged(va, model, dev, steps):
-    """32 sequences, one new token each, key-value lengths U{128..8192} (seeded), values N(0,1)."""
+def bench_ragged(va, model, dev, steps, reps=None):
+    """32 sequences, one new token each, key-value lengths U{128..8192} (seeded), values N(0,1).
+    Times max(steps / 5, 5) rows steps, or reps of them."""
     cfg = model.cfg
     rng = np.random.RandomState(20260103)
     lengths = rng.randint(128, 8193, size=32)
     t0 = time.time()
     dev.kv_fill(3, [int(n) for n in lengths])
     rows = [(int(rng.randint(0, cfg.vocab)), int(lengths[s]), s) for s in range(32)]
-    ms = dev.time_rows(rows, max(steps // 5, 5))
+    ms = dev.time_rows(rows, reps if reps else max(steps // 5, 5))
     L, kd = cfg.n_layers, cfg.n_kv_heads * cfg.head_dim
     kv_bytes = float(np.sum(lengths + 1)) * kd * 4 * 2 * L
     # expected distinct experts a layer when 32 tokens each choose 8 of 128 (uniform routing)
