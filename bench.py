@@ -72,7 +72,7 @@ def main():
 
     if args.only:
         if args.only == "4":
-            res = bench_prefill(va)
+            res = bench_prefill(va, reps=args.steps)
         else:
             model = va.Model(va.shape(n_layers=args.layers, ctx=8193, seqs=32, kv_host=0), 20260101, threads=16)
             dev = va.Device(model)
@@ -211,13 +211,13 @@ def bench_ragged(va, model, dev, steps, reps=None):
             "est_note": "key-value bytes exact; expert bytes for the expected %.1f distinct experts a layer" % uniq}
 
 
-def bench_prefill(va):
+def bench_prefill(va, reps=10):
     """4096 rows N(0,1) through one Qwen3-shaped MoE layer, Q8_0 experts, top-8 of 128."""
     model = va.Model(va.shape(**va.CONFIGS[4]), 20260104, threads=16)
     dev = va.Device(model)
     try:
         n = 4096
-        tot, ph = dev.time_prefill(0, n, seed=11, reps=10)
+        tot, ph = dev.time_prefill(0, n, seed=11, reps=reps)
         cfg = model.cfg
         flops = 2.0 * n * cfg.n_experts_used * 3 * cfg.intermediate * cfg.hidden
         gemm_us = ph[2] + ph[3]
