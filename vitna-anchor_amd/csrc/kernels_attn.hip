@@ -332,11 +332,244 @@ __global__ __launch_bounds__(256) void attention_prepare_kernel(attn_args a) {
 }
 
 
+/* ---- the same attention on the matrix cores (head dimension 128, up to 8 query heads a kv head) ----
+   For passes of several rows, where the cache reads are long and the vector arithmetic of the VALU kernel
+   above (a quarter of its instructions are the score and value products, the rest their reductions and
+   addressing) sets the pace. Per wave, its 16 positions of the chunk:
+     scores  S[16 positions][16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16: lane l supplies position l % 16
+             (A) and head l % 16 (B, zero past G) over dimensions 32 t + 8 (l / 16) .. + 7, t < 4, and holds
+             S[4 (l / 16) + r][l % 16];
+     softmax per head over the wave's positions: a lane's four, then lanes l ^ 16, l ^ 32;
+     values  O[16 heads][128] = P . V on v_mfma_f32_16x16x16_bf16, eight tiles of 16 dimensions: the scores'
+             layout is already P's A operand (head l % 16, positions 4 (l / 16) .. + 3), and lane l supplies
+             dimension 16 j + l % 16 of those four positions (B); O lands in lanes l / 16 < 2 (heads 0..7).
+   Both products take fp32 operands split into bf16 hi + lo, three MFMAs (hi hi, hi lo, lo hi), fp32
+   accumulate: about 2^-16 relative a product. The partial per (chunk, head) is the VALU kernel's, so the same
+   merge follows. */
+typedef __bf16 at_bf8 __attribute__((ext_vector_type(8)));
+typedef short at_s4 __attribute__((ext_vector_type(4)));
+typedef float at_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t at_u2 __attribute__((ext_vector_type(2)));
+
+/* hi = bf16(x), lo = bf16(x - hi), packed two a dword */
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+    const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+    hi = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+    lo = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void attention_mma_kernel(attn_args a) {
+    constexpr int HD = 128, QF4 = HD / 4, PS = HD + 4;
+    const int split = blockIdx.x, h = blockIdx.y, row = blockIdx.z;
+    const row_rec rr = a.rows[row];
+    const int pos = rr.pos, seq = rr.seq;
+    const int n_act = pos / ATTN_CHUNK + 1;
+    if (split >= n_act) return;
+    const int kv_dim = a.n_kv * HD, half = HD / 2;
+    float* kc = a.k_cache + (size_t)seq * a.seq_stride;
+    float* vc = a.v_cache + (size_t)seq * a.seq_stride;
+    __shared__ __attribute__((aligned(16))) float sq[GMAX * HD]; /* the G query heads, normalized, scaled */
+    __shared__ __attribute__((aligned(16))) float nk[HD];
+    __shared__ __attribute__((aligned(16))) float nvs[HD];
+    __shared__ float wm[4][GMAX], wl[4][GMAX];
+    __shared__ __attribute__((aligned(16))) float wacc[4][GMAX][HD];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c16 = lane & 15, kq = lane >> 4;
+    const bool fresh_block = !a.prepared && split == n_act - 1;
+    const int t0 = split * ATTN_CHUNK + wave * 16;
+
+    /* keys: position t0 + c16, dimensions 32 t + 8 kq .. + 7 */
+    const int tk = t0 + c16;
+    const bool kvalid = tk <= pos, kfresh = fresh_block && tk == pos;
+    float4 kr[8];
+    if (kvalid && !kfresh) {
+        const float4* src = reinterpret_cast<const float4*>(kc + (size_t)tk * kv_dim + (size_t)h * HD + 8 * kq);
+#pragma unroll
+        for (int t = 0; t < 4; t++) { kr[2 * t] = src[8 * t]; kr[2 * t + 1] = src[8 * t + 1]; }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    /* values: dimension 16 j + c16 of positions t0 + 4 kq + i */
+    float vv[8][4];
+    if (t0 + 15 < pos) {
+        const float* vrow = vc + (size_t)(t0 + 4 * kq) * kv_dim + (size_t)h * HD + c16;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) vv[j][i] = vrow[(size_t)i * kv_dim + 16 * j];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tt = t0 + 4 * kq + i;
+            const bool ok = tt <= pos && !(fresh_block && tt == pos);
+            const float* vrow = vc + (size_t)(ok ? tt : 0) * kv_dim + (size_t)h * HD + c16;
+#pragma unroll
+            for (int j = 0; j < 8; j++) vv[j][i] = ok ? vrow[16 * j] : 0.0f;
+        }
+    }
+
+    /* the G query heads (normalized, rotated, scaled by 1 / sqrt(hd)); this row's own key and value */
+    {
+        const int g = tid / QF4, j = tid % QF4;
+        const bool qt = g < G;
+        float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (qt) qv = reinterpret_cast<const float4*>(a.q_raw + (size_t)row * a.n_heads * HD + (size_t)(h * G + g) * HD)[j];
+        if (!a.prepared) {
+            const float* cs = a.cos_tab + (size_t)pos * half;
+            const float* sn = a.sin_tab + (size_t)pos * half;
+            if (g < GMAX) qv = head_norm_rope<HD>(qv, j, a.q_norm, a.eps, cs, sn);
+            if (fresh_block && wave == 0) {
+                float4 kv4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (lane < QF4) kv4 = reinterpret_cast<const float4*>(a.k_raw + (size_t)row * kv_dim + (size_t)h * HD)[lane];
+                kv4 = head_norm_rope<HD>(kv4, lane % QF4, a.k_norm, a.eps, cs, sn);
+                if (lane < QF4) {
+                    const float4 vn = reinterpret_cast<const float4*>(a.v_raw + (size_t)row * kv_dim + (size_t)h * HD)[lane];
+                    reinterpret_cast<float4*>(nk)[lane] = kv4;
+                    reinterpret_cast<float4*>(nvs)[lane] = vn;
+                    reinterpret_cast<float4*>(kc + (size_t)pos * kv_dim + (size_t)h * HD)[lane] = kv4;
+                    reinterpret_cast<float4*>(vc + (size_t)pos * kv_dim + (size_t)h * HD)[lane] = vn;
+                }
+            }
+        }
+        const float sc = 1.0f / sqrtf((float)HD);
+        qv.x *= sc; qv.y *= sc; qv.z *= sc; qv.w *= sc;
+        if (qt) reinterpret_cast<float4*>(sq)[tid] = qv;
+    }
+    __syncthreads();
+    if (kfresh) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            kr[2 * t] = reinterpret_cast<const float4*>(nk + 32 * t + 8 * kq)[0];
+            kr[2 * t + 1] = reinterpret_cast<const float4*>(nk + 32 * t + 8 * kq)[1];
+        }
+    }
+    if (fresh_block && pos >= t0 + 4 * kq && pos < t0 + 4 * kq + 4) {
+        const int i = pos - t0 - 4 * kq;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float nv = nvs[16 * j + c16];
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++)
+                if (ii == i) vv[j][ii] = nv;
+        }
+    }
+
+    /* scores */
+    at_f4 S = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        uint32_t ah[4], al[4], bh[4], bl[4];
+        const float4 k0 = kr[2 * t], k1 = kr[2 * t + 1];
+        split2(k0.x, k0.y, ah[0], al[0]); split2(k0.z, k0.w, ah[1], al[1]);
+        split2(k1.x, k1.y, ah[2], al[2]); split2(k1.z, k1.w, ah[3], al[3]);
+        float4 q0 = make_float4(0.f, 0.f, 0.f, 0.f), q1 = q0;
+        if (c16 < G) {
+            q0 = reinterpret_cast<const float4*>(sq + c16 * HD + 32 * t + 8 * kq)[0];
+            q1 = reinterpret_cast<const float4*>(sq + c16 * HD + 32 * t + 8 * kq)[1];
+        }
+        split2(q0.x, q0.y, bh[0], bl[0]); split2(q0.z, q0.w, bh[1], bl[1]);
+        split2(q1.x, q1.y, bh[2], bl[2]); split2(q1.z, q1.w, bh[3], bl[3]);
+        const at_bf8 Ah = __builtin_bit_cast(at_bf8, u32x4{ah[0], ah[1], ah[2], ah[3]});
+        const at_bf8 Al = __builtin_bit_cast(at_bf8, u32x4{al[0], al[1], al[2], al[3]});
+        const at_bf8 Bh = __builtin_bit_cast(at_bf8, u32x4{bh[0], bh[1], bh[2], bh[3]});
+        const at_bf8 Bl = __builtin_bit_cast(at_bf8, u32x4{bl[0], bl[1], bl[2], bl[3]});
+        S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bh, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bl, S, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bh, S, 0, 0, 0);
+    }
+    /* softmax over the wave's positions, per head (lane l % 16): position 4 kq + r of the wave */
+    float m = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const bool ok = t0 + 4 * kq + r <= pos;
+        S[r] = ok ? S[r] : -INFINITY;
+        m = fmaxf(m, S[r]);
+    }
+    m = fmaxf(m, __shfl_xor(m, 16, WAVE));
+    m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+    float P[4], l = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        P[r] = S[r] == -INFINITY ? 0.0f : __expf(S[r] - m);
+        l += P[r];
+    }
+    l += __shfl_xor(l, 16, WAVE);
+    l += __shfl_xor(l, 32, WAVE);
+    uint32_t ph[2], pl[2];
+    split2(P[0], P[1], ph[0], pl[0]);
+    split2(P[2], P[3], ph[1], pl[1]);
+    const at_s4 Ph = __builtin_bit_cast(at_s4, at_u2{ph[0], ph[1]}), Pl = __builtin_bit_cast(at_s4, at_u2{pl[0], pl[1]});
+
+    /* values: eight tiles of 16 dimensions */
+    at_f4 O[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        uint32_t vh[2], vl[2];
+        split2(vv[j][0], vv[j][1], vh[0], vl[0]);
+        split2(vv[j][2], vv[j][3], vh[1], vl[1]);
+        const at_s4 Vh = __builtin_bit_cast(at_s4, at_u2{vh[0], vh[1]}), Vl = __builtin_bit_cast(at_s4, at_u2{vl[0], vl[1]});
+        at_f4 o = {0.f, 0.f, 0.f, 0.f};
+        o = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(Ph, Vh, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(Ph, Vl, o, 0, 0, 0);
+        o = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(Pl, Vh, o, 0, 0, 0);
+        O[j] = o;
+    }
+    if (kq == 0 && c16 < G) {
+        wm[wave][c16] = m;
+        wl[wave][c16] = l;
+    }
+    if (kq < 2) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int g = 4 * kq + r;
+            if (g < G) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) wacc[wave][g][16 * j + c16] = O[j][r];
+            }
+        }
+    }
+    __syncthreads();
+
+    /* this chunk's partial: the four waves merged, a float4 of one head a thread */
+    {
+        const int g = tid / QF4, j = tid % QF4;
+        if (g < G) {
+            float* part = a.partial + (((size_t)row * a.n_kv + h) * a.splits_max + split) * G * PS + (size_t)g * PS;
+            float M = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][g]);
+            float L = 0.f;
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float f = wm[w][g] == -INFINITY ? 0.0f : expf(wm[w][g] - M);
+                const float4 x = reinterpret_cast<const float4*>(&wacc[w][g][0])[j];
+                L = fmaf(wl[w][g], f, L);
+                o.x = fmaf(x.x, f, o.x); o.y = fmaf(x.y, f, o.y); o.z = fmaf(x.z, f, o.z); o.w = fmaf(x.w, f, o.w);
+            }
+            reinterpret_cast<float4*>(part)[j] = o;
+            if (j == 0) {
+                part[HD] = M;
+                part[HD + 1] = L;
+            }
+        }
+    }
+}
+
 hipError_t launch_attention(const attn_args& a, hipStream_t s) {
     if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > GMAX || a.n_rows < 1) return hipErrorInvalidValue;
     if (a.splits_max * ATTN_CHUNK < a.ctx) return hipErrorInvalidValue;
     const dim3 grid(a.splits_max, a.n_kv, a.n_rows);
     const int G = a.n_heads / a.n_kv;
+    if (a.mma && a.hd == 128) {
+#define ATTN_MMA(GG) \
+        if (G == GG) { attention_mma_kernel<GG><<<grid, 256, 0, s>>>(a); return hipGetLastError(); }
+        ATTN_MMA(8) ATTN_MMA(4) ATTN_MMA(2) ATTN_MMA(1)
+#undef ATTN_MMA
+    }
 #define ATTN_CASE(HD, GG) \
     if (a.hd == HD && G == GG) { attention_kernel<HD, GG><<<grid, 256, 0, s>>>(a); return hipGetLastError(); }
     ATTN_CASE(128, 8) ATTN_CASE(128, 4) ATTN_CASE(128, 2) ATTN_CASE(128, 1)

@@ -253,7 +253,10 @@ hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
     /* wide matrices (the LM head) take four 32-row tiles a wave, so each token tile's activations are read
        a quarter as often; the rest one */
     const bool wide = rows >= 32768;
-    const int RB = wide ? 128 : 32, ks_max = wide ? 2 : 16;
+#ifndef SK_KS_MAX
+#define SK_KS_MAX 16
+#endif
+    const int RB = wide ? 128 : 32, ks_max = wide ? 2 : SK_KS_MAX;
     int blocks = 0;
     for (int i = 0; i < a.nm; i++) blocks += (a.w[i].rows + RB - 1) / RB;
     int ks = 1;
