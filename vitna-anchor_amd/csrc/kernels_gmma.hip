@@ -187,42 +187,68 @@ struct ggran {
     static constexpr int per = 128 / g;                        /* scale blocks a step */
 };
 
+/* Chunk T's four weights of matrix k of the step, as the MFMA's B operand. */
+template <int DT, int T>
+__device__ __forceinline__ u32x2 gweights(const gstep<DT>& s) {
+    constexpr int G = ggran<DT>::g, B = T / (G / 4); /* scale block of the chunk */
+    if constexpr (DT == VITNA_DTYPE_Q4_K) {
+        /* group B of the step: pair B / 2, nibble B & 1; dword 8 (B / 2) + T % 8 */
+        constexpr int dw = 8 * (B >> 1) + (T & 7);
+        const uint32_t q = s.q[dw >> 2][dw & 3];
+        return mag4((B & 1) ? (q >> 4) & 0x0f0f0f0fu : q & 0x0f0f0f0fu);
+    } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
+        /* run B of the step: r = B / 2, l16 = B % 2; ql dword 8 (r & 1) + 4 l16 + T % 4, qh 4 l16 + T % 4 */
+        constexpr int r = B >> 1, l16 = B & 1, qld = 8 * (r & 1) + 4 * l16 + (T & 3), qhd = 4 * l16 + (T & 3);
+        const uint32_t ql = s.ql[qld >> 2][qld & 3] >> (4 * (r >> 1));
+        const uint32_t qh = s.qh[qhd >> 2][qhd & 3];
+        uint32_t hi;
+        if constexpr (r < 2) hi = qh << (4 - 2 * r);
+        else hi = qh >> (2 * r - 4);
+        return mag4((ql & 0x0f0f0f0fu) | (hi & 0x30303030u));
+    } else {
+        constexpr int dw = 8 * B + (T & 7);
+        return cvt4(s.q[dw >> 2][dw & 3] ^ 0x80808080u);
+    }
+}
+
 /* Step st (HALF = st & 1) of NM matrices: av the lane's activation registers (chunks lane / 4 and 16 + lane / 4
-   of its token lane % 4), S[i][b] the sum of token i over the step's scale block b. */
+   of its token lane % 4), S[i][b] the sum of token i over the step's scale block b. Every scale block of every
+   matrix keeps its own MFMA sum through the step, so a chunk's MFMAs (block by block, hi parts then lo parts)
+   never wait on one another. */
 template <int DT, int NM, int HALF>
 __device__ __forceinline__ void gcompute(const gstep<DT> s[NM], const u32x4 av[2], const sv<ggran<DT>::per> S[GM_TT],
                                          f32x4 acc[NM]) {
-    constexpr int CPB = ggran<DT>::g / 4; /* chunks a scale block */
-    sfor<ggran<DT>::per>([&](auto bi) {
+    constexpr int PER = ggran<DT>::per, CPB = ggran<DT>::g / 4; /* scale blocks a step, chunks a block */
+    f32x4 P[PER][NM];
+#pragma unroll
+    for (int b = 0; b < PER; b++)
+#pragma unroll
+        for (int k = 0; k < NM; k++) P[b][k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    sfor<CPB>([&](auto ui) {
+        constexpr int U = decltype(ui)::value;
+        u32x2 w[PER][NM];
+        sfor<PER>([&](auto bi) {
+            constexpr int B = decltype(bi)::value;
+#pragma unroll
+            for (int k = 0; k < NM; k++) w[B][k] = gweights<DT, B * CPB + U>(s[k]);
+        });
+        sfor<PER>([&](auto bi) {
+            constexpr int B = decltype(bi)::value, T = B * CPB + U;
+            const u32x4 a = av[T >> 4];
+#pragma unroll
+            for (int k = 0; k < NM; k++) P[B][k] = mma4<T & 15>(u32x2{a.x, a.y}, w[B][k], P[B][k]);
+        });
+        sfor<PER>([&](auto bi) {
+            constexpr int B = decltype(bi)::value, T = B * CPB + U;
+            const u32x4 a = av[T >> 4];
+#pragma unroll
+            for (int k = 0; k < NM; k++) P[B][k] = mma4<T & 15>(u32x2{a.z, a.w}, w[B][k], P[B][k]);
+        });
+    });
+    sfor<PER>([&](auto bi) {
         constexpr int B = decltype(bi)::value;
 #pragma unroll
         for (int k = 0; k < NM; k++) {
-            f32x4 P = {0.f, 0.f, 0.f, 0.f};
-            sfor<CPB>([&](auto ui) {
-                constexpr int T = B * CPB + decltype(ui)::value; /* chunk of the step */
-                u32x2 w;
-                if constexpr (DT == VITNA_DTYPE_Q4_K) {
-                    /* group B of the step: pair B / 2, nibble B & 1; dword 8 (B / 2) + T % 8 */
-                    constexpr int dw = 8 * (B >> 1) + (T & 7);
-                    const uint32_t q = s[k].q[dw >> 2][dw & 3];
-                    w = mag4((B & 1) ? (q >> 4) & 0x0f0f0f0fu : q & 0x0f0f0f0fu);
-                } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
-                    /* run B of the step: r = B / 2, l16 = B % 2; ql dword 8 (r & 1) + 4 l16 + T % 4, qh 4 l16 + T % 4 */
-                    constexpr int r = B >> 1, l16 = B & 1, qld = 8 * (r & 1) + 4 * l16 + (T & 3), qhd = 4 * l16 + (T & 3);
-                    const uint32_t ql = s[k].ql[qld >> 2][qld & 3] >> (4 * (r >> 1));
-                    const uint32_t qh = s[k].qh[qhd >> 2][qhd & 3];
-                    uint32_t hi;
-                    if constexpr (r < 2) hi = qh << (4 - 2 * r);
-                    else hi = qh >> (2 * r - 4);
-                    w = mag4((ql & 0x0f0f0f0fu) | (hi & 0x30303030u));
-                } else {
-                    constexpr int dw = 8 * B + (T & 7);
-                    w = cvt4(s[k].q[dw >> 2][dw & 3] ^ 0x80808080u);
-                }
-                const u32x4 a = av[T >> 4];
-                P = mma4<T & 15>(u32x2{a.x, a.y}, w, P);
-                P = mma4<T & 15>(u32x2{a.z, a.w}, w, P);
-            });
             if constexpr (DT == VITNA_DTYPE_Q4_K) {
                 constexpr int g = 4 * HALF + B; /* group of the block */
                 const uint32_t h0 = s[k].h.x, s03 = s[k].h.y, s47 = s[k].h.z, s8b = s[k].h.w;
@@ -239,16 +265,16 @@ __device__ __forceinline__ void gcompute(const gstep<DT> s[NM], const u32x4 av[2
                 const float m1 = f16_bits_to_f32(h0 >> 16) * (float)mn;
                 const float mp = m1 + 128.0f * d1;
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[k][i] = fmaf(-mp, S[i][B], fmaf(d1, P[i], acc[k][i]));
+                for (int i = 0; i < 4; i++) acc[k][i] = fmaf(-mp, S[i][B], fmaf(d1, P[B][k][i], acc[k][i]));
             } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
                 const uint32_t scw = B < 4 ? s[k].sc.x : s[k].sc.y;
                 const float ds = f16_bits_to_f32(s[k].d & 0xffffu) * (float)(int8_t)((scw >> (8 * (B & 3))) & 0xff);
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[k][i] = fmaf(ds, fmaf(-160.0f, S[i][B], P[i]), acc[k][i]);
+                for (int i = 0; i < 4; i++) acc[k][i] = fmaf(ds, fmaf(-160.0f, S[i][B], P[B][k][i]), acc[k][i]);
             } else {
                 const float d = f16_bits_to_f32(s[k].d[B] & 0xffffu);
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[k][i] = fmaf(d, fmaf(-128.0f, S[i][B], P[i]), acc[k][i]);
+                for (int i = 0; i < 4; i++) acc[k][i] = fmaf(d, fmaf(-128.0f, S[i][B], P[B][k][i]), acc[k][i]);
             }
         }
     });
@@ -272,6 +298,9 @@ __device__ __forceinline__ void grows(const qmat& m0, const qmat& m1, int e, int
         av[1] = arow[32 * st + 16 + c16];
 #pragma unroll
         for (int i = 0; i < GM_TT; i++) S[i] = sloadf<PER>(srow[i] + PER * st);
+        /* the loads stay where they are, a step ahead of their use (the scheduler would otherwise sink them to
+           their first use to save registers, leaving nothing in flight) */
+        __builtin_amdgcn_sched_barrier(0);
     };
     /* steps in pairs from an even step (half 0, half 1 of a block); a range starting odd or ending early takes
        its lone step separately */
