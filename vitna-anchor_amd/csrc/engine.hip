@@ -479,7 +479,7 @@ static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, 
     a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx; a.splits_max = g->splits_max;
     a.eps = g->eps;
     a.prepared = prepared ? 1 : 0;
-    a.mma = 0;
+    a.mma = 1;
     e = launch_attention(a, g->stream);
     if (e == hipSuccess) e = launch_attention_merge(a, g->stream);
     if (e != hipSuccess) return e;
@@ -967,7 +967,7 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
                 a.k_cache = g->k_cache + (size_t)l * g->layer_kv; a.v_cache = g->v_cache + (size_t)l * g->layer_kv;
                 a.seq_stride = (size_t)g->NL * g->layer_kv; a.rows = g->rows_dev; a.n_rows = 1; a.partial = g->partial;
                 a.att = g->att; a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx;
-                a.splits_max = g->splits_max; a.eps = g->eps; a.mma = 0;
+                a.splits_max = g->splits_max; a.eps = g->eps; a.mma = 1;
                 b = 0; /* set by the caller from the position */
                 const hipError_t e = launch_attention(a, g->stream);
                 return e == hipSuccess ? launch_attention_merge(a, g->stream) : e;
