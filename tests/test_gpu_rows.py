@@ -138,3 +138,44 @@ def test_rows_crowded_experts(name):
     finally:
         dev.close()
         model.free()
+
+
+WIDE = dict(n_layers=1, hidden=256, intermediate=256, n_heads=32, n_kv_heads=4, head_dim=128, vocab=40000,
+            n_experts=8, n_experts_used=2, norm_std=0.1, ctx=40, kv_host=1)
+
+
+@pytest.mark.parametrize("dt", ["k", "q8"])
+def test_rows_wide_projections(dt):
+    """Projections wider than 2048 columns (the o-projection's 4096 = 16 superblocks, two splits) are split across
+    blocks, the last block of a tile adding the splits' sums in order; a head of 40000 rows (1250 tiles) takes the
+    wide kernel, whose activations go through LDS; 36 rows take two token tiles. A rows step of 36 sequences
+    against the CPU checker, twice through one graph, so the split counters must come back to zero."""
+    say("rows wide projections", dt)
+    spec = dict(WIDE)
+    if dt == "q8":
+        spec.update(dt_q=va.Q8_0, dt_k=va.Q8_0, dt_v=va.Q8_0, dt_o=va.Q8_0, dt_head=va.Q8_0)
+    seqs = 36
+    prefill = [1 + (5 * s) % 30 for s in range(seqs)]
+    spec["seqs"] = seqs
+    model = va.Model(va.shape(**spec), 4242)
+    cfg = model.cfg
+    kd = cfg.n_kv_heads * cfg.head_dim
+    L, ctx = cfg.n_layers, model.m.ctx
+    kc = np.ctypeslib.as_array(model.m.k_cache, shape=(seqs, L, ctx, kd))
+    vc = np.ctypeslib.as_array(model.m.v_cache, shape=(seqs, L, ctx, kd))
+    kc[:] = va.normal(4242, 101, kc.size).reshape(kc.shape)
+    vc[:] = va.normal(4242, 102, vc.size).reshape(vc.shape)
+    dev = va.Device(model)
+    try:
+        for s in range(seqs):
+            dev.kv(s, 0, 0, prefill[s] + 1, kc[s, 0, :prefill[s] + 1], vc[s, 0, :prefill[s] + 1])
+        for shift in (0, 1):
+            rows = [(7 * s + 2, prefill[s] - 1 + shift, s) for s in range(seqs)]
+            ref = cpu_rows(model, rows)
+            logits = dev.rows_step(rows)
+            worst = max(rel(logits[i], ref[i][0]) for i in range(seqs))
+            say("  pass", shift, "max rel err", worst)
+            assert worst <= REL
+    finally:
+        dev.close()
+        model.free()

@@ -60,6 +60,10 @@ struct vitna_cuda_model {
     hipGraph_t step_graph_src; /* kept until free: graph tools may refer to its nodes */
     int *grp_count, *grp_pairs; /* expert grouping of a pass of rows: [E], [E][ROWS_MAX] */
     uint16_t *sk_xh, *sk_xl;    /* a pass's activations split into bf16 hi and lo, [ROWS_MAX][widest row] */
+    uint16_t* sk_sum[2];        /* their sums over 16 and 32 columns, three bf16 pieces: [3][ROWS_MAX][widest / 16 or / 32] */
+    float* sk_part;             /* split sums of the multi-row projections wider than 2048 columns */
+    int* sk_cnt;                /* their per-tile counters, zero between calls */
+    size_t sk_part_cap, sk_cnt_cap;
     uint16_t *gm_xs, *gm_as;    /* the grouped experts' split activations: [ROWS_MAX][2H], [ROWS_MAX * K][2I] */
     float *gm_xsum, *gm_asum;   /* and their sums over runs of 16 or more columns */
     bool rows_shared_seq;       /* the pass's rows include two of one sequence (attention prepares first) */
@@ -418,6 +422,8 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
          dalloc(g, &g->ypart, R * K * H * 4, "scratch", err, err_len) &&
          dalloc(g, &g->sk_xh, R * std::max<size_t>(H, (size_t)c->n_heads * c->head_dim) * 2, "scratch", err, err_len) &&
          dalloc(g, &g->sk_xl, R * std::max<size_t>(H, (size_t)c->n_heads * c->head_dim) * 2, "scratch", err, err_len) &&
+         dalloc(g, &g->sk_sum[0], 3 * R * std::max<size_t>(H, qd) / 16 * 2, "scratch", err, err_len) &&
+         dalloc(g, &g->sk_sum[1], 3 * R * std::max<size_t>(H, qd) / 32 * 2, "scratch", err, err_len) &&
          dalloc(g, &g->gm_xs, R * 2 * H * 2, "scratch", err, err_len) &&
          dalloc(g, &g->gm_as, R * K * 2 * c->intermediate * 2, "scratch", err, err_len) &&
          dalloc(g, &g->gm_xsum, R * (H / 16) * 4, "scratch", err, err_len) &&
@@ -434,6 +440,25 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
              dalloc(g, &g->partial, (size_t)R * c->n_kv_heads * g->splits_max * G * (c->head_dim + 4) * 4, "attention partials", err, err_len) &&
              dalloc(g, &g->k_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the key cache", err, err_len) &&
              dalloc(g, &g->v_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the value cache", err, err_len);
+    }
+    if (ok && g->attention) {
+        /* the multi-row projections' split sums: per token tile, each 32-row tile of a launch (q/k/v, o, head)
+           takes one counter and ceil(width / 2048) sums of 32 x 32 */
+        const size_t mt = (R + 31) / 32, t32 = 32;
+        const size_t lt[3] = {(qd + 2 * kd + 3 * (t32 - 1)) / t32, (H + t32 - 1) / t32, (c->vocab + t32 - 1) / t32};
+        const size_t lw[3] = {H, qd, H};
+        size_t cnt = 1, part = 1;
+        for (int i = 0; i < 3; i++) {
+            const size_t sp = (lw[i] / 256 + 7) / 8;
+            if (sp > 1) {
+                cnt = std::max(cnt, mt * lt[i]);
+                part = std::max(part, mt * lt[i] * sp * 1024);
+            }
+        }
+        g->sk_cnt_cap = cnt;
+        g->sk_part_cap = part;
+        ok = dalloc(g, &g->sk_part, part * 4, "scratch", err, err_len) && dalloc(g, &g->sk_cnt, cnt * 4, "scratch", err, err_len) &&
+             hipMemset(g->sk_cnt, 0, cnt * 4) == hipSuccess;
     }
     if (!ok) return bail();
     if (hipMemset(g->x, 0, R * H * 4) != hipSuccess || hipMemset(g->rt, 0, R * sizeof(route_out)) != hipSuccess) {
@@ -1219,12 +1244,16 @@ static hipError_t enqueue_multi(vitna_cuda_model* g, const gemv_multi_args& m) {
     for (int i = 0; i < m.nm; i++) quant &= m.w[i].dtype != VITNA_DTYPE_F32;
     if (m.n < SKINNY_MIN || !quant) return launch_gemv_multi(m, g->stream);
     const int K = m.w[0].cols;
-    hipError_t e = launch_split_rows(m.x, m.n, K, m.xstride, g->sk_xh, g->sk_xl, g->stream);
+    /* group sums for the exact-integer kernel when the width allows it */
+    const bool sums = K % 256 == 0 && m.xstride % 4 == 0 && (uintptr_t)m.x % 16 == 0;
+    hipError_t e = launch_split_rows(m.x, m.n, K, m.xstride, g->sk_xh, g->sk_xl, sums ? g->sk_sum : nullptr, g->stream);
     if (e != hipSuccess) return e;
     skinny_args a;
     memset(&a, 0, sizeof(a));
     for (int i = 0; i < m.nm; i++) { a.w[i] = m.w[i]; a.y[i] = m.y[i]; }
     a.nm = m.nm; a.xh = g->sk_xh; a.xl = g->sk_xl; a.n = m.n; a.add = m.add;
+    if (sums) { a.s16 = g->sk_sum[0]; a.s32 = g->sk_sum[1]; }
+    a.part = g->sk_part; a.cnt = g->sk_cnt; a.part_cap = g->sk_part_cap; a.cnt_cap = g->sk_cnt_cap;
     return launch_skinny(a, g->stream);
 }
 

@@ -26,6 +26,8 @@
 
 #include "vitna_kernels.h"
 
+#include <algorithm>
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -45,9 +47,67 @@ __global__ void split_rows_kernel(const float* __restrict__ x, int n, int K, int
     }
 }
 
-hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, hipStream_t s) {
+__device__ __forceinline__ uint16_t bf16_bits(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
+
+/* S as three bf16 pieces: S = p0 + p1 + p2 to about 2^-24 relative */
+__device__ __forceinline__ void bf16x3(float S, uint16_t* d, size_t plane, size_t i) {
+    const __bf16 p0 = (__bf16)S;
+    const float r0 = S - (float)p0;
+    const __bf16 p1 = (__bf16)r0;
+    const __bf16 p2 = (__bf16)(r0 - (float)p1);
+    d[i] = __builtin_bit_cast(uint16_t, p0);
+    d[plane + i] = __builtin_bit_cast(uint16_t, p1);
+    d[2 * plane + i] = __builtin_bit_cast(uint16_t, p2);
+}
+
+/* The split plus each row's group sums: thread i of row r takes columns 16 i .. 16 i + 15, sums the split
+   values hi + lo (what the matrix cores see: each hi + lo is exact in fp32) in column order, and adds its
+   pair's sum for the 32-column group (the even thread's sum first). The sums go out as three bf16 pieces,
+   planes of n x K / 16 (s16) and n x K / 32 (s32). */
+__global__ void split_sums_kernel(const float* __restrict__ x, int n, int K, int xstride, uint16_t* __restrict__ xh,
+                                  uint16_t* __restrict__ xl, uint16_t* __restrict__ s16, uint16_t* __restrict__ s32) {
+    const int r = blockIdx.y, G = K / 16;
+    const int g = blockIdx.x * blockDim.x + threadIdx.x; /* G is even: a pair never straddles the row's end */
+    float s = 0.0f;
+    if (g < G) {
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)r * xstride + 16 * g);
+        uint32_t h[8], l[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = src[i];
+            const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; j += 2) {
+                const __bf16 h0 = (__bf16)e[j], h1 = (__bf16)e[j + 1];
+                const __bf16 l0 = (__bf16)(e[j] - (float)h0), l1 = (__bf16)(e[j + 1] - (float)h1);
+                h[2 * i + j / 2] = __builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                l[2 * i + j / 2] = __builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+                s += (float)h0 + (float)l0;
+                s += (float)h1 + (float)l1;
+            }
+        }
+        u32x4* dh = reinterpret_cast<u32x4*>(xh + (size_t)r * K + 16 * g);
+        u32x4* dl = reinterpret_cast<u32x4*>(xl + (size_t)r * K + 16 * g);
+        dh[0] = u32x4{h[0], h[1], h[2], h[3]};
+        dh[1] = u32x4{h[4], h[5], h[6], h[7]};
+        dl[0] = u32x4{l[0], l[1], l[2], l[3]};
+        dl[1] = u32x4{l[4], l[5], l[6], l[7]};
+        bf16x3(s, s16, (size_t)n * G, (size_t)r * G + g);
+    }
+    const float o = __shfl_xor(s, 1, WAVE);
+    if (g < G && !(g & 1)) bf16x3(s + o, s32, (size_t)n * (G / 2), (size_t)r * (G / 2) + g / 2);
+}
+
+hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, uint16_t* const* sums,
+                             hipStream_t s) {
     if (n < 1 || K < 1) return hipErrorInvalidValue;
-    split_rows_kernel<<<dim3((K + 255) / 256, n), 256, 0, s>>>(x, n, K, xstride, xh, xl);
+    if (sums) {
+        if (K % 32 || xstride % 4 || (uintptr_t)x % 16) return hipErrorInvalidValue;
+        const int G = K / 16;
+        split_sums_kernel<<<dim3((G + 255) / 256, n), 256, 0, s>>>(x, n, K, xstride, xh, xl, sums[0], sums[1]);
+    } else {
+        split_rows_kernel<<<dim3((K + 255) / 256, n), 256, 0, s>>>(x, n, K, xstride, xh, xl);
+    }
     return hipGetLastError();
 }
 
@@ -235,6 +295,499 @@ __global__ __launch_bounds__(NT == 1 ? 1024 : 256) void skinny_kernel(skinny_arg
     }
 }
 
+/* ---- exact-integer quants ------------------------------------------------ */
+/*
+ * Widths a multiple of 256 take this path. A wave owns one tile of 32 weight rows x 32 token rows over one
+ * 256-column superblock (one Q4_K or Q6_K block, eight Q8_0 blocks), four units of 64 columns each: the
+ * work is a few microseconds of loads a wave, so it is spread as wide as it goes and every load of the
+ * wave's weights is issued at once. Within a unit every scale group (Q4_K 32 columns, Q6_K 16, Q8_0 32) keeps its own MFMA sum
+ * P over its columns, and the group's scale is applied to P in fp32:
+ *   Q8_0  bf16(q) exactly (signed):            acc += d P
+ *   Q4_K  bf16(128 + q), q in 0..15:           acc += d sc P  -  (dmin m + 128 d sc) S
+ *   Q6_K  bf16(128 + q6), q6 in 0..63:         acc += d sc P  -  160 d sc S
+ * where S is the group's sum of the activations. 128 + q is the byte q under the exponent byte of 2^7 (two
+ * v_perm_b32 for four weights). The S terms of eight groups go through the matrix cores too, as one
+ * 32x32x8 product of the groups' sums (bf16 hi + lo, split on the host side of the pass) by their
+ * coefficients, both as three bf16 pieces. S is the sum of the split activations hi + lo, so the offset
+ * 128 S cancels exactly what the 128 in the weights added.
+ *
+ * A unit's k order: lane half kq (lane / 32) of each 16-column MFMA supplies 8 columns, and both operands
+ * take them in the same order. Q4_K and Q8_0: the MFMAs of unit u cover columns 64 u + 16 kq + {0, 8} (the
+ * first group) and + 32 (the second); Q4_K's byte 32 u + j holds columns 64 u + j (low nibble) and
+ * 64 u + 32 + j (high). Q6_K unit u = (h, r0) = (u / 2, u % 2) covers the groups at columns
+ * 128 h + 32 r + 16 s, r in {r0, r0 + 2}, s in {0, 1}, of which lane half kq takes columns + 8 kq .. + 8 kq + 7:
+ * ql byte 64 h + 32 r0 + 16 s + j holds column 128 h + 32 r0 + 16 s + j (low nibble) and 128 h + 32 (r0 + 2)
+ * + 16 s + j (high), qh byte 32 h + 16 s + j its high bits (bits 2 r).
+ */
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t sx_u2 __attribute__((ext_vector_type(2)));
+
+/* four bytes (each below 128) as bf16 128 + byte */
+__device__ __forceinline__ sx_u2 sx_mag4(uint32_t v) {
+    return sx_u2{__builtin_amdgcn_perm(0x43434343u, v, 0x04010400u), __builtin_amdgcn_perm(0x43434343u, v, 0x04030402u)};
+}
+__device__ __forceinline__ bf16x8 sx_join(sx_u2 a, sx_u2 b) { return __builtin_bit_cast(bf16x8, u32x4{a.x, a.y, b.x, b.y}); }
+/* eight signed bytes as bf16, exactly */
+__device__ __forceinline__ bf16x8 sx_i8(uint32_t a, uint32_t b) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r[i] = (__bf16)(float)(int8_t)(a >> (8 * i));
+        r[4 + i] = (__bf16)(float)(int8_t)(b >> (8 * i));
+    }
+    return r;
+}
+
+/* One superblock of one 32-row tile: the lane's row's bytes for all four units. */
+template <int DT> struct sx_w;
+template <> struct sx_w<VITNA_DTYPE_Q4_K> { u32x4 q[4], h; };
+template <> struct sx_w<VITNA_DTYPE_Q6_K> { sx_u2 ql[4][2], qh[2][2]; u32x4 sc; uint32_t d; };
+template <> struct sx_w<VITNA_DTYPE_Q8_0> { u32x4 q[4][2], d; };
+
+/* a unit's activations for the lane's token: four 8-column operands, hi and lo, and (when the unit applies
+   S terms) the four group sums of the lane half */
+struct sx_a {
+    u32x4 h[4], l[4];
+    sx_u2 sp[3];
+};
+
+template <int DT>
+__device__ __forceinline__ void sx_load_w(const qmat& w, int row, int b, int kq, sx_w<DT>& o) {
+    if constexpr (DT == VITNA_DTYPE_Q4_K) {
+        const size_t blk = (size_t)row * w.nb + b;
+#pragma unroll
+        for (int u = 0; u < 4; u++) o.q[u] = WLOAD(reinterpret_cast<const u32x4*>(w.p[0] + blk * 128 + 32 * u + 16 * kq));
+        o.h = *reinterpret_cast<const u32x4*>(w.p[1] + blk * 16);
+    } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
+        const size_t blk = (size_t)row * w.nb + b;
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int s = 0; s < 2; s++)
+                o.ql[u][s] = WLOAD(reinterpret_cast<const sx_u2*>(w.p[0] + blk * 128 + 64 * (u >> 1) + 32 * (u & 1) + 16 * s + 8 * kq));
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int s = 0; s < 2; s++) o.qh[h][s] = *reinterpret_cast<const sx_u2*>(w.p[1] + blk * 64 + 32 * h + 16 * s + 8 * kq);
+        o.sc = *reinterpret_cast<const u32x4*>(w.p[2] + blk * 16);
+        o.d = *reinterpret_cast<const uint16_t*>(w.p[3] + blk * 2);
+    } else {
+        const size_t blk = (size_t)row * w.nb + 8 * b;
+#pragma unroll
+        for (int j = 0; j < 8; j++) o.q[j >> 1][j & 1] = WLOAD(reinterpret_cast<const u32x4*>(w.p[0] + (blk + j) * 32 + 16 * kq));
+        o.d = *reinterpret_cast<const u32x4*>(w.p[1] + blk * 2);
+    }
+}
+
+template <int DT> struct sx_unit_sums { static constexpr bool at(int U) { return DT == VITNA_DTYPE_Q4_K ? U == 3 : DT == VITNA_DTYPE_Q6_K ? (U & 1) : false; } };
+
+template <int DT, int U>
+__device__ __forceinline__ void sx_load_a(const skinny_args& a, int tok, int K, int b, int kq, sx_a& o) {
+    const uint16_t* xh = a.xh + (size_t)tok * K + 256 * b;
+    const uint16_t* xl = a.xl + (size_t)tok * K + 256 * b;
+    constexpr int base = DT == VITNA_DTYPE_Q6_K ? 128 * (U >> 1) + 32 * (U & 1) : 64 * U;
+    constexpr int step1 = DT == VITNA_DTYPE_Q6_K ? 16 : 8, step2 = DT == VITNA_DTYPE_Q6_K ? 64 : 32;
+    const int k0 = base + (DT == VITNA_DTYPE_Q6_K ? 8 : 16) * kq;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = k0 + (i & 1) * step1 + (i >> 1) * step2;
+        o.h[i] = *reinterpret_cast<const u32x4*>(xh + c);
+        o.l[i] = *reinterpret_cast<const u32x4*>(xl + c);
+    }
+    if constexpr (sx_unit_sums<DT>::at(U)) {
+        /* the sums' planes: Q4_K the 32-column groups, Q6_K the 16-column ones */
+        const size_t G = DT == VITNA_DTYPE_Q4_K ? K / 32 : K / 16, plane = (size_t)a.n * G;
+        const size_t off = (size_t)tok * G + (DT == VITNA_DTYPE_Q4_K ? 8 * b : 16 * b + 8 * (U >> 1)) + 4 * kq;
+        const uint16_t* sp = DT == VITNA_DTYPE_Q4_K ? a.s32 : a.s16;
+#pragma unroll
+        for (int i = 0; i < 3; i++) o.sp[i] = *reinterpret_cast<const sx_u2*>(sp + i * plane + off);
+    }}
+
+__device__ __forceinline__ void sx_scale(f32x16& acc, float d, const f32x16& P) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = fmaf(d, P[r], acc[r]);
+}
+#define SX_MMA(A, B, C) __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, A), B, C, 0, 0, 0)
+
+/* Q4_K scale and min of group g from the 12 scale bytes (header dwords 1..3) */
+template <int G>
+__device__ __forceinline__ void sx_q4k_sm(const u32x4& h, uint32_t& sc, uint32_t& mn) {
+    if constexpr (G < 4) {
+        sc = (h.y >> (8 * G)) & 63;
+        mn = (h.z >> (8 * G)) & 63;
+    } else {
+        constexpr int j = G - 4;
+        sc = ((h.w >> (8 * j)) & 15) | (((h.y >> (8 * j + 6)) & 3) << 4);
+        mn = ((h.w >> (8 * j + 4)) & 15) | (((h.z >> (8 * j + 6)) & 3) << 4);
+    }
+}
+
+/* the S terms of eight groups: the lane half's four sums times its four coefficients c, each as three bf16
+   pieces, the six products down to 2^-24 of the largest (the offset part of c S cancels against the MFMA sums
+   of 128 + q, so it is carried to fp32 accuracy) */
+__device__ __forceinline__ void sx_sterm(const sx_a& x, const float c[4], f32x16& acc) {
+    s16x4 cp[3];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const __bf16 p0 = (__bf16)c[i];
+        const float r0 = c[i] - (float)p0;
+        const __bf16 p1 = (__bf16)r0;
+        cp[0][i] = __builtin_bit_cast(short, p0);
+        cp[1][i] = __builtin_bit_cast(short, p1);
+        cp[2][i] = __builtin_bit_cast(short, (__bf16)(r0 - (float)p1));
+    }
+    const s16x4 s0 = __builtin_bit_cast(s16x4, x.sp[0]), s1 = __builtin_bit_cast(s16x4, x.sp[1]), s2 = __builtin_bit_cast(s16x4, x.sp[2]);
+    acc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(s2, cp[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(s1, cp[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(s0, cp[2], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(s1, cp[0], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(s0, cp[1], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(s0, cp[0], acc, 0, 0, 0);
+}
+
+/* Unit U: its groups' sums and scales into acc; cs carries the superblock's S coefficients (Q4_K) from the
+   units that make them to the unit that applies them. */
+template <int DT, int U>
+__device__ __forceinline__ void sx_compute(const sx_w<DT>& w, const sx_a& x, int kq, f32x16& acc, float cs[8]) {
+    const f32x16 Z = {};
+    if constexpr (DT == VITNA_DTYPE_Q4_K) {
+        constexpr uint32_t M = 0x0f0f0f0fu;
+        const u32x4 q = w.q[U];
+        const bf16x8 a0 = sx_join(sx_mag4(q.x & M), sx_mag4(q.y & M)), a1 = sx_join(sx_mag4(q.z & M), sx_mag4(q.w & M));
+        const bf16x8 b0 = sx_join(sx_mag4((q.x >> 4) & M), sx_mag4((q.y >> 4) & M));
+        const bf16x8 b1 = sx_join(sx_mag4((q.z >> 4) & M), sx_mag4((q.w >> 4) & M));
+        f32x16 P0 = SX_MMA(x.h[0], a0, Z), P1 = SX_MMA(x.h[2], b0, Z);
+        P0 = SX_MMA(x.h[1], a1, P0);
+        P1 = SX_MMA(x.h[3], b1, P1);
+        P0 = SX_MMA(x.l[0], a0, P0);
+        P1 = SX_MMA(x.l[2], b0, P1);
+        P0 = SX_MMA(x.l[1], a1, P0);
+        P1 = SX_MMA(x.l[3], b1, P1);
+        const float d = f16_bits_to_f32(w.h.x & 0xffffu), dmin = f16_bits_to_f32(w.h.x >> 16);
+        uint32_t sc0, mn0, sc1, mn1;
+        sx_q4k_sm<2 * U>(w.h, sc0, mn0);
+        sx_q4k_sm<2 * U + 1>(w.h, sc1, mn1);
+        const float d0 = d * (float)sc0, d1 = d * (float)sc1;
+        sx_scale(acc, d0, P0);
+        sx_scale(acc, d1, P1);
+        cs[2 * U] = -fmaf(128.0f, d0, dmin * (float)mn0);
+        cs[2 * U + 1] = -fmaf(128.0f, d1, dmin * (float)mn1);
+        if constexpr (U == 3) {
+            float c[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) c[j] = kq ? cs[4 + j] : cs[j];
+            sx_sterm(x, c, acc);
+        }
+    } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
+        constexpr int h = U >> 1, r0 = U & 1;
+        bf16x8 wq[4]; /* groups (r0, 0), (r0, 1), (r0 + 2, 0), (r0 + 2, 1) */
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int s = i & 1, hi = i >> 1, r = r0 + 2 * hi;
+            uint32_t v[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t ql = hi ? (w.ql[U][s][j] >> 4) : w.ql[U][s][j];
+                const uint32_t qh = w.qh[h][s][j];
+                const uint32_t top = r == 0 ? qh << 4 : r == 1 ? qh << 2 : r == 2 ? qh : qh >> 2;
+                v[j] = (ql & 0x0f0f0f0fu) | (top & 0x30303030u);
+            }
+            wq[i] = sx_join(sx_mag4(v[0]), sx_mag4(v[1]));
+        }
+        f32x16 P[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) P[i] = SX_MMA(x.h[i], wq[i], Z);
+#pragma unroll
+        for (int i = 0; i < 4; i++) P[i] = SX_MMA(x.l[i], wq[i], P[i]);
+        const float d = f16_bits_to_f32(w.d);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int g = 8 * h + 2 * (r0 + 2 * (i >> 1)) + (i & 1); /* the group's scale index */
+            sx_scale(acc, d * (float)(int8_t)(w.sc[g >> 2] >> (8 * (g & 3))), P[i]);
+        }
+        if constexpr (r0 == 1) {
+            /* the S terms of groups 8 h .. 8 h + 7: lane half kq supplies 8 h + 4 kq .. + 3 */
+            const uint32_t scw = kq ? w.sc[2 * h + 1] : w.sc[2 * h];
+            const float m = -160.0f * d;
+            float c[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) c[j] = m * (float)(int8_t)(scw >> (8 * j));
+            sx_sterm(x, c, acc);
+        }
+    } else {
+        const bf16x8 a0 = sx_i8(w.q[U][0].x, w.q[U][0].y), a1 = sx_i8(w.q[U][0].z, w.q[U][0].w);
+        const bf16x8 b0 = sx_i8(w.q[U][1].x, w.q[U][1].y), b1 = sx_i8(w.q[U][1].z, w.q[U][1].w);
+        f32x16 P0 = SX_MMA(x.h[0], a0, Z), P1 = SX_MMA(x.h[2], b0, Z);
+        P0 = SX_MMA(x.h[1], a1, P0);
+        P1 = SX_MMA(x.h[3], b1, P1);
+        P0 = SX_MMA(x.l[0], a0, P0);
+        P1 = SX_MMA(x.l[2], b0, P1);
+        P0 = SX_MMA(x.l[1], a1, P0);
+        P1 = SX_MMA(x.l[3], b1, P1);
+        const uint32_t dw = w.d[U];
+        sx_scale(acc, f16_bits_to_f32(dw & 0xffffu), P0);
+        sx_scale(acc, f16_bits_to_f32(dw >> 16), P1);
+    }
+}
+
+/* Superblock b of the lane's weight row: every weight load issued first, the activations two units ahead. */
+template <int DT>
+__device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& w, int row, int tok, int b, int kq, f32x16& acc) {
+    const int K = w.cols;
+    float cs[8];
+    sx_w<DT> W;
+    sx_a x0, x1;
+    sx_load_w<DT>(w, row, b, kq, W);
+    sx_load_a<DT, 0>(a, tok, K, b, kq, x0);
+    sx_load_a<DT, 1>(a, tok, K, b, kq, x1);
+    __builtin_amdgcn_sched_barrier(0);
+    sx_compute<DT, 0>(W, x0, kq, acc, cs);
+    sx_load_a<DT, 2>(a, tok, K, b, kq, x0);
+    __builtin_amdgcn_sched_barrier(0);
+    sx_compute<DT, 1>(W, x1, kq, acc, cs);
+    sx_load_a<DT, 3>(a, tok, K, b, kq, x1);
+    __builtin_amdgcn_sched_barrier(0);
+    sx_compute<DT, 2>(W, x0, kq, acc, cs);
+    sx_compute<DT, 3>(W, x1, kq, acc, cs);
+}
+
+/*
+ * Block (blockIdx.x = (32-row tile of matrix i, split), blockIdx.y = token tile): KS waves, wave v on superblock
+ * 8 split + v. The waves' sums are added through LDS in wave order. A matrix wider than 8 superblocks takes
+ * several splits: each block stores its tile's sum in part[], and the block that finishes a tile last (its
+ * counter in cnt[]) adds the splits' sums in split order, writes the result and clears the counter, so the
+ * result does not depend on which block finishes last.
+ */
+__global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
+    extern __shared__ float red[]; /* [KS][16][64] */
+    __shared__ int last;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, KS = blockDim.x >> 6;
+    const int l32 = lane & 31, kq = lane >> 5;
+    int bx = blockIdx.x, mi = 0, tile0 = 0;
+    for (; mi < a.nm - 1; mi++) {
+        const int nb = (a.w[mi].rows + 31) / 32 * a.splits[mi];
+        if (bx < nb) break;
+        bx -= nb;
+        tile0 += (a.w[mi].rows + 31) / 32;
+    }
+    const qmat& w = a.w[mi];
+    const int splits = a.splits[mi], sp = bx % splits, tile = bx / splits;
+    const int row0 = 32 * tile, tok0 = blockIdx.y * SK_TOK;
+    const int row = min(row0 + l32, w.rows - 1);
+    const int tok = min(tok0 + l32, a.n - 1); /* rows past n compute on row n - 1 and are never written */
+    const int b = 8 * sp + wv;
+    f32x16 acc = {};
+    if (b < w.cols / 256) {
+        if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K>(a, w, row, tok, b, kq, acc);
+        else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K>(a, w, row, tok, b, kq, acc);
+        else sx_superblock<VITNA_DTYPE_Q8_0>(a, w, row, tok, b, kq, acc);
+    }
+
+    /* accumulator r of a lane: token 8 (r / 4) + 4 (lane / 32) + r % 4 of the tile, weight row lane % 32 */
+    float* y = a.y[mi];
+    auto put = [&](int r, float v) {
+        const int n = row0 + l32;
+        const int tk = tok0 + 8 * (r >> 2) + 4 * kq + (r & 3);
+        if (n < w.rows && tk < a.n) {
+            float* o = y + (size_t)tk * w.rows + n;
+            *o = a.add ? *o + v : v;
+        }
+    };
+    if (KS > 1) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) red[(wv * 16 + r) * 64 + lane] = acc[r];
+        __syncthreads();
+    }
+    if (splits == 1) {
+        if (KS == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) put(r, acc[r]);
+            return;
+        }
+        for (int r = wv; r < 16; r += KS) {
+            float v = 0.0f;
+            for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
+            put(r, v);
+        }
+        return;
+    }
+    /* several splits: this block's sum of the tile into part[], then the last block of the tile adds them */
+    const size_t slot = (size_t)blockIdx.y * a.tiles + tile0 + tile; /* the tile's counter */
+    float* part = a.part + slot * a.split_max * 1024;
+    /* The sums are stored as agent-scope atomics, which write through this XCD's L2, and the workgroup barrier
+       waits for their completion before the counter moves; the last block reads them back the same way. A
+       device-wide fence would instead write back the whole L2. */
+    for (int r = wv; r < 16; r += KS) {
+        float v = 0.0f;
+        for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
+        __hip_atomic_store(part + (size_t)sp * 1024 + r * 64 + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    __syncthreads();
+    if (!last) return;
+    for (int r = wv; r < 16; r += KS) {
+        float v = 0.0f;
+        for (int u = 0; u < splits; u++) v += __hip_atomic_load(part + (size_t)u * 1024 + r * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        put(r, v);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* ---- wide matrices (the LM head): activations staged in LDS ---------------- */
+
+/* Column (within the superblock) of operand i of unit U for lane half kq: the order sx_load_a reads. */
+template <int DT>
+__device__ __forceinline__ int sx_col(int U, int i, int kq) {
+    if constexpr (DT == VITNA_DTYPE_Q6_K) return 128 * (U >> 1) + 32 * (U & 1) + 8 * kq + (i & 1) * 16 + (i >> 1) * 64;
+    else return 64 * U + 16 * kq + (i & 1) * 8 + (i >> 1) * 32;
+}
+
+/* LDS image of one superblock's operands for 32 tokens: piece p = ((U * 4 + i) * 2 + hl) * 64 + lane, 16 bytes
+   each, so a wave's ds_read_b128 of one operand reads 1 KB in lane order. */
+#define SXW_PIECES 2048
+
+typedef __attribute__((address_space(3))) void* sx_lds_void;
+typedef __attribute__((address_space(1))) void* sx_glb_void;
+
+/* Thread t's pieces of superblock b (NW waves share the image's 2048), from the split activations straight into
+   the image (global-to-LDS loads: lane l of a wave lands at the wave's base + 16 l, which is piece order).
+   Counted by vmcnt. */
+template <int DT, int NW>
+__device__ __forceinline__ void sxw_fetch(const skinny_args& a, int K, int tok0, int b, u32x4* img) {
+    const int wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < SXW_PIECES / (64 * NW); j++) {
+        const int p = threadIdx.x + 64 * NW * j;
+        const int lane = p & 63, rest = p >> 6, hl = rest & 1, i = (rest >> 1) & 3, U = rest >> 3;
+        const int tok = min(tok0 + (lane & 31), a.n - 1);
+        const uint16_t* src = (hl ? a.xl : a.xh) + (size_t)tok * K + 256 * b + sx_col<DT>(U, i, lane >> 5);
+        __builtin_amdgcn_global_load_lds((sx_glb_void)src, (sx_lds_void)(img + wv * 64 + 64 * NW * j), 16, 0, 0);
+    }
+}
+
+template <int DT, int U>
+__device__ __forceinline__ void sxw_read(const u32x4* img, const skinny_args& a, int tok, int K, int b, int kq, sx_a& o) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        o.h[i] = img[((U * 4 + i) * 2 + 0) * 64 + lane];
+        o.l[i] = img[((U * 4 + i) * 2 + 1) * 64 + lane];
+    }
+    if constexpr (sx_unit_sums<DT>::at(U)) {
+        const size_t G = DT == VITNA_DTYPE_Q4_K ? K / 32 : K / 16, plane = (size_t)a.n * G;
+        const size_t off = (size_t)tok * G + (DT == VITNA_DTYPE_Q4_K ? 8 * b : 16 * b + 8 * (U >> 1)) + 4 * kq;
+        const uint16_t* sp = DT == VITNA_DTYPE_Q4_K ? a.s32 : a.s16;
+#pragma unroll
+        for (int i = 0; i < 3; i++) o.sp[i] = *reinterpret_cast<const sx_u2*>(sp + i * plane + off);
+    }
+}
+
+/* NW waves, wave v on tile NW blockIdx.x + v of the matrix, every superblock in turn: the block stages
+   superblock b + 1's activations and each wave loads its weights for b + 1 while b computes. */
+template <int DT, int NW>
+__device__ __forceinline__ void sxw_body(const skinny_args& a, const qmat& w, int tile, int tok0, u32x4* img, f32x16& acc) {
+    const int lane = threadIdx.x & 63, l32 = lane & 31, kq = lane >> 5;
+    const int K = w.cols, S = K / 256;
+    const int row = min(32 * tile + l32, w.rows - 1);
+    const int tok = min(tok0 + l32, a.n - 1);
+    sx_w<DT> W0, W1;
+    float cs[8];
+    sxw_fetch<DT, NW>(a, K, tok0, 0, img);
+    sx_load_w<DT>(w, row, 0, kq, W0);
+    auto step = [&](int b, const sx_w<DT>& W, sx_w<DT>& Wn) {
+        /* image b landed (each wave waits for its own loads, the barrier for the others'); image b + 1's
+           buffer was last read in step b - 1, which every wave has left */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const u32x4* cur = img + (b & 1) * SXW_PIECES;
+        if (b + 1 < S) {
+            sxw_fetch<DT, NW>(a, K, tok0, b + 1, img + ((b + 1) & 1) * SXW_PIECES);
+            sx_load_w<DT>(w, row, b + 1, kq, Wn);
+        }
+        /* one unit's operands at a time (the barriers keep the scheduler from hoisting every unit's reads) */
+        sx_a x;
+        sxw_read<DT, 0>(cur, a, tok, K, b, kq, x);
+        sx_compute<DT, 0>(W, x, kq, acc, cs);
+        __builtin_amdgcn_sched_barrier(0);
+        sxw_read<DT, 1>(cur, a, tok, K, b, kq, x);
+        sx_compute<DT, 1>(W, x, kq, acc, cs);
+        __builtin_amdgcn_sched_barrier(0);
+        sxw_read<DT, 2>(cur, a, tok, K, b, kq, x);
+        sx_compute<DT, 2>(W, x, kq, acc, cs);
+        __builtin_amdgcn_sched_barrier(0);
+        sxw_read<DT, 3>(cur, a, tok, K, b, kq, x);
+        sx_compute<DT, 3>(W, x, kq, acc, cs);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int b = 0; b < S; b += 2) {
+        step(b, W0, W1);
+        if (b + 1 < S) step(b + 1, W1, W0);
+    }
+}
+
+/* Every matrix of the launch has dtype DT. */
+template <int DT, int NW>
+__global__ __launch_bounds__(64 * NW) void skinny_wide_kernel(skinny_args a) {
+    __shared__ u32x4 img[2 * SXW_PIECES]; /* 64 KB */
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l32 = lane & 31, kq = lane >> 5;
+    int bx = blockIdx.x, mi = 0;
+    for (; mi < a.nm - 1; mi++) {
+        const int nb = ((a.w[mi].rows + 31) / 32 + NW - 1) / NW;
+        if (bx < nb) break;
+        bx -= nb;
+    }
+    const qmat& w = a.w[mi];
+    const int tile = NW * bx + wv, tok0 = blockIdx.y * SK_TOK;
+    f32x16 acc = {};
+    sxw_body<DT, NW>(a, w, tile, tok0, img, acc);
+    float* y = a.y[mi];
+    const int n = 32 * tile + l32;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int tk = tok0 + 8 * (r >> 2) + 4 * kq + (r & 3);
+        if (n < w.rows && tk < a.n) {
+            float* o = y + (size_t)tk * w.rows + n;
+            *o = a.add ? *o + acc[r] : acc[r];
+        }
+    }
+}
+
+static hipError_t launch_skinny_exact(const skinny_args& a0, hipStream_t s) {
+    skinny_args a = a0;
+    const int mt = (a.n + SK_TOK - 1) / SK_TOK;
+    int blocks = 0, ks = 1, tiles = 0, split_max = 1;
+    for (int i = 0; i < a.nm; i++) {
+        const int S = a.w[i].cols / 256;
+        a.splits[i] = (S + 7) / 8;
+        ks = std::max(ks, std::min(S, 8));
+        split_max = std::max(split_max, a.splits[i]);
+        tiles += (a.w[i].rows + 31) / 32;
+        blocks += (a.w[i].rows + 31) / 32 * a.splits[i];
+    }
+    a.tiles = tiles;
+    a.split_max = split_max;
+    bool one_dt = true;
+    for (int i = 1; i < a.nm; i++) one_dt &= a.w[i].dtype == a.w[0].dtype;
+    if (tiles >= 1024 && one_dt) {
+        /* wide: NW tiles a block over the whole width, the activations shared through LDS (Q8_0 takes four
+           waves a block: its two superblocks of weights in flight need more registers than eight allow) */
+        const int dt = a.w[0].dtype, NW = dt == VITNA_DTYPE_Q8_0 ? 4 : 8;
+        int wb = 0;
+        for (int i = 0; i < a.nm; i++) wb += ((a.w[i].rows + 31) / 32 + NW - 1) / NW;
+        const dim3 grid(wb, mt);
+        if (dt == VITNA_DTYPE_Q4_K) skinny_wide_kernel<VITNA_DTYPE_Q4_K, 8><<<grid, 512, 0, s>>>(a);
+        else if (dt == VITNA_DTYPE_Q6_K) skinny_wide_kernel<VITNA_DTYPE_Q6_K, 8><<<grid, 512, 0, s>>>(a);
+        else skinny_wide_kernel<VITNA_DTYPE_Q8_0, 4><<<grid, 256, 0, s>>>(a);
+        return hipGetLastError();
+    }
+    if (split_max > 1 && (!a.part || !a.cnt || (size_t)mt * tiles > a.cnt_cap || (size_t)mt * tiles * split_max * 1024 > a.part_cap))
+        return hipErrorInvalidValue;
+    skinny_exact_kernel<<<dim3(blocks, mt), 64 * ks, (size_t)ks * 16 * 64 * sizeof(float), s>>>(a);
+    return hipGetLastError();
+}
+
 hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
     if (a.nm < 1 || a.nm > 3 || a.n < 1 || !a.xh || !a.xl) return hipErrorInvalidValue;
     for (int i = 0; i < a.nm; i++) {
@@ -245,6 +798,12 @@ hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
     int cus = 0, dev = 0;
     hipGetDevice(&dev);
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    bool exact = a.s16 && a.s32;
+    for (int i = 0; i < a.nm; i++) exact &= a.w[i].cols % 256 == 0;
+#ifndef SK_EXACT
+#define SK_EXACT 1
+#endif
+    if (exact && SK_EXACT) return launch_skinny_exact(a, s);
     const int want = 8 * cus; /* two waves a SIMD */
     const int mt = (a.n + SK_TOK - 1) / SK_TOK;
     const int S = a.w[0].cols / 32;

@@ -173,16 +173,29 @@ hipError_t launch_gemv_multi(const gemv_multi_args& a, hipStream_t s);
 
 /* Multi-row projections on the matrix cores (kernels_skinny.hip): y_i[t][r]
    (+)= W_i[r] . x[t] for t < n, to fp32 accuracy; x comes split into bf16
-   hi and lo parts ([n][cols] each, launch_split_rows). */
+   hi and lo parts ([n][cols] each, launch_split_rows). With the group sums
+   (s16, s32: each row's sums of hi + lo over 16 and 32 consecutive columns,
+   as three bf16 pieces, planes [3][n][cols / 16] and [3][n][cols / 32]) and
+   widths a multiple of 256 the quants enter the matrix cores as exact
+   integers; otherwise each weight is widened and split. */
 struct skinny_args {
     qmat w[3];
     float* y[3];
     int nm;
     const uint16_t* xh;
     const uint16_t* xl;
+    const uint16_t *s16, *s32;
     int n, add;
+    /* matrices wider than 2048 columns split across blocks: part (part_cap floats) holds each split's sum of a
+       tile and cnt (cnt_cap ints, zero before the first call, left zero by every call) counts finished splits */
+    float* part;
+    int* cnt;
+    size_t part_cap, cnt_cap;
+    int splits[3], tiles, split_max; /* set by launch_skinny */
 };
-hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, hipStream_t s);
+/* sums: null, or [2] = s16, s32 as above */
+hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, uint16_t* const* sums,
+                             hipStream_t s);
 hipError_t launch_skinny(const skinny_args& a, hipStream_t s);
 
 /* The per-expert lists of (row, slot) pairs of n rows' routing: count[E],
