@@ -154,6 +154,14 @@ bool vitna_hip_residual(struct vitna_cuda_model* g, size_t row, float* host, boo
 bool vitna_hip_routing(struct vitna_cuda_model* g, size_t row, float* logits, int32_t* chosen, int32_t* ids, float* weights, char* err,
                        size_t err_len);
 
+/** One projection of a pass of n rows (1 <= n <= the rows maximum) as the
+    rows step runs it: y[t] = W x[t] for W = layer's q, k, v, o (which = 0..3)
+    or the LM head (which = 4, layer ignored); x is n x W's columns, y n x W's
+    rows, both on the host. Synchronous. A test hook: the reference has no
+    counterpart (its multi-row kernels are only reachable through a step). */
+bool vitna_hip_rows_project(struct vitna_cuda_model* g, size_t layer, int which, const float* x, size_t n, float* y, char* err,
+                            size_t err_len);
+
 /** Keys and values of positions pos0 .. pos0 + n - 1 of one layer of one
     sequence, n x (n_kv_heads * head_dim) each, to (write) or from the device. */
 bool vitna_hip_kv(struct vitna_cuda_model* g, size_t seq, size_t layer, size_t pos0, size_t n, float* k, float* v, bool write, char* err,

@@ -179,3 +179,42 @@ def test_rows_wide_projections(dt):
     finally:
         dev.close()
         model.free()
+
+
+def _matrix(model, layer, which):
+    m = model.m
+    return [m.layers[layer].q, m.layers[layer].k, m.layers[layer].v, m.layers[layer].o, m.lm_head][which]
+
+
+@pytest.mark.parametrize("name", ["q8", "q4km", "wide_k", "wide_q8"])
+def test_rows_projections_isolated(name):
+    """Each projection of a rows step alone (vitna_hip_rows_project) against the checker's widening of the same
+    matrix times the same rows in float64: q, k, v, o of layer 0 and the head, for 5, 32 and 40 rows (one token
+    tile, a full one, two). Independent of how well-conditioned a model's logits are, so the bound is tight:
+    within 2e-5 of max |ref| (the activations' bf16 hi + lo split leaves about 2^-17 a product)."""
+    say("rows projections", name)
+    if name.startswith("wide"):
+        spec = dict(WIDE, seqs=1)
+        if name == "wide_q8":
+            spec.update(dt_q=va.Q8_0, dt_k=va.Q8_0, dt_v=va.Q8_0, dt_o=va.Q8_0, dt_head=va.Q8_0)
+    else:
+        spec = dict(SMALL[name])
+    model = va.Model(va.shape(**spec), 5150)
+    dev = va.Device(model)
+    try:
+        rng = np.random.RandomState(7)
+        worst = 0.0
+        for which in range(5):
+            mat = _matrix(model, 0, which)
+            W = oracle.widen(mat.bytes(), mat.dtype, mat.rows * mat.cols).reshape(mat.rows, mat.cols).astype(np.float64)
+            for n in (5, 32, 40):
+                x = rng.standard_normal((n, mat.cols)).astype(np.float32)
+                y = dev.rows_project(0, which, x)
+                ref = x.astype(np.float64) @ W.T
+                r = float(np.max(np.abs(y - ref)) / np.max(np.abs(ref)))
+                worst = max(worst, r)
+                assert r <= 2e-5, (which, n, r)
+        say("  worst rel err", worst)
+    finally:
+        dev.close()
+        model.free()

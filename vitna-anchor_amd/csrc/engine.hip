@@ -60,7 +60,7 @@ struct vitna_cuda_model {
     hipGraph_t step_graph_src; /* kept until free: graph tools may refer to its nodes */
     int *grp_count, *grp_pairs; /* expert grouping of a pass of rows: [E], [E][ROWS_MAX] */
     uint16_t *sk_xh, *sk_xl;    /* a pass's activations split into bf16 hi and lo, [ROWS_MAX][widest row] */
-    uint16_t* sk_sum[2];        /* their sums over 16 and 32 columns, three bf16 pieces: [3][ROWS_MAX][widest / 16 or / 32] */
+    uint32_t* sk_img[4];        /* or their operand images (orders A and B) and 32- and 16-column sums */
     float* sk_part;             /* split sums of the multi-row projections wider than 2048 columns */
     int* sk_cnt;                /* their per-tile counters, zero between calls */
     size_t sk_part_cap, sk_cnt_cap;
@@ -422,8 +422,11 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
          dalloc(g, &g->ypart, R * K * H * 4, "scratch", err, err_len) &&
          dalloc(g, &g->sk_xh, R * std::max<size_t>(H, (size_t)c->n_heads * c->head_dim) * 2, "scratch", err, err_len) &&
          dalloc(g, &g->sk_xl, R * std::max<size_t>(H, (size_t)c->n_heads * c->head_dim) * 2, "scratch", err, err_len) &&
-         dalloc(g, &g->sk_sum[0], 3 * R * std::max<size_t>(H, qd) / 16 * 2, "scratch", err, err_len) &&
-         dalloc(g, &g->sk_sum[1], 3 * R * std::max<size_t>(H, qd) / 32 * 2, "scratch", err, err_len) &&
+         dalloc(g, &g->sk_img[0], R * std::max<size_t>(H, qd) * 4, "scratch", err, err_len) &&
+         dalloc(g, &g->sk_img[1], R * std::max<size_t>(H, qd) * 4, "scratch", err, err_len) &&
+         /* a row's window of eight groups: three pieces of 8 bf16 */
+         dalloc(g, &g->sk_img[2], R * std::max<size_t>(H, qd) / 256 * 48, "scratch", err, err_len) &&
+         dalloc(g, &g->sk_img[3], R * std::max<size_t>(H, qd) / 128 * 48, "scratch", err, err_len) &&
          dalloc(g, &g->gm_xs, R * 2 * H * 2, "scratch", err, err_len) &&
          dalloc(g, &g->gm_as, R * K * 2 * c->intermediate * 2, "scratch", err, err_len) &&
          dalloc(g, &g->gm_xsum, R * (H / 16) * 4, "scratch", err, err_len) &&
@@ -873,6 +876,30 @@ extern "C" bool vitna_hip_residual(struct vitna_cuda_model* g, size_t row, float
     return true;
 }
 
+static hipError_t enqueue_multi(vitna_cuda_model* g, const gemv_multi_args& m);
+
+extern "C" bool vitna_hip_rows_project(struct vitna_cuda_model* g, size_t layer, int which, const float* x, size_t n, float* y,
+                                       char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no model");
+    if (!g->attention) return fail(err, err_len, "the model has no attention projections");
+    if (n < 1 || n > ROWS_MAX) return fail(err, err_len, "%zu rows: 1 .. %d", n, ROWS_MAX);
+    if (which < 0 || which > 4 || (which < 4 && layer >= (size_t)g->NL)) return fail(err, err_len, "no such projection");
+    const qmat w = which == 0 ? g->L[layer].q : which == 1 ? g->L[layer].k : which == 2 ? g->L[layer].v : which == 3 ? g->L[layer].o : g->head;
+    /* the input where the step keeps it (normed rows, or the attention output for o), the output in scratch of
+       at least n x rows floats */
+    float* dx = which == 3 ? g->att : g->xn;
+    float* dy = which == 0 ? g->q : which == 1 ? g->k : which == 2 ? g->v : which == 3 ? g->ypart : g->vocab;
+    HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
+    HIP_TRY(hipMemcpy(dx, x, n * w.cols * 4, hipMemcpyHostToDevice), "copying the rows");
+    gemv_multi_args m;
+    memset(&m, 0, sizeof(m));
+    m.w[0] = w; m.y[0] = dy; m.nm = 1; m.x = dx; m.n = (int)n; m.xstride = w.cols;
+    HIP_TRY(enqueue_multi(g, m), "the projection");
+    HIP_TRY(hipStreamSynchronize(g->stream), "the projection");
+    HIP_TRY(hipMemcpy(y, dy, n * w.rows * 4, hipMemcpyDeviceToHost), "copying the result");
+    return true;
+}
+
 extern "C" bool vitna_hip_routing(struct vitna_cuda_model* g, size_t row, float* logits, int32_t* chosen, int32_t* ids, float* weights,
                                   char* err, size_t err_len) {
     if (!g) return fail(err, err_len, "no model");
@@ -1246,13 +1273,13 @@ static hipError_t enqueue_multi(vitna_cuda_model* g, const gemv_multi_args& m) {
     const int K = m.w[0].cols;
     /* group sums for the exact-integer kernel when the width allows it */
     const bool sums = K % 256 == 0 && m.xstride % 4 == 0 && (uintptr_t)m.x % 16 == 0;
-    hipError_t e = launch_split_rows(m.x, m.n, K, m.xstride, g->sk_xh, g->sk_xl, sums ? g->sk_sum : nullptr, g->stream);
+    hipError_t e = launch_split_rows(m.x, m.n, K, m.xstride, g->sk_xh, g->sk_xl, sums ? g->sk_img : nullptr, g->stream);
     if (e != hipSuccess) return e;
     skinny_args a;
     memset(&a, 0, sizeof(a));
     for (int i = 0; i < m.nm; i++) { a.w[i] = m.w[i]; a.y[i] = m.y[i]; }
     a.nm = m.nm; a.xh = g->sk_xh; a.xl = g->sk_xl; a.n = m.n; a.add = m.add;
-    if (sums) { a.s16 = g->sk_sum[0]; a.s32 = g->sk_sum[1]; }
+    if (sums) { a.img[0] = g->sk_img[0]; a.img[1] = g->sk_img[1]; a.s32 = g->sk_img[2]; a.s16 = g->sk_img[3]; }
     a.part = g->sk_part; a.cnt = g->sk_cnt; a.part_cap = g->sk_part_cap; a.cnt_cap = g->sk_cnt_cap;
     return launch_skinny(a, g->stream);
 }

@@ -50,61 +50,82 @@ __global__ void split_rows_kernel(const float* __restrict__ x, int n, int K, int
 __device__ __forceinline__ uint16_t bf16_bits(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
 
 /* S as three bf16 pieces: S = p0 + p1 + p2 to about 2^-24 relative */
-__device__ __forceinline__ void bf16x3(float S, uint16_t* d, size_t plane, size_t i) {
+__device__ __forceinline__ void bf16x3(float S, uint16_t* d, size_t stride) {
     const __bf16 p0 = (__bf16)S;
     const float r0 = S - (float)p0;
     const __bf16 p1 = (__bf16)r0;
-    const __bf16 p2 = (__bf16)(r0 - (float)p1);
-    d[i] = __builtin_bit_cast(uint16_t, p0);
-    d[plane + i] = __builtin_bit_cast(uint16_t, p1);
-    d[2 * plane + i] = __builtin_bit_cast(uint16_t, p2);
+    d[0] = __builtin_bit_cast(uint16_t, p0);
+    d[stride] = __builtin_bit_cast(uint16_t, p1);
+    d[2 * stride] = __builtin_bit_cast(uint16_t, (__bf16)(r0 - (float)p1));
 }
 
-/* The split plus each row's group sums: thread i of row r takes columns 16 i .. 16 i + 15, sums the split
-   values hi + lo (what the matrix cores see: each hi + lo is exact in fp32) in column order, and adds its
-   pair's sum for the 32-column group (the even thread's sum first). The sums go out as three bf16 pieces,
-   planes of n x K / 16 (s16) and n x K / 32 (s32). */
-__global__ void split_sums_kernel(const float* __restrict__ x, int n, int K, int xstride, uint16_t* __restrict__ xh,
-                                  uint16_t* __restrict__ xl, uint16_t* __restrict__ s16, uint16_t* __restrict__ s32) {
-    const int r = blockIdx.y, G = K / 16;
-    const int g = blockIdx.x * blockDim.x + threadIdx.x; /* G is even: a pair never straddles the row's end */
-    float s = 0.0f;
-    if (g < G) {
-        const float4* src = reinterpret_cast<const float4*>(x + (size_t)r * xstride + 16 * g);
-        uint32_t h[8], l[8];
+/*
+ * Operand images for the exact-integer kernels. For each token tile tt (32 rows) and 256-column superblock b,
+ * one image of 2048 pieces of 16 bytes: piece ((U * 4 + i) * 2 + hl) * 64 + lane holds the 8 columns of MFMA
+ * operand i of unit U for lane half kq = lane / 32 of token 32 tt + lane % 32, bf16 hi (hl 0) or lo (1), so a
+ * wave reads each operand as 1 KB in lane order. Two column orders: A (Q4_K, Q8_0) puts operand i of unit U
+ * at 64 U + 16 kq + 8 (i % 2) + 32 (i / 2), B (Q6_K) at 128 (U / 2) + 32 (U % 2) + 8 kq + 16 (i % 2)
+ * + 64 (i / 2). Rows past n repeat row n - 1.
+ * Group sums of the split values (hi + lo, in column order), as three bf16 pieces, in the lane order of the
+ * S-term operand: per window of eight groups, piece p, lane: u32x2 of groups 4 kq .. 4 kq + 3. s32 has a
+ * window of 32-column groups a superblock, s16 two windows of 16-column groups.
+ */
+__global__ void split_image_kernel(const float* __restrict__ x, int n, int K, int xstride, u32x4* __restrict__ imga,
+                                   u32x4* __restrict__ imgb, uint16_t* __restrict__ s32, uint16_t* __restrict__ s16) {
+    const int b = blockIdx.x, tt = blockIdx.y, S = K / 256;
+    const size_t base = ((size_t)tt * S + b) * 2048;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 v = src[i];
-            const float e[4] = {v.x, v.y, v.z, v.w};
+    for (int j = 0; j < 4; j++) {
+        const int item = threadIdx.x + 256 * j, l = item >> 5, c8 = item & 31, c = 8 * c8;
+        const int tok = min(32 * tt + l, n - 1);
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)tok * xstride + 256 * b + c);
+        const float4 v0 = src[0], v1 = src[1];
+        const float e[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        uint32_t h[4], lo[4];
+        float sum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; j += 2) {
-                const __bf16 h0 = (__bf16)e[j], h1 = (__bf16)e[j + 1];
-                const __bf16 l0 = (__bf16)(e[j] - (float)h0), l1 = (__bf16)(e[j + 1] - (float)h1);
-                h[2 * i + j / 2] = __builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-                l[2 * i + j / 2] = __builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-                s += (float)h0 + (float)l0;
-                s += (float)h1 + (float)l1;
-            }
+        for (int k = 0; k < 4; k++) {
+            const __bf16 h0 = (__bf16)e[2 * k], h1 = (__bf16)e[2 * k + 1];
+            const __bf16 l0 = (__bf16)(e[2 * k] - (float)h0), l1 = (__bf16)(e[2 * k + 1] - (float)h1);
+            h[k] = __builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+            lo[k] = __builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            sum += (float)h0 + (float)l0;
+            sum += (float)h1 + (float)l1;
         }
-        u32x4* dh = reinterpret_cast<u32x4*>(xh + (size_t)r * K + 16 * g);
-        u32x4* dl = reinterpret_cast<u32x4*>(xl + (size_t)r * K + 16 * g);
-        dh[0] = u32x4{h[0], h[1], h[2], h[3]};
-        dh[1] = u32x4{h[4], h[5], h[6], h[7]};
-        dl[0] = u32x4{l[0], l[1], l[2], l[3]};
-        dl[1] = u32x4{l[4], l[5], l[6], l[7]};
-        bf16x3(s, s16, (size_t)n * G, (size_t)r * G + g);
+        const u32x4 vh = {h[0], h[1], h[2], h[3]}, vl = {lo[0], lo[1], lo[2], lo[3]};
+        {
+            const int U = c >> 6, r = c & 63, i = ((r >> 5) << 1) | ((r >> 3) & 1), kq = (r >> 4) & 1;
+            const size_t q = base + (size_t)((U * 4 + i) * 2) * 64 + l + 32 * kq;
+            imga[q] = vh;
+            imga[q + 64] = vl;
+        }
+        {
+            const int r = c & 127, U = 2 * (c >> 7) + ((r >> 5) & 1), i = ((r >> 4) & 1) + 2 * (r >> 6), kq = (r >> 3) & 1;
+            const size_t q = base + (size_t)((U * 4 + i) * 2) * 64 + l + 32 * kq;
+            imgb[q] = vh;
+            imgb[q + 64] = vl;
+        }
+        /* the 16- and 32-column sums (the pair's, then the quad's: lanes of consecutive c8, one token) */
+        const float t16 = sum + __shfl_xor(sum, 1, WAVE);
+        const float t32 = t16 + __shfl_xor(t16, 2, WAVE);
+        if (!(c8 & 1)) {
+            const int w = 2 * b + (c8 >> 4), gi = (c8 >> 1) & 7; /* window, group in it */
+            bf16x3(t16, s16 + (((size_t)tt * (K / 128) + w) * 3 * 64 + l + 32 * (gi >> 2)) * 4 + (gi & 3), 256);
+        }
+        if (!(c8 & 3)) {
+            const int gi = c8 >> 2;
+            bf16x3(t32, s32 + (((size_t)tt * S + b) * 3 * 64 + l + 32 * (gi >> 2)) * 4 + (gi & 3), 256);
+        }
     }
-    const float o = __shfl_xor(s, 1, WAVE);
-    if (g < G && !(g & 1)) bf16x3(s + o, s32, (size_t)n * (G / 2), (size_t)r * (G / 2) + g / 2);
 }
 
-hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, uint16_t* const* sums,
+hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, uint32_t* const* img,
                              hipStream_t s) {
     if (n < 1 || K < 1) return hipErrorInvalidValue;
-    if (sums) {
-        if (K % 32 || xstride % 4 || (uintptr_t)x % 16) return hipErrorInvalidValue;
-        const int G = K / 16;
-        split_sums_kernel<<<dim3((G + 255) / 256, n), 256, 0, s>>>(x, n, K, xstride, xh, xl, sums[0], sums[1]);
+    if (img) {
+        if (K % 256 || xstride % 4 || (uintptr_t)x % 16) return hipErrorInvalidValue;
+        split_image_kernel<<<dim3(K / 256, (n + 31) / 32), 256, 0, s>>>(x, n, K, xstride, (u32x4*)img[0], (u32x4*)img[1],
+                                                                        (uint16_t*)img[2], (uint16_t*)img[3]);
     } else {
         split_rows_kernel<<<dim3((K + 255) / 256, n), 256, 0, s>>>(x, n, K, xstride, xh, xl);
     }
@@ -382,27 +403,25 @@ __device__ __forceinline__ void sx_load_w(const qmat& w, int row, int b, int kq,
 
 template <int DT> struct sx_unit_sums { static constexpr bool at(int U) { return DT == VITNA_DTYPE_Q4_K ? U == 3 : DT == VITNA_DTYPE_Q6_K ? (U & 1) : false; } };
 
+/* Unit U's operands of token tile tt, superblock b (and the S-term sums when the unit applies them), from the
+   images: every load is 1 KB (512 bytes for the sums) in lane order. */
 template <int DT, int U>
-__device__ __forceinline__ void sx_load_a(const skinny_args& a, int tok, int K, int b, int kq, sx_a& o) {
-    const uint16_t* xh = a.xh + (size_t)tok * K + 256 * b;
-    const uint16_t* xl = a.xl + (size_t)tok * K + 256 * b;
-    constexpr int base = DT == VITNA_DTYPE_Q6_K ? 128 * (U >> 1) + 32 * (U & 1) : 64 * U;
-    constexpr int step1 = DT == VITNA_DTYPE_Q6_K ? 16 : 8, step2 = DT == VITNA_DTYPE_Q6_K ? 64 : 32;
-    const int k0 = base + (DT == VITNA_DTYPE_Q6_K ? 8 : 16) * kq;
+__device__ __forceinline__ void sx_load_a(const skinny_args& a, int tt, int K, int b, int lane, sx_a& o) {
+    const u32x4* img = reinterpret_cast<const u32x4*>(DT == VITNA_DTYPE_Q6_K ? a.img[1] : a.img[0]) +
+                       ((size_t)tt * (K / 256) + b) * 2048 + (size_t)U * 512 + lane;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int c = k0 + (i & 1) * step1 + (i >> 1) * step2;
-        o.h[i] = *reinterpret_cast<const u32x4*>(xh + c);
-        o.l[i] = *reinterpret_cast<const u32x4*>(xl + c);
+        o.h[i] = img[i * 128];
+        o.l[i] = img[i * 128 + 64];
     }
     if constexpr (sx_unit_sums<DT>::at(U)) {
-        /* the sums' planes: Q4_K the 32-column groups, Q6_K the 16-column ones */
-        const size_t G = DT == VITNA_DTYPE_Q4_K ? K / 32 : K / 16, plane = (size_t)a.n * G;
-        const size_t off = (size_t)tok * G + (DT == VITNA_DTYPE_Q4_K ? 8 * b : 16 * b + 8 * (U >> 1)) + 4 * kq;
-        const uint16_t* sp = DT == VITNA_DTYPE_Q4_K ? a.s32 : a.s16;
+        const sx_u2* sp = DT == VITNA_DTYPE_Q4_K
+                              ? reinterpret_cast<const sx_u2*>(a.s32) + ((size_t)tt * (K / 256) + b) * 192 + lane
+                              : reinterpret_cast<const sx_u2*>(a.s16) + ((size_t)tt * (K / 128) + 2 * b + (U >> 1)) * 192 + lane;
 #pragma unroll
-        for (int i = 0; i < 3; i++) o.sp[i] = *reinterpret_cast<const sx_u2*>(sp + i * plane + off);
-    }}
+        for (int i = 0; i < 3; i++) o.sp[i] = sp[64 * i];
+    }
+}
 
 __device__ __forceinline__ void sx_scale(f32x16& acc, float d, const f32x16& P) {
 #pragma unroll
@@ -533,20 +552,21 @@ __device__ __forceinline__ void sx_compute(const sx_w<DT>& w, const sx_a& x, int
 
 /* Superblock b of the lane's weight row: every weight load issued first, the activations two units ahead. */
 template <int DT>
-__device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& w, int row, int tok, int b, int kq, f32x16& acc) {
+__device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& w, int row, int tt, int b, int lane, f32x16& acc) {
+    const int kq = lane >> 5;
     const int K = w.cols;
     float cs[8];
     sx_w<DT> W;
     sx_a x0, x1;
     sx_load_w<DT>(w, row, b, kq, W);
-    sx_load_a<DT, 0>(a, tok, K, b, kq, x0);
-    sx_load_a<DT, 1>(a, tok, K, b, kq, x1);
+    sx_load_a<DT, 0>(a, tt, K, b, lane, x0);
+    sx_load_a<DT, 1>(a, tt, K, b, lane, x1);
     __builtin_amdgcn_sched_barrier(0);
     sx_compute<DT, 0>(W, x0, kq, acc, cs);
-    sx_load_a<DT, 2>(a, tok, K, b, kq, x0);
+    sx_load_a<DT, 2>(a, tt, K, b, lane, x0);
     __builtin_amdgcn_sched_barrier(0);
     sx_compute<DT, 1>(W, x1, kq, acc, cs);
-    sx_load_a<DT, 3>(a, tok, K, b, kq, x1);
+    sx_load_a<DT, 3>(a, tt, K, b, lane, x1);
     __builtin_amdgcn_sched_barrier(0);
     sx_compute<DT, 2>(W, x0, kq, acc, cs);
     sx_compute<DT, 3>(W, x1, kq, acc, cs);
@@ -559,6 +579,15 @@ __device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& 
  * counter in cnt[]) adds the splits' sums in split order, writes the result and clears the counter, so the
  * result does not depend on which block finishes last.
  */
+#ifdef SX_PROBE
+__device__ unsigned long long sx_probe[2][1024][8][4];
+extern "C" int vitna_sx_probe(unsigned long long* out) {
+    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(sx_probe), sizeof(sx_probe));
+}
+#define SXP(i) do { if (lane == 0 && blockIdx.x < 1024) sx_probe[a.splits[mi] > 1][blockIdx.x][wv][i] = (i == 3 ? (unsigned long long)__smid() : __builtin_amdgcn_s_memrealtime()); } while (0)
+#else
+#define SXP(i) do {} while (0)
+#endif
 __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     extern __shared__ float red[]; /* [KS][16][64] */
     __shared__ int last;
@@ -575,14 +604,16 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     const int splits = a.splits[mi], sp = bx % splits, tile = bx / splits;
     const int row0 = 32 * tile, tok0 = blockIdx.y * SK_TOK;
     const int row = min(row0 + l32, w.rows - 1);
-    const int tok = min(tok0 + l32, a.n - 1); /* rows past n compute on row n - 1 and are never written */
     const int b = 8 * sp + wv;
+    SXP(0);
+    SXP(3);
     f32x16 acc = {};
     if (b < w.cols / 256) {
-        if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K>(a, w, row, tok, b, kq, acc);
-        else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K>(a, w, row, tok, b, kq, acc);
-        else sx_superblock<VITNA_DTYPE_Q8_0>(a, w, row, tok, b, kq, acc);
+        if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K>(a, w, row, blockIdx.y, b, lane, acc);
+        else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K>(a, w, row, blockIdx.y, b, lane, acc);
+        else sx_superblock<VITNA_DTYPE_Q8_0>(a, w, row, blockIdx.y, b, lane, acc);
     }
+    SXP(1);
 
     /* accumulator r of a lane: token 8 (r / 4) + 4 (lane / 32) + r % 4 of the tile, weight row lane % 32 */
     float* y = a.y[mi];
@@ -610,6 +641,7 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
             for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
             put(r, v);
         }
+        SXP(2);
         return;
     }
     /* several splits: this block's sum of the tile into part[], then the last block of the tile adds them */
@@ -626,6 +658,7 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     __syncthreads();
     if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
     __syncthreads();
+    SXP(2);
     if (!last) return;
     for (int r = wv; r < 16; r += KS) {
         float v = 0.0f;
@@ -637,64 +670,50 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
 
 /* ---- wide matrices (the LM head): activations staged in LDS ---------------- */
 
-/* Column (within the superblock) of operand i of unit U for lane half kq: the order sx_load_a reads. */
-template <int DT>
-__device__ __forceinline__ int sx_col(int U, int i, int kq) {
-    if constexpr (DT == VITNA_DTYPE_Q6_K) return 128 * (U >> 1) + 32 * (U & 1) + 8 * kq + (i & 1) * 16 + (i >> 1) * 64;
-    else return 64 * U + 16 * kq + (i & 1) * 8 + (i >> 1) * 32;
-}
-
-/* LDS image of one superblock's operands for 32 tokens: piece p = ((U * 4 + i) * 2 + hl) * 64 + lane, 16 bytes
-   each, so a wave's ds_read_b128 of one operand reads 1 KB in lane order. */
 #define SXW_PIECES 2048
 
 typedef __attribute__((address_space(3))) void* sx_lds_void;
 typedef __attribute__((address_space(1))) void* sx_glb_void;
 
-/* Thread t's pieces of superblock b (NW waves share the image's 2048), from the split activations straight into
-   the image (global-to-LDS loads: lane l of a wave lands at the wave's base + 16 l, which is piece order).
-   Counted by vmcnt. */
+/* Superblock b's image of token tile tt, copied into LDS by global-to-LDS loads (lane l of a wave lands at the
+   wave's base + 16 l: a straight copy). Counted by vmcnt. */
 template <int DT, int NW>
-__device__ __forceinline__ void sxw_fetch(const skinny_args& a, int K, int tok0, int b, u32x4* img) {
+__device__ __forceinline__ void sxw_fetch(const skinny_args& a, int K, int tt, int b, u32x4* img) {
     const int wv = threadIdx.x >> 6;
+    const u32x4* src = reinterpret_cast<const u32x4*>(DT == VITNA_DTYPE_Q6_K ? a.img[1] : a.img[0]) + ((size_t)tt * (K / 256) + b) * 2048;
 #pragma unroll
     for (int j = 0; j < SXW_PIECES / (64 * NW); j++) {
         const int p = threadIdx.x + 64 * NW * j;
-        const int lane = p & 63, rest = p >> 6, hl = rest & 1, i = (rest >> 1) & 3, U = rest >> 3;
-        const int tok = min(tok0 + (lane & 31), a.n - 1);
-        const uint16_t* src = (hl ? a.xl : a.xh) + (size_t)tok * K + 256 * b + sx_col<DT>(U, i, lane >> 5);
-        __builtin_amdgcn_global_load_lds((sx_glb_void)src, (sx_lds_void)(img + wv * 64 + 64 * NW * j), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((sx_glb_void)(src + p), (sx_lds_void)(img + wv * 64 + 64 * NW * j), 16, 0, 0);
     }
 }
 
 template <int DT, int U>
-__device__ __forceinline__ void sxw_read(const u32x4* img, const skinny_args& a, int tok, int K, int b, int kq, sx_a& o) {
-    const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void sxw_read(const u32x4* img, const skinny_args& a, int tt, int K, int b, int lane, sx_a& o) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        o.h[i] = img[((U * 4 + i) * 2 + 0) * 64 + lane];
-        o.l[i] = img[((U * 4 + i) * 2 + 1) * 64 + lane];
+        o.h[i] = img[U * 512 + i * 128 + lane];
+        o.l[i] = img[U * 512 + i * 128 + 64 + lane];
     }
     if constexpr (sx_unit_sums<DT>::at(U)) {
-        const size_t G = DT == VITNA_DTYPE_Q4_K ? K / 32 : K / 16, plane = (size_t)a.n * G;
-        const size_t off = (size_t)tok * G + (DT == VITNA_DTYPE_Q4_K ? 8 * b : 16 * b + 8 * (U >> 1)) + 4 * kq;
-        const uint16_t* sp = DT == VITNA_DTYPE_Q4_K ? a.s32 : a.s16;
+        const sx_u2* sp = DT == VITNA_DTYPE_Q4_K
+                              ? reinterpret_cast<const sx_u2*>(a.s32) + ((size_t)tt * (K / 256) + b) * 192 + lane
+                              : reinterpret_cast<const sx_u2*>(a.s16) + ((size_t)tt * (K / 128) + 2 * b + (U >> 1)) * 192 + lane;
 #pragma unroll
-        for (int i = 0; i < 3; i++) o.sp[i] = *reinterpret_cast<const sx_u2*>(sp + i * plane + off);
+        for (int i = 0; i < 3; i++) o.sp[i] = sp[64 * i];
     }
 }
 
 /* NW waves, wave v on tile NW blockIdx.x + v of the matrix, every superblock in turn: the block stages
    superblock b + 1's activations and each wave loads its weights for b + 1 while b computes. */
 template <int DT, int NW>
-__device__ __forceinline__ void sxw_body(const skinny_args& a, const qmat& w, int tile, int tok0, u32x4* img, f32x16& acc) {
+__device__ __forceinline__ void sxw_body(const skinny_args& a, const qmat& w, int tile, int tt, u32x4* img, f32x16& acc) {
     const int lane = threadIdx.x & 63, l32 = lane & 31, kq = lane >> 5;
     const int K = w.cols, S = K / 256;
     const int row = min(32 * tile + l32, w.rows - 1);
-    const int tok = min(tok0 + l32, a.n - 1);
     sx_w<DT> W0, W1;
     float cs[8];
-    sxw_fetch<DT, NW>(a, K, tok0, 0, img);
+    sxw_fetch<DT, NW>(a, K, tt, 0, img);
     sx_load_w<DT>(w, row, 0, kq, W0);
     auto step = [&](int b, const sx_w<DT>& W, sx_w<DT>& Wn) {
         /* image b landed (each wave waits for its own loads, the barrier for the others'); image b + 1's
@@ -703,21 +722,21 @@ __device__ __forceinline__ void sxw_body(const skinny_args& a, const qmat& w, in
         __syncthreads();
         const u32x4* cur = img + (b & 1) * SXW_PIECES;
         if (b + 1 < S) {
-            sxw_fetch<DT, NW>(a, K, tok0, b + 1, img + ((b + 1) & 1) * SXW_PIECES);
+            sxw_fetch<DT, NW>(a, K, tt, b + 1, img + ((b + 1) & 1) * SXW_PIECES);
             sx_load_w<DT>(w, row, b + 1, kq, Wn);
         }
         /* one unit's operands at a time (the barriers keep the scheduler from hoisting every unit's reads) */
         sx_a x;
-        sxw_read<DT, 0>(cur, a, tok, K, b, kq, x);
+        sxw_read<DT, 0>(cur, a, tt, K, b, lane, x);
         sx_compute<DT, 0>(W, x, kq, acc, cs);
         __builtin_amdgcn_sched_barrier(0);
-        sxw_read<DT, 1>(cur, a, tok, K, b, kq, x);
+        sxw_read<DT, 1>(cur, a, tt, K, b, lane, x);
         sx_compute<DT, 1>(W, x, kq, acc, cs);
         __builtin_amdgcn_sched_barrier(0);
-        sxw_read<DT, 2>(cur, a, tok, K, b, kq, x);
+        sxw_read<DT, 2>(cur, a, tt, K, b, lane, x);
         sx_compute<DT, 2>(W, x, kq, acc, cs);
         __builtin_amdgcn_sched_barrier(0);
-        sxw_read<DT, 3>(cur, a, tok, K, b, kq, x);
+        sxw_read<DT, 3>(cur, a, tt, K, b, lane, x);
         sx_compute<DT, 3>(W, x, kq, acc, cs);
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -741,7 +760,7 @@ __global__ __launch_bounds__(64 * NW) void skinny_wide_kernel(skinny_args a) {
     const qmat& w = a.w[mi];
     const int tile = NW * bx + wv, tok0 = blockIdx.y * SK_TOK;
     f32x16 acc = {};
-    sxw_body<DT, NW>(a, w, tile, tok0, img, acc);
+    sxw_body<DT, NW>(a, w, tile, blockIdx.y, img, acc);
     float* y = a.y[mi];
     const int n = 32 * tile + l32;
 #pragma unroll
@@ -789,7 +808,7 @@ static hipError_t launch_skinny_exact(const skinny_args& a0, hipStream_t s) {
 }
 
 hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
-    if (a.nm < 1 || a.nm > 3 || a.n < 1 || !a.xh || !a.xl) return hipErrorInvalidValue;
+    if (a.nm < 1 || a.nm > 3 || a.n < 1) return hipErrorInvalidValue;
     for (int i = 0; i < a.nm; i++) {
         const int d = a.w[i].dtype;
         if (a.w[i].cols != a.w[0].cols || a.w[i].cols % 32) return hipErrorInvalidValue;
@@ -798,7 +817,7 @@ hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
     int cus = 0, dev = 0;
     hipGetDevice(&dev);
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
-    bool exact = a.s16 && a.s32;
+    bool exact = a.img[0] && a.img[1] && a.s16 && a.s32;
     for (int i = 0; i < a.nm; i++) exact &= a.w[i].cols % 256 == 0;
 #ifndef SK_EXACT
 #define SK_EXACT 1

@@ -172,19 +172,21 @@ struct gemv_multi_args {
 hipError_t launch_gemv_multi(const gemv_multi_args& a, hipStream_t s);
 
 /* Multi-row projections on the matrix cores (kernels_skinny.hip): y_i[t][r]
-   (+)= W_i[r] . x[t] for t < n, to fp32 accuracy; x comes split into bf16
-   hi and lo parts ([n][cols] each, launch_split_rows). With the group sums
-   (s16, s32: each row's sums of hi + lo over 16 and 32 consecutive columns,
-   as three bf16 pieces, planes [3][n][cols / 16] and [3][n][cols / 32]) and
-   widths a multiple of 256 the quants enter the matrix cores as exact
-   integers; otherwise each weight is widened and split. */
+   (+)= W_i[r] . x[t] for t < n, to fp32 accuracy. launch_split_rows splits x
+   into bf16 hi and lo parts: with img (widths a multiple of 256) into the
+   operand images and group sums of the exact-integer kernels (img[0], img[1]:
+   column orders A and B, [n / 32][cols / 256][2048] x 16 bytes each; img[2],
+   img[3]: 32- and 16-column sums, [n / 32][cols / 256 or cols / 128][3][64]
+   x 8 bytes), otherwise row-major into xh and xl ([n][cols] each), for the
+   kernel that widens and splits each weight. */
 struct skinny_args {
     qmat w[3];
     float* y[3];
     int nm;
     const uint16_t* xh;
     const uint16_t* xl;
-    const uint16_t *s16, *s32;
+    const uint32_t* img[2];
+    const uint32_t *s32, *s16;
     int n, add;
     /* matrices wider than 2048 columns split across blocks: part (part_cap floats) holds each split's sum of a
        tile and cnt (cnt_cap ints, zero before the first call, left zero by every call) counts finished splits */
@@ -193,8 +195,7 @@ struct skinny_args {
     size_t part_cap, cnt_cap;
     int splits[3], tiles, split_max; /* set by launch_skinny */
 };
-/* sums: null, or [2] = s16, s32 as above */
-hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, uint16_t* const* sums,
+hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, uint32_t* const* img,
                              hipStream_t s);
 hipError_t launch_skinny(const skinny_args& a, hipStream_t s);
 

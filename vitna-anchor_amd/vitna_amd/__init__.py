@@ -235,6 +235,7 @@ def _hip():
         "vitna_hip_moe_ffn": (C.c_bool, [P, C.c_size_t, *E]),
         "vitna_hip_moe_rows_step": (C.c_bool, [P, C.POINTER(RowT), C.c_size_t, C.POINTER(_FP), *E]),
         "vitna_hip_residual": (C.c_bool, [P, C.c_size_t, _FP, C.c_bool, *E]),
+        "vitna_hip_rows_project": (C.c_bool, [P, C.c_size_t, C.c_int, _FP, C.c_size_t, _FP, *E]),
         "vitna_hip_routing": (C.c_bool, [P, C.c_size_t, _FP, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _FP, *E]),
         "vitna_hip_kv": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, _FP, _FP, C.c_bool, *E]),
         "vitna_hip_kv_fill": (C.c_bool, [P, C.c_uint64, C.POINTER(C.c_size_t), *E]),
@@ -370,6 +371,17 @@ class Device:
     def set_residual(self, x, row=0):
         x = np.ascontiguousarray(x, np.float32)
         self._ok(self.lib.vitna_hip_residual(self.g, row, fptr(x), True, self.err, 512))
+
+    def rows_project(self, layer, which, x):
+        """y = W x for n rows x (n x cols), W = layer's q, k, v, o (which 0..3) or the head (4), on the multi-row
+        kernels of a rows step."""
+        cfg = self.model.cfg
+        qd, kd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+        rows = [qd, kd, kd, cfg.hidden, cfg.vocab][which]
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty((x.shape[0], rows), np.float32)
+        self._ok(self.lib.vitna_hip_rows_project(self.g, layer, which, fptr(x), x.shape[0], fptr(y), self.err, 512))
+        return y
 
     def residual(self, row=0):
         x = np.empty(self.model.cfg.hidden, np.float32)
