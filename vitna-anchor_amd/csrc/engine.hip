@@ -271,6 +271,18 @@ static bool upload_matrix(vitna_cuda_model* g, qmat* out, const vitna_matrix_t* 
     return upload_set(g, one, 1, *out, staging, staging_bytes, err, err_len);
 }
 
+/* The tiled copy the multi-row kernels read (dense matrices whose width is a multiple of 256). */
+static bool make_tiled(vitna_cuda_model* g, qmat* m, const char* what, char* err, size_t err_len) {
+    const size_t tb = tile_bytes(m->dtype);
+    if (!tb || m->cols % 256) return true;
+    uint8_t* mem;
+    if (!dalloc(g, &mem, tb * ((m->rows + 31) / 32) * (m->cols / 256), what, err, err_len)) return false;
+    HIP_TRY(launch_tile(*m, mem, g->stream), "tiling a matrix");
+    HIP_TRY(hipStreamSynchronize(g->stream), "tiling a matrix");
+    m->tiled = mem;
+    return true;
+}
+
 extern "C" bool vitna_cuda_probe(char* err, size_t err_len) {
     int n = 0;
     const hipError_t e = hipGetDeviceCount(&n);
@@ -394,6 +406,8 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
                  upload_matrix(g, &d.k, &L->k, staging, staging_bytes, "k", err, err_len) &&
                  upload_matrix(g, &d.v, &L->v, staging, staging_bytes, "v", err, err_len) &&
                  upload_matrix(g, &d.o, &L->o, staging, staging_bytes, "o", err, err_len) &&
+                 make_tiled(g, &d.q, "q", err, err_len) && make_tiled(g, &d.k, "k", err, err_len) &&
+                 make_tiled(g, &d.v, "v", err, err_len) && make_tiled(g, &d.o, "o", err, err_len) &&
                  upload_f32(g, &d.attn_norm, L->attn_norm, c->hidden, "the attention norm", err, err_len);
             if (ok && c->qk_norm)
                 ok = upload_f32(g, &d.q_norm, L->q_norm, c->head_dim, "the q norm", err, err_len) &&
@@ -403,6 +417,7 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
     if (ok && g->attention) {
         ok = upload_matrix(g, &g->embed, &m->embed, staging, staging_bytes, "the embedding", err, err_len) &&
              upload_matrix(g, &g->head, &m->lm_head, staging, staging_bytes, "the output projection", err, err_len) &&
+             make_tiled(g, &g->head, "the output projection", err, err_len) &&
              upload_f32(g, &g->final_norm, m->final_norm, c->hidden, "the final norm", err, err_len);
         const size_t half = c->head_dim / 2;
         ok = ok && upload_f32(g, &g->cos_tab, cos_tab, m->ctx * half, "the rotary cosines", err, err_len) &&

@@ -373,31 +373,101 @@ struct sx_a {
     sx_u2 sp[3];
 };
 
-template <int DT>
-__device__ __forceinline__ void sx_load_w(const qmat& w, int row, int b, int kq, sx_w<DT>& o) {
-    if constexpr (DT == VITNA_DTYPE_Q4_K) {
-        const size_t blk = (size_t)row * w.nb + b;
-#pragma unroll
-        for (int u = 0; u < 4; u++) o.q[u] = WLOAD(reinterpret_cast<const u32x4*>(w.p[0] + blk * 128 + 32 * u + 16 * kq));
-        o.h = *reinterpret_cast<const u32x4*>(w.p[1] + blk * 16);
-    } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
-        const size_t blk = (size_t)row * w.nb + b;
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-#pragma unroll
-            for (int s = 0; s < 2; s++)
-                o.ql[u][s] = WLOAD(reinterpret_cast<const sx_u2*>(w.p[0] + blk * 128 + 64 * (u >> 1) + 32 * (u & 1) + 16 * s + 8 * kq));
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int s = 0; s < 2; s++) o.qh[h][s] = *reinterpret_cast<const sx_u2*>(w.p[1] + blk * 64 + 32 * h + 16 * s + 8 * kq);
-        o.sc = *reinterpret_cast<const u32x4*>(w.p[2] + blk * 16);
-        o.d = *reinterpret_cast<const uint16_t*>(w.p[3] + blk * 2);
+/*
+ * The tiled copy: per tile (32 rows; rows past the matrix repeat its last) and superblock, lane l = l32 + 32 kq
+ * reads 16-byte pieces at lane-order offsets, so every load is 1 KB contiguous (512 bytes for the per-row
+ * fields, which both lane halves read):
+ *   Q4_K  [u][lane] q bytes 32 u + 16 kq + 0..15 (u < 4); at 4096 [l32] the 16-byte header
+ *   Q6_K  [u][lane] ql bytes 64 (u / 2) + 32 (u % 2) + 16 s + 8 kq + 0..7 for s = 0, 1; at 4096 [h][lane] qh
+ *         bytes 32 h + 16 s + 8 kq + 0..7 for s = 0, 1; at 6144 [l32] the 16 scales; at 6656 [l32] d
+ *   Q8_0  [2 u + j][lane] q bytes 16 kq + 0..15 of block 8 b + 2 u + j; at 8192 [l32] the 8 blocks' d
+ */
+__device__ __forceinline__ uint32_t tile_src(const qmat& m, int tile, int b, int o) {
+    /* the byte of the planes that byte o of tile / superblock b copies */
+    const int S = m.cols / 256;
+    (void)S;
+    if (m.dtype == VITNA_DTYPE_Q4_K) {
+        if (o < 4096) {
+            const int u = o >> 10, lane = (o >> 4) & 63, j = o & 15;
+            const size_t row = min(32 * tile + (lane & 31), m.rows - 1);
+            return m.p[0][(row * m.nb + b) * 128 + 32 * u + 16 * (lane >> 5) + j];
+        }
+        const int l32 = (o - 4096) >> 4, j = o & 15;
+        const size_t row = min(32 * tile + l32, m.rows - 1);
+        return m.p[1][(row * m.nb + b) * 16 + j];
+    } else if (m.dtype == VITNA_DTYPE_Q6_K) {
+        if (o < 4096) {
+            const int u = o >> 10, lane = (o >> 4) & 63, j = o & 15, sh = j >> 3, jj = j & 7;
+            const size_t row = min(32 * tile + (lane & 31), m.rows - 1);
+            return m.p[0][(row * m.nb + b) * 128 + 64 * (u >> 1) + 32 * (u & 1) + 16 * sh + 8 * (lane >> 5) + jj];
+        }
+        if (o < 6144) {
+            const int q = o - 4096, h = q >> 10, lane = (q >> 4) & 63, j = q & 15, sh = j >> 3, jj = j & 7;
+            const size_t row = min(32 * tile + (lane & 31), m.rows - 1);
+            return m.p[1][(row * m.nb + b) * 64 + 32 * h + 16 * sh + 8 * (lane >> 5) + jj];
+        }
+        if (o < 6656) {
+            const int l32 = (o - 6144) >> 4, j = o & 15;
+            const size_t row = min(32 * tile + l32, m.rows - 1);
+            return m.p[2][(row * m.nb + b) * 16 + j];
+        }
+        const int l32 = (o - 6656) >> 1, j = o & 1;
+        const size_t row = min(32 * tile + l32, m.rows - 1);
+        return m.p[3][(row * m.nb + b) * 2 + j];
     } else {
-        const size_t blk = (size_t)row * w.nb + 8 * b;
+        if (o < 8192) {
+            const int v = o >> 10, lane = (o >> 4) & 63, j = o & 15;
+            const size_t row = min(32 * tile + (lane & 31), m.rows - 1);
+            return m.p[0][(row * m.nb + 8 * b + v) * 32 + 16 * (lane >> 5) + j];
+        }
+        const int l32 = (o - 8192) >> 4, j = o & 15;
+        const size_t row = min(32 * tile + l32, m.rows - 1);
+        return m.p[1][(row * m.nb + 8 * b) * 2 + j];
+    }
+}
+
+/* One block a tile / superblock, a thread a byte (the copy is made once, at upload). */
+__global__ void tile_kernel(qmat m, uint8_t* __restrict__ dst) {
+    const int S = m.cols / 256, tile = blockIdx.x / S, b = blockIdx.x % S;
+    const int tb = (int)tile_bytes(m.dtype);
+    uint8_t* out = dst + (size_t)blockIdx.x * tb;
+    for (int o = threadIdx.x; o < tb; o += blockDim.x) out[o] = (uint8_t)tile_src(m, tile, b, o);
+}
+
+hipError_t launch_tile(const qmat& m, uint8_t* dst, hipStream_t s) {
+    if (!tile_bytes(m.dtype) || m.cols % 256 || m.rows < 1) return hipErrorInvalidValue;
+    tile_kernel<<<((m.rows + 31) / 32) * (m.cols / 256), 256, 0, s>>>(m, dst);
+    return hipGetLastError();
+}
+
+/* The lane's bytes of tile / superblock b from the tiled copy: 1 KB (512-byte) loads in lane order. */
+template <int DT>
+__device__ __forceinline__ void sx_load_w(const qmat& w, int tile, int b, int lane, sx_w<DT>& o) {
+    const uint8_t* T = w.tiled + ((size_t)tile * (w.cols / 256) + b) * (DT == VITNA_DTYPE_Q4_K ? 4608 : DT == VITNA_DTYPE_Q6_K ? 6720 : 8704);
+    const int l32 = lane & 31;
+    if constexpr (DT == VITNA_DTYPE_Q4_K) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) o.q[j >> 1][j & 1] = WLOAD(reinterpret_cast<const u32x4*>(w.p[0] + (blk + j) * 32 + 16 * kq));
-        o.d = *reinterpret_cast<const u32x4*>(w.p[1] + blk * 2);
+        for (int u = 0; u < 4; u++) o.q[u] = WLOAD(reinterpret_cast<const u32x4*>(T + u * 1024 + lane * 16));
+        o.h = *reinterpret_cast<const u32x4*>(T + 4096 + l32 * 16);
+    } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const u32x4 v = WLOAD(reinterpret_cast<const u32x4*>(T + u * 1024 + lane * 16));
+            o.ql[u][0] = sx_u2{v.x, v.y};
+            o.ql[u][1] = sx_u2{v.z, v.w};
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(T + 4096 + h * 1024 + lane * 16);
+            o.qh[h][0] = sx_u2{v.x, v.y};
+            o.qh[h][1] = sx_u2{v.z, v.w};
+        }
+        o.sc = *reinterpret_cast<const u32x4*>(T + 6144 + l32 * 16);
+        o.d = *reinterpret_cast<const uint16_t*>(T + 6656 + l32 * 2);
+    } else {
+#pragma unroll
+        for (int v = 0; v < 8; v++) o.q[v >> 1][v & 1] = WLOAD(reinterpret_cast<const u32x4*>(T + v * 1024 + lane * 16));
+        o.d = *reinterpret_cast<const u32x4*>(T + 8192 + l32 * 16);
     }
 }
 
@@ -552,13 +622,13 @@ __device__ __forceinline__ void sx_compute(const sx_w<DT>& w, const sx_a& x, int
 
 /* Superblock b of the lane's weight row: every weight load issued first, the activations two units ahead. */
 template <int DT>
-__device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& w, int row, int tt, int b, int lane, f32x16& acc) {
+__device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& w, int tile, int tt, int b, int lane, f32x16& acc) {
     const int kq = lane >> 5;
     const int K = w.cols;
     float cs[8];
     sx_w<DT> W;
     sx_a x0, x1;
-    sx_load_w<DT>(w, row, b, kq, W);
+    sx_load_w<DT>(w, tile, b, lane, W);
     sx_load_a<DT, 0>(a, tt, K, b, lane, x0);
     sx_load_a<DT, 1>(a, tt, K, b, lane, x1);
     __builtin_amdgcn_sched_barrier(0);
@@ -603,15 +673,14 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     const qmat& w = a.w[mi];
     const int splits = a.splits[mi], sp = bx % splits, tile = bx / splits;
     const int row0 = 32 * tile, tok0 = blockIdx.y * SK_TOK;
-    const int row = min(row0 + l32, w.rows - 1);
     const int b = 8 * sp + wv;
     SXP(0);
     SXP(3);
     f32x16 acc = {};
     if (b < w.cols / 256) {
-        if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K>(a, w, row, blockIdx.y, b, lane, acc);
-        else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K>(a, w, row, blockIdx.y, b, lane, acc);
-        else sx_superblock<VITNA_DTYPE_Q8_0>(a, w, row, blockIdx.y, b, lane, acc);
+        if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K>(a, w, tile, blockIdx.y, b, lane, acc);
+        else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K>(a, w, tile, blockIdx.y, b, lane, acc);
+        else sx_superblock<VITNA_DTYPE_Q8_0>(a, w, tile, blockIdx.y, b, lane, acc);
     }
     SXP(1);
 
@@ -710,11 +779,11 @@ template <int DT, int NW>
 __device__ __forceinline__ void sxw_body(const skinny_args& a, const qmat& w, int tile, int tt, u32x4* img, f32x16& acc) {
     const int lane = threadIdx.x & 63, l32 = lane & 31, kq = lane >> 5;
     const int K = w.cols, S = K / 256;
-    const int row = min(32 * tile + l32, w.rows - 1);
+
     sx_w<DT> W0, W1;
     float cs[8];
     sxw_fetch<DT, NW>(a, K, tt, 0, img);
-    sx_load_w<DT>(w, row, 0, kq, W0);
+    sx_load_w<DT>(w, tile, 0, lane, W0);
     auto step = [&](int b, const sx_w<DT>& W, sx_w<DT>& Wn) {
         /* image b landed (each wave waits for its own loads, the barrier for the others'); image b + 1's
            buffer was last read in step b - 1, which every wave has left */
@@ -723,7 +792,7 @@ __device__ __forceinline__ void sxw_body(const skinny_args& a, const qmat& w, in
         const u32x4* cur = img + (b & 1) * SXW_PIECES;
         if (b + 1 < S) {
             sxw_fetch<DT, NW>(a, K, tt, b + 1, img + ((b + 1) & 1) * SXW_PIECES);
-            sx_load_w<DT>(w, row, b + 1, kq, Wn);
+            sx_load_w<DT>(w, tile, b + 1, lane, Wn);
         }
         /* one unit's operands at a time (the barriers keep the scheduler from hoisting every unit's reads) */
         sx_a x;
@@ -814,15 +883,16 @@ hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
         if (a.w[i].cols != a.w[0].cols || a.w[i].cols % 32) return hipErrorInvalidValue;
         if (d != VITNA_DTYPE_Q8_0 && d != VITNA_DTYPE_Q4_K && d != VITNA_DTYPE_Q6_K) return hipErrorInvalidValue;
     }
-    int cus = 0, dev = 0;
-    hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
     bool exact = a.img[0] && a.img[1] && a.s16 && a.s32;
-    for (int i = 0; i < a.nm; i++) exact &= a.w[i].cols % 256 == 0;
+    for (int i = 0; i < a.nm; i++) exact &= a.w[i].cols % 256 == 0 && a.w[i].tiled;
 #ifndef SK_EXACT
 #define SK_EXACT 1
 #endif
     if (exact && SK_EXACT) return launch_skinny_exact(a, s);
+    if (!a.xh || !a.xl) return hipErrorInvalidValue;
+    int cus = 0, dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+        cus = 256;
     const int want = 8 * cus; /* two waves a SIMD */
     const int mt = (a.n + SK_TOK - 1) / SK_TOK;
     const int S = a.w[0].cols / 32;

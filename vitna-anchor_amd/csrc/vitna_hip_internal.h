@@ -52,7 +52,15 @@ struct qmat {
     uint64_t estride[4];  /* bytes between experts' planes; 0 for a single matrix */
     int rows, cols, nb;   /* nb: blocks a row */
     int dtype;
+    /* A second copy of a dense matrix for the multi-row kernels, or null: per 32-row tile and 256-column
+       superblock, tile_bytes() bytes in the order the MFMA lanes read them (kernels_skinny.hip). */
+    const uint8_t* tiled;
 };
+
+/* Bytes of one 32-row tile's superblock in the tiled copy; 0 for a dtype without one. */
+__host__ __device__ static inline size_t tile_bytes(int dtype) {
+    return dtype == VITNA_DTYPE_Q4_K ? 4608 : dtype == VITNA_DTYPE_Q6_K ? 6720 : dtype == VITNA_DTYPE_Q8_0 ? 8704 : 0;
+}
 
 /* ---- host-side layout arithmetic, shared with the upload code ---- */
 

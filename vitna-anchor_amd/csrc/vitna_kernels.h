@@ -198,6 +198,8 @@ struct skinny_args {
 hipError_t launch_split_rows(const float* x, int n, int K, int xstride, uint16_t* xh, uint16_t* xl, uint32_t* const* img,
                              hipStream_t s);
 hipError_t launch_skinny(const skinny_args& a, hipStream_t s);
+/* The tiled copy of m (tile_bytes(dtype) x ceil(rows / 32) x cols / 256 bytes at dst) from its planes. */
+hipError_t launch_tile(const qmat& m, uint8_t* dst, hipStream_t s);
 
 /* The per-expert lists of (row, slot) pairs of n rows' routing: count[E],
    pairs[E][cap] = row * ROUTE_K_MAX + slot, in order of row. */
