@@ -401,6 +401,17 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
         ok = ok && upload_set(g, mats.data(), E, d.up, staging, staging_bytes, err, err_len);
         for (size_t e = 0; ok && e < E; e++) mats[e] = &L->experts[e].down;
         ok = ok && upload_set(g, mats.data(), E, d.down, staging, staging_bytes, err, err_len);
+        /* the grouped experts' tiled copies (read by the rows path; the decode kernels read the planes) */
+        if (ok && gmma_fits(d.gate, d.up, d.down)) {
+            qmat* sets[3] = {&d.gate, &d.up, &d.down};
+            for (int i = 0; ok && i < 3; i++) {
+                uint8_t* t;
+                ok = dalloc(g, &t, gmma_tiled_bytes(*sets[i], (int)E), "the experts' tiled copy", err, err_len);
+                if (ok && (launch_gmma_tile(*sets[i], (int)E, t, g->stream) != hipSuccess || hipStreamSynchronize(g->stream) != hipSuccess))
+                    ok = fail(err, err_len, "tiling the experts");
+                if (ok) sets[i]->tiled = t;
+            }
+        }
         if (ok && g->attention) {
             ok = upload_matrix(g, &d.q, &L->q, staging, staging_bytes, "q", err, err_len) &&
                  upload_matrix(g, &d.k, &L->k, staging, staging_bytes, "k", err, err_len) &&

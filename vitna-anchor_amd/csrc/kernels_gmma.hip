@@ -36,8 +36,9 @@
  *
  * Layouts. Split activations: rows of K / 4 chunks of 16 bytes, [4 hi bf16]
  * [4 lo bf16]; sums: rows of K / G floats, G = 16 for Q6_K and 32 otherwise.
- * Weights stream through registers one step ahead: a lane reads its own row,
- * 80 (Q4_K), 106 (Q6_K) or 136 (Q8_0) bytes a step.
+ * Weights stream through registers one step ahead: a lane takes its own row's
+ * 80 (Q4_K), 106 (Q6_K) or 136 (Q8_0) bytes a step, from the tiled copy (below),
+ * where a wave's loads are contiguous.
  */
 
 #include "vitna_kernels.h"
@@ -150,34 +151,102 @@ struct gstep<VITNA_DTYPE_Q8_0> { /* blocks 4 st .. 4 st + 3 */
     uint32_t d[4];
 };
 
-/* A lane reads its row's step in 16-byte pieces of one line: cached loads, so the line's later pieces come
-   from the vector cache. */
+/* ---- the tiled copy of an expert set ------------------------------------- */
+/*
+ * Per expert, per group of 64 rows (a wave's rows, lane l = row 64 g + l) and unit (Q4_K, Q6_K: a 256-column
+ * block; Q8_0: a 128-column step), the bytes a lane's step loads, in 16-byte pieces in lane order, so that each
+ * load of a wave is 1 KB contiguous (512 or 128 bytes for the small fields):
+ *   Q4_K (9216): q half 0 [4][64] x 16, q half 1 [4][64] x 16, header [64] x 16
+ *   Q6_K (13440): ql half 0, ql half 1 [4][64] x 16, qh half 0, half 1 [2][64] x 16, scales [2][64] x 8, d [64] x 2
+ *   Q8_0 (8704): q [8][64] x 16 (the four blocks' 128 bytes), d [64] x 8
+ * Experts back to back, gmma_tile_stride bytes apart.
+ */
+__host__ __device__ static inline size_t gmma_unit_bytes(int dtype) {
+    return dtype == VITNA_DTYPE_Q4_K ? 9216 : dtype == VITNA_DTYPE_Q6_K ? 13440 : dtype == VITNA_DTYPE_Q8_0 ? 8704 : 0;
+}
+__host__ __device__ static inline size_t gmma_units(int dtype, int cols) { return dtype == VITNA_DTYPE_Q8_0 ? cols / 128 : cols / 256; }
+__host__ __device__ static inline size_t gmma_tile_stride(const qmat& m) {
+    return (size_t)(m.rows / 64) * gmma_units(m.dtype, m.cols) * gmma_unit_bytes(m.dtype);
+}
+
+/* the byte of expert e's planes that byte o of (group g, unit u) copies */
+__device__ static uint32_t gtile_src(const qmat& m, int e, int g, int u, int o) {
+    const uint8_t* P0 = m.p[0] + e * m.estride[0];
+    const uint8_t* P1 = m.p[1] + e * m.estride[1];
+    if (m.dtype == VITNA_DTYPE_Q4_K) {
+        if (o < 8192) {
+            const int half = o >> 12, i = (o >> 10) & 3, lane = (o >> 4) & 63, j = o & 15;
+            return P0[((size_t)(64 * g + lane) * m.nb + u) * 128 + 64 * half + 16 * i + j];
+        }
+        const int lane = (o - 8192) >> 4, j = o & 15;
+        return P1[((size_t)(64 * g + lane) * m.nb + u) * 16 + j];
+    } else if (m.dtype == VITNA_DTYPE_Q6_K) {
+        if (o < 8192) {
+            const int h = o >> 12, i = (o >> 10) & 3, lane = (o >> 4) & 63, j = o & 15;
+            return P0[((size_t)(64 * g + lane) * m.nb + u) * 128 + 64 * h + 16 * i + j];
+        }
+        if (o < 12288) {
+            const int q = o - 8192, h = q >> 11, i = (q >> 10) & 1, lane = (q >> 4) & 63, j = q & 15;
+            return P1[((size_t)(64 * g + lane) * m.nb + u) * 64 + 32 * h + 16 * i + j];
+        }
+        if (o < 13312) {
+            const int q = o - 12288, h = q >> 9, lane = (q >> 3) & 63, j = q & 7;
+            return (m.p[2] + e * m.estride[2])[((size_t)(64 * g + lane) * m.nb + u) * 16 + 8 * h + j];
+        }
+        const int q = o - 13312, lane = q >> 1, j = q & 1;
+        return (m.p[3] + e * m.estride[3])[((size_t)(64 * g + lane) * m.nb + u) * 2 + j];
+    } else {
+        if (o < 8192) {
+            const int i = o >> 10, lane = (o >> 4) & 63, j = o & 15;
+            return P0[((size_t)(64 * g + lane) * m.nb + 4 * u) * 32 + 16 * i + j];
+        }
+        const int q = o - 8192, lane = q >> 3, b = (q & 7) >> 1, j = q & 1;
+        return P1[((size_t)(64 * g + lane) * m.nb + 4 * u + b) * 2 + j];
+    }
+}
+
+/* One block a (expert, group, unit), a thread a byte: made once, at upload. */
+__global__ void gtile_kernel(qmat m, int groups, int units, uint8_t* __restrict__ dst) {
+    const int u = blockIdx.x % units, g = (blockIdx.x / units) % groups, e = blockIdx.x / (units * groups);
+    const int ub = (int)gmma_unit_bytes(m.dtype);
+    uint8_t* out = dst + (size_t)blockIdx.x * ub;
+    for (int o = threadIdx.x; o < ub; o += blockDim.x) out[o] = (uint8_t)gtile_src(m, e, g, u, o);
+}
+
+size_t gmma_tiled_bytes(const qmat& m, int n_experts) { return gmma_tile_stride(m) * n_experts; }
+
+hipError_t launch_gmma_tile(const qmat& m, int n_experts, uint8_t* dst, hipStream_t s) {
+    if (!gmma_unit_bytes(m.dtype) || m.rows % 64 || m.cols % 256 || n_experts < 1) return hipErrorInvalidValue;
+    const int groups = m.rows / 64, units = (int)gmma_units(m.dtype, m.cols);
+    gtile_kernel<<<n_experts * groups * units, 256, 0, s>>>(m, groups, units, dst);
+    return hipGetLastError();
+}
+
+/* A lane's step from the tiled copy: every load of the wave 1 KB (or 512 / 128 bytes) contiguous. */
 template <int DT>
 __device__ __forceinline__ void gload(const qmat& m, int e, int row, int st, gstep<DT>& s) {
+    const int g = row >> 6, lane = row & 63;
+    const uint8_t* E = m.tiled + (size_t)e * gmma_tile_stride(m);
     if constexpr (DT == VITNA_DTYPE_Q4_K) {
-        const size_t blk = (size_t)row * m.nb + (st >> 1);
-        const u32x4* q = reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 128 + 64 * (st & 1));
+        const uint8_t* T = E + ((size_t)g * (m.cols / 256) + (st >> 1)) * 9216;
 #pragma unroll
-        for (int i = 0; i < 4; i++) s.q[i] = q[i];
-        s.h = *reinterpret_cast<const u32x4*>(m.p[1] + e * m.estride[1] + blk * 16);
+        for (int i = 0; i < 4; i++) s.q[i] = *reinterpret_cast<const u32x4*>(T + (st & 1) * 4096 + i * 1024 + lane * 16);
+        s.h = *reinterpret_cast<const u32x4*>(T + 8192 + lane * 16);
     } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
-        const size_t blk = (size_t)row * m.nb + (st >> 1);
+        const uint8_t* T = E + ((size_t)g * (m.cols / 256) + (st >> 1)) * 13440;
         const int h = st & 1;
-        const u32x4* ql = reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 128 + 64 * h);
-        const u32x4* qh = reinterpret_cast<const u32x4*>(m.p[1] + e * m.estride[1] + blk * 64 + 32 * h);
 #pragma unroll
-        for (int i = 0; i < 4; i++) s.ql[i] = ql[i];
-        s.qh[0] = qh[0];
-        s.qh[1] = qh[1];
-        s.sc = *reinterpret_cast<const u32x2*>(m.p[2] + e * m.estride[2] + blk * 16 + 8 * h);
-        s.d = *reinterpret_cast<const uint16_t*>(m.p[3] + e * m.estride[3] + blk * 2);
+        for (int i = 0; i < 4; i++) s.ql[i] = *reinterpret_cast<const u32x4*>(T + h * 4096 + i * 1024 + lane * 16);
+#pragma unroll
+        for (int i = 0; i < 2; i++) s.qh[i] = *reinterpret_cast<const u32x4*>(T + 8192 + h * 2048 + i * 1024 + lane * 16);
+        s.sc = *reinterpret_cast<const u32x2*>(T + 12288 + h * 512 + lane * 8);
+        s.d = *reinterpret_cast<const uint16_t*>(T + 13312 + lane * 2);
     } else {
-        const size_t blk = (size_t)row * m.nb + 4 * st;
-        const u32x4* q = reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 32);
+        const uint8_t* T = E + ((size_t)g * (m.cols / 128) + st) * 8704;
 #pragma unroll
-        for (int i = 0; i < 8; i++) s.q[i] = q[i];
-#pragma unroll
-        for (int b = 0; b < 4; b++) s.d[b] = *reinterpret_cast<const uint16_t*>(m.p[1] + e * m.estride[1] + (blk + b) * 2);
+        for (int i = 0; i < 8; i++) s.q[i] = *reinterpret_cast<const u32x4*>(T + i * 1024 + lane * 16);
+        const u32x2 d = *reinterpret_cast<const u32x2*>(T + 8192 + lane * 8);
+        s.d[0] = d.x & 0xffffu; s.d[1] = d.x >> 16; s.d[2] = d.y & 0xffffu; s.d[3] = d.y >> 16;
     }
 }
 
@@ -469,7 +538,8 @@ hipError_t launch_gmma_split(const float* x, int n, int K, int xstride, int gran
 }
 
 hipError_t launch_gmma_in(const gmma_args& a, hipStream_t s) {
-    if (!gmma_fits(a.gate, a.up, a.down) || a.K < 1 || a.K > ROUTE_K_MAX || a.cap % 4) return hipErrorInvalidValue;
+    if (!gmma_fits(a.gate, a.up, a.down) || !a.gate.tiled || !a.up.tiled || a.K < 1 || a.K > ROUTE_K_MAX || a.cap % 4)
+        return hipErrorInvalidValue;
     /* KS waves split each row group's columns: enough waves to fill the SIMDs */
     const int wpe = a.gate.rows / 64, blocks = a.E * wpe;
     const bool g16 = gmma_gran(a.down.dtype) == 16;
@@ -484,7 +554,7 @@ hipError_t launch_gmma_in(const gmma_args& a, hipStream_t s) {
 }
 
 hipError_t launch_gmma_down(const gmma_args& a, hipStream_t s) {
-    if (!gmma_fits(a.gate, a.up, a.down) || a.K < 1 || a.K > ROUTE_K_MAX || a.cap % 4) return hipErrorInvalidValue;
+    if (!gmma_fits(a.gate, a.up, a.down) || !a.down.tiled || a.K < 1 || a.K > ROUTE_K_MAX || a.cap % 4) return hipErrorInvalidValue;
     const int wpe = a.down.rows / 64, blocks = a.E * wpe;
     switch (a.down.dtype) {
     case VITNA_DTYPE_Q4_K: gmma_down_kernel<VITNA_DTYPE_Q4_K, GDN_KS><<<blocks, 64 * GDN_KS, 0, s>>>(a, wpe); return hipGetLastError();

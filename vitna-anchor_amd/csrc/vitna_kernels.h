@@ -232,6 +232,9 @@ struct gmma_args {
     int E, K, cap;
     float* ypart;          /* [n][K][H] */
 };
+/* The grouped experts' tiled copy of an expert set (kernels_gmma.hip): its size, and making it from the planes. */
+size_t gmma_tiled_bytes(const qmat& m, int n_experts);
+hipError_t launch_gmma_tile(const qmat& m, int n_experts, uint8_t* dst, hipStream_t s);
 bool gmma_fits(const qmat& gate, const qmat& up, const qmat& down);
 int gmma_gran(int dtype);
 hipError_t launch_gmma_split(const float* x, int n, int K, int xstride, int gran, uint16_t* xs, float* sums, hipStream_t s);
