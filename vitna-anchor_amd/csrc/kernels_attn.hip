@@ -333,31 +333,21 @@ __global__ __launch_bounds__(256) void attention_prepare_kernel(attn_args a) {
 
 
 /* ---- the same attention on the matrix cores (head dimension 128, up to 8 query heads a kv head) ----
-   For passes of several rows, where the cache reads are long and the vector arithmetic of the VALU kernel
-   above (a quarter of its instructions are the score and value products, the rest their reductions and
-   addressing) sets the pace. Per wave, its 16 positions of the chunk:
-     scores  S[16 positions][16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16: lane l supplies position l % 16
-             (A) and head l % 16 (B, zero past G) over dimensions 32 t + 8 (l / 16) .. + 7, t < 4, and holds
-             S[4 (l / 16) + r][l % 16];
+   The VALU kernel above spends most of its instructions on the products' reductions and addressing; here
+   both products run on v_mfma_f32_16x16x4_f32, fp32 operands and products, fp32 accumulate. Per wave, its
+   16 positions of the chunk:
+     scores  S[16 positions][16 heads] = K . Q^T: step (t, m) takes dimension 32 t + 8 (l / 16) + m of
+             position l % 16 (A) and of head l % 16 (B, zero past G); four chunk sums t < 4, added; lane l
+             holds S[4 (l / 16) + r][l % 16];
      softmax per head over the wave's positions: a lane's four, then lanes l ^ 16, l ^ 32;
-     values  O[16 heads][128] = P . V on v_mfma_f32_16x16x16_bf16, eight tiles of 16 dimensions: the scores'
-             layout is already P's A operand (head l % 16, positions 4 (l / 16) .. + 3), and lane l supplies
-             dimension 16 j + l % 16 of those four positions (B); O lands in lanes l / 16 < 2 (heads 0..7).
-   Both products take fp32 operands split into bf16 hi + lo, three MFMAs (hi hi, hi lo, lo hi), fp32
-   accumulate: about 2^-16 relative a product. The partial per (chunk, head) is the VALU kernel's, so the same
-   merge follows. */
-typedef __bf16 at_bf8 __attribute__((ext_vector_type(8)));
-typedef short at_s4 __attribute__((ext_vector_type(4)));
+     values  O[16 heads][128] = P . V, eight tiles of 16 columns: step r takes position 4 (l / 16) + r, so A
+             is the lane's own weight P[r] of head l % 16, and B its value of that position at dimension
+             VDIM(j, l % 16) (the column-to-dimension map that makes a lane's loads two float4s a position);
+             O lands in lanes l / 16 < 2 (heads 0..7).
+   The cache reads (546 MB a layer at config 3) run at about 4.7 TB/s, near what this HBM streams (a copy
+   runs at 5.1 TB/s), so the kernel is bound by them. The partial per (chunk, head) is the VALU kernel's,
+   so the same merge follows. */
 typedef float at_f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t at_u2 __attribute__((ext_vector_type(2)));
-
-/* hi = bf16(x), lo = bf16(x - hi), packed two a dword */
-__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
-    const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
-    const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
-    hi = (uint32_t)__builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-    lo = (uint32_t)__builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-}
 
 template <int G>
 __global__ __launch_bounds__(256) void attention_mma_kernel(attn_args a) {
@@ -392,22 +382,23 @@ __global__ __launch_bounds__(256) void attention_mma_kernel(attn_args a) {
 #pragma unroll
         for (int i = 0; i < 8; i++) kr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    /* values: dimension 16 j + c16 of positions t0 + 4 kq + i */
+    /* values of positions t0 + 4 kq + i: column c16 of output tile j is dimension VDIM(j, c16), so a lane's
+       dimensions of a position are two float4s and a wave's load reads whole lines (the columns of an MFMA
+       are independent: which dimension each one carries is free) */
+#define VDIM(j, c) (64 * ((j) >> 2) + 4 * (c) + ((j) & 3))
     float vv[8][4];
-    if (t0 + 15 < pos) {
-        const float* vrow = vc + (size_t)(t0 + 4 * kq) * kv_dim + (size_t)h * HD + c16;
 #pragma unroll
-        for (int j = 0; j < 8; j++)
+    for (int i = 0; i < 4; i++) {
+        const int tt = t0 + 4 * kq + i;
+        const bool ok = tt <= pos && !(fresh_block && tt == pos);
+        const float4* vrow = reinterpret_cast<const float4*>(vc + (size_t)(ok ? tt : 0) * kv_dim + (size_t)h * HD + 4 * c16);
 #pragma unroll
-            for (int i = 0; i < 4; i++) vv[j][i] = vrow[(size_t)i * kv_dim + 16 * j];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int tt = t0 + 4 * kq + i;
-            const bool ok = tt <= pos && !(fresh_block && tt == pos);
-            const float* vrow = vc + (size_t)(ok ? tt : 0) * kv_dim + (size_t)h * HD + c16;
-#pragma unroll
-            for (int j = 0; j < 8; j++) vv[j][i] = ok ? vrow[16 * j] : 0.0f;
+        for (int hh = 0; hh < 2; hh++) {
+            const float4 f = ok ? vrow[16 * hh] : make_float4(0.f, 0.f, 0.f, 0.f);
+            vv[4 * hh][i] = f.x;
+            vv[4 * hh + 1][i] = f.y;
+            vv[4 * hh + 2][i] = f.z;
+            vv[4 * hh + 3][i] = f.w;
         }
     }
 
@@ -450,36 +441,34 @@ __global__ __launch_bounds__(256) void attention_mma_kernel(attn_args a) {
         const int i = pos - t0 - 4 * kq;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float nv = nvs[16 * j + c16];
+            const float nv = nvs[VDIM(j, c16)];
 #pragma unroll
             for (int ii = 0; ii < 4; ii++)
                 if (ii == i) vv[j][ii] = nv;
         }
     }
 
-    /* scores */
-    at_f4 S = {0.f, 0.f, 0.f, 0.f};
+    /* scores on v_mfma_f32_16x16x4_f32, exact fp32 products: step (t, m) takes dimension 32 t + 8 kq + m of
+       position c16 (A) and of head c16 (B); four independent sums, one a chunk t */
+    at_f4 St[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        uint32_t ah[4], al[4], bh[4], bl[4];
-        const float4 k0 = kr[2 * t], k1 = kr[2 * t + 1];
-        split2(k0.x, k0.y, ah[0], al[0]); split2(k0.z, k0.w, ah[1], al[1]);
-        split2(k1.x, k1.y, ah[2], al[2]); split2(k1.z, k1.w, ah[3], al[3]);
         float4 q0 = make_float4(0.f, 0.f, 0.f, 0.f), q1 = q0;
         if (c16 < G) {
             q0 = reinterpret_cast<const float4*>(sq + c16 * HD + 32 * t + 8 * kq)[0];
             q1 = reinterpret_cast<const float4*>(sq + c16 * HD + 32 * t + 8 * kq)[1];
         }
-        split2(q0.x, q0.y, bh[0], bl[0]); split2(q0.z, q0.w, bh[1], bl[1]);
-        split2(q1.x, q1.y, bh[2], bl[2]); split2(q1.z, q1.w, bh[3], bl[3]);
-        const at_bf8 Ah = __builtin_bit_cast(at_bf8, u32x4{ah[0], ah[1], ah[2], ah[3]});
-        const at_bf8 Al = __builtin_bit_cast(at_bf8, u32x4{al[0], al[1], al[2], al[3]});
-        const at_bf8 Bh = __builtin_bit_cast(at_bf8, u32x4{bh[0], bh[1], bh[2], bh[3]});
-        const at_bf8 Bl = __builtin_bit_cast(at_bf8, u32x4{bl[0], bl[1], bl[2], bl[3]});
-        S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bh, S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Ah, Bl, S, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(Al, Bh, S, 0, 0, 0);
+        const float4 k0 = kr[2 * t], k1 = kr[2 * t + 1];
+        const float ka[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        const float qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        at_f4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m8 = 0; m8 < 8; m8++) c = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[m8], qa[m8], c, 0, 0, 0);
+        St[t] = c;
     }
+    at_f4 S;
+#pragma unroll
+    for (int r = 0; r < 4; r++) S[r] = (St[0][r] + St[1][r]) + (St[2][r] + St[3][r]);
     /* softmax over the wave's positions, per head (lane l % 16): position 4 kq + r of the wave */
     float m = -INFINITY;
 #pragma unroll
@@ -498,25 +487,16 @@ __global__ __launch_bounds__(256) void attention_mma_kernel(attn_args a) {
     }
     l += __shfl_xor(l, 16, WAVE);
     l += __shfl_xor(l, 32, WAVE);
-    uint32_t ph[2], pl[2];
-    split2(P[0], P[1], ph[0], pl[0]);
-    split2(P[2], P[3], ph[1], pl[1]);
-    const at_s4 Ph = __builtin_bit_cast(at_s4, at_u2{ph[0], ph[1]}), Pl = __builtin_bit_cast(at_s4, at_u2{pl[0], pl[1]});
 
-    /* values: eight tiles of 16 dimensions */
+    /* values: eight tiles of 16 dimensions (tile j, column c: dimension VDIM(j, c)) */
     at_f4 O[8];
+    /* step r takes position 4 kq + r: A is the lane's own weight P[r] of head c16, B its value vv[j][r] */
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        uint32_t vh[2], vl[2];
-        split2(vv[j][0], vv[j][1], vh[0], vl[0]);
-        split2(vv[j][2], vv[j][3], vh[1], vl[1]);
-        const at_s4 Vh = __builtin_bit_cast(at_s4, at_u2{vh[0], vh[1]}), Vl = __builtin_bit_cast(at_s4, at_u2{vl[0], vl[1]});
-        at_f4 o = {0.f, 0.f, 0.f, 0.f};
-        o = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(Ph, Vh, o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(Ph, Vl, o, 0, 0, 0);
-        o = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(Pl, Vh, o, 0, 0, 0);
-        O[j] = o;
-    }
+    for (int j = 0; j < 8; j++) O[j] = at_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) O[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(P[r], vv[j][r], O[j], 0, 0, 0);
     if (kq == 0 && c16 < G) {
         wm[wave][c16] = m;
         wl[wave][c16] = l;
@@ -527,7 +507,7 @@ __global__ __launch_bounds__(256) void attention_mma_kernel(attn_args a) {
             const int g = 4 * kq + r;
             if (g < G) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) wacc[wave][g][16 * j + c16] = O[j][r];
+                for (int j = 0; j < 8; j++) wacc[wave][g][VDIM(j, c16)] = O[j][r];
             }
         }
     }

@@ -145,8 +145,8 @@ struct attn_args {
        (launch_attention_prepare ran first: rows may share a sequence). */
     int prepared;
     float* q_out;          /* prepare: where the prepared queries go */
-    /* 1: the score and value products on the matrix cores (split bf16, about 2^-16 relative a product; head
-       dimension 128): for passes of many rows. 0: the fp32 vector kernel. */
+    /* 1: the score and value products on the fp32 matrix cores (head dimension 128). 0: the fp32 vector
+       kernel. */
     int mma;
 };
 hipError_t launch_attention(const attn_args& a, hipStream_t s);
