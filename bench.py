@@ -17,7 +17,8 @@ Prints one JSON line. Besides the step throughput it carries:
             achieved GB/s against the 8 TB/s HBM peak;
   cpu_baseline: the CPU checker's decode step (the reference's CPU arithmetic
             restated, oracle/) on this host, single-threaded, over a bounded
-            number of tokens;
+            number of tokens; cpu_baseline_mt the same with each matrix's rows
+            split over up to 16 host threads;
   configs:  the other BASELINE workloads measured on the same device (unless
             --no-extra): configs[3], 32 sequences of one new token each at
             key-value lengths drawn from U{128..8192}, one rows step (device
@@ -141,7 +142,7 @@ def main():
     copy_gbs = 2.0 * copy_bytes / copy_us / 1e3
     log("copy probe: %d MiB in %.1f us -> %.1f GB/s (read + write)" % (copy_bytes >> 20, copy_us, copy_gbs))
 
-    cpu = None
+    cpu = cpu_mt = None
     if not args.no_cpu:
         import oracle
         n, t_cpu = 0, 0.0
@@ -150,10 +151,30 @@ def main():
             oracle.step(model, 0, token, pos, threads=1, trace=False)
             t_cpu += time.perf_counter() - t1
             n += 1
+        cpu_model = "unknown"
+        try:
+            with open("/proc/cpuinfo") as f:
+                cpu_model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "unknown")
+        except OSError:
+            pass
         cpu = {"value": round(n / t_cpu, 4), "unit": "tok/s", "cores": 1, "kind": "port",
                "sample": "%d whole decode steps of the same model and position (48 layers + head), single thread, "
-                         "the reference's CPU arithmetic (AVX2 order) restated in oracle/vitna_oracle.c" % n}
+                         "the reference's CPU arithmetic (AVX2 order) restated in oracle/vitna_oracle.c" % n,
+               "cpu": cpu_model}
         log("cpu baseline: %d steps in %.1f s -> %.3f tok/s" % (n, t_cpu, n / t_cpu))
+        # the same arithmetic with each matrix's rows split over the host cores (the reference's pool pattern);
+        # 16 threads: this box's CPU share for one GPU
+        threads = max(1, min(16, os.cpu_count() or 1))
+        n2, t2 = 0, 0.0
+        while t2 < args.cpu_seconds / 2 and n2 < 40:
+            t1 = time.perf_counter()
+            oracle.step(model, 0, token, pos, threads=threads, trace=False)
+            t2 += time.perf_counter() - t1
+            n2 += 1
+        cpu_mt = {"value": round(n2 / t2, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+                  "sample": "%d whole decode steps, rows of each matrix split over %d threads (same sums in the same "
+                            "order per row)" % (n2, threads), "cpu": cpu_model}
+        log("cpu baseline, %d threads: %d steps in %.1f s -> %.3f tok/s" % (threads, n2, t2, n2 / t2))
 
     dev.close()
     extra = None
@@ -180,6 +201,7 @@ def main():
         "step_algorithmic_GBps": round(step_bytes / ms / 1e6, 1),
         "copy_probe_GBps": round(copy_gbs, 1),
         "cpu_baseline": cpu,
+        "cpu_baseline_mt": cpu_mt,
         "configs": extra,
     }
     print(json.dumps(out), flush=True)
