@@ -902,7 +902,7 @@ extern "C" bool vitna_hip_residual(struct vitna_cuda_model* g, size_t row, float
     return true;
 }
 
-static hipError_t enqueue_multi(vitna_cuda_model* g, const gemv_multi_args& m);
+static hipError_t enqueue_multi(vitna_cuda_model* g, const gemv_multi_args& m, bool imaged);
 
 extern "C" bool vitna_hip_rows_project(struct vitna_cuda_model* g, size_t layer, int which, const float* x, size_t n, float* y,
                                        char* err, size_t err_len) {
@@ -920,7 +920,7 @@ extern "C" bool vitna_hip_rows_project(struct vitna_cuda_model* g, size_t layer,
     gemv_multi_args m;
     memset(&m, 0, sizeof(m));
     m.w[0] = w; m.y[0] = dy; m.nm = 1; m.x = dx; m.n = (int)n; m.xstride = w.cols;
-    HIP_TRY(enqueue_multi(g, m), "the projection");
+    HIP_TRY(enqueue_multi(g, m, false), "the projection");
     HIP_TRY(hipStreamSynchronize(g->stream), "the projection");
     HIP_TRY(hipMemcpy(y, dy, n * w.rows * 4, hipMemcpyDeviceToHost), "copying the result");
     return true;
@@ -1292,34 +1292,53 @@ extern "C" size_t vitna_cuda_moe_rows_max(const struct vitna_cuda_model* g) { re
 /* Several rows times up to three matrices: from SKINNY_MIN rows on, on the matrix cores (kernels_skinny.hip),
    the rows split into bf16 hi and lo first; below, the multi-row GEMV. */
 #define SKINNY_MIN 4
-static hipError_t enqueue_multi(vitna_cuda_model* g, const gemv_multi_args& m) {
+static bool multi_quant(const gemv_multi_args& m) {
     bool quant = true;
     for (int i = 0; i < m.nm; i++) quant &= m.w[i].dtype != VITNA_DTYPE_F32;
-    if (m.n < SKINNY_MIN || !quant) return launch_gemv_multi(m, g->stream);
+    return quant;
+}
+/* Whether launch_skinny takes its exact-integer path for m (the operand images then replace x's split). */
+static bool multi_exact(const gemv_multi_args& m) {
+    if (m.n < SKINNY_MIN || !multi_quant(m) || m.w[0].cols % 256 || m.xstride % 4 || (uintptr_t)m.x % 16) return false;
+    for (int i = 0; i < m.nm; i++)
+        if (!m.w[i].tiled || m.w[i].cols != m.w[0].cols) return false;
+    return true;
+}
+static img_out model_img(const vitna_cuda_model* g) {
+    return img_out{(u32x4*)g->sk_img[0], (u32x4*)g->sk_img[1], (uint16_t*)g->sk_img[2], (uint16_t*)g->sk_img[3]};
+}
+
+/* imaged: the producer of m.x wrote its operand images already (when multi_exact(m)). */
+static hipError_t enqueue_multi(vitna_cuda_model* g, const gemv_multi_args& m, bool imaged) {
+    if (m.n < SKINNY_MIN || !multi_quant(m)) return launch_gemv_multi(m, g->stream);
     const int K = m.w[0].cols;
-    /* group sums for the exact-integer kernel when the width allows it */
-    const bool sums = K % 256 == 0 && m.xstride % 4 == 0 && (uintptr_t)m.x % 16 == 0;
-    hipError_t e = launch_split_rows(m.x, m.n, K, m.xstride, g->sk_xh, g->sk_xl, sums ? g->sk_img : nullptr, g->stream);
+    const bool exact = multi_exact(m);
+    hipError_t e = hipSuccess;
+    if (!exact || !imaged) e = launch_split_rows(m.x, m.n, K, m.xstride, g->sk_xh, g->sk_xl, exact ? g->sk_img : nullptr, g->stream);
     if (e != hipSuccess) return e;
     skinny_args a;
     memset(&a, 0, sizeof(a));
     for (int i = 0; i < m.nm; i++) { a.w[i] = m.w[i]; a.y[i] = m.y[i]; }
     a.nm = m.nm; a.xh = g->sk_xh; a.xl = g->sk_xl; a.n = m.n; a.add = m.add;
-    if (sums) { a.img[0] = g->sk_img[0]; a.img[1] = g->sk_img[1]; a.s32 = g->sk_img[2]; a.s16 = g->sk_img[3]; }
+    if (exact) { a.img[0] = g->sk_img[0]; a.img[1] = g->sk_img[1]; a.s32 = g->sk_img[2]; a.s16 = g->sk_img[3]; }
     a.part = g->sk_part; a.cnt = g->sk_cnt; a.part_cap = g->sk_part_cap; a.cnt_cap = g->sk_cnt_cap;
     return launch_skinny(a, g->stream);
 }
 
-static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n) {
+/* ypart: the previous layer's experts' outputs still to be added onto the residual rows (or null), added here
+   in slot order by the kernel that normalizes the rows and writes the q/k/v operands. */
+static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n, const float* ypart) {
     const dlayer& d = g->L[layer];
-    hipError_t e = launch_norm_rows(g->x, d.attn_norm, g->xn, n, g->H, g->eps, g->stream);
-    if (e != hipSuccess) return e;
     gemv_multi_args ga;
     memset(&ga, 0, sizeof(ga));
     ga.w[0] = d.q; ga.w[1] = d.k; ga.w[2] = d.v;
     ga.y[0] = g->q; ga.y[1] = g->k; ga.y[2] = g->v;
     ga.nm = 3; ga.x = g->xn; ga.n = n; ga.xstride = g->H;
-    e = enqueue_multi(g, ga);
+    const bool img = multi_exact(ga);
+    hipError_t e = launch_residual_norm(g->x, ypart, g->K, d.attn_norm, g->xn, n, g->H, g->eps,
+                                        img ? model_img(g) : img_out{nullptr, nullptr, nullptr, nullptr}, g->stream);
+    if (e != hipSuccess) return e;
+    e = enqueue_multi(g, ga, img);
     if (e != hipSuccess) return e;
     attn_args a;
     memset(&a, 0, sizeof(a));
@@ -1351,11 +1370,12 @@ static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n) 
     gemv_multi_args go;
     memset(&go, 0, sizeof(go));
     go.w[0] = d.o; go.y[0] = g->x; go.nm = 1; go.x = g->att; go.n = n; go.xstride = g->nh * g->hd; go.add = 1;
-    return enqueue_multi(g, go);
+    return enqueue_multi(g, go, false);
 }
 
-/* The grouped experts of the pass's n rows, routed as g->rt[0..n) holds it, added onto the residual rows. */
-static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n) {
+/* The grouped experts of the pass's n rows, routed as g->rt[0..n) holds it, added onto the residual rows (or,
+   defer_sum, left in g->ypart for the next kernel that reads the rows to add). */
+static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n, bool defer_sum) {
     const dlayer& d = g->L[layer];
     hipError_t e = launch_group(g->rt, n, g->E, g->K, ROWS_MAX, g->grp_count, g->grp_pairs, g->stream);
     if (e != hipSuccess) return e;
@@ -1367,7 +1387,7 @@ static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n) {
         m.E = g->E; m.K = g->K; m.cap = ROWS_MAX; m.ypart = g->ypart;
         if (e == hipSuccess) e = launch_gmma_in(m, g->stream);
         if (e == hipSuccess) e = launch_gmma_down(m, g->stream);
-        if (e == hipSuccess) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
+        if (e == hipSuccess && !defer_sum) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
         return e;
     }
     grouped_args a;
@@ -1376,17 +1396,19 @@ static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n) {
     a.E = g->E; a.K = g->K; a.cap = ROWS_MAX; a.act = g->act; a.ypart = g->ypart;
     e = launch_grouped_in(a, g->stream);
     if (e == hipSuccess) e = launch_grouped_down(a, g->stream);
-    if (e == hipSuccess) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
+    if (e == hipSuccess && !defer_sum) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
     return e;
 }
 
-static hipError_t enqueue_rows_head(vitna_cuda_model* g, int n) {
-    hipError_t e = launch_norm_rows(g->x, g->final_norm, g->xn, n, g->H, g->eps, g->stream);
-    if (e != hipSuccess) return e;
+static hipError_t enqueue_rows_head(vitna_cuda_model* g, int n, const float* ypart) {
     gemv_multi_args gh;
     memset(&gh, 0, sizeof(gh));
     gh.w[0] = g->head; gh.y[0] = g->vocab; gh.nm = 1; gh.x = g->xn; gh.n = n; gh.xstride = g->H;
-    return enqueue_multi(g, gh);
+    const bool img = multi_exact(gh);
+    hipError_t e = launch_residual_norm(g->x, ypart, g->K, g->final_norm, g->xn, n, g->H, g->eps,
+                                        img ? model_img(g) : img_out{nullptr, nullptr, nullptr, nullptr}, g->stream);
+    if (e != hipSuccess) return e;
+    return enqueue_multi(g, gh, img);
 }
 
 /* The pass's rows to the device, checked as a step checks its token (model.c:1190-1200). */
@@ -1420,7 +1442,7 @@ extern "C" bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitn
     } else if (n != (size_t)g->rows_n) {
         return fail(err, err_len, "%zu rows at layer %zu; the pass took %d at layer 0", n, layer, g->rows_n);
     }
-    hipError_t e = enqueue_rows_attention(g, (int)layer, (int)n);
+    hipError_t e = enqueue_rows_attention(g, (int)layer, (int)n, nullptr);
     if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, (int)n, g->x, g->xn, false);
     const bool nx = next && layer + 1 < (size_t)g->NL;
     if (e == hipSuccess && nx) {
@@ -1446,14 +1468,14 @@ extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t l
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
     if (!put_routing(g, n, ids, weights, k, err, err_len)) return false;
-    return check_launch(g, enqueue_rows_experts(g, (int)layer, (int)n), "the rows' experts", err, err_len);
+    return check_launch(g, enqueue_rows_experts(g, (int)layer, (int)n, false), "the rows' experts", err, err_len);
 }
 
 extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, float* const* logits, char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (!g->attention) return fail(err, err_len, "this model has no output projection");
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
-    if (!check_launch(g, enqueue_rows_head(g, (int)n), "the head", err, err_len)) return false;
+    if (!check_launch(g, enqueue_rows_head(g, (int)n, nullptr), "the head", err, err_len)) return false;
     for (size_t i = 0; i < n; i++)
         if (logits && logits[i])
             HIP_TRY(hipMemcpyAsync(logits[i], g->vocab + i * g->V, (size_t)g->V * 4, hipMemcpyDeviceToHost, g->stream), "copying logits");
@@ -1464,13 +1486,14 @@ extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, f
 /* A whole decode step of n rows on the device, routing included. */
 static hipError_t enqueue_rows_step_body(vitna_cuda_model* g, int n) {
     hipError_t e = launch_embed_rows(g->embed, g->rows_dev, n, g->x, g->stream);
+    /* each layer's experts' outputs are added onto the rows by the next layer's (or the head's) norm kernel */
     for (int l = 0; e == hipSuccess && l < g->NL; l++) {
-        e = enqueue_rows_attention(g, l, n);
+        e = enqueue_rows_attention(g, l, n, l ? g->ypart : nullptr);
         if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, n, g->x, g->xn, true);
         if (e == hipSuccess && n == 1) e = launch_topk(g->rlogits, 1, g->E, g->K, g->renorm, g->rt, g->stream);
-        if (e == hipSuccess) e = enqueue_rows_experts(g, l, n);
+        if (e == hipSuccess) e = enqueue_rows_experts(g, l, n, true);
     }
-    if (e == hipSuccess) e = enqueue_rows_head(g, n);
+    if (e == hipSuccess) e = enqueue_rows_head(g, n, g->NL ? g->ypart : nullptr);
     return e;
 }
 

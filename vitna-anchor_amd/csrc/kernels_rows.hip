@@ -21,6 +21,7 @@
  */
 
 #include "vitna_kernels.h"
+#include "skinny_image.h"
 #include <algorithm>
 
 template <int LPR>
@@ -82,6 +83,82 @@ __global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict_
 hipError_t launch_norm_rows(const float* x, const float* w, float* y, int n, int H, float eps, hipStream_t s) {
     if (n < 1 || H % 4 || H > 8192) return hipErrorInvalidValue;
     norm_rows_kernel<<<n, 256, 0, s>>>(x, w, y, H, eps);
+    return hipGetLastError();
+}
+
+/* One block a row: x += the K parts of the row in slot order (when ypart is given: the experts' outputs, as
+   reduce_rows_kernel adds them), then y = RMSNorm(x) * w, and (when img.a is given) y split into the multi-row
+   projections' operand images (skinny_image.h). Thread t takes the 8-column groups t + 256 j; the sum of
+   squares runs over a thread's columns in order, then the block's threads in wave order. */
+__global__ __launch_bounds__(256) void residual_norm_kernel(float* __restrict__ x, const float* __restrict__ ypart, int K,
+                                                            const float* __restrict__ w, float* __restrict__ y, int H, float eps,
+                                                            img_out img) {
+    const int r = blockIdx.x, t = threadIdx.x, G8 = H / 8;
+    float v[4][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int c8 = t + 256 * j;
+        if (c8 >= G8) continue;
+        float4* xp = reinterpret_cast<float4*>(x + (size_t)r * H + 8 * c8);
+        float4 a0 = xp[0], a1 = xp[1];
+        if (ypart) {
+            float s8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int k = 0; k < K; k++) {
+                const float4* yp = reinterpret_cast<const float4*>(ypart + ((size_t)r * K + k) * H + 8 * c8);
+                const float4 b0 = yp[0], b1 = yp[1];
+                s8[0] = s8[0] + b0.x; s8[1] = s8[1] + b0.y; s8[2] = s8[2] + b0.z; s8[3] = s8[3] + b0.w;
+                s8[4] = s8[4] + b1.x; s8[5] = s8[5] + b1.y; s8[6] = s8[6] + b1.z; s8[7] = s8[7] + b1.w;
+            }
+            a0.x = a0.x + s8[0]; a0.y = a0.y + s8[1]; a0.z = a0.z + s8[2]; a0.w = a0.w + s8[3];
+            a1.x = a1.x + s8[4]; a1.y = a1.y + s8[5]; a1.z = a1.z + s8[6]; a1.w = a1.w + s8[7];
+            xp[0] = a0;
+            xp[1] = a1;
+        }
+        const float e[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            v[j][i] = e[i];
+            ss = fmaf(e[i], e[i], ss);
+        }
+    }
+    __shared__ float red[4];
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int c8 = t + 256 * j;
+        if (c8 >= G8) continue; /* G8 is a multiple of 32 when images are written: every shuffle partner is active */
+        const float4* wp = reinterpret_cast<const float4*>(w + 8 * c8);
+        const float4 w0 = wp[0], w1 = wp[1];
+        const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = (v[j][i] * inv) * ww[i];
+        float4* yp = reinterpret_cast<float4*>(y + (size_t)r * H + 8 * c8);
+        yp[0] = make_float4(o[0], o[1], o[2], o[3]);
+        yp[1] = make_float4(o[4], o[5], o[6], o[7]);
+        if (img.a) {
+            u32x4 vh, vl;
+            float sum;
+            img_split8(o, vh, vl, sum);
+            img_put(img.a, img.b, r, H, c8, vh, vl);
+            const float t16 = sum + __shfl_xor(sum, 1, WAVE);
+            const float t32 = t16 + __shfl_xor(t16, 2, WAVE);
+            if (!(c8 & 1)) img_sum16(img.s16, r, H, c8 >> 1, t16);
+            if (!(c8 & 3)) img_sum32(img.s32, r, H, c8 >> 2, t32);
+        }
+    }
+}
+
+hipError_t launch_residual_norm(float* x, const float* ypart, int K, const float* w, float* y, int n, int H, float eps,
+                                const img_out& img, hipStream_t s) {
+    if (n < 1 || H % 8 || H > 8192 || (ypart && K < 1)) return hipErrorInvalidValue;
+    if (img.a && (H % 256 || !img.b || !img.s32 || !img.s16)) return hipErrorInvalidValue;
+    residual_norm_kernel<<<n, 256, 0, s>>>(x, ypart, K, w, y, H, eps, img);
     return hipGetLastError();
 }
 

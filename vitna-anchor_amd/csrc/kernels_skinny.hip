@@ -25,6 +25,7 @@
  */
 
 #include "vitna_kernels.h"
+#include "skinny_image.h"
 
 #include <algorithm>
 
@@ -49,73 +50,27 @@ __global__ void split_rows_kernel(const float* __restrict__ x, int n, int K, int
 
 __device__ __forceinline__ uint16_t bf16_bits(float v) { return __builtin_bit_cast(uint16_t, (__bf16)v); }
 
-/* S as three bf16 pieces: S = p0 + p1 + p2 to about 2^-24 relative */
-__device__ __forceinline__ void bf16x3(float S, uint16_t* d, size_t stride) {
-    const __bf16 p0 = (__bf16)S;
-    const float r0 = S - (float)p0;
-    const __bf16 p1 = (__bf16)r0;
-    d[0] = __builtin_bit_cast(uint16_t, p0);
-    d[stride] = __builtin_bit_cast(uint16_t, p1);
-    d[2 * stride] = __builtin_bit_cast(uint16_t, (__bf16)(r0 - (float)p1));
-}
-
-/*
- * Operand images for the exact-integer kernels. For each token tile tt (32 rows) and 256-column superblock b,
- * one image of 2048 pieces of 16 bytes: piece ((U * 4 + i) * 2 + hl) * 64 + lane holds the 8 columns of MFMA
- * operand i of unit U for lane half kq = lane / 32 of token 32 tt + lane % 32, bf16 hi (hl 0) or lo (1), so a
- * wave reads each operand as 1 KB in lane order. Two column orders: A (Q4_K, Q8_0) puts operand i of unit U
- * at 64 U + 16 kq + 8 (i % 2) + 32 (i / 2), B (Q6_K) at 128 (U / 2) + 32 (U % 2) + 8 kq + 16 (i % 2)
- * + 64 (i / 2). Rows past n repeat row n - 1.
- * Group sums of the split values (hi + lo, in column order), as three bf16 pieces, in the lane order of the
- * S-term operand: per window of eight groups, piece p, lane: u32x2 of groups 4 kq .. 4 kq + 3. s32 has a
- * window of 32-column groups a superblock, s16 two windows of 16-column groups.
- */
+/* The operand images of a pass (skinny_image.h): block (b, tt) takes superblock b of token tile tt, thread t
+   its 8-column groups t + 256 j; rows past n repeat row n - 1. */
 __global__ void split_image_kernel(const float* __restrict__ x, int n, int K, int xstride, u32x4* __restrict__ imga,
                                    u32x4* __restrict__ imgb, uint16_t* __restrict__ s32, uint16_t* __restrict__ s16) {
-    const int b = blockIdx.x, tt = blockIdx.y, S = K / 256;
-    const size_t base = ((size_t)tt * S + b) * 2048;
+    const int b = blockIdx.x, tt = blockIdx.y;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int item = threadIdx.x + 256 * j, l = item >> 5, c8 = item & 31, c = 8 * c8;
-        const int tok = min(32 * tt + l, n - 1);
-        const float4* src = reinterpret_cast<const float4*>(x + (size_t)tok * xstride + 256 * b + c);
+        const int item = threadIdx.x + 256 * j, l = item >> 5, c8 = 32 * b + (item & 31);
+        const int tok = min(32 * tt + l, n - 1), row = 32 * tt + l;
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)tok * xstride + 8 * c8);
         const float4 v0 = src[0], v1 = src[1];
         const float e[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        uint32_t h[4], lo[4];
-        float sum = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const __bf16 h0 = (__bf16)e[2 * k], h1 = (__bf16)e[2 * k + 1];
-            const __bf16 l0 = (__bf16)(e[2 * k] - (float)h0), l1 = (__bf16)(e[2 * k + 1] - (float)h1);
-            h[k] = __builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-            lo[k] = __builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-            sum += (float)h0 + (float)l0;
-            sum += (float)h1 + (float)l1;
-        }
-        const u32x4 vh = {h[0], h[1], h[2], h[3]}, vl = {lo[0], lo[1], lo[2], lo[3]};
-        {
-            const int U = c >> 6, r = c & 63, i = ((r >> 5) << 1) | ((r >> 3) & 1), kq = (r >> 4) & 1;
-            const size_t q = base + (size_t)((U * 4 + i) * 2) * 64 + l + 32 * kq;
-            imga[q] = vh;
-            imga[q + 64] = vl;
-        }
-        {
-            const int r = c & 127, U = 2 * (c >> 7) + ((r >> 5) & 1), i = ((r >> 4) & 1) + 2 * (r >> 6), kq = (r >> 3) & 1;
-            const size_t q = base + (size_t)((U * 4 + i) * 2) * 64 + l + 32 * kq;
-            imgb[q] = vh;
-            imgb[q + 64] = vl;
-        }
+        u32x4 vh, vl;
+        float sum;
+        img_split8(e, vh, vl, sum);
+        img_put(imga, imgb, row, K, c8, vh, vl);
         /* the 16- and 32-column sums (the pair's, then the quad's: lanes of consecutive c8, one token) */
         const float t16 = sum + __shfl_xor(sum, 1, WAVE);
         const float t32 = t16 + __shfl_xor(t16, 2, WAVE);
-        if (!(c8 & 1)) {
-            const int w = 2 * b + (c8 >> 4), gi = (c8 >> 1) & 7; /* window, group in it */
-            bf16x3(t16, s16 + (((size_t)tt * (K / 128) + w) * 3 * 64 + l + 32 * (gi >> 2)) * 4 + (gi & 3), 256);
-        }
-        if (!(c8 & 3)) {
-            const int gi = c8 >> 2;
-            bf16x3(t32, s32 + (((size_t)tt * S + b) * 3 * 64 + l + 32 * (gi >> 2)) * 4 + (gi & 3), 256);
-        }
+        if (!(c8 & 1)) img_sum16(s16, row, K, c8 >> 1, t16);
+        if (!(c8 & 3)) img_sum32(s32, row, K, c8 >> 2, t32);
     }
 }
 

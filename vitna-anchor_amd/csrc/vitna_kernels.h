@@ -160,6 +160,17 @@ hipError_t launch_attention_prepare(const attn_args& a, hipStream_t s);
 
 hipError_t launch_embed_rows(const qmat& embed, const row_rec* rows, int n, float* x, hipStream_t s);
 hipError_t launch_norm_rows(const float* x, const float* w, float* y, int n, int H, float eps, hipStream_t s);
+/* Where a pass's operand images for the multi-row projections go (skinny_image.h); a null: none. */
+struct img_out {
+    u32x4* a;
+    u32x4* b;
+    uint16_t* s32;
+    uint16_t* s16;
+};
+/* x[row] += the K parts of ypart in slot order (when ypart), y = RMSNorm(x) * w, and y's operand images when
+   img.a (H a multiple of 256 then). */
+hipError_t launch_residual_norm(float* x, const float* ypart, int K, const float* w, float* y, int n, int H, float eps,
+                                const img_out& img, hipStream_t s);
 
 /* y_i[row][r] (+)= W_i[r] . x[row] for n rows of x (row stride xstride); up to three matrices of one width. */
 struct gemv_multi_args {
