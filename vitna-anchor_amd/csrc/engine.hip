@@ -547,7 +547,9 @@ static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, 
     return launch_gemv(go, g->stream);
 }
 
-static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, int n_rows, const float* x, float* xn_out, bool topk) {
+/* sp: the grouped experts' split of xn_out, run by the top-k kernel (several rows), or null */
+static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, int n_rows, const float* x, float* xn_out, bool topk,
+                                const topk_split* sp = nullptr) {
     const dlayer& d = g->L[layer];
     route_args r;
     memset(&r, 0, sizeof(r));
@@ -560,7 +562,7 @@ static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, i
     r.eps = g->eps;
     hipError_t e = launch_route(r, g->stream);
     /* one token's top-k runs in the experts' prologue (enqueue_experts); several rows' in a kernel of its own */
-    if (e == hipSuccess && topk && n_rows > 1) e = launch_topk(logits, n_rows, g->E, g->K, g->renorm, g->rt, g->stream);
+    if (e == hipSuccess && topk && n_rows > 1) e = launch_topk(logits, n_rows, g->E, g->K, g->renorm, g->rt, g->stream, sp);
     return e;
 }
 
@@ -1364,23 +1366,26 @@ static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n, 
         a.q_raw = g->qp;
         a.prepared = 1;
     }
-    e = launch_attention(a, g->stream);
-    if (e == hipSuccess) e = launch_attention_merge(a, g->stream);
-    if (e != hipSuccess) return e;
     gemv_multi_args go;
     memset(&go, 0, sizeof(go));
     go.w[0] = d.o; go.y[0] = g->x; go.nm = 1; go.x = g->att; go.n = n; go.xstride = g->nh * g->hd; go.add = 1;
-    return enqueue_multi(g, go, false);
+    /* the merge writes the o-projection's operands too */
+    const bool oimg = multi_exact(go);
+    e = launch_attention(a, g->stream);
+    if (oimg) a.img = model_img(g);
+    if (e == hipSuccess) e = launch_attention_merge(a, g->stream);
+    if (e != hipSuccess) return e;
+    return enqueue_multi(g, go, oimg);
 }
 
 /* The grouped experts of the pass's n rows, routed as g->rt[0..n) holds it, added onto the residual rows (or,
    defer_sum, left in g->ypart for the next kernel that reads the rows to add). */
-static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n, bool defer_sum) {
+static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n, bool defer_sum, bool split_done = false) {
     const dlayer& d = g->L[layer];
     hipError_t e = launch_group(g->rt, n, g->E, g->K, ROWS_MAX, g->grp_count, g->grp_pairs, g->stream);
     if (e != hipSuccess) return e;
     if (gmma_fits(d.gate, d.up, d.down)) {
-        e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
+        if (!split_done) e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
         gmma_args m;
         m.gate = d.gate; m.up = d.up; m.down = d.down;
         m.xs = g->gm_xs; m.xsum = g->gm_xsum; m.as = g->gm_as; m.asum = g->gm_asum; m.rt = g->rt; m.count = g->grp_count; m.pairs = g->grp_pairs;
@@ -1489,9 +1494,13 @@ static hipError_t enqueue_rows_step_body(vitna_cuda_model* g, int n) {
     /* each layer's experts' outputs are added onto the rows by the next layer's (or the head's) norm kernel */
     for (int l = 0; e == hipSuccess && l < g->NL; l++) {
         e = enqueue_rows_attention(g, l, n, l ? g->ypart : nullptr);
-        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, n, g->x, g->xn, true);
+        /* several rows: the top-k kernel also splits the normed rows for the grouped experts */
+        const dlayer& d = g->L[l];
+        const bool fused_split = n > 1 && gmma_fits(d.gate, d.up, d.down);
+        const topk_split sp = {g->xn, g->gm_xs, g->gm_xsum, (int)g->H, gmma_gran(d.gate.dtype)};
+        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, n, g->x, g->xn, true, fused_split ? &sp : nullptr);
         if (e == hipSuccess && n == 1) e = launch_topk(g->rlogits, 1, g->E, g->K, g->renorm, g->rt, g->stream);
-        if (e == hipSuccess) e = enqueue_rows_experts(g, l, n, true);
+        if (e == hipSuccess) e = enqueue_rows_experts(g, l, n, true, fused_split);
     }
     if (e == hipSuccess) e = enqueue_rows_head(g, n, g->NL ? g->ypart : nullptr);
     return e;

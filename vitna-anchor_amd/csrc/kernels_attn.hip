@@ -19,6 +19,7 @@
  */
 
 #include "vitna_kernels.h"
+#include "skinny_image.h"
 
 #define GMAX 8
 
@@ -612,12 +613,34 @@ __global__ void attention_merge_kernel(attn_args a) {
         L = fmaf(fl[s], fm[s], L);
         o = fmaf(base[s * stride + d], fm[s], o);
     }
-    a.att[(size_t)row * a.n_heads * HD + (size_t)hq * HD + d] = o / L;
+    const float val = o / L;
+    a.att[(size_t)row * a.n_heads * HD + (size_t)hq * HD + d] = val;
+    if (a.img.a) {
+        /* the head's HD columns of the row into the o-projection's operand images: 8 columns a thread */
+        __shared__ float sv[128];
+        sv[d] = val;
+        __syncthreads();
+        if (d < HD / 8) {
+            float e[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) e[i] = sv[8 * d + i];
+            u32x4 vh, vl;
+            float sum;
+            img_split8(e, vh, vl, sum);
+            const int K = a.n_heads * HD, c8 = hq * (HD / 8) + d;
+            img_put(a.img.a, a.img.b, row, K, c8, vh, vl);
+            const float t16 = sum + __shfl_xor(sum, 1, WAVE);
+            const float t32 = t16 + __shfl_xor(t16, 2, WAVE);
+            if (!(c8 & 1)) img_sum16(a.img.s16, row, K, c8 >> 1, t16);
+            if (!(c8 & 3)) img_sum32(a.img.s32, row, K, c8 >> 2, t32);
+        }
+    }
 }
 
 hipError_t launch_attention_merge(const attn_args& a, hipStream_t s) {
     if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_rows < 1 || (a.hd != 64 && a.hd != 128) || a.splits_max > MERGE_MAX)
         return hipErrorInvalidValue;
+    if (a.img.a && ((a.n_heads * a.hd) % 256 || !a.img.b || !a.img.s32 || !a.img.s16)) return hipErrorInvalidValue;
     attention_merge_kernel<<<dim3(a.n_heads, a.n_rows), a.hd, 0, s>>>(a);
     return hipGetLastError();
 }

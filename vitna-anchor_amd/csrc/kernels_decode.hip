@@ -16,6 +16,7 @@
  */
 
 #include "gemv_impl.h"
+#include "gmma_split.h"
 
 /* ------------------------------------------------------------------ */
 /* Upload: GGUF blocks into planes                                     */
@@ -363,15 +364,29 @@ __global__ void route_check_kernel(const float* __restrict__ logits, int E, int 
     if (threadIdx.x < sizeof(route_out) / 4) reinterpret_cast<int32_t*>(out)[threadIdx.x] = reinterpret_cast<const int32_t*>(&o)[threadIdx.x];
 }
 
-/* One wave a row: the routing of n_rows rows of logits (row stride E) into out. */
-__global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ logits, int E, int K, int renorm, route_out* out) {
+/* One wave a row: the routing of n_rows rows of logits (row stride E) into out; with sp.xs, then the row's
+   split for the grouped experts (gmma_split.h, runs of G columns). */
+template <int G>
+__global__ __launch_bounds__(64) void topk_kernel(const float* __restrict__ logits, int E, int K, int renorm, route_out* out,
+                                                  topk_split sp) {
     __shared__ float slg[ROUTE_E_MAX];
-    wave_route(logits + (size_t)blockIdx.x * E, E, K, renorm, out + blockIdx.x, slg);
+    const int r = blockIdx.x;
+    wave_route(logits + (size_t)r * E, E, K, renorm, out + r, slg);
+    if constexpr (G > 0)
+        for (int g = threadIdx.x; g < sp.H / G; g += 64)
+            gsplit_run<G>(sp.x + (size_t)r * sp.H, sp.H, g, sp.xs + (size_t)r * 2 * sp.H, sp.sums + (size_t)r * (sp.H / G));
 }
 
-hipError_t launch_topk(const float* logits, int n_rows, int E, int K, int renorm, route_out* out, hipStream_t s) {
+hipError_t launch_topk(const float* logits, int n_rows, int E, int K, int renorm, route_out* out, hipStream_t s, const topk_split* sp) {
     if (n_rows < 1 || E < 1 || E > ROUTE_E_MAX || E % 4 || K < 1 || K > ROUTE_K_MAX || K > E) return hipErrorInvalidValue;
-    topk_kernel<<<n_rows, 64, 0, s>>>(logits, E, K, renorm, out);
+    const topk_split none = {nullptr, nullptr, nullptr, 0, 0};
+    if (sp && sp->xs) {
+        if (sp->H % sp->gran || (sp->gran != 16 && sp->gran != 32)) return hipErrorInvalidValue;
+        if (sp->gran == 32) topk_kernel<32><<<n_rows, 64, 0, s>>>(logits, E, K, renorm, out, *sp);
+        else topk_kernel<16><<<n_rows, 64, 0, s>>>(logits, E, K, renorm, out, *sp);
+    } else {
+        topk_kernel<0><<<n_rows, 64, 0, s>>>(logits, E, K, renorm, out, none);
+    }
     return hipGetLastError();
 }
 

@@ -42,6 +42,7 @@
  */
 
 #include "vitna_kernels.h"
+#include "gmma_split.h"
 
 #include <type_traits>
 #include <utility>
@@ -109,25 +110,7 @@ template <int G>
 __global__ void gsplit_kernel(const float* __restrict__ x, int K, int xstride, uint16_t* __restrict__ xs, float* __restrict__ sums) {
     const int r = blockIdx.y, g = blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= K / G) return;
-    const float* src = x + (size_t)r * xstride + g * G;
-    uint16_t* dst = xs + (size_t)r * 2 * K + 2 * G * g;
-    float s = 0.0f;
-#pragma unroll
-    for (int c = 0; c < G / 4; c++) {
-        const float4 v = reinterpret_cast<const float4*>(src)[c];
-        const float e[4] = {v.x, v.y, v.z, v.w};
-        uint32_t hb[4], lb[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const __bf16 h = (__bf16)e[i];
-            const __bf16 l = (__bf16)(e[i] - (float)h);
-            hb[i] = __builtin_bit_cast(uint16_t, h);
-            lb[i] = __builtin_bit_cast(uint16_t, l);
-            s += (float)h + (float)l;
-        }
-        reinterpret_cast<u32x4*>(dst)[c] = u32x4{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16)};
-    }
-    sums[(size_t)r * (K / G) + g] = s;
+    gsplit_run<G>(x + (size_t)r * xstride, K, g, xs + (size_t)r * 2 * K, sums + (size_t)r * (K / G));
 }
 
 /* ---- one 128-column step of a lane's weight row ------------------------- */

@@ -56,7 +56,16 @@ hipError_t launch_route(const route_args& a, hipStream_t s);
 hipError_t launch_route_check(const float* logits, int E, int K, int renorm, route_out* out, hipStream_t s);
 
 /* The routing of n_rows rows of logits (row stride E), one wave a row. */
-hipError_t launch_topk(const float* logits, int n_rows, int E, int K, int renorm, route_out* out, hipStream_t s);
+/* The grouped experts' split of the routed rows (gmma_split.h), run by the routing kernel: x rows of H floats
+   into xs and sums, runs of gran columns; xs null: none. */
+struct topk_split {
+    const float* x;
+    uint16_t* xs;
+    float* sums;
+    int H, gran;
+};
+hipError_t launch_topk(const float* logits, int n_rows, int E, int K, int renorm, route_out* out, hipStream_t s,
+                       const topk_split* sp = nullptr);
 
 /* ---- experts, one token ---- */
 
@@ -122,6 +131,14 @@ struct row_rec {
    sum, weighted values) in partial; launch_attention_merge combines them into
    att. */
 #define ATTN_CHUNK 64
+/* Where a pass's operand images for the multi-row projections go (skinny_image.h); a null: none. */
+struct img_out {
+    u32x4* a;
+    u32x4* b;
+    uint16_t* s32;
+    uint16_t* s16;
+};
+
 struct attn_args {
     const float* q_raw;    /* [n_rows][n_heads * hd] */
     const float* k_raw;    /* [n_rows][n_kv * hd] */
@@ -148,6 +165,8 @@ struct attn_args {
     /* 1: the score and value products on the fp32 matrix cores (head dimension 128). 0: the fp32 vector
        kernel. */
     int mma;
+    /* merge: att's operand images for the o-projection too, when img.a (n_heads * hd a multiple of 256) */
+    img_out img;
 };
 hipError_t launch_attention(const attn_args& a, hipStream_t s);
 /* The chunks' partials of every (row, query head) combined into att. */
@@ -160,13 +179,6 @@ hipError_t launch_attention_prepare(const attn_args& a, hipStream_t s);
 
 hipError_t launch_embed_rows(const qmat& embed, const row_rec* rows, int n, float* x, hipStream_t s);
 hipError_t launch_norm_rows(const float* x, const float* w, float* y, int n, int H, float eps, hipStream_t s);
-/* Where a pass's operand images for the multi-row projections go (skinny_image.h); a null: none. */
-struct img_out {
-    u32x4* a;
-    u32x4* b;
-    uint16_t* s32;
-    uint16_t* s16;
-};
 /* x[row] += the K parts of ypart in slot order (when ypart), y = RMSNorm(x) * w, and y's operand images when
    img.a (H a multiple of 256 then). */
 hipError_t launch_residual_norm(float* x, const float* ypart, int K, const float* w, float* y, int n, int H, float eps,
