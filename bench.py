@@ -1,7 +1,7 @@
 """Benchmark: Qwen3-30B-A3B-shaped Q4_K_M batch-1 decode on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
-    python bench.py --only 3|4 [--steps K]     one of the other configs alone (profiling)
+    python bench.py --only 0|1|3|4 [--steps K] one of the other configs alone (profiling)
 
 Workload: a full 48-layer Qwen3-30B-A3B-shaped model
 with seeded random weights (Q4_K gate/up/q/k/o, Q6_K down/v/LM head, Q4_K
@@ -62,7 +62,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-extra", action="store_true", help="measure configs[2] only")
-    ap.add_argument("--only", choices=["3", "4"], help="run one of the other configs alone (profiling) and print its object")
+    ap.add_argument("--only", choices=["0", "1", "3", "4"], help="run one of the other configs alone (profiling) and print its object")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU). "
@@ -72,7 +72,9 @@ def main():
     import vitna_amd as va
 
     if args.only:
-        if args.only == "4":
+        if args.only in ("0", "1"):
+            res = bench_layer(va, int(args.only), reps=args.steps)
+        elif args.only == "4":
             res = bench_prefill(va, reps=args.steps)
         else:
             model = va.Model(va.shape(n_layers=args.layers, ctx=8193, seqs=32, kv_host=0), 20260101, threads=16)
@@ -185,6 +187,8 @@ def main():
         extra = {"3": bench_ragged(va, model, dev, args.steps)}
         dev.close()
         extra["4"] = bench_prefill(va)
+        extra["0"] = bench_layer(va, 0)
+        extra["1"] = bench_layer(va, 1)
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -231,6 +235,36 @@ def bench_ragged(va, model, dev, steps, reps=None):
             "kv_positions": int(np.sum(lengths)),
             "est_GBps": round((kv_bytes + expert_bytes + 5.2258e8 + 5.0332e7 + 2.5525e8) / ms / 1e6, 1),
             "est_note": "key-value bytes exact; expert bytes for the expected %.1f distinct experts a layer" % uniq}
+
+
+def bench_layer(va, c, reps=20):
+    """configs[0] / [1]: one MoE layer of one token (norm, router, top-k, experts, weighted sum), batch 1. The
+    model holds `copies` distinct layers, more weight than the 256 MB MALL, timed one after another in one graph,
+    so each layer's experts stream from HBM as in a real step."""
+    copies = 8 if c == 0 else 12
+    model = va.Model(va.shape(**dict(va.CONFIGS[c], n_layers=copies)), 20260100 + c, threads=16)
+    dev = va.Device(model)
+    try:
+        cfg = model.cfg
+        x = va.normal(7, 1, cfg.hidden).astype(np.float32)
+        dev.set_residual(x)
+        us = dev.time_ffn(reps)
+        e0 = model.m.layers[0].experts[0]
+        expert_bytes = sum(va.row_bytes(m.dtype, m.cols) * m.rows for m in (e0.gate, e0.up, e0.down))
+        b = cfg.n_experts_used * expert_bytes + cfg.n_experts * cfg.hidden * 4
+        gbs = b / us / 1e3
+        log("configs[%d]: one MoE layer %.2f us (%d layers cycled), %d bytes -> %.1f GB/s" % (c, us, copies, b, gbs))
+        name = ("BASELINE configs[0]: OLMoE-1B-7B-shaped MoE layer, batch 1, Q8_0, 64 experts top-8" if c == 0 else
+                "BASELINE configs[1]: Qwen3-30B-A3B-shaped MoE layer, batch 1, Q4_K gate/up, Q6_K down, 128 experts top-8")
+        return {"workload": name, "value": round(1e6 / us, 1), "unit": "MoE layers/s (one token)", "us": round(us, 3),
+                "layers_cycled": copies, "bytes_per_layer": b,
+                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(gbs / HBM_PEAK_GBS, 4),
+                             "note": "the 8 chosen experts' gate, up and down plus the fp32 router, over the whole "
+                                     "layer (norm, router, top-k, experts, sum: three launches)"}}
+    finally:
+        dev.close()
+        model.free()
 
 
 def bench_prefill(va, reps=10):

@@ -216,6 +216,12 @@ bool vitna_hip_prefill_rows(struct vitna_cuda_model* g, size_t n, float* x_in, f
 bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int reps, int warmup, double* avg_us, double* bytes, char* err,
                            size_t err_len);
 
+/** Timing: every layer's mixture-of-experts half (norm, router, top-k, experts, weighted sum) on residual row 0,
+    one after another in one graph, reps times after two warm-up passes; *us_per_layer the mean per layer. A
+    model of distinct layers larger than the MALL measures streaming from HBM (configs 0 and 1 of the
+    benchmark). No counterpart in the reference. */
+bool vitna_hip_time_ffn(struct vitna_cuda_model* g, int reps, double* us_per_layer, char* err, size_t err_len);
+
 /** steps device-resident decode steps (as vitna_hip_moe_step_async, the
     same token and position each time) timed with HIP events on the model's
     stream: the average milliseconds a step. */

@@ -1245,6 +1245,39 @@ extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int
     return true;
 }
 
+extern "C" bool vitna_hip_time_ffn(struct vitna_cuda_model* g, int reps, double* us_per_layer, char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (reps < 1) return fail(err, err_len, "at least one repetition");
+    /* every layer's mixture-of-experts half on residual row 0, one after another, captured once */
+    HIP_TRY(hipStreamSynchronize(g->stream), "before capturing the layers");
+    HIP_TRY(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "capturing the layers");
+    hipError_t e = hipSuccess;
+    for (int l = 0; e == hipSuccess && l < g->NL; l++) {
+        e = enqueue_route(g, l, g->rlogits, 1, g->x, g->xn, true);
+        if (e == hipSuccess) e = enqueue_experts(g, l, g->rlogits, g->x, 1);
+    }
+    hipGraph_t graph = nullptr;
+    const hipError_t e2 = hipStreamEndCapture(g->stream, &graph);
+    if (e != hipSuccess) { if (graph) hipGraphDestroy(graph); return check_launch(g, e, "capturing the layers", err, err_len); }
+    HIP_TRY(e2, "ending the capture of the layers");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e3 = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    HIP_TRY(e3, "instantiating the layers' graph");
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    bool ok = hipGraphLaunch(exec, g->stream) == hipSuccess && hipGraphLaunch(exec, g->stream) == hipSuccess &&
+              hipEventCreate(&t0) == hipSuccess && hipEventCreate(&t1) == hipSuccess && hipEventRecord(t0, g->stream) == hipSuccess;
+    for (int i = 0; ok && i < reps; i++) ok = hipGraphLaunch(exec, g->stream) == hipSuccess;
+    float ms = 0;
+    ok = ok && hipEventRecord(t1, g->stream) == hipSuccess && hipEventSynchronize(t1) == hipSuccess && hipEventElapsedTime(&ms, t0, t1) == hipSuccess;
+    if (t0) hipEventDestroy(t0);
+    if (t1) hipEventDestroy(t1);
+    hipGraphExecDestroy(exec);
+    if (!ok) return fail(err, err_len, "timing the layers failed");
+    *us_per_layer = 1000.0 * ms / ((double)reps * g->NL);
+    return true;
+}
+
 extern "C" bool vitna_hip_route_check(const float* logits, int n_experts, int k, bool renormalize, int32_t* chosen, int32_t* ids,
                                       float* weights, char* err, size_t err_len) {
     if (!logits || n_experts < 1 || n_experts > ROUTE_E_MAX || n_experts % 4 || k < 1 || k > ROUTE_K_MAX || k > n_experts)

@@ -250,6 +250,7 @@ def _hip():
                                              _FP, *E]),
         "vitna_hip_copy_probe": (C.c_bool, [C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_steps": (C.c_bool, [P, C.c_size_t, C.c_int32, C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
+        "vitna_hip_time_ffn": (C.c_bool, [P, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_kernel": (C.c_bool, [P, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double),
                                              C.POINTER(C.c_double), *E]),
     }
@@ -444,6 +445,12 @@ class Device:
         b = C.c_double()
         self._ok(self.lib.vitna_hip_time_kernel(self.g, which, reps, warmup, C.byref(us), C.byref(b), self.err, 512))
         return us.value, b.value
+
+    def time_ffn(self, reps):
+        """Mean microseconds of one layer's mixture-of-experts half, every layer in turn in one graph."""
+        us = C.c_double()
+        self._ok(self.lib.vitna_hip_time_ffn(self.g, reps, C.byref(us), self.err, 512))
+        return us.value
 
     def time_steps(self, seq, token, pos, steps):
         ms = C.c_double()
