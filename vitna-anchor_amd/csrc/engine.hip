@@ -73,6 +73,7 @@ struct vitna_cuda_model {
     bool rows_graph_shared;
     hipGraphExec_t step_graph;
     bool graph_ready;
+    bool tiled_ready;           /* the multi-row paths' tiled copies made (ensure_tiled) */
     bool lost;
     size_t fast_rows, long_from;
     int rows_n;         /* rows of the pass in flight (vitna_cuda_moe_rows_*) */
@@ -283,6 +284,32 @@ static bool make_tiled(vitna_cuda_model* g, qmat* m, const char* what, char* err
     return true;
 }
 
+/* The tiled copies only the multi-row paths read (the dense matrices' for the projections, the experts' for the
+   grouped experts), made on the first multi-row call, before any graph is captured: a model that only decodes
+   never holds them. */
+static bool ensure_tiled(vitna_cuda_model* g, char* err, size_t err_len) {
+    if (g->tiled_ready) return true;
+    for (int l = 0; l < g->NL; l++) {
+        dlayer& d = g->L[l];
+        if (g->attention && !(make_tiled(g, &d.q, "q", err, err_len) && make_tiled(g, &d.k, "k", err, err_len) &&
+                              make_tiled(g, &d.v, "v", err, err_len) && make_tiled(g, &d.o, "o", err, err_len)))
+            return false;
+        if (gmma_fits(d.gate, d.up, d.down)) {
+            qmat* sets[3] = {&d.gate, &d.up, &d.down};
+            for (int i = 0; i < 3; i++) {
+                uint8_t* t;
+                if (!dalloc(g, &t, gmma_tiled_bytes(*sets[i], g->E), "the experts' tiled copy", err, err_len)) return false;
+                HIP_TRY(launch_gmma_tile(*sets[i], g->E, t, g->stream), "tiling the experts");
+                HIP_TRY(hipStreamSynchronize(g->stream), "tiling the experts");
+                sets[i]->tiled = t;
+            }
+        }
+    }
+    if (g->attention && !make_tiled(g, &g->head, "the output projection", err, err_len)) return false;
+    g->tiled_ready = true;
+    return true;
+}
+
 extern "C" bool vitna_cuda_probe(char* err, size_t err_len) {
     int n = 0;
     const hipError_t e = hipGetDeviceCount(&n);
@@ -401,24 +428,11 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
         ok = ok && upload_set(g, mats.data(), E, d.up, staging, staging_bytes, err, err_len);
         for (size_t e = 0; ok && e < E; e++) mats[e] = &L->experts[e].down;
         ok = ok && upload_set(g, mats.data(), E, d.down, staging, staging_bytes, err, err_len);
-        /* the grouped experts' tiled copies (read by the rows path; the decode kernels read the planes) */
-        if (ok && gmma_fits(d.gate, d.up, d.down)) {
-            qmat* sets[3] = {&d.gate, &d.up, &d.down};
-            for (int i = 0; ok && i < 3; i++) {
-                uint8_t* t;
-                ok = dalloc(g, &t, gmma_tiled_bytes(*sets[i], (int)E), "the experts' tiled copy", err, err_len);
-                if (ok && (launch_gmma_tile(*sets[i], (int)E, t, g->stream) != hipSuccess || hipStreamSynchronize(g->stream) != hipSuccess))
-                    ok = fail(err, err_len, "tiling the experts");
-                if (ok) sets[i]->tiled = t;
-            }
-        }
         if (ok && g->attention) {
             ok = upload_matrix(g, &d.q, &L->q, staging, staging_bytes, "q", err, err_len) &&
                  upload_matrix(g, &d.k, &L->k, staging, staging_bytes, "k", err, err_len) &&
                  upload_matrix(g, &d.v, &L->v, staging, staging_bytes, "v", err, err_len) &&
                  upload_matrix(g, &d.o, &L->o, staging, staging_bytes, "o", err, err_len) &&
-                 make_tiled(g, &d.q, "q", err, err_len) && make_tiled(g, &d.k, "k", err, err_len) &&
-                 make_tiled(g, &d.v, "v", err, err_len) && make_tiled(g, &d.o, "o", err, err_len) &&
                  upload_f32(g, &d.attn_norm, L->attn_norm, c->hidden, "the attention norm", err, err_len);
             if (ok && c->qk_norm)
                 ok = upload_f32(g, &d.q_norm, L->q_norm, c->head_dim, "the q norm", err, err_len) &&
@@ -428,7 +442,6 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
     if (ok && g->attention) {
         ok = upload_matrix(g, &g->embed, &m->embed, staging, staging_bytes, "the embedding", err, err_len) &&
              upload_matrix(g, &g->head, &m->lm_head, staging, staging_bytes, "the output projection", err, err_len) &&
-             make_tiled(g, &g->head, "the output projection", err, err_len) &&
              upload_f32(g, &g->final_norm, m->final_norm, c->hidden, "the final norm", err, err_len);
         const size_t half = c->head_dim / 2;
         ok = ok && upload_f32(g, &g->cos_tab, cos_tab, m->ctx * half, "the rotary cosines", err, err_len) &&
@@ -909,6 +922,7 @@ static hipError_t enqueue_multi(vitna_cuda_model* g, const gemv_multi_args& m, b
 extern "C" bool vitna_hip_rows_project(struct vitna_cuda_model* g, size_t layer, int which, const float* x, size_t n, float* y,
                                        char* err, size_t err_len) {
     if (!g) return fail(err, err_len, "no model");
+    if (!ensure_tiled(g, err, err_len)) return false;
     if (!g->attention) return fail(err, err_len, "the model has no attention projections");
     if (n < 1 || n > ROWS_MAX) return fail(err, err_len, "%zu rows: 1 .. %d", n, ROWS_MAX);
     if (which < 0 || which > 4 || (which < 4 && layer >= (size_t)g->NL)) return fail(err, err_len, "no such projection");
@@ -1472,6 +1486,7 @@ static bool set_rows(vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n
 extern "C" bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, size_t layer, float* logits,
                                           float* next, char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!ensure_tiled(g, err, err_len)) return false;
     if (!g->attention) return fail(err, err_len, "this model has no attention");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (layer == 0) {
@@ -1503,6 +1518,7 @@ extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t l
                                             size_t k, const int32_t* guess, char* err, size_t err_len) {
     (void)guess;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!ensure_tiled(g, err, err_len)) return false;
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
     if (!put_routing(g, n, ids, weights, k, err, err_len)) return false;
@@ -1511,6 +1527,7 @@ extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t l
 
 extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, float* const* logits, char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!ensure_tiled(g, err, err_len)) return false;
     if (!g->attention) return fail(err, err_len, "this model has no output projection");
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
     if (!check_launch(g, enqueue_rows_head(g, (int)n, nullptr), "the head", err, err_len)) return false;
@@ -1540,6 +1557,7 @@ static hipError_t enqueue_rows_step_body(vitna_cuda_model* g, int n) {
 }
 
 static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_len) {
+    if (!ensure_tiled(g, err, err_len)) return false;
     if (g->rows_graph_n == n && g->rows_graph_shared == g->rows_shared_seq) return true;
     if (g->rows_graph_n) {
         HIP_TRY(hipStreamSynchronize(g->stream), "before recapturing the rows step");
