@@ -19,7 +19,11 @@ REL = 1e-3
 
 
 def model_with_cache(name, seed, prefill, seqs):
-    spec = dict(SMALL[name], seqs=seqs)
+    return model_with_cache_spec(dict(SMALL[name]), seed, prefill, seqs)
+
+
+def model_with_cache_spec(spec, seed, prefill, seqs):
+    spec = dict(spec, seqs=seqs)
     model = va.Model(va.shape(**spec), seed)
     cfg = model.cfg
     kd = cfg.n_kv_heads * cfg.head_dim
@@ -215,6 +219,61 @@ def test_rows_projections_isolated(name):
                 worst = max(worst, r)
                 assert r <= 2e-5, (which, n, r)
         say("  worst rel err", worst)
+    finally:
+        dev.close()
+        model.free()
+
+
+NARROW = dict(n_layers=2, hidden=256, intermediate=256, n_heads=2, n_kv_heads=1, head_dim=64, vocab=300, n_experts=8,
+              n_experts_used=2, renormalize=0, rms_eps=1e-5, rope_theta=10000.0, dt_gate_up=va.Q8_0, dt_down=va.Q8_0,
+              dt_q=va.Q8_0, dt_k=va.Q8_0, dt_v=va.Q8_0, dt_o=va.Q8_0, dt_head=va.Q8_0, dt_embed=va.Q8_0, norm_std=0.1,
+              ctx=40, kv_host=1)
+
+
+def test_rows_narrow_fallbacks():
+    """An o-projection width that is not a multiple of 256 (2 heads x 64 = 128) takes the kernel that widens and
+    splits each weight; head dimension 64 takes the fp32 vector attention. A rows step of 6 sequences against the
+    CPU checker, and each projection alone (q, k, v and the head on the exact-integer kernel, o on the fallback)
+    against the oracle in float64."""
+    say("rows narrow fallbacks")
+    seqs = 6
+    prefill = [3, 17, 9, 30, 1, 22]
+    model, dev = model_with_cache_spec(dict(NARROW), 3131, [p + 1 for p in prefill], seqs)
+    try:
+        rows = [(13 * s + 5, prefill[s] - 1, s) for s in range(seqs)]
+        ref = cpu_rows(model, rows)
+        logits = dev.rows_step(rows)
+        worst = max(rel(logits[i], ref[i][0]) for i in range(seqs))
+        say("  rows step max rel err", worst)
+        assert worst <= REL
+        rng = np.random.RandomState(11)
+        for which in range(5):
+            mat = _matrix(model, 0, which)
+            W = oracle.widen(mat.bytes(), mat.dtype, mat.rows * mat.cols).reshape(mat.rows, mat.cols).astype(np.float64)
+            x = rng.standard_normal((7, mat.cols)).astype(np.float32)
+            y = dev.rows_project(0, which, x)
+            ref_y = x.astype(np.float64) @ W.T
+            r = float(np.max(np.abs(y - ref_y)) / np.max(np.abs(ref_y)))
+            assert r <= 2e-5, (which, r)
+    finally:
+        dev.close()
+        model.free()
+
+
+@pytest.mark.parametrize("n", [1, 2, 3])
+def test_rows_step_few_rows(n):
+    """Passes of fewer than four rows take the multi-row GEMV for the projections (the matrix-core kernels start at
+    four): a rows step of n sequences against the CPU checker."""
+    say("rows step few rows", n)
+    prefill = [12, 40, 5][:n]
+    model, dev = model_with_cache("q4km", 600 + n, [p + 1 for p in prefill], n)
+    try:
+        rows = [(3 * s + 7, prefill[s] - 1, s) for s in range(n)]
+        ref = cpu_rows(model, rows)
+        logits = dev.rows_step(rows)
+        worst = max(rel(logits[i], ref[i][0]) for i in range(n))
+        say("  max rel err", worst)
+        assert worst <= REL
     finally:
         dev.close()
         model.free()

@@ -1431,23 +1431,15 @@ static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n, bo
     const dlayer& d = g->L[layer];
     hipError_t e = launch_group(g->rt, n, g->E, g->K, ROWS_MAX, g->grp_count, g->grp_pairs, g->stream);
     if (e != hipSuccess) return e;
-    if (gmma_fits(d.gate, d.up, d.down)) {
-        if (!split_done) e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
-        gmma_args m;
-        m.gate = d.gate; m.up = d.up; m.down = d.down;
-        m.xs = g->gm_xs; m.xsum = g->gm_xsum; m.as = g->gm_as; m.asum = g->gm_asum; m.rt = g->rt; m.count = g->grp_count; m.pairs = g->grp_pairs;
-        m.E = g->E; m.K = g->K; m.cap = ROWS_MAX; m.ypart = g->ypart;
-        if (e == hipSuccess) e = launch_gmma_in(m, g->stream);
-        if (e == hipSuccess) e = launch_gmma_down(m, g->stream);
-        if (e == hipSuccess && !defer_sum) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
-        return e;
-    }
-    grouped_args a;
-    a.gate = d.gate; a.up = d.up; a.down = d.down;
-    a.xn = g->xn; a.rt = g->rt; a.count = g->grp_count; a.pairs = g->grp_pairs;
-    a.E = g->E; a.K = g->K; a.cap = ROWS_MAX; a.act = g->act; a.ypart = g->ypart;
-    e = launch_grouped_in(a, g->stream);
-    if (e == hipSuccess) e = launch_grouped_down(a, g->stream);
+    /* every expert set check_shapes accepts (quantized, widths multiples of 256) fits the matrix-core kernels */
+    if (!gmma_fits(d.gate, d.up, d.down)) return hipErrorInvalidValue;
+    if (!split_done) e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
+    gmma_args m;
+    m.gate = d.gate; m.up = d.up; m.down = d.down;
+    m.xs = g->gm_xs; m.xsum = g->gm_xsum; m.as = g->gm_as; m.asum = g->gm_asum; m.rt = g->rt; m.count = g->grp_count; m.pairs = g->grp_pairs;
+    m.E = g->E; m.K = g->K; m.cap = ROWS_MAX; m.ypart = g->ypart;
+    if (e == hipSuccess) e = launch_gmma_in(m, g->stream);
+    if (e == hipSuccess) e = launch_gmma_down(m, g->stream);
     if (e == hipSuccess && !defer_sum) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
     return e;
 }

@@ -6,10 +6,10 @@
  * weights read once for all the rows routed to it.
  *
  * Reference counterparts (engine/src/model_cuda.cu): the host counting sort
- * of (row, expert) pairs :5151-5176, gather_rows_kernel :2059,
- * experts_in_rows_kernel :2071, experts_down_rows_kernel :2101,
- * add_rows_kernel :2120, norm_rows_kernel :2020, embed_multi_kernel :1858,
- * the *_multi kernels :1872-2006.
+ * of (row, expert) pairs :5151-5176, add_rows_kernel :2120,
+ * norm_rows_kernel :2020, embed_multi_kernel :1858, the *_multi kernels
+ * :1872-2006. The grouped experts themselves are kernels_gmma.hip's
+ * (experts_in_rows_kernel :2071, experts_down_rows_kernel :2101).
  *
  * The grouping is built on the device (group_kernel): one block per expert
  * scans every row's routing and lists the (row, slot) pairs routed to it in
@@ -287,161 +287,6 @@ hipError_t launch_group(const route_out* rt, int n, int E, int K, int cap, int* 
     if (n < 1 || n > cap || E < 1 || K < 1 || K > ROUTE_K_MAX) return hipErrorInvalidValue;
     group_kernel<<<E, 256, 0, s>>>(rt, n, K, cap, count, pairs);
     return hipGetLastError();
-}
-
-/* ---- grouped experts -------------------------------------------------- */
-
-/* Units (expert, weight row); a wave takes a unit's gate and up slices once
-   and applies them to every row routed to the expert:
-   act[row * K + slot][r] = silu(gate_e[r] . xn[row]) * (up_e[r] . xn[row]). */
-template <int DT, int LPR, int SPL>
-__global__ __launch_bounds__(256) void grouped_in_kernel(grouped_args a) {
-    constexpr int RPW = WAVE / LPR;
-    const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
-    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
-    const int I = a.gate.rows, H = a.gate.cols;
-    const int upe = (I + RPW - 1) / RPW; /* units an expert */
-    for (int u = wave; u < a.E * upe; u += nwaves) {
-        const int e = u / upe, r = (u - e * upe) * RPW + sub;
-        const int c = a.count[e];
-        if (c == 0) continue;
-        const int rr = r < I ? r : I - 1;
-        qraw g[SPL], v[SPL];
-#pragma unroll
-        for (int j = 0; j < SPL; j++) {
-            slice_load<DT>(a.gate, e, rr, al + LPR * j, g[j]);
-            slice_load<DT>(a.up, e, rr, al + LPR * j, v[j]);
-        }
-        for (int i = 0; i < c; i++) {
-            const int pr = a.pairs[(size_t)e * a.cap + i], row = pr / ROUTE_K_MAX, slot = pr % ROUTE_K_MAX;
-            float pg = 0.f, pu = 0.f;
-#pragma unroll
-            for (int j = 0; j < SPL; j++) {
-                xslice xs;
-                load_xslice(DT, al + LPR * j, a.xn + (size_t)row * H, xs);
-                pg += slice_dot<DT>(g[j], al + LPR * j, xs);
-                pu += slice_dot<DT>(v[j], al + LPR * j, xs);
-            }
-            pg = rsum<LPR>(pg);
-            pu = rsum<LPR>(pu);
-            if (al == 0 && r < I) {
-                const float den = 1.0f + expf(-pg);
-                a.act[((size_t)row * a.K + slot) * I + r] = (pg / den) * pu;
-            }
-        }
-    }
-}
-
-/* A down wave takes one expert and up to UMAX of its output rows (units): all of their slices are requested
-   at once, then applied to the rows routed to the expert, GB rows' activations at a time; wpe waves an expert
-   cover its rows. */
-#define GB 2
-
-/* ypart[row * K + slot][r] = w_slot * (down_e[r] . act[row * K + slot]): the down row's slices (S = I / 32 of
-   them, among LPR lanes). */
-template <int DT, int LPR, int SPL, int UMAX>
-__global__ __launch_bounds__(256) void grouped_down_kernel(grouped_args a, int wpe) {
-    constexpr int RPW = WAVE / LPR;
-    const int lane = threadIdx.x & 63, sub = lane / LPR, al = lane % LPR;
-    const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
-    const int e = wave / wpe, part = wave % wpe;
-    if (e >= a.E) return;
-    const int c = a.count[e];
-    if (c == 0) return;
-    const int H = a.down.rows, I = a.down.cols, S = I / 32;
-    const int upe = (H + RPW - 1) / RPW;
-    const int u0 = part * UMAX, nu = min(UMAX, upe - u0);
-    if (nu <= 0) return;
-    bool on[SPL];
-#pragma unroll
-    for (int j = 0; j < SPL; j++) on[j] = al + LPR * j < S;
-    qraw q[UMAX][SPL];
-#pragma unroll
-    for (int k = 0; k < UMAX; k++) {
-        if (k >= nu) break;
-        const int r = min((u0 + k) * RPW + sub, H - 1);
-#pragma unroll
-        for (int j = 0; j < SPL; j++) slice_load<DT>(a.down, e, r, on[j] ? al + LPR * j : 0, q[k][j]);
-    }
-    for (int b0 = 0; b0 < c; b0 += GB) {
-        const int nb = min(GB, c - b0);
-        int prow[GB], pslot[GB];
-        float pw[GB];
-        xslice xs[GB][SPL];
-#pragma unroll
-        for (int i = 0; i < GB; i++) {
-            const int pr = a.pairs[(size_t)e * a.cap + b0 + min(i, nb - 1)];
-            prow[i] = pr / ROUTE_K_MAX;
-            pslot[i] = pr % ROUTE_K_MAX;
-            pw[i] = a.rt[prow[i]].weights[pslot[i]];
-            const float* act = a.act + ((size_t)prow[i] * a.K + pslot[i]) * I;
-#pragma unroll
-            for (int j = 0; j < SPL; j++) load_xslice(DT, on[j] ? al + LPR * j : 0, act, xs[i][j]);
-        }
-#pragma unroll
-        for (int k = 0; k < UMAX; k++) {
-            if (k >= nu) break;
-            const int r = (u0 + k) * RPW + sub;
-#pragma unroll
-            for (int i = 0; i < GB; i++) {
-                if (i >= nb) break;
-                float p = 0.f;
-#pragma unroll
-                for (int j = 0; j < SPL; j++)
-                    if (on[j]) p += slice_dot<DT>(q[k][j], al + LPR * j, xs[i][j]);
-                p = row_sum<LPR>(p);
-                if (al == LPR - 1 && r < H) a.ypart[((size_t)prow[i] * a.K + pslot[i]) * H + r] = pw[i] * p;
-            }
-        }
-    }
-}
-
-template <int DT>
-static hipError_t grouped_dispatch(const grouped_args& a, bool down, hipStream_t s) {
-    const int cols = down ? a.down.cols : a.gate.cols;
-    const int rows = down ? a.down.rows : a.gate.rows;
-    const int S = cols / 32;
-    /* lanes a row: the smallest power of two holding the row's slices, at most 64 */
-    int lpr = 4;
-    while (lpr < S && lpr < 64) lpr *= 2;
-    const int rpw = WAVE / lpr, spl = (S + lpr - 1) / lpr;
-    constexpr int UDN = 8; /* output rows a down wave */
-    const int upe = (rows + rpw - 1) / rpw;
-    const int umax = std::max(1, UDN / spl); /* as the down kernel's UMAX */
-    const int wpe = (upe + umax - 1) / umax;
-    const int blocks = down ? (a.E * wpe + 3) / 4 : (int)std::min<long>(4096, ((long)a.E * upe + 3) / 4);
-#define GD(L, P)                                                                                           \
-    if (lpr == L && spl == P) {                                                                            \
-        if (down) grouped_down_kernel<DT, L, P, (UDN / P > 0 ? UDN / P : 1)><<<blocks, 256, 0, s>>>(a, wpe); \
-        else grouped_in_kernel<DT, L, P><<<blocks, 256, 0, s>>>(a);                                          \
-        return hipGetLastError();                                                                          \
-    }
-    GD(4, 1) GD(8, 1) GD(16, 1) GD(32, 1) GD(64, 1) GD(64, 2) GD(64, 3) GD(64, 4)
-#undef GD
-    return hipErrorInvalidValue;
-}
-
-hipError_t launch_grouped_in(const grouped_args& a, hipStream_t s) {
-    if (a.gate.dtype != a.up.dtype || a.gate.cols % 32 || a.gate.cols / 32 > 256 || a.K < 1 || a.K > ROUTE_K_MAX) return hipErrorInvalidValue;
-    /* the gate/up slices of a row must fill the lanes: a power-of-two width */
-    const int S = a.gate.cols / 32;
-    if (S & (S - 1)) return hipErrorInvalidValue;
-    switch (a.gate.dtype) {
-        case VITNA_DTYPE_Q8_0: return grouped_dispatch<VITNA_DTYPE_Q8_0>(a, false, s);
-        case VITNA_DTYPE_Q4_K: return grouped_dispatch<VITNA_DTYPE_Q4_K>(a, false, s);
-        case VITNA_DTYPE_Q6_K: return grouped_dispatch<VITNA_DTYPE_Q6_K>(a, false, s);
-        default: return hipErrorInvalidValue;
-    }
-}
-
-hipError_t launch_grouped_down(const grouped_args& a, hipStream_t s) {
-    if (a.down.cols % 32 || a.K < 1 || a.K > ROUTE_K_MAX) return hipErrorInvalidValue;
-    switch (a.down.dtype) {
-        case VITNA_DTYPE_Q8_0: return grouped_dispatch<VITNA_DTYPE_Q8_0>(a, true, s);
-        case VITNA_DTYPE_Q4_K: return grouped_dispatch<VITNA_DTYPE_Q4_K>(a, true, s);
-        case VITNA_DTYPE_Q6_K: return grouped_dispatch<VITNA_DTYPE_Q6_K>(a, true, s);
-        default: return hipErrorInvalidValue;
-    }
 }
 
 /* x[row][r] = x[row][r] + sum over slots k (in order) of ypart[row * K + k][r]. */

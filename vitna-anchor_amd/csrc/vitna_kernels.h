@@ -228,19 +228,7 @@ hipError_t launch_tile(const qmat& m, uint8_t* dst, hipStream_t s);
    pairs[E][cap] = row * ROUTE_K_MAX + slot, in order of row. */
 hipError_t launch_group(const route_out* rt, int n, int E, int K, int cap, int* count, int* pairs, hipStream_t s);
 
-struct grouped_args {
-    qmat gate, up, down;
-    const float* xn;       /* [n][H] */
-    const route_out* rt;   /* [n] */
-    const int* count;      /* [E] */
-    const int* pairs;      /* [E][cap] */
-    int E, K, cap;
-    float* act;            /* [n][K][I] */
-    float* ypart;          /* [n][K][H] */
-};
-hipError_t launch_grouped_in(const grouped_args& a, hipStream_t s);
-hipError_t launch_grouped_down(const grouped_args& a, hipStream_t s);
-/* The same grouped experts on the bf16 matrix cores (kernels_gmma.hip): activations split into bf16 hi/lo
+/* The grouped experts on the bf16 matrix cores (kernels_gmma.hip): activations split into bf16 hi/lo
    chunks with sums over runs of gmma_gran(dtype) columns (launch_gmma_split), gate/up writing the SwiGLU output
    split the same way, down into ypart. */
 struct gmma_args {
