@@ -6,9 +6,9 @@
  * weights read once for all the rows routed to it.
  *
  * Reference counterparts (engine/src/model_cuda.cu): the host counting sort
- * of (row, expert) pairs :5151-5176, add_rows_kernel :2120,
- * norm_rows_kernel :2020, embed_multi_kernel :1858, the *_multi kernels
- * :1872-2006. The grouped experts themselves are kernels_gmma.hip's
+ * of (row, expert) pairs :5151-5176, add_rows_kernel :2120 and
+ * norm_rows_kernel :2020 (residual_norm_kernel here), embed_multi_kernel
+ * :1858, the *_multi kernels :1872-2006. The grouped experts themselves are kernels_gmma.hip's
  * (experts_in_rows_kernel :2071, experts_down_rows_kernel :2101).
  *
  * The grouping is built on the device (group_kernel): one block per expert
@@ -42,47 +42,6 @@ __global__ void embed_rows_kernel(qmat m, const row_rec* __restrict__ rows, floa
 hipError_t launch_embed_rows(const qmat& embed, const row_rec* rows, int n, float* x, hipStream_t s) {
     if (n < 1) return hipErrorInvalidValue;
     embed_rows_kernel<<<dim3((embed.cols + 255) / 256, n), 256, 0, s>>>(embed, rows, x, embed.cols);
-    return hipGetLastError();
-}
-
-/* RMSNorm of each row (block per row), y = (x * inv) * w. */
-__global__ __launch_bounds__(256) void norm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y, int H,
-                                                        float eps) {
-    const int r = blockIdx.x;
-    const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)r * H);
-    const float4* w4 = reinterpret_cast<const float4*>(w);
-    float4 xv[8], wv[8];
-    const int n4 = H / 4;
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-        if ((int)threadIdx.x + 256 * i < n4) { xv[i] = x4[threadIdx.x + 256 * i]; wv[i] = w4[threadIdx.x + 256 * i]; }
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-        if ((int)threadIdx.x + 256 * i < n4) {
-            ss = fmaf(xv[i].x, xv[i].x, ss); ss = fmaf(xv[i].y, xv[i].y, ss);
-            ss = fmaf(xv[i].z, xv[i].z, ss); ss = fmaf(xv[i].w, xv[i].w, ss);
-        }
-    __shared__ float red[4];
-    ss = wave_sum(ss);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    ss = (red[0] + red[1]) + (red[2] + red[3]);
-    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    float4* y4 = reinterpret_cast<float4*>(y + (size_t)r * H);
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-        if ((int)threadIdx.x + 256 * i < n4) {
-            float4 o;
-            o.x = (xv[i].x * inv) * wv[i].x; o.y = (xv[i].y * inv) * wv[i].y;
-            o.z = (xv[i].z * inv) * wv[i].z; o.w = (xv[i].w * inv) * wv[i].w;
-            y4[threadIdx.x + 256 * i] = o;
-        }
-}
-
-hipError_t launch_norm_rows(const float* x, const float* w, float* y, int n, int H, float eps, hipStream_t s) {
-    if (n < 1 || H % 4 || H > 8192) return hipErrorInvalidValue;
-    norm_rows_kernel<<<n, 256, 0, s>>>(x, w, y, H, eps);
     return hipGetLastError();
 }
 

@@ -178,7 +178,6 @@ hipError_t launch_attention_prepare(const attn_args& a, hipStream_t s);
 /* ---- several rows (kernels_rows.hip) ---- */
 
 hipError_t launch_embed_rows(const qmat& embed, const row_rec* rows, int n, float* x, hipStream_t s);
-hipError_t launch_norm_rows(const float* x, const float* w, float* y, int n, int H, float eps, hipStream_t s);
 /* x[row] += the K parts of ypart in slot order (when ypart), y = RMSNorm(x) * w, and y's operand images when
    img.a (H a multiple of 256 then). */
 hipError_t launch_residual_norm(float* x, const float* ypart, int K, const float* w, float* y, int n, int H, float eps,
