@@ -43,7 +43,7 @@ METRIC = "Qwen3-30B-A3B Q4_K_M decode tok/s @1 GPU; expert GEMV HBM GB/s (% of p
 # HBM bytes a launch of experts_in_kernel<Q4_K> moves at this workload, from two rocprofv3 --pmc passes
 # (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, each factor calibrated on copy_probe_kernel):
 # profiles/decode_step_qwen3_hbm_traffic.md
-EXPERTS_IN_TRAFFIC = 14445631 + 49344
+EXPERTS_IN_TRAFFIC = 14405141 + 24704
 KERNELS = {0: "experts_in (gate/up + SiLU)", 1: "experts_down (+ weighted sum)", 2: "route (norm + router + top-k)",
            3: "q/k/v projections", 4: "attention (+ merge)", 5: "o-projection", 6: "LM head",
            7: "route without top-k", 8: "routing rule alone (1 block)", 9: "tiny launch (floor)"}
