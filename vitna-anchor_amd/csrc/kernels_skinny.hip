@@ -8,20 +8,24 @@
  * rows, on the CUDA cores); the CPU arithmetic checked against is
  * engine/src/model.c:887-979, one row at a time.
  *
- * Each weight is widened as the reference widens it (engine/src/quant.c:40-188,
- * every product rounded) and split into bf16 hi + lo (hi = bf16(w),
- * lo = bf16(w - hi)); the activations come split the same way
- * (split_rows_kernel). A product is hi*hi + hi*lo + lo*hi on
- * v_mfma_f32_32x32x16_bf16 (three MFMAs, fp32 accumulate): the dropped lo*lo
- * term and the splits leave about 2^-16 relative error a product, far inside
- * the 1e-3 the decode path is held to.
- *
- * Tiling: a workgroup is KS waves over one tile of 32 token rows x (32 NT)
- * weight rows; wave w takes every KS-th 32-weight slice of K, and the waves'
- * accumulators are added through LDS in wave order. A lane supplies weight row
- * lane % 32 (tile k) and the k-octet lane / 32 of both runs of each slice, as
- * the activations' lanes do for token lane % 32: the MFMA's k order is the
- * slice's, the same on both sides.
+ * Two kernels:
+ *   skinny_exact_kernel / skinny_wide_kernel (widths a multiple of 256): the
+ *     quants enter the MFMA as exact bf16 integers, each scale group keeps its
+ *     own MFMA sum and its scale is applied in fp32 (the section "exact-integer
+ *     quants" below); the operands come from images in MFMA lane order
+ *     (skinny_image.h) and the weights from a tiled copy, so every load of a
+ *     wave is 1 KB contiguous.
+ *   skinny_kernel (other widths): each weight is widened as the reference
+ *     widens it (engine/src/quant.c:40-188) and split into bf16 hi + lo, the
+ *     activations likewise (split_rows_kernel), and a product is
+ *     hi*hi + hi*lo + lo*hi on v_mfma_f32_32x32x16_bf16: about 2^-16 relative
+ *     a product. A workgroup is KS waves over one tile of 32 token rows x
+ *     (32 NT) weight rows; wave w takes every KS-th 32-weight slice of K, and
+ *     the waves' accumulators are added through LDS in wave order. A lane
+ *     supplies weight row lane % 32 and the k-octet lane / 32 of both runs of
+ *     each slice, as the activations' lanes do for token lane % 32.
+ * Both stay within 1e-3 of the CPU checker; each projection alone is held to
+ * 2e-5 of max |ref| against the widened matrix in float64.
  */
 
 #include "vitna_kernels.h"
