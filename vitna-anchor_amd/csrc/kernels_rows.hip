@@ -214,29 +214,44 @@ hipError_t launch_gemv_multi(const gemv_multi_args& a, hipStream_t s) {
 /* ---- grouping --------------------------------------------------------- */
 
 /* Block e lists the (row, slot) pairs whose routing names expert e, in order
-   of row: pairs[e * cap + i] = row * ROUTE_K_MAX + slot, count[e] = how many. */
-__global__ __launch_bounds__(256) void group_kernel(const route_out* __restrict__ rt, int n, int K, int cap, int* __restrict__ count,
-                                                    int* __restrict__ pairs) {
+   of row: pairs[e * cap + i] = row * ROUTE_K_MAX + slot, count[e] = how many.
+   A thread a row, GROUP_T rows a pass. */
+#define GROUP_T 1024
+__global__ __launch_bounds__(GROUP_T) void group_kernel(const route_out* __restrict__ rt, int n, int K, int cap, int* __restrict__ count,
+                                                        int* __restrict__ pairs) {
     const int e = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    __shared__ int wave_n[4];
+    __shared__ int wave_n[GROUP_T / WAVE];
     int base = 0;
-    for (int r0 = 0; r0 < n; r0 += 256) {
+    for (int r0 = 0; r0 < n; r0 += GROUP_T) {
         const int r = r0 + tid;
         int slot = -1;
-        if (r < n)
-            for (int k = 0; k < K; k++)
-                if (rt[r].ids[k] == e) slot = k;
+        if (r < n) {
+            const int4* ip = reinterpret_cast<const int4*>(rt[r].ids);
+#pragma unroll
+            for (int q = 0; q < ROUTE_K_MAX / 4; q++)
+                if (4 * q < K) {
+                    const int4 v = ip[q];
+                    if (4 * q + 0 < K && v.x == e) slot = 4 * q + 0;
+                    if (4 * q + 1 < K && v.y == e) slot = 4 * q + 1;
+                    if (4 * q + 2 < K && v.z == e) slot = 4 * q + 2;
+                    if (4 * q + 3 < K && v.w == e) slot = 4 * q + 3;
+                }
+        }
         const uint64_t b = __ballot(slot >= 0);
         const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
         if (lane == 0) wave_n[wave] = __popcll(b);
         __syncthreads();
-        int before = base;
-        for (int w = 0; w < wave; w++) before += wave_n[w];
+        int before = base, total = 0;
+#pragma unroll
+        for (int w = 0; w < GROUP_T / WAVE; w++) {
+            if (w < wave) before += wave_n[w];
+            total += wave_n[w];
+        }
         if (slot >= 0) {
             const int at = before + __popcll(b & below);
             if (at < cap) pairs[(size_t)e * cap + at] = r * ROUTE_K_MAX + slot;
         }
-        base += wave_n[0] + wave_n[1] + wave_n[2] + wave_n[3];
+        base += total;
         __syncthreads();
     }
     if (tid == 0) count[e] = base < cap ? base : cap;
@@ -244,22 +259,35 @@ __global__ __launch_bounds__(256) void group_kernel(const route_out* __restrict_
 
 hipError_t launch_group(const route_out* rt, int n, int E, int K, int cap, int* count, int* pairs, hipStream_t s) {
     if (n < 1 || n > cap || E < 1 || K < 1 || K > ROUTE_K_MAX) return hipErrorInvalidValue;
-    group_kernel<<<E, 256, 0, s>>>(rt, n, K, cap, count, pairs);
+    group_kernel<<<E, GROUP_T, 0, s>>>(rt, n, K, cap, count, pairs);
     return hipGetLastError();
 }
 
-/* x[row][r] = x[row][r] + sum over slots k (in order) of ypart[row * K + k][r]. */
-__global__ void reduce_rows_kernel(const float* __restrict__ ypart, float* __restrict__ x, int n, int K, int H) {
-    const int row = blockIdx.y;
-    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < H; r += gridDim.x * blockDim.x) {
-        float sum = 0.0f;
-        for (int k = 0; k < K; k++) sum = sum + ypart[((size_t)row * K + k) * H + r];
-        x[(size_t)row * H + r] = x[(size_t)row * H + r] + sum;
-    }
+/* x[row][r] = x[row][r] + sum over slots k (in order) of ypart[row * K + k][r]: a float4 of columns a thread,
+   its K parts all requested before the first add. */
+__global__ __launch_bounds__(256) void reduce_rows_kernel(const float* __restrict__ ypart, float* __restrict__ x, int n, int K, int H) {
+    const int row = blockIdx.y, c4 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c4 >= H / 4) return;
+    const float4* yp = reinterpret_cast<const float4*>(ypart + (size_t)row * K * H) + c4;
+    float4 p[ROUTE_K_MAX];
+#pragma unroll
+    for (int k = 0; k < ROUTE_K_MAX; k++)
+        if (k < K) p[k] = yp[(size_t)k * (H / 4)];
+    float4 sum = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int k = 0; k < ROUTE_K_MAX; k++)
+        if (k < K) {
+            sum.x = sum.x + p[k].x; sum.y = sum.y + p[k].y;
+            sum.z = sum.z + p[k].z; sum.w = sum.w + p[k].w;
+        }
+    float4* xp = reinterpret_cast<float4*>(x + (size_t)row * H) + c4;
+    float4 v = *xp;
+    v.x = v.x + sum.x; v.y = v.y + sum.y; v.z = v.z + sum.z; v.w = v.w + sum.w;
+    *xp = v;
 }
 
 hipError_t launch_reduce_rows(const float* ypart, float* x, int n, int K, int H, hipStream_t s) {
-    if (n < 1 || K < 1) return hipErrorInvalidValue;
-    reduce_rows_kernel<<<dim3((H + 255) / 256, n), 256, 0, s>>>(ypart, x, n, K, H);
+    if (n < 1 || K < 1 || K > ROUTE_K_MAX || H % 4) return hipErrorInvalidValue;
+    reduce_rows_kernel<<<dim3((H / 4 + 255) / 256, n), 256, 0, s>>>(ypart, x, n, K, H);
     return hipGetLastError();
 }
