@@ -32,7 +32,9 @@
  * v_mfma_f32_32x32x16_bf16. K advances 64 a stage (two Q8_0 blocks) through
  * a three-stage LDS ring filled by global-to-LDS loads, two stages ahead. Work items (tile, column block) are split into eight
  * contiguous ranges, one per XCD (workgroup i runs on XCD i mod 8), so the
- * column blocks of one tile and the tiles of one expert share an L2.
+ * column blocks of one tile and the tiles of one expert share an L2. A stage
+ * has two phases: waves 0-3 run their MFMAs while waves 4-7 dequantize and
+ * load, then the other way round.
  */
 
 #include "vitna_kernels.h"
@@ -281,14 +283,13 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
     issue_a(0);
     store_b(0);
     if (S > 1) { load_b(1); issue_a(1); }
-    for (int s = 0; s < S; s++) {
-        /* A of stage s landed (the seven loads of stage s + 1 may be in flight); this thread's B writes done */
-        if (s + 1 < S) asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        if (s + 1 < S) store_b(s + 1);
-        if (s + 2 < S) { load_b(s + 2); issue_a(s + 2); }
-        if (!live0) continue;
+    /* Two phases a stage, split by a barrier. Waves 0-3 (one on each SIMD) read their fragments and run their
+       MFMAs in the first phase while waves 4-7 dequantize their share of the next stage and issue their loads;
+       in the second phase the two groups swap. So each SIMD's matrix core works in both phases while the other
+       wave uses the VALU and the LDS. */
+    const bool first = wv < 4;
+    auto mma = [&](int s) {
+        if (!live0) return;
         /* Fragment reads are ds_read instructions of our own: the compiler would otherwise wait for every
            global-to-LDS load in flight (vmcnt(0)) before any LDS read. */
         const uint32_t abase = lds0 + (s % PF_A_STAGES) * PF_TILE_BYTES, bbase = bstage0 + (s & 1) * PF_TILE_BYTES;
@@ -318,6 +319,21 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
                 }
             }
         }
+    };
+    auto feed = [&](int s) {
+        if (s + 1 < S) store_b(s + 1);
+        if (s + 2 < S) { load_b(s + 2); issue_a(s + 2); }
+    };
+    for (int s = 0; s < S; s++) {
+        /* A of stage s landed (the seven loads of stage s + 1 may be in flight); this thread's B writes done */
+        if (s + 1 < S) asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        if (first) mma(s);
+        else feed(s);
+        __builtin_amdgcn_s_barrier();
+        if (first) feed(s);
+        else mma(s);
     }
 
     /* accumulator r of a lane: row 8 (r / 4) + 4 (lane / 32) + r % 4 of the 32 x 32 tile, column lane % 32 */
