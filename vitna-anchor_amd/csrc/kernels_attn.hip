@@ -350,10 +350,8 @@ __global__ __launch_bounds__(256) void attention_prepare_kernel(attn_args a) {
    so the same merge follows. */
 typedef float at_f4 __attribute__((ext_vector_type(4)));
 
+#define ATTN_MMA_OCC 4 /* waves a SIMD: the kernel is held to 128 registers */
 template <int G>
-#ifndef ATTN_MMA_OCC
-#define ATTN_MMA_OCC 4
-#endif
 __global__ __launch_bounds__(256, ATTN_MMA_OCC) void attention_mma_kernel(attn_args a) {
     constexpr int HD = 128, QF4 = HD / 4, PS = HD + 4;
     const int split = blockIdx.x, h = blockIdx.y, row = blockIdx.z;

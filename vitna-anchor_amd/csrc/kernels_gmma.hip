@@ -494,12 +494,8 @@ __global__ __launch_bounds__(64 * KS, 8 / KS) void gmma_down_kernel(gmma_args a,
 
 /* ---- launches ------------------------------------------------------------ */
 
-#ifndef GIN_KS
 #define GIN_KS 4 /* gate/up: 2048 columns, four ranges of 512 */
-#endif
-#ifndef GDN_KS
 #define GDN_KS 3 /* down: 768 columns, three ranges of 256 */
-#endif
 
 static bool gm_dtype(int d) { return d == VITNA_DTYPE_Q8_0 || d == VITNA_DTYPE_Q4_K || d == VITNA_DTYPE_Q6_K; }
 

@@ -406,12 +406,12 @@ __device__ __forceinline__ void sx_load_w(const qmat& w, int tile, int b, int la
     const int l32 = lane & 31;
     if constexpr (DT == VITNA_DTYPE_Q4_K) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) o.q[u] = WLOAD(reinterpret_cast<const u32x4*>(T + u * 1024 + lane * 16));
+        for (int u = 0; u < 4; u++) o.q[u] = *reinterpret_cast<const u32x4*>(T + u * 1024 + lane * 16);
         o.h = *reinterpret_cast<const u32x4*>(T + 4096 + l32 * 16);
     } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const u32x4 v = WLOAD(reinterpret_cast<const u32x4*>(T + u * 1024 + lane * 16));
+            const u32x4 v = *reinterpret_cast<const u32x4*>(T + u * 1024 + lane * 16);
             o.ql[u][0] = sx_u2{v.x, v.y};
             o.ql[u][1] = sx_u2{v.z, v.w};
         }
@@ -425,7 +425,7 @@ __device__ __forceinline__ void sx_load_w(const qmat& w, int tile, int b, int la
         o.d = *reinterpret_cast<const uint16_t*>(T + 6656 + l32 * 2);
     } else {
 #pragma unroll
-        for (int v = 0; v < 8; v++) o.q[v >> 1][v & 1] = WLOAD(reinterpret_cast<const u32x4*>(T + v * 1024 + lane * 16));
+        for (int v = 0; v < 8; v++) o.q[v >> 1][v & 1] = *reinterpret_cast<const u32x4*>(T + v * 1024 + lane * 16);
         o.d = *reinterpret_cast<const u32x4*>(T + 8192 + l32 * 16);
     }
 }
@@ -608,15 +608,6 @@ __device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& 
  * counter in cnt[]) adds the splits' sums in split order, writes the result and clears the counter, so the
  * result does not depend on which block finishes last.
  */
-#ifdef SX_PROBE
-__device__ unsigned long long sx_probe[2][1024][8][4];
-extern "C" int vitna_sx_probe(unsigned long long* out) {
-    return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(sx_probe), sizeof(sx_probe));
-}
-#define SXP(i) do { if (lane == 0 && blockIdx.x < 1024) sx_probe[a.splits[mi] > 1][blockIdx.x][wv][i] = (i == 3 ? (unsigned long long)__smid() : __builtin_amdgcn_s_memrealtime()); } while (0)
-#else
-#define SXP(i) do {} while (0)
-#endif
 __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     extern __shared__ float red[]; /* [KS][16][64] */
     __shared__ int last;
@@ -633,15 +624,12 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     const int splits = a.splits[mi], sp = bx % splits, tile = bx / splits;
     const int row0 = 32 * tile, tok0 = blockIdx.y * SK_TOK;
     const int b = 8 * sp + wv;
-    SXP(0);
-    SXP(3);
     f32x16 acc = {};
     if (b < w.cols / 256) {
         if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K>(a, w, tile, blockIdx.y, b, lane, acc);
         else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K>(a, w, tile, blockIdx.y, b, lane, acc);
         else sx_superblock<VITNA_DTYPE_Q8_0>(a, w, tile, blockIdx.y, b, lane, acc);
     }
-    SXP(1);
 
     /* accumulator r of a lane: token 8 (r / 4) + 4 (lane / 32) + r % 4 of the tile, weight row lane % 32 */
     float* y = a.y[mi];
@@ -669,7 +657,6 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
             for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
             put(r, v);
         }
-        SXP(2);
         return;
     }
     /* several splits: this block's sum of the tile into part[], then the last block of the tile adds them */
@@ -687,7 +674,6 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     __syncthreads();
     if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
     __syncthreads();
-    SXP(2);
     if (!last) return;
     for (int r = wv; r < 16; r += KS) {
         float v = 0.0f;
@@ -845,10 +831,7 @@ hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
     }
     bool exact = a.img[0] && a.img[1] && a.s16 && a.s32;
     for (int i = 0; i < a.nm; i++) exact &= a.w[i].cols % 256 == 0 && a.w[i].tiled;
-#ifndef SK_EXACT
-#define SK_EXACT 1
-#endif
-    if (exact && SK_EXACT) return launch_skinny_exact(a, s);
+    if (exact) return launch_skinny_exact(a, s);
     if (!a.xh || !a.xl) return hipErrorInvalidValue;
     int cus = 0, dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
@@ -861,10 +844,7 @@ hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
     /* wide matrices (the LM head) take four 32-row tiles a wave, so each token tile's activations are read
        a quarter as often; the rest one */
     const bool wide = rows >= 32768;
-#ifndef SK_KS_MAX
-#define SK_KS_MAX 16
-#endif
-    const int RB = wide ? 128 : 32, ks_max = wide ? 2 : SK_KS_MAX;
+    const int RB = wide ? 128 : 32, ks_max = wide ? 2 : 16;
     int blocks = 0;
     for (int i = 0; i < a.nm; i++) blocks += (a.w[i].rows + RB - 1) / RB;
     int ks = 1;

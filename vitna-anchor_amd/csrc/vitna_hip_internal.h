@@ -39,13 +39,6 @@
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-/* Weight streams are read once a step: VITNA_WEIGHT_NT marks those loads
-   nontemporal (streaming) instead of ordinary cached loads. */
-#ifdef VITNA_WEIGHT_NT
-#define WLOAD(p) __builtin_nontemporal_load(p)
-#else
-#define WLOAD(p) (*(p))
-#endif
 
 struct qmat {
     const uint8_t* p[4];
@@ -266,15 +259,15 @@ __device__ __forceinline__ void slice_load(const qmat& m, int e, int row, int t,
     const size_t blk = (size_t)row * m.nb + (t >> (DT == VITNA_DTYPE_Q8_0 ? 0 : 3));
     if (DT == VITNA_DTYPE_Q8_0) {
         const u32x4* q = reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 32);
-        r.a = WLOAD(q);
-        r.b = WLOAD(q + 1);
+        r.a = *q;
+        r.b = *(q + 1);
         r.c = *reinterpret_cast<const uint16_t*>(m.p[1] + e * m.estride[1] + blk * 2);
     } else if (DT == VITNA_DTYPE_Q4_K) {
-        r.a = WLOAD(reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 128 + 16 * (t & 7)));
+        r.a = *reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 128 + 16 * (t & 7));
         r.b = *reinterpret_cast<const u32x4*>(m.p[1] + e * m.estride[1] + blk * 16);
     } else if (DT == VITNA_DTYPE_Q6_K) {
         const int u = t & 7, h = u >> 2, r0 = (u >> 1) & 1, s = u & 1;
-        r.a = WLOAD(reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 128 + 64 * h + 32 * r0 + 16 * s));
+        r.a = *reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 128 + 64 * h + 32 * r0 + 16 * s);
         r.b = *reinterpret_cast<const u32x4*>(m.p[1] + e * m.estride[1] + blk * 64 + 32 * h + 16 * s);
         const uint8_t* sc = m.p[2] + e * m.estride[2] + blk * 16;
         /* scale of weights i: i / 16 = 8h + 2r + s, for r = r0 and r0 + 2 */
