@@ -12,8 +12,8 @@
  * sixteen-chain order (engine/src/kernels.c:115-146, ops.c:212-229), so every
  * row chooses the experts the CPU chooses, with the same weights.
  *
- * The experts: each Q8_0 weight q * d (exact in fp32) is rounded to bf16 as
- * its fragment is read from LDS; the normed rows and the SwiGLU output are
+ * The experts: each Q8_0 weight q * d (exact in fp32) is rounded to bf16 once a
+ * workgroup, into a bf16 stage in LDS; the normed rows and the SwiGLU output are
  * rounded to bf16 too; products accumulate in fp32 on the matrix cores.
  *
  * Pipeline, one stream:
@@ -21,7 +21,7 @@
  *   prefill_router_kernel   exact router logits, 8 rows x 8 experts a thread
  *   topk_kernel             the routing rule on every row (kernels_decode.hip)
  *   group_kernel            (row, slot) pairs of each expert in row order (kernels_rows.hip)
- *   prefill_plan_kernel     pair offsets of each expert; the list of 128-pair tiles
+ *   prefill_plan_kernel     pair offsets of each expert; the list of 256-pair tiles
  *   prefill_gemm_kernel<1>  act = silu(X_e G_e^T) * (X_e U_e^T), bf16, pairs in expert order
  *   prefill_gemm_kernel<0>  ypart[row * K + slot] = w * (act_e D_e^T)
  *   reduce_rows_kernel      x += the K parts of a row in slot order (kernels_rows.hip)
@@ -29,8 +29,9 @@
  * GEMM tiling: a 512-thread workgroup owns 256 pairs x 256 weight rows (for
  * gate/up: 128 gate rows and the 128 up rows of the same columns, so SwiGLU is
  * local to a lane). Each wave owns 64 x 128 as 2 x 4 tiles of
- * v_mfma_f32_32x32x16_bf16. K advances 64 a stage (two Q8_0 blocks) through
- * a three-stage LDS ring filled by global-to-LDS loads, two stages ahead. Work items (tile, column block) are split into eight
+ * v_mfma_f32_32x32x16_bf16. K advances 64 a stage (two Q8_0 blocks); the
+ * activations come through a three-stage LDS ring filled by global-to-LDS
+ * loads two stages ahead. Work items (tile, column block) are split into eight
  * contiguous ranges, one per XCD (workgroup i runs on XCD i mod 8), so the
  * column blocks of one tile and the tiles of one expert share an L2. A stage
  * has two phases: waves 0-3 run their MFMAs while waves 4-7 dequantize and
