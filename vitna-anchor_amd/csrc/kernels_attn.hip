@@ -345,7 +345,7 @@ __global__ __launch_bounds__(256) void attention_prepare_kernel(attn_args a) {
              is the lane's own weight P[r] of head l % 16, and B its value of that position at dimension
              VDIM(j, l % 16) (the column-to-dimension map that makes a lane's loads two float4s a position);
              O lands in lanes l / 16 < 2 (heads 0..7).
-   The cache reads (546 MB a layer at config 3) run at about 4.7 TB/s, near what this HBM streams (a copy
+   The cache reads (546 MB a layer at config 3) run at about 5.0 TB/s, near what this HBM streams (a copy
    runs at 5.1 TB/s), so the kernel is bound by them. The partial per (chunk, head) is the VALU kernel's,
    so the same merge follows. */
 typedef float at_f4 __attribute__((ext_vector_type(4)));
