@@ -268,7 +268,7 @@ struct prefill_args {
     const int* count;       /* [E] pairs of each expert */
     const int* pairs;       /* [E][cap] row * ROUTE_K_MAX + slot, rows ascending */
     const int* off;         /* [E] first pair of each expert in act */
-    const int* tiles;       /* (expert << 16) | tile of 128 pairs */
+    const int* tiles;       /* (expert << 16) | tile of 256 pairs */
     const int* n_tiles;
     uint16_t* act;          /* bf16 [n * K][I], pairs in expert order */
     float* ypart;           /* [n * K][H], row * K + slot */
