@@ -339,22 +339,22 @@ extern "C" int vitna_cuda_devices(vitna_cuda_device_t* out, int max) {
 
 extern "C" void vitna_cuda_free(struct vitna_cuda_model* g) {
     if (!g) return;
-    hipSetDevice(g->device);
-    if (g->stream) hipStreamSynchronize(g->stream);
+    (void)hipSetDevice(g->device);
+    if (g->stream) (void)hipStreamSynchronize(g->stream);
     if (g->graph_ready) {
-        hipGraphExecDestroy(g->step_graph);
-        hipGraphDestroy(g->step_graph_src);
+        (void)hipGraphExecDestroy(g->step_graph);
+        (void)hipGraphDestroy(g->step_graph_src);
     }
     if (g->rows_graph_n) {
-        hipGraphExecDestroy(g->rows_graph);
-        hipGraphDestroy(g->rows_graph_src);
+        (void)hipGraphExecDestroy(g->rows_graph);
+        (void)hipGraphDestroy(g->rows_graph_src);
     }
-    for (void* p : g->allocs) hipFree(p);
-    for (void* p : g->pf_allocs) hipFree(p);
-    if (g->rows_host) hipHostFree(g->rows_host);
-    if (g->h_logits) hipHostFree(g->h_logits);
-    if (g->rows_copied) hipEventDestroy(g->rows_copied);
-    if (g->stream) hipStreamDestroy(g->stream);
+    for (void* p : g->allocs) (void)hipFree(p);
+    for (void* p : g->pf_allocs) (void)hipFree(p);
+    if (g->rows_host) (void)hipHostFree(g->rows_host);
+    if (g->h_logits) (void)hipHostFree(g->h_logits);
+    if (g->rows_copied) (void)hipEventDestroy(g->rows_copied);
+    if (g->stream) (void)hipStreamDestroy(g->stream);
     delete g;
 }
 
@@ -447,7 +447,7 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
         ok = ok && upload_f32(g, &g->cos_tab, cos_tab, m->ctx * half, "the rotary cosines", err, err_len) &&
              upload_f32(g, &g->sin_tab, sin_tab, m->ctx * half, "the rotary sines", err, err_len);
     }
-    hipFree(staging);
+    (void)hipFree(staging);
     if (!ok) return bail();
 
     /* key-value cache and scratch */
@@ -726,7 +726,7 @@ extern "C" bool vitna_cuda_steps(struct vitna_cuda_model* g, size_t seq, const i
 extern "C" const char* vitna_cuda_device_name(const struct vitna_cuda_model* g) { return g ? g->name : ""; }
 
 extern "C" void vitna_cuda_wait(struct vitna_cuda_model* g) {
-    if (g) hipStreamSynchronize(g->stream);
+    if (g) (void)hipStreamSynchronize(g->stream);
 }
 
 extern "C" bool vitna_cuda_lost(struct vitna_cuda_model* g, char* err, size_t err_len) {
@@ -779,7 +779,7 @@ extern "C" bool vitna_cuda_widen(const vitna_matrix_t* w, float* out, char* err,
     }
     if (ok && memcmp(a.data(), b.data(), n * 4) != 0) ok = fail(err, err_len, "the two ways of reading the blocks disagree");
     if (ok) memcpy(out, a.data(), n * 4);
-    hipFree(src); hipFree(planes); hipFree(o1); hipFree(o2);
+    (void)hipFree(src); (void)hipFree(planes); (void)hipFree(o1); (void)hipFree(o2);
     return ok;
 }
 
@@ -811,7 +811,7 @@ extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_
     route_out* drt = (route_out*)dm(sizeof(route_out));
     unsigned* dctr = (unsigned*)dm(16);
     for (void* p : mem) ok = ok && p;
-    if (!ok) { for (void* p : mem) hipFree(p); return fail(err, err_len, "device memory for the expert check"); }
+    if (!ok) { for (void* p : mem) (void)hipFree(p); return fail(err, err_len, "device memory for the expert check"); }
     qmat qg = place(gm, gate->dtype, I, H, 1), qu = place(um, up->dtype, I, H, 1), qd = place(dmem, down->dtype, H, I, 1);
     auto up_one = [&](const vitna_matrix_t* w, const qmat& q) {
         const size_t b = vitna_matrix_row_bytes(w->dtype, w->cols) * w->rows;
@@ -848,7 +848,7 @@ extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_
              (!y || hipMemcpy(y, dy, H * 4, hipMemcpyDeviceToHost) == hipSuccess);
         if (!ok) fail(err, err_len, "copying the expert's results back");
     }
-    for (void* p : mem) hipFree(p);
+    for (void* p : mem) (void)hipFree(p);
     return ok;
 }
 
@@ -872,10 +872,10 @@ static bool ensure_graph(vitna_cuda_model* g, char* err, size_t err_len) {
     const hipError_t e = enqueue_step_body(g);
     hipGraph_t graph = nullptr;
     const hipError_t e2 = hipStreamEndCapture(g->stream, &graph);
-    if (e != hipSuccess) { if (graph) hipGraphDestroy(graph); return check_launch(g, e, "capturing the step", err, err_len); }
+    if (e != hipSuccess) { if (graph) (void)hipGraphDestroy(graph); return check_launch(g, e, "capturing the step", err, err_len); }
     HIP_TRY(e2, "ending the capture of the step");
     const hipError_t e3 = hipGraphInstantiate(&g->step_graph, graph, nullptr, nullptr, 0);
-    if (e3 != hipSuccess) hipGraphDestroy(graph);
+    if (e3 != hipSuccess) (void)hipGraphDestroy(graph);
     HIP_TRY(e3, "instantiating the step's graph");
     g->step_graph_src = graph;
     g->graph_ready = true;
@@ -1087,8 +1087,8 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
     HIP_TRY(hipEventSynchronize(t1), "timing");
     float ms = 0;
     HIP_TRY(hipEventElapsedTime(&ms, t0, t1), "events");
-    hipEventDestroy(t0);
-    hipEventDestroy(t1);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
     if (avg_us) *avg_us = 1000.0 * ms / reps;
     if (bytes) *bytes = b;
     return true;
@@ -1106,7 +1106,7 @@ static bool sync_stream(vitna_cuda_model* g, const char* what, char* err, size_t
 static bool prefill_reserve(vitna_cuda_model* g, size_t n, char* err, size_t err_len) {
     if (n <= g->pf_cap) return true;
     HIP_TRY(hipStreamSynchronize(g->stream), "waiting before the prefill buffers grow");
-    for (void* p : g->pf_allocs) hipFree(p);
+    for (void* p : g->pf_allocs) (void)hipFree(p);
     g->pf_allocs.clear();
     g->pf_cap = 0;
     const size_t H = g->H, E = g->E, K = g->K, I = g->I;
@@ -1174,7 +1174,7 @@ extern "C" bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, 
                                       size_t err_len) {
     if (!prefill_check(g, layer, n, err, err_len)) return false;
     if (!x) return fail(err, err_len, "no rows");
-    hipSetDevice(g->device);
+    HIP_TRY(hipSetDevice(g->device), "selecting the model's device");
     if (!prefill_reserve(g, n, err, err_len)) return false;
     HIP_TRY(hipMemcpyAsync(g->pf_x, x, n * g->H * 4, hipMemcpyHostToDevice, g->stream), "copying the rows to the device");
     if (!check_launch(g, enqueue_prefill(g, (int)layer, (int)n, nullptr), "the prefill", err, err_len)) return false;
@@ -1194,7 +1194,7 @@ extern "C" bool vitna_hip_time_prefill(struct vitna_cuda_model* g, size_t layer,
                                        double* us_phase, char* err, size_t err_len) {
     if (!prefill_check(g, layer, n, err, err_len)) return false;
     if (reps < 1) return fail(err, err_len, "reps must be positive");
-    hipSetDevice(g->device);
+    HIP_TRY(hipSetDevice(g->device), "selecting the model's device");
     if (!prefill_reserve(g, n, err, err_len)) return false;
     HIP_TRY(launch_fill_normal(g->pf_x0, n * g->H, seed, g->stream), "filling the rows");
     hipEvent_t ev[6];
@@ -1208,11 +1208,11 @@ extern "C" bool vitna_hip_time_prefill(struct vitna_cuda_model* g, size_t layer,
         if (e != hipSuccess) { ok = fail_hip(err, err_len, "the timed prefill", e); break; }
         for (int i = 0; r >= 0 && i < 5; i++) {
             float ms = 0;
-            hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+            if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) != hipSuccess) ms = 0;
             ph[i] += ms * 1000.0 / reps;
         }
     }
-    for (int i = 0; i < 6; i++) hipEventDestroy(ev[i]);
+    for (int i = 0; i < 6; i++) (void)hipEventDestroy(ev[i]);
     if (!ok) return false;
     if (us_total) *us_total = ph[0] + ph[1] + ph[2] + ph[3] + ph[4];
     for (int i = 0; us_phase && i < 5; i++) us_phase[i] = ph[i];
@@ -1223,7 +1223,7 @@ extern "C" bool vitna_hip_time_prefill(struct vitna_cuda_model* g, size_t layer,
 extern "C" bool vitna_hip_prefill_rows(struct vitna_cuda_model* g, size_t n, float* x_in, float* x_out, int32_t* chosen, char* err,
                                        size_t err_len) {
     if (!g || n > g->pf_cap) return fail(err, err_len, "%zu rows: the last prefill held %zu", n, g ? g->pf_cap : 0);
-    hipSetDevice(g->device);
+    HIP_TRY(hipSetDevice(g->device), "selecting the model's device");
     if (x_in) HIP_TRY(hipMemcpyAsync(x_in, g->pf_x0, n * g->H * 4, hipMemcpyDeviceToHost, g->stream), "copying the input rows");
     if (x_out) HIP_TRY(hipMemcpyAsync(x_out, g->pf_x, n * g->H * 4, hipMemcpyDeviceToHost, g->stream), "copying the output rows");
     std::vector<route_out> rt(chosen ? n : 0);
@@ -1253,8 +1253,8 @@ extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int
     HIP_TRY(hipEventSynchronize(t1), "timing the steps");
     float ms = 0;
     HIP_TRY(hipEventElapsedTime(&ms, t0, t1), "events");
-    hipEventDestroy(t0);
-    hipEventDestroy(t1);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
     *ms_per_step = (double)ms / steps;
     return true;
 }
@@ -1272,11 +1272,11 @@ extern "C" bool vitna_hip_time_ffn(struct vitna_cuda_model* g, int reps, double*
     }
     hipGraph_t graph = nullptr;
     const hipError_t e2 = hipStreamEndCapture(g->stream, &graph);
-    if (e != hipSuccess) { if (graph) hipGraphDestroy(graph); return check_launch(g, e, "capturing the layers", err, err_len); }
+    if (e != hipSuccess) { if (graph) (void)hipGraphDestroy(graph); return check_launch(g, e, "capturing the layers", err, err_len); }
     HIP_TRY(e2, "ending the capture of the layers");
     hipGraphExec_t exec = nullptr;
     const hipError_t e3 = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-    hipGraphDestroy(graph);
+    (void)hipGraphDestroy(graph);
     HIP_TRY(e3, "instantiating the layers' graph");
     hipEvent_t t0 = nullptr, t1 = nullptr;
     bool ok = hipGraphLaunch(exec, g->stream) == hipSuccess && hipGraphLaunch(exec, g->stream) == hipSuccess &&
@@ -1284,9 +1284,9 @@ extern "C" bool vitna_hip_time_ffn(struct vitna_cuda_model* g, int reps, double*
     for (int i = 0; ok && i < reps; i++) ok = hipGraphLaunch(exec, g->stream) == hipSuccess;
     float ms = 0;
     ok = ok && hipEventRecord(t1, g->stream) == hipSuccess && hipEventSynchronize(t1) == hipSuccess && hipEventElapsedTime(&ms, t0, t1) == hipSuccess;
-    if (t0) hipEventDestroy(t0);
-    if (t1) hipEventDestroy(t1);
-    hipGraphExecDestroy(exec);
+    if (t0) (void)hipEventDestroy(t0);
+    if (t1) (void)hipEventDestroy(t1);
+    (void)hipGraphExecDestroy(exec);
     if (!ok) return fail(err, err_len, "timing the layers failed");
     *us_per_layer = 1000.0 * ms / ((double)reps * g->NL);
     return true;
@@ -1304,8 +1304,8 @@ extern "C" bool vitna_hip_route_check(const float* logits, int n_experts, int k,
     ok = ok && hipMemcpy(dl, logits, n_experts * 4, hipMemcpyHostToDevice) == hipSuccess &&
          launch_route_check(dl, n_experts, k, renormalize ? 1 : 0, dro, 0) == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
          hipMemcpy(&r, dro, sizeof(r), hipMemcpyDeviceToHost) == hipSuccess;
-    hipFree(dl);
-    hipFree(dro);
+    (void)hipFree(dl);
+    (void)hipFree(dro);
     if (!ok) return fail(err, err_len, "the device routing failed");
     for (int i = 0; i < k; i++) {
         if (chosen) chosen[i] = r.chosen[i];
@@ -1325,10 +1325,10 @@ extern "C" bool vitna_hip_copy_probe(size_t bytes, int reps, double* avg_us, cha
     for (int i = 0; ok && i < reps; i++) ok = launch_copy_probe(a, b, bytes, 0) == hipSuccess;
     float ms = 0;
     ok = ok && hipEventRecord(t1, 0) == hipSuccess && hipEventSynchronize(t1) == hipSuccess && hipEventElapsedTime(&ms, t0, t1) == hipSuccess;
-    if (t0) hipEventDestroy(t0);
-    if (t1) hipEventDestroy(t1);
-    hipFree(a);
-    hipFree(b);
+    if (t0) (void)hipEventDestroy(t0);
+    if (t1) (void)hipEventDestroy(t1);
+    (void)hipFree(a);
+    (void)hipFree(b);
     if (!ok) return fail(err, err_len, "the copy probe failed");
     if (avg_us) *avg_us = 1000.0 * ms / reps;
     return true;
@@ -1553,8 +1553,8 @@ static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_
     if (g->rows_graph_n == n && g->rows_graph_shared == g->rows_shared_seq) return true;
     if (g->rows_graph_n) {
         HIP_TRY(hipStreamSynchronize(g->stream), "before recapturing the rows step");
-        hipGraphExecDestroy(g->rows_graph);
-        hipGraphDestroy(g->rows_graph_src);
+        (void)hipGraphExecDestroy(g->rows_graph);
+        (void)hipGraphDestroy(g->rows_graph_src);
         g->rows_graph_n = 0;
     }
     HIP_TRY(hipStreamSynchronize(g->stream), "before capturing the rows step");
@@ -1562,10 +1562,10 @@ static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_
     const hipError_t e = enqueue_rows_step_body(g, n);
     hipGraph_t graph = nullptr;
     const hipError_t e2 = hipStreamEndCapture(g->stream, &graph);
-    if (e != hipSuccess) { if (graph) hipGraphDestroy(graph); return check_launch(g, e, "capturing the rows step", err, err_len); }
+    if (e != hipSuccess) { if (graph) (void)hipGraphDestroy(graph); return check_launch(g, e, "capturing the rows step", err, err_len); }
     HIP_TRY(e2, "ending the capture of the rows step");
     const hipError_t e3 = hipGraphInstantiate(&g->rows_graph, graph, nullptr, nullptr, 0);
-    if (e3 != hipSuccess) hipGraphDestroy(graph);
+    if (e3 != hipSuccess) (void)hipGraphDestroy(graph);
     HIP_TRY(e3, "instantiating the rows step's graph");
     g->rows_graph_src = graph;
     g->rows_graph_n = n;
@@ -1605,8 +1605,8 @@ extern "C" bool vitna_hip_time_rows(struct vitna_cuda_model* g, const vitna_cuda
     HIP_TRY(hipEventSynchronize(t1), "timing the rows steps");
     float ms = 0;
     HIP_TRY(hipEventElapsedTime(&ms, t0, t1), "events");
-    hipEventDestroy(t0);
-    hipEventDestroy(t1);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
     *ms_per_step = (double)ms / steps;
     return true;
 }

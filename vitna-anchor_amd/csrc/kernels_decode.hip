@@ -630,7 +630,7 @@ int gemv_device_cus() {
     static int cus = 0;
     if (!cus) {
         int dev = 0;
-        hipGetDevice(&dev);
+        if (hipGetDevice(&dev) != hipSuccess) dev = 0;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
     }
     return cus;

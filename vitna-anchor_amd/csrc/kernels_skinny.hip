@@ -723,7 +723,7 @@ __device__ __forceinline__ void sxw_read(const u32x4* img, const skinny_args& a,
    superblock b + 1's activations and each wave loads its weights for b + 1 while b computes. */
 template <int DT, int NW>
 __device__ __forceinline__ void sxw_body(const skinny_args& a, const qmat& w, int tile, int tt, u32x4* img, f32x16& acc) {
-    const int lane = threadIdx.x & 63, l32 = lane & 31, kq = lane >> 5;
+    const int lane = threadIdx.x & 63, kq = lane >> 5;
     const int K = w.cols, S = K / 256;
 
     sx_w<DT> W0, W1;
