@@ -72,6 +72,22 @@ def test_library_exports_every_declared_function():
         assert getattr(lib, n) is not None
 
 
+def test_headers_compile_as_c_and_cpp():
+    """The engine's C code includes the ABI header (model.c is C); it compiles as C99 and as C++, warning-free."""
+    with tempfile.TemporaryDirectory() as d:
+        src_c = os.path.join(d, "t.c")
+        with open(src_c, "w") as f:
+            f.write('#include "vitna_hip.h"\nint main(void) { return vitna_cuda_probe(0, 0) ? 0 : 0; }\n')
+        src_cc = os.path.join(d, "t.cc")
+        with open(src_cc, "w") as f:
+            f.write('#include "vitna_hip.h"\nint main() { return 0; }\n')
+        inc = os.path.join(ROOT, "include")
+        for cmd in (["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-I", inc, "-c", src_c, "-o", os.path.join(d, "c.o")],
+                    ["g++", "-std=c++11", "-Wall", "-Wextra", "-Werror", "-I", inc, "-c", src_cc, "-o", os.path.join(d, "cc.o")]):
+            r = subprocess.run(cmd, capture_output=True, text=True)
+            assert r.returncode == 0, r.stderr
+
+
 def test_library_is_gfx950():
     """The offload bundle's target ids name gfx950 and nothing else."""
     import re
