@@ -185,10 +185,12 @@ def C_f32(addr):
     return ctypes.cast(addr, ctypes.POINTER(ctypes.c_float))
 
 
-@pytest.mark.parametrize("name,pos,token", [("q4km", 150, 7), ("q8", 79, 250)])
+@pytest.mark.parametrize("name,pos,token", [("q4km", 150, 7), ("q8", 79, 250), ("q4km", 192, 11), ("q4km", 199, 5)])
 def test_device_step_matches_cpu(name, pos, token):
     """vitna_hip_moe_step (device routing, one graph): logits within tolerance of the CPU step, replayed at two
-    positions through the same graph."""
+    positions through the same graph. Cases: mid-chunk; the last position of the context (q8: 79 of 80, q4km:
+    199 of 200); 191 then 192, the last position of a full 64-position attention chunk then the first of the
+    next."""
     say("device step", name, pos, token)
     model, dev, kc, vc = prefilled(name, 654, pos + 1)
     try:
