@@ -154,6 +154,19 @@ bool vitna_hip_residual(struct vitna_cuda_model* g, size_t row, float* host, boo
 bool vitna_hip_routing(struct vitna_cuda_model* g, size_t row, float* logits, int32_t* chosen, int32_t* ids, float* weights, char* err,
                        size_t err_len);
 
+/** Row row's query projection (before its QK-norm and RoPE) and attention
+    output (heads x head_dim each) as the last step or rows pass left them at
+    its last layer. Either pointer may be NULL. Synchronous. A checker's hook
+    for the split-position attention and its merge; no reference counterpart. */
+bool vitna_hip_attention_io(struct vitna_cuda_model* g, size_t row, float* q, float* att, char* err, size_t err_len);
+
+/** The routing the last device-routed step (vitna_hip_moe_step) chose at
+    layer layer: the choice largest first (K), the experts in order of id (K)
+    and their weights (K). Any pointer may be NULL. Synchronous. A checker's
+    hook: the reference traces its routing on the host (main.c --experts-out). */
+bool vitna_hip_step_routing(struct vitna_cuda_model* g, size_t layer, int32_t* chosen, int32_t* ids, float* weights, char* err,
+                            size_t err_len);
+
 /** One projection of a pass of n rows (1 <= n <= the rows maximum) as the
     rows step runs it: y[t] = W x[t] for W = layer's q, k, v, o (which = 0..3)
     or the LM head (which = 4, layer ignored); x is n x W's columns, y n x W's

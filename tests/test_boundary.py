@@ -131,6 +131,22 @@ def test_create_refuses_bad_shapes_before_touching_a_device():
         m.free()
 
 
+def test_create_refuses_a_context_the_merge_cannot_take():
+    """More than 1024 attention chunks of 64 positions is refused by check_shapes, before any HIP call."""
+    lib = va.hip()
+    m = va.Model(va.shape(n_layers=1, hidden=256, intermediate=256, n_heads=4, n_kv_heads=2, head_dim=64, vocab=300,
+                          n_experts=8, n_experts_used=2, dt_gate_up=va.Q8_0, dt_down=va.Q8_0, dt_q=va.Q8_0,
+                          dt_k=va.Q8_0, dt_v=va.Q8_0, dt_o=va.Q8_0, dt_head=va.Q8_0, dt_embed=va.Q8_0, ctx=64), 1)
+    try:
+        err = C.create_string_buffer(256)
+        m.m.ctx = 65537
+        assert not lib.vitna_cuda_create(m.ptr, None, None, 0, err, 256)
+        assert b"context of 65537 positions" in err.value
+    finally:
+        m.m.ctx = 64
+        m.free()
+
+
 def test_probe_without_gpu_says_why():
     if os.path.exists("/dev/kfd"):
         pytest.skip("a GPU driver is present")
@@ -138,3 +154,28 @@ def test_probe_without_gpu_says_why():
     err = C.create_string_buffer(256)
     assert not lib.vitna_cuda_probe(err, 256)
     assert err.value
+
+
+REF_ENGINE = "/root/reference/engine/src"
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_ENGINE), reason="the reference's sources are not here (the GPU box)")
+def test_reference_engine_links_against_library():
+    """The drop-in claim: the reference engine's own C sources, compiled with -DVITNA_CUDA=1 as its CUDA build
+    compiles them (engine/Makefile:24-52), link against libvitna_hip.so in place of model_cuda.cu with no
+    undefined symbol (oracle/Makefile target link), and the linked engine starts."""
+    r = subprocess.run(["make", "-C", os.path.join(ROOT, "oracle"), "link", "-j8"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    objs = os.path.join(ROOT, "oracle", "_ref", "cuda_obj")
+    need = set()
+    for o in os.listdir(objs):
+        out = subprocess.run(["nm", "-u", os.path.join(objs, o)], capture_output=True, text=True).stdout
+        need |= {l.split()[-1] for l in out.splitlines() if "vitna_cuda_" in l}
+    assert len(need) >= 20, sorted(need)
+    have = subprocess.run(["nm", "-D", "--defined-only", os.path.join(ROOT, "vitna-anchor_amd", "libvitna_hip.so")],
+                          capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in have.splitlines()}
+    assert need <= exported, sorted(need - exported)
+    run = subprocess.run([os.path.join(ROOT, "oracle", "_ref", "vitna-anchor-hip"), "--help"], capture_output=True,
+                         text=True, timeout=60)
+    assert "--device cuda" in run.stdout + run.stderr

@@ -1,0 +1,204 @@
+"""BASELINE configs[2] and [3] at their full size, and the split-position
+attention at long contexts, against the CPU checker (oracle/) on the GPU.
+
+  * the 48-layer Qwen3-30B-A3B-shaped Q4_K_M model, one token at
+    position 2048 over a 2048-position cache (33 attention chunks), the
+    bench's model and seed. Chosen experts identical in every layer; logits
+    within 1e-3 of max |cpu| and the reference's LOGIT_ATOL 1e-2
+    (reference/compare.mjs:84).
+  * 32 sequences at key-value lengths drawn from U{128..8192}
+    (one forced to 8192: 129 chunks), one rows step; the shortest, the
+    longest and two rows between against the checker's step of each.
+  * The attention and its merge alone at 33, 34 and 129 chunks, on the
+    batch-1 matrix-core path (8 query heads a key-value head), the rows'
+    matrix-core path and the one-row vector path: the device's attention
+    output against a float64 restatement of engine/src/model.c:932-957 from
+    the device's own q and cache, within 1e-4 of max |ref|.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import vitna_amd as va
+from test_gpu_decode import rel, say
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-3
+
+
+def margins(tl, K):
+    """Gap between the K-th and (K+1)-th largest router logit of each layer."""
+    s = -np.sort(-tl.astype(np.float64), axis=1)
+    return s[:, K - 1] - s[:, K]
+
+
+def test_config2_full_step():
+    """a whole 48-layer decode step at position 2048, device routing, one graph."""
+    pos, token, seed = 2048, 1234, 20260101
+    say("configs[2] full step: building the model")
+    model = va.Model(va.shape(ctx=pos + 1, seqs=1, kv_host=1), seed, threads=16)
+    try:
+        cfg = model.cfg
+        L, K = cfg.n_layers, cfg.n_experts_used
+        kd = cfg.n_kv_heads * cfg.head_dim
+        kc = np.ctypeslib.as_array(model.m.k_cache, shape=(L, model.m.ctx, kd))
+        vc = np.ctypeslib.as_array(model.m.v_cache, shape=(L, model.m.ctx, kd))
+        for l in range(L):
+            kc[l, :pos] = va.normal(7, 2 * l, pos * kd).reshape(pos, kd)
+            vc[l, :pos] = va.normal(7, 2 * l + 1, pos * kd).reshape(pos, kd)
+        dev = va.Device(model)
+        try:
+            for l in range(L):
+                dev.kv(0, l, 0, pos, kc[l, :pos], vc[l, :pos])
+            say("  device step")
+            logits = dev.step(0, token, pos)
+            chosen = np.stack([dev.step_routing(l)[0] for l in range(L)])
+            say("  CPU step")
+            ref, tl, tc, _ = oracle.step(model, 0, token, pos, threads=16)
+            m = margins(tl, K)
+            say("  smallest 8th/9th router margin %.3g (layer %d)" % (m.min(), int(np.argmin(m))))
+            for l in range(L):
+                assert np.array_equal(chosen[l], tc[l]), ("layer", l, chosen[l], tc[l], "margin", m[l])
+            r = rel(logits, ref)
+            a = float(np.max(np.abs(logits - ref)))
+            say("  logits rel err %.3g, max abs %.3g" % (r, a))
+            assert r <= REL and a <= 1e-2
+        finally:
+            dev.close()
+    finally:
+        model.free()
+
+
+def test_config3_rows_full():
+    """32 sequences, one new token each, key-value lengths U{128..8192} with 8192 among them, the
+    full 48-layer model, one device-routed rows step; four rows against the checker."""
+    seed = 20260103
+    say("configs[3] rows: building the model")
+    model = va.Model(va.shape(ctx=8193, seqs=32, kv_host=1), seed, threads=16)
+    try:
+        cfg = model.cfg
+        L, K = cfg.n_layers, cfg.n_experts_used
+        kd = cfg.n_kv_heads * cfg.head_dim
+        rng = np.random.RandomState(seed)
+        lengths = rng.randint(128, 8193, size=32)
+        lengths[int(np.argmax(lengths))] = 8192
+        rows = [(int(rng.randint(0, cfg.vocab)), int(lengths[s]), s) for s in range(32)]
+        dev = va.Device(model)
+        try:
+            dev.kv_fill(3, [int(n) for n in lengths])
+            say("  device rows step")
+            logits = dev.rows_step(rows)
+            order = np.argsort(lengths)
+            pick = [int(order[0]), int(order[10]), int(order[21]), int(order[-1])]
+            kc = np.ctypeslib.as_array(model.m.k_cache, shape=(32, L, model.m.ctx, kd))
+            vc = np.ctypeslib.as_array(model.m.v_cache, shape=(32, L, model.m.ctx, kd))
+            last = {}
+            for s in pick:
+                last[s] = dev.routing(s)[1]
+            for s in pick:
+                n = int(lengths[s])
+                # the cache the device step read (positions before the row's own), copied to the host model
+                for l in range(L):
+                    k, v = dev.kv(s, l, 0, n)
+                    kc[s, l, :n] = k
+                    vc[s, l, :n] = v
+                tok, pos, seq = rows[s]
+                ref, tl, tc, _ = oracle.step(model, seq, tok, pos, threads=16)
+                r = rel(logits[s], ref)
+                a = float(np.max(np.abs(logits[s] - ref)))
+                say("  row %d (kv length %d): logits rel err %.3g, max abs %.3g, smallest margin %.3g"
+                    % (s, n, r, a, margins(tl, K).min()))
+                assert np.array_equal(last[s], tc[-1]), ("row", s, last[s], tc[-1])
+                assert r <= REL and a <= 1e-2
+        finally:
+            dev.close()
+    finally:
+        model.free()
+
+
+LONG = dict(n_layers=2, hidden=512, intermediate=256, n_heads=32, n_kv_heads=4, head_dim=128, vocab=1000,
+            n_experts=32, n_experts_used=8, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q6_K, norm_std=0.1,
+            ctx=8193, seqs=4, kv_host=1)
+
+
+def attention_ref(model, dev, q_raw, seq, layer, pos):
+    """float64 restatement of engine/src/model.c:915-957 for one row: per-head RMSNorm of q with the layer's
+    q_norm (model.c:919), half-split RoPE at pos (ops.c:273-281), scores against the cache's keys 0..pos (the
+    device's cache, its own row at pos included), softmax, weighted values."""
+    cfg = model.cfg
+    hd, nh, nkv = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
+    half, G = hd // 2, nh // nkv
+    qn = np.ctypeslib.as_array(model.m.layers[layer].q_norm, shape=(hd,)).astype(np.float64)
+    k, v = dev.kv(seq, layer, 0, pos + 1)
+    k = k.astype(np.float64).reshape(pos + 1, nkv, hd)
+    v = v.astype(np.float64).reshape(pos + 1, nkv, hd)
+    cs, sn = dev.cos[pos].astype(np.float64), dev.sin[pos].astype(np.float64)
+    out = np.empty((nh, hd))
+    for h in range(nh):
+        q = q_raw[h * hd:(h + 1) * hd].astype(np.float64)
+        q = q / np.sqrt(np.mean(q * q) + cfg.rms_eps) * qn
+        a, b = q[:half].copy(), q[half:].copy()
+        q[:half] = a * cs - b * sn
+        q[half:] = b * cs + a * sn
+        s = k[:, h // G, :] @ q / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ v[:, h // G, :]
+    return out.ravel()
+
+
+@pytest.fixture(scope="module")
+def long_model():
+    model = va.Model(va.shape(**LONG), 8080)
+    cfg = model.cfg
+    kd = cfg.n_kv_heads * cfg.head_dim
+    kc = np.ctypeslib.as_array(model.m.k_cache, shape=(model.m.seqs, cfg.n_layers, model.m.ctx, kd))
+    vc = np.ctypeslib.as_array(model.m.v_cache, shape=(model.m.seqs, cfg.n_layers, model.m.ctx, kd))
+    kc[:] = va.normal(8080, 101, kc.size).reshape(kc.shape)
+    vc[:] = va.normal(8080, 102, vc.size).reshape(vc.shape)
+    dev = va.Device(model)
+    for s in range(model.m.seqs):
+        for l in range(cfg.n_layers):
+            dev.kv(s, l, 0, model.m.ctx, kc[s, l], vc[s, l])
+    yield model, dev
+    dev.close()
+    model.free()
+
+
+@pytest.mark.parametrize("pos", [2047, 2048, 2111, 8192])
+def test_long_context_decode(long_model, pos):
+    """Batch-1 device step at positions that end the 32nd chunk, start the 33rd, fill 33 chunks and a part, and
+    take the context's last position (129 chunks): the attention output against the float64 restatement, the
+    logits against the checker's step."""
+    model, dev = long_model
+    say("long-context decode step at", pos)
+    token = 17 + pos % 50
+    logits = dev.step(0, token, pos)
+    q, att = dev.attention_io(0)
+    ref_att = attention_ref(model, dev, q, 0, model.cfg.n_layers - 1, pos)
+    ra = rel(att, ref_att)
+    ref, _, tc, _ = oracle.step(model, 0, token, pos)
+    r = rel(logits, ref)
+    say("  attention rel err %.3g, logits rel err %.3g" % (ra, r))
+    assert ra <= 1e-4
+    assert np.array_equal(dev.step_routing(model.cfg.n_layers - 1)[0], tc[-1])
+    assert r <= REL
+
+
+def test_long_context_rows(long_model):
+    """A rows pass of four sequences at positions straddling 2048 and at 8192 (the matrix-core attention of
+    several rows), then a pass of one row at 8192 (the vector attention): each row's attention output against
+    the float64 restatement, and its logits against the checker."""
+    model, dev = long_model
+    L = model.cfg.n_layers
+    for rows in ([(5, 2047, 0), (6, 2048, 1), (7, 2111, 2), (8, 8192, 3)], [(9, 8192, 3)]):
+        say("long-context rows", rows)
+        logits = dev.rows_step(rows)
+        for i, (tok, pos, seq) in enumerate(rows):
+            q, att = dev.attention_io(i)
+            ra = rel(att, attention_ref(model, dev, q, seq, L - 1, pos))
+            ref, _, _, _ = oracle.step(model, seq, tok, pos)
+            r = rel(logits[i], ref)
+            say("  row %d pos %d: attention rel err %.3g, logits rel err %.3g" % (i, pos, ra, r))
+            assert ra <= 1e-4
+            assert r <= REL

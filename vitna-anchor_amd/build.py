@@ -2,6 +2,7 @@
 
     python vitna-anchor_amd/build.py          # HIP library + synthetic-model library
     python vitna-anchor_amd/build.py --all    # also the CPU checker (oracle/)
+    python vitna-anchor_amd/build.py --incremental   # recompile only what changed
 
 Outputs (git-ignored, carried to the GPU box with the tree):
   vitna-anchor_amd/libvitna_hip.so          the HIP kernels and the C ABI (include/vitna_hip.h)
@@ -35,18 +36,25 @@ def _run(cmd):
     return r
 
 
-def build_hip():
+def build_hip(incremental=False):
     srcs = sorted(glob.glob(os.path.join(PKG, "csrc", "*.hip")))
     objdir = os.path.join(PKG, "_build")
     os.makedirs(objdir, exist_ok=True)
-    jobs = []
+    # every object depends on its source and on every header it may include
+    deps = glob.glob(os.path.join(PKG, "csrc", "*.h")) + glob.glob(os.path.join(ROOT, "include", "*.h"))
+    newest_dep = max((os.path.getmtime(d) for d in deps), default=0.0)
+    jobs, objs = [], []
     for s in srcs:
         o = os.path.join(objdir, os.path.basename(s) + ".o")
+        objs.append(o)
+        if incremental and os.path.exists(o) and os.path.getmtime(o) > max(os.path.getmtime(s), newest_dep):
+            continue
         jobs.append((s, o))
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
-        list(ex.map(lambda so: _run([HIPCC] + HIP_FLAGS + ["-c", so[0], "-o", so[1]]), jobs))
+    if jobs:
+        with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+            list(ex.map(lambda so: _run([HIPCC] + HIP_FLAGS + ["-c", so[0], "-o", so[1]]), jobs))
     out = os.path.join(PKG, "libvitna_hip.so")
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out] + [o for _, o in jobs])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out] + objs)
     return out
 
 
@@ -66,7 +74,8 @@ def build_oracle():
 
 def main(argv):
     build_synth()
-    build_hip()
+    # --incremental (a developer's rebuild): objects newer than their source and every header are kept
+    build_hip(incremental="--incremental" in argv)
     if "--all" in argv:
         build_oracle()
 

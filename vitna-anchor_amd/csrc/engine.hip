@@ -53,6 +53,7 @@ struct vitna_cuda_model {
     /* scratch, ROWS_MAX rows */
     float *x, *xn, *q, *k, *v, *qp, *att, *act, *ypart, *rlogits, *vocab, *partial;
     route_out* rt;
+    route_out* rt_layers; /* the device-routed step's routing of every layer (the last layer's is also in rt) */
     row_rec* rows_dev;
     row_rec* rows_host; /* pinned */
     hipEvent_t rows_copied;
@@ -99,6 +100,19 @@ static bool fail(char* err, size_t len, const char* fmt, ...) {
 static bool fail_hip(char* err, size_t len, const char* what, hipError_t e) {
     return fail(err, len, "%s: %s (%s)", what, hipGetErrorString(e), hipGetErrorName(e));
 }
+
+/* Two timing events, destroyed on every path out. */
+struct event_pair {
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    hipError_t make() {
+        hipError_t e = hipEventCreate(&t0);
+        return e == hipSuccess ? hipEventCreate(&t1) : e;
+    }
+    ~event_pair() {
+        if (t0) (void)hipEventDestroy(t0);
+        if (t1) (void)hipEventDestroy(t1);
+    }
+};
 
 #define HIP_TRY(call, what)                                          \
     do {                                                             \
@@ -156,6 +170,9 @@ static bool check_shapes(const vitna_llama_t* m, char* err, size_t err_len) {
         return fail(err, err_len, "expert width %zu with %zu experts a token is not a shape the down kernel takes", c->intermediate,
                     c->n_experts_used);
     if (!m->ctx || !m->seqs) return fail(err, err_len, "the model has no key-value cache shape (ctx %zu, seqs %zu)", m->ctx, m->seqs);
+    if (c->n_heads && m->ctx > (size_t)ATTN_SPLITS_MAX * ATTN_CHUNK)
+        return fail(err, err_len, "a context of %zu positions: the device attention merges at most %d chunks of %d (%d positions)", m->ctx,
+                    ATTN_SPLITS_MAX, ATTN_CHUNK, ATTN_SPLITS_MAX * ATTN_CHUNK);
     char what[96];
     for (size_t l = 0; l < c->n_layers; l++) {
         const vitna_llama_layer_t* L = &m->layers[l];
@@ -471,6 +488,7 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
          dalloc(g, &g->gm_xsum, R * (H / 16) * 4, "scratch", err, err_len) &&
          dalloc(g, &g->gm_asum, R * K * (c->intermediate / 16) * 4, "scratch", err, err_len) &&
          dalloc(g, &g->rlogits, 2 * R * E * 4, "scratch", err, err_len) && dalloc(g, &g->rt, R * sizeof(route_out), "scratch", err, err_len) &&
+         dalloc(g, &g->rt_layers, c->n_layers * sizeof(route_out), "scratch", err, err_len) &&
          dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len) &&
          dalloc(g, &g->grp_count, E * sizeof(int), "scratch", err, err_len) &&
          dalloc(g, &g->grp_pairs, E * R * sizeof(int), "scratch", err, err_len);
@@ -580,15 +598,16 @@ static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, i
 }
 
 /* The experts of one token: routed from logits in the kernel's prologue when they are given, else as g->rt holds it. */
-static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, const float* logits, float* y, int add) {
+static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, const float* logits, float* y, int add, route_out* rt = nullptr) {
     const dlayer& d = g->L[layer];
+    if (!rt) rt = g->rt;
     experts_in_args ai;
-    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = g->rt; ai.logits = logits; ai.E = g->E; ai.renorm = g->renorm;
+    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn; ai.rt = rt; ai.logits = logits; ai.E = g->E; ai.renorm = g->renorm;
     ai.act = g->act; ai.K = g->K;
     hipError_t e = launch_experts_in(ai, g->stream);
     if (e != hipSuccess) return e;
     experts_down_args ad;
-    ad.down = d.down; ad.act = g->act; ad.rt = g->rt; ad.y = y; ad.K = g->K; ad.add = add;
+    ad.down = d.down; ad.act = g->act; ad.rt = rt; ad.y = y; ad.K = g->K; ad.add = add;
     return launch_experts_down(ad, g->stream);
 }
 
@@ -859,7 +878,8 @@ static hipError_t enqueue_step_body(vitna_cuda_model* g) {
     for (int l = 0; e == hipSuccess && l < g->NL; l++) {
         e = enqueue_attention(g, l, 1, false);
         if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, 1, g->x, g->xn, true);
-        if (e == hipSuccess) e = enqueue_experts(g, l, g->rlogits, g->x, 1);
+        /* each layer's routing kept for the checkers; the last layer's where the rows' routing is read */
+        if (e == hipSuccess) e = enqueue_experts(g, l, g->rlogits, g->x, 1, l + 1 < g->NL ? g->rt_layers + l : g->rt);
     }
     if (e == hipSuccess) e = enqueue_head(g);
     return e;
@@ -958,6 +978,32 @@ extern "C" bool vitna_hip_routing(struct vitna_cuda_model* g, size_t row, float*
     return true;
 }
 
+extern "C" bool vitna_hip_step_routing(struct vitna_cuda_model* g, size_t layer, int32_t* chosen, int32_t* ids, float* weights,
+                                       char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no model");
+    if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
+    route_out r;
+    const route_out* src = layer + 1 < (size_t)g->NL ? g->rt_layers + layer : g->rt;
+    HIP_TRY(hipMemcpy(&r, src, sizeof(r), hipMemcpyDeviceToHost), "copying the routing");
+    for (int k = 0; k < g->K; k++) {
+        if (chosen) chosen[k] = r.chosen[k];
+        if (ids) ids[k] = r.ids[k];
+        if (weights) weights[k] = r.weights[k];
+    }
+    return true;
+}
+
+extern "C" bool vitna_hip_attention_io(struct vitna_cuda_model* g, size_t row, float* q, float* att, char* err, size_t err_len) {
+    if (!g || !g->attention) return fail(err, err_len, "no attention");
+    if (row >= ROWS_MAX) return fail(err, err_len, "row %zu: at most %d", row, ROWS_MAX);
+    const size_t qd = (size_t)g->nh * g->hd;
+    HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
+    if (q) HIP_TRY(hipMemcpy(q, g->q + row * qd, qd * 4, hipMemcpyDeviceToHost), "copying q");
+    if (att) HIP_TRY(hipMemcpy(att, g->att + row * qd, qd * 4, hipMemcpyDeviceToHost), "copying the attention output");
+    return true;
+}
+
 extern "C" bool vitna_hip_kv(struct vitna_cuda_model* g, size_t seq, size_t layer, size_t pos0, size_t n, float* k, float* v, bool write,
                              char* err, size_t err_len) {
     if (!g || !g->attention) return fail(err, err_len, "no key-value cache");
@@ -1007,9 +1053,9 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if ((which >= 3 && which <= 6 && !g->attention) || which < 0 || which > 9)
         return fail(err, err_len, "no such kernel (%d) in this model", which);
-    hipEvent_t t0, t1;
-    HIP_TRY(hipEventCreate(&t0), "events");
-    HIP_TRY(hipEventCreate(&t1), "events");
+    event_pair ev;
+    HIP_TRY(ev.make(), "events");
+    hipEvent_t t0 = ev.t0, t1 = ev.t1;
     double b = 0;
     const int H = g->H, K = g->K;
     auto one = [&](int i) -> hipError_t {
@@ -1087,8 +1133,6 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
     HIP_TRY(hipEventSynchronize(t1), "timing");
     float ms = 0;
     HIP_TRY(hipEventElapsedTime(&ms, t0, t1), "events");
-    (void)hipEventDestroy(t0);
-    (void)hipEventDestroy(t1);
     if (avg_us) *avg_us = 1000.0 * ms / reps;
     if (bytes) *bytes = b;
     return true;
@@ -1239,22 +1283,17 @@ extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (steps < 1) return fail(err, err_len, "at least one step");
     if (!ensure_graph(g, err, err_len)) return false;
+    /* every timed step decodes the same row, copied in once */
     if (!set_row(g, seq, token, pos, err, err_len)) return false;
-    hipEvent_t t0, t1;
-    HIP_TRY(hipEventCreate(&t0), "events");
-    HIP_TRY(hipEventCreate(&t1), "events");
+    event_pair ev;
+    HIP_TRY(ev.make(), "events");
     HIP_TRY(hipStreamSynchronize(g->stream), "before timing");
-    HIP_TRY(hipEventRecord(t0, g->stream), "events");
-    for (int i = 0; i < steps; i++) {
-        if (!set_row(g, seq, token, pos, err, err_len)) return false;
-        HIP_TRY(hipGraphLaunch(g->step_graph, g->stream), "launching the step");
-    }
-    HIP_TRY(hipEventRecord(t1, g->stream), "events");
-    HIP_TRY(hipEventSynchronize(t1), "timing the steps");
+    HIP_TRY(hipEventRecord(ev.t0, g->stream), "events");
+    for (int i = 0; i < steps; i++) HIP_TRY(hipGraphLaunch(g->step_graph, g->stream), "launching the step");
+    HIP_TRY(hipEventRecord(ev.t1, g->stream), "events");
+    HIP_TRY(hipEventSynchronize(ev.t1), "timing the steps");
     float ms = 0;
-    HIP_TRY(hipEventElapsedTime(&ms, t0, t1), "events");
-    (void)hipEventDestroy(t0);
-    (void)hipEventDestroy(t1);
+    HIP_TRY(hipEventElapsedTime(&ms, ev.t0, ev.t1), "events");
     *ms_per_step = (double)ms / steps;
     return true;
 }
@@ -1594,19 +1633,16 @@ extern "C" bool vitna_hip_time_rows(struct vitna_cuda_model* g, const vitna_cuda
     if (steps < 1) return fail(err, err_len, "at least one step");
     if (!set_rows(g, rows, n, err, err_len)) return false;
     if (!ensure_rows_graph(g, (int)n, err, err_len)) return false;
-    hipEvent_t t0, t1;
-    HIP_TRY(hipEventCreate(&t0), "events");
-    HIP_TRY(hipEventCreate(&t1), "events");
+    event_pair ev;
+    HIP_TRY(ev.make(), "events");
     HIP_TRY(hipGraphLaunch(g->rows_graph, g->stream), "launching the rows step"); /* warm-up */
     HIP_TRY(hipStreamSynchronize(g->stream), "before timing");
-    HIP_TRY(hipEventRecord(t0, g->stream), "events");
+    HIP_TRY(hipEventRecord(ev.t0, g->stream), "events");
     for (int i = 0; i < steps; i++) HIP_TRY(hipGraphLaunch(g->rows_graph, g->stream), "launching the rows step");
-    HIP_TRY(hipEventRecord(t1, g->stream), "events");
-    HIP_TRY(hipEventSynchronize(t1), "timing the rows steps");
+    HIP_TRY(hipEventRecord(ev.t1, g->stream), "events");
+    HIP_TRY(hipEventSynchronize(ev.t1), "timing the rows steps");
     float ms = 0;
-    HIP_TRY(hipEventElapsedTime(&ms, t0, t1), "events");
-    (void)hipEventDestroy(t0);
-    (void)hipEventDestroy(t1);
+    HIP_TRY(hipEventElapsedTime(&ms, ev.t0, ev.t1), "events");
     *ms_per_step = (double)ms / steps;
     return true;
 }

@@ -565,7 +565,7 @@ hipError_t launch_attention(const attn_args& a, hipStream_t s) {
    maxima and sums read in parallel, each chunk's scale exp(m_s - M) computed
    once, then each dimension's weighted values summed, eight chunks' loads in
    flight at a time. */
-#define MERGE_MAX 1024
+#define MERGE_MAX ATTN_SPLITS_MAX
 #define MERGE_PRE 32 /* chunks whose values are requested with their maxima and sums */
 __global__ void attention_merge_kernel(attn_args a) {
     const int hq = blockIdx.x, row = blockIdx.y, d = threadIdx.x;

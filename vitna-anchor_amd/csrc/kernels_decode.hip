@@ -645,7 +645,17 @@ hipError_t launch_gemv(const gemv_args& a, hipStream_t s) {
     hipError_t e = gemv_combo_q4(a, d0, d1, d2, s, &served);
     if (!served) e = gemv_combo_q6(a, d0, d1, d2, s, &served);
     if (!served) e = gemv_combo_q8(a, d0, d1, d2, s, &served);
-    return served ? e : hipErrorInvalidValue;
+    if (served || a.n == 1) return served ? e : hipErrorInvalidValue;
+    /* a mix of dtypes no fused instantiation holds: one launch a matrix, each a single-dtype kernel */
+    for (int i = 0; i < a.n; i++) {
+        gemv_args one = a;
+        one.n = 1;
+        one.w[0] = a.w[i];
+        one.y[0] = a.y[i];
+        e = launch_gemv(one, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 /* ------------------------------------------------------------------ */

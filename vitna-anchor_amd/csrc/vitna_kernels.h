@@ -131,6 +131,9 @@ struct row_rec {
    sum, weighted values) in partial; launch_attention_merge combines them into
    att. */
 #define ATTN_CHUNK 64
+/* The most chunks a row's merge combines (its LDS holds one maximum and one sum a chunk): a context of at most
+   ATTN_SPLITS_MAX * ATTN_CHUNK positions. */
+#define ATTN_SPLITS_MAX 1024
 /* Where a pass's operand images for the multi-row projections go (skinny_image.h); a null: none. */
 struct img_out {
     u32x4* a;

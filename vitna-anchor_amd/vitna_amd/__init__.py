@@ -237,6 +237,8 @@ def _hip():
         "vitna_hip_residual": (C.c_bool, [P, C.c_size_t, _FP, C.c_bool, *E]),
         "vitna_hip_rows_project": (C.c_bool, [P, C.c_size_t, C.c_int, _FP, C.c_size_t, _FP, *E]),
         "vitna_hip_routing": (C.c_bool, [P, C.c_size_t, _FP, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _FP, *E]),
+        "vitna_hip_step_routing": (C.c_bool, [P, C.c_size_t, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _FP, *E]),
+        "vitna_hip_attention_io": (C.c_bool, [P, C.c_size_t, _FP, _FP, *E]),
         "vitna_hip_kv": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, _FP, _FP, C.c_bool, *E]),
         "vitna_hip_kv_fill": (C.c_bool, [P, C.c_uint64, C.POINTER(C.c_size_t), *E]),
         "vitna_hip_sync": (C.c_bool, [P, *E]),
@@ -397,6 +399,24 @@ class Device:
         w = np.empty(cfg.n_experts_used, np.float32)
         self._ok(self.lib.vitna_hip_routing(self.g, row, fptr(lg), _i32(ch), _i32(ids), fptr(w), self.err, 512))
         return lg, ch, ids, w
+
+    def step_routing(self, layer):
+        """(chosen largest first, ids in order, weights) of layer in the last device-routed step."""
+        K = self.model.cfg.n_experts_used
+        ch = np.empty(K, np.int32)
+        ids = np.empty(K, np.int32)
+        w = np.empty(K, np.float32)
+        self._ok(self.lib.vitna_hip_step_routing(self.g, layer, _i32(ch), _i32(ids), fptr(w), self.err, 512))
+        return ch, ids, w
+
+    def attention_io(self, row=0):
+        """(q before its norm and rotation, attention output) of row at the last layer of the last step or pass."""
+        cfg = self.model.cfg
+        qd = cfg.n_heads * cfg.head_dim
+        q = np.empty(qd, np.float32)
+        att = np.empty(qd, np.float32)
+        self._ok(self.lib.vitna_hip_attention_io(self.g, row, fptr(q), fptr(att), self.err, 512))
+        return q, att
 
     def kv(self, seq, layer, pos0, n, k=None, v=None):
         cfg = self.model.cfg
