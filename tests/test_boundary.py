@@ -53,10 +53,14 @@ def test_ctypes_mirror_matches_reference():
 
 
 def declared_functions():
-    with open(os.path.join(ROOT, "include", "vitna_hip.h")) as f:
-        text = f.read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(vitna_(?:cuda|hip)_\w+)\s*\(", text)))
+    """Every function the library's headers (include/vitna_hip.h, include/vitna_gguf.h) declare."""
+    names = set()
+    for h in ("vitna_hip.h", "vitna_gguf.h"):
+        with open(os.path.join(ROOT, "include", h)) as f:
+            text = f.read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"\b(vitna_(?:cuda|hip)_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_function():
@@ -77,10 +81,10 @@ def test_headers_compile_as_c_and_cpp():
     with tempfile.TemporaryDirectory() as d:
         src_c = os.path.join(d, "t.c")
         with open(src_c, "w") as f:
-            f.write('#include "vitna_hip.h"\nint main(void) { return vitna_cuda_probe(0, 0) ? 0 : 0; }\n')
+            f.write('#include "vitna_hip.h"\n#include "vitna_gguf.h"\nint main(void) { return vitna_cuda_probe(0, 0) ? 0 : 0; }\n')
         src_cc = os.path.join(d, "t.cc")
         with open(src_cc, "w") as f:
-            f.write('#include "vitna_hip.h"\nint main() { return 0; }\n')
+            f.write('#include "vitna_hip.h"\n#include "vitna_gguf.h"\nint main() { return 0; }\n')
         inc = os.path.join(ROOT, "include")
         for cmd in (["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-I", inc, "-c", src_c, "-o", os.path.join(d, "c.o")],
                     ["g++", "-std=c++11", "-Wall", "-Wextra", "-Werror", "-I", inc, "-c", src_cc, "-o", os.path.join(d, "cc.o")]):

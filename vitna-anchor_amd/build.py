@@ -50,9 +50,19 @@ def build_hip(incremental=False):
         if incremental and os.path.exists(o) and os.path.getmtime(o) > max(os.path.getmtime(s), newest_dep):
             continue
         jobs.append((s, o))
+    # host-only C++ (the GGUF reader) compiles with the host compiler
+    for s in sorted(glob.glob(os.path.join(PKG, "csrc", "*.cpp"))):
+        o = os.path.join(objdir, os.path.basename(s) + ".o")
+        objs.append(o)
+        if not (incremental and os.path.exists(o) and os.path.getmtime(o) > max(os.path.getmtime(s), newest_dep)):
+            jobs.append((s, o))
     if jobs:
+        def compile_one(so):
+            if so[0].endswith(".cpp"):
+                return _run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-c", so[0], "-o", so[1]])
+            return _run([HIPCC] + HIP_FLAGS + ["-c", so[0], "-o", so[1]])
         with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
-            list(ex.map(lambda so: _run([HIPCC] + HIP_FLAGS + ["-c", so[0], "-o", so[1]]), jobs))
+            list(ex.map(compile_one, jobs))
     out = os.path.join(PKG, "libvitna_hip.so")
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", out] + objs)
     return out
@@ -61,7 +71,7 @@ def build_hip(incremental=False):
 def build_synth():
     out = os.path.join(PKG, "synth", "libvitna_synth.so")
     _run(["gcc", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", os.path.join(PKG, "synth", "vitna_synth.c"),
-          "-o", out, "-lm", "-lpthread"])
+          os.path.join(PKG, "synth", "gguf_write.c"), "-o", out, "-lm", "-lpthread"])
     return out
 
 

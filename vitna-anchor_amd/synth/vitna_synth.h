@@ -56,6 +56,11 @@ void vitna_synth_normal(uint64_t seed, uint64_t tag, float* out, size_t n);
    unsupported dtype or shape. */
 int vitna_synth_matrix(int dtype, uint64_t seed, uint64_t tag, size_t rows, size_t cols, float scale, void* out, int threads);
 
+/* The model written into directory dir as model.gguf (GGUF version 3, llama.cpp's tensor names, expert stacks,
+   data aligned to alignment, norm weights stored as norm_dtype: F32, F16 or BF16) and config.json (the keys the
+   engine's loader reads). The model must hold attention and a mixture of experts. Returns 0, or -1 with err. */
+int vitna_synth_write_gguf(const vitna_llama_t* m, const char* dir, int norm_dtype, uint32_t alignment, char* err, size_t err_len);
+
 /* Round-to-nearest-even float32 to float16 bits. */
 uint16_t vitna_synth_f32_to_f16(float f);
 

@@ -124,6 +124,7 @@ def _synth():
     lib.vitna_synth_normal.argtypes = [C.c_uint64, C.c_uint64, _FP, C.c_size_t]
     lib.vitna_synth_matrix.argtypes = [C.c_int, C.c_uint64, C.c_uint64, C.c_size_t, C.c_size_t, C.c_float, C.c_void_p,
                                        C.c_int]
+    lib.vitna_synth_write_gguf.argtypes = [C.POINTER(Llama), C.c_char_p, C.c_int, C.c_uint32, C.c_char_p, C.c_size_t]
     lib.vitna_synth_f32_to_f16.restype = C.c_uint16
     lib.vitna_synth_f32_to_f16.argtypes = [C.c_float]
     return lib
@@ -202,6 +203,109 @@ class VitnaError(RuntimeError):
     pass
 
 
+def write_gguf(model, directory, norm_dtype=F32, alignment=32):
+    """model (a synthetic Model) written into directory as model.gguf and config.json."""
+    err = C.create_string_buffer(512)
+    if synth().vitna_synth_write_gguf(model.ptr, directory.encode(), norm_dtype, alignment, err, 512):
+        raise VitnaError(err.value.decode())
+    return os.path.join(directory, "model.gguf")
+
+
+class GgufInfo(C.Structure):
+    """vitna_hip_gguf_info_t (include/vitna_gguf.h)."""
+    _fields_ = [("arch", C.c_char * 64), ("version", C.c_uint32), ("alignment", C.c_uint64)] + \
+               [(n, C.c_uint64) for n in ("block_count", "embedding_length", "feed_forward_length",
+                                          "expert_feed_forward_length", "head_count", "head_count_kv", "key_length",
+                                          "context_length", "expert_count", "expert_used_count")] + \
+               [("rms_eps", C.c_double), ("rope_freq_base", C.c_double), ("file_tensors", C.c_size_t),
+                ("split_no", C.c_uint16), ("split_count", C.c_uint16), ("split_tensors_count", C.c_uint64)]
+
+
+class GgufTensor(C.Structure):
+    """vitna_hip_gguf_tensor_t (include/vitna_gguf.h)."""
+    _fields_ = [("name", C.c_char * 256), ("dtype", C.c_int), ("ndim", C.c_size_t), ("shape", C.c_size_t * 2),
+                ("offset_begin", C.c_uint64), ("offset_end", C.c_uint64), ("data", C.c_void_p)]
+
+
+def config_from_json(path):
+    """The engine's config from a checkpoint's config.json, as engine/src/model.c:54-137 (read_config) reads it for
+    the mixture-of-experts models (model_type olmoe or qwen3_moe); other model types are refused."""
+    import json
+    with open(path) as f:
+        j = json.load(f)
+    mt = j.get("model_type")
+    if mt not in ("olmoe", "qwen3_moe"):
+        raise VitnaError("config.json: model_type is %s, and only olmoe and qwen3_moe are served" % mt)
+    if j.get("hidden_act") != "silu":
+        raise VitnaError("config.json: hidden_act is %s, and only silu is supported" % j.get("hidden_act"))
+    qwen3 = mt == "qwen3_moe"
+    c = Config()
+    c.n_layers = j["num_hidden_layers"]
+    c.hidden = j["hidden_size"]
+    c.intermediate = j["moe_intermediate_size"] if qwen3 else j["intermediate_size"]
+    c.n_heads = j["num_attention_heads"]
+    c.vocab = j["vocab_size"]
+    c.max_positions = j["max_position_embeddings"]
+    c.n_kv_heads = j.get("num_key_value_heads", c.n_heads)
+    c.head_dim = j.get("head_dim", c.hidden // c.n_heads)
+    if c.n_heads % c.n_kv_heads or c.head_dim % 2:
+        raise VitnaError("config.json: heads do not divide into key-value groups, or head_dim is odd")
+    c.n_experts = j["num_experts"]
+    c.n_experts_used = j["num_experts_per_tok"]
+    c.rms_eps = float(j.get("rms_norm_eps", 1e-6 if qwen3 else 1e-5))
+    c.rope_theta = float(j.get("rope_theta", 10000.0))
+    c.tied_embeddings = bool(j.get("tie_word_embeddings", False))
+    c.qk_norm = True
+    c.qk_norm_per_head = qwen3
+    c.qwen3 = qwen3
+    c.renormalize = bool(j.get("norm_topk_prob", False))
+    return c
+
+
+class GgufModel:
+    """A GGUF checkpoint (model.gguf with its config.json) read by the library's GGUF reader into the engine's
+    vitna_llama_t: the same interface as Model (ptr, m, cfg, rope_tables, free), so Device and the checker take it."""
+
+    def __init__(self, path, ctx=0, seqs=1, config=None):
+        lib = hip()
+        self.err = C.create_string_buffer(512)
+        self.info = GgufInfo()
+        self.g = lib.vitna_hip_gguf_open(path.encode(), C.byref(self.info), self.err, 512)
+        if not self.g:
+            raise VitnaError(self.err.value.decode())
+        cfg = config if config is not None else config_from_json(os.path.join(os.path.dirname(path), "config.json"))
+        self._llama = Llama()
+        if not lib.vitna_hip_gguf_llama(self.g, C.byref(cfg), ctx, seqs, C.byref(self._llama), self.err, 512):
+            lib.vitna_hip_gguf_close(self.g)
+            self.g = None
+            raise VitnaError(self.err.value.decode())
+        self.ptr = C.pointer(self._llama)
+        self.m = self._llama
+
+    cfg = Model.cfg
+    rope_tables = Model.rope_tables
+
+    def tensors(self):
+        """The directory: (name, dtype, ndim, shape0, shape1, offset_begin, offset_end) per tensor."""
+        lib = hip()
+        out = []
+        t = GgufTensor()
+        for i in range(lib.vitna_hip_gguf_count(self.g)):
+            assert lib.vitna_hip_gguf_tensor(self.g, i, C.byref(t))
+            out.append((t.name.decode(), t.dtype, t.ndim, t.shape[0], t.shape[1] if t.ndim > 1 else 0, t.offset_begin,
+                        t.offset_end))
+        return out
+
+    def data_offset(self):
+        return hip().vitna_hip_gguf_data_offset(self.g)
+
+    def free(self):
+        if self.g:
+            hip().vitna_hip_gguf_llama_free(C.byref(self._llama))
+            hip().vitna_hip_gguf_close(self.g)
+            self.g = None
+
+
 class RowT(C.Structure):
     _fields_ = [("token", C.c_int32), ("pos", C.c_int32), ("seq", C.c_int32)]
 
@@ -239,6 +343,13 @@ def _hip():
         "vitna_hip_routing": (C.c_bool, [P, C.c_size_t, _FP, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _FP, *E]),
         "vitna_hip_step_routing": (C.c_bool, [P, C.c_size_t, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _FP, *E]),
         "vitna_hip_attention_io": (C.c_bool, [P, C.c_size_t, _FP, _FP, *E]),
+        "vitna_hip_gguf_open": (P, [C.c_char_p, C.POINTER(GgufInfo), *E]),
+        "vitna_hip_gguf_count": (C.c_size_t, [P]),
+        "vitna_hip_gguf_tensor": (C.c_bool, [P, C.c_size_t, C.POINTER(GgufTensor)]),
+        "vitna_hip_gguf_data_offset": (C.c_uint64, [P]),
+        "vitna_hip_gguf_llama": (C.c_bool, [P, C.POINTER(Config), C.c_size_t, C.c_size_t, C.POINTER(Llama), *E]),
+        "vitna_hip_gguf_llama_free": (None, [C.POINTER(Llama)]),
+        "vitna_hip_gguf_close": (None, [P]),
         "vitna_hip_kv": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, _FP, _FP, C.c_bool, *E]),
         "vitna_hip_kv_fill": (C.c_bool, [P, C.c_uint64, C.POINTER(C.c_size_t), *E]),
         "vitna_hip_sync": (C.c_bool, [P, *E]),
