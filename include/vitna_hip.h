@@ -154,6 +154,26 @@ bool vitna_hip_residual(struct vitna_cuda_model* g, size_t row, float* host, boo
 bool vitna_hip_routing(struct vitna_cuda_model* g, size_t row, float* logits, int32_t* chosen, int32_t* ids, float* weights, char* err,
                        size_t err_len);
 
+/** Which kernels a decode step runs: on = 0 (the default) the per-layer
+    kernels replayed as one HIP graph; on = 1 the persistent step kernel, one
+    cooperative launch that runs every layer with device-scope flags between
+    its phases, where the model's shape takes it (*taken, if not NULL, says
+    whether it does). Both give the same bits. An engine choice with no
+    reference counterpart. */
+bool vitna_hip_set_step_kernel(struct vitna_cuda_model* g, int on, int* taken, char* err, size_t err_len);
+
+/** One decode step (or, for a model without attention, one pass over its
+    layers on residual row 0) on the persistent step kernel with block
+    block's control wave stamping each phase: for every layer,
+    VITNA_HIP_TRACE_PER_LAYER 64-bit s_memrealtime readings (100 MHz) into out
+    (n >= layers * that), in order: for each of the six phases (q/k/v,
+    attention, o-projection, router, experts in, experts down) the start of
+    its wait, its inputs ready, its results published; 0 where the block has
+    no part. A measurement hook: no reference counterpart. */
+#define VITNA_HIP_TRACE_PER_LAYER 32
+bool vitna_hip_step_trace(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, int block, uint64_t* out, size_t n, char* err,
+                          size_t err_len);
+
 /** Row row's query projection (before its QK-norm and RoPE) and attention
     output (heads x head_dim each) as the last step or rows pass left them at
     its last layer. Either pointer may be NULL. Synchronous. A checker's hook

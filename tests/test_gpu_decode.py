@@ -57,12 +57,16 @@ def ffn_case(cfg_id, seed, x_tag):
     return model, dev
 
 
+@pytest.mark.parametrize("persistent", [False, True], ids=["graph", "persistent"])
 @pytest.mark.parametrize("cfg_id", [0, 1])
-def test_moe_layer_full_size(cfg_id):
-    """BASELINE configs 0 and 1: one MoE layer, batch 1, full size, device routing."""
-    say("moe layer config", cfg_id)
+def test_moe_layer_full_size(cfg_id, persistent):
+    """BASELINE configs 0 and 1: one MoE layer, batch 1, full size, device routing; on the per-layer kernels and on
+    the persistent step kernel."""
+    say("moe layer config", cfg_id, "persistent" if persistent else "graph")
     model, dev = ffn_case(cfg_id, 1000 + cfg_id, 7)
     try:
+        if persistent:
+            assert dev.set_step_kernel(True)
         cfg = model.cfg
         H = cfg.hidden
         for trial in range(3):
@@ -185,15 +189,18 @@ def C_f32(addr):
     return ctypes.cast(addr, ctypes.POINTER(ctypes.c_float))
 
 
+@pytest.mark.parametrize("persistent", [False, True], ids=["graph", "persistent"])
 @pytest.mark.parametrize("name,pos,token", [("q4km", 150, 7), ("q8", 79, 250), ("q4km", 192, 11), ("q4km", 199, 5)])
-def test_device_step_matches_cpu(name, pos, token):
+def test_device_step_matches_cpu(name, pos, token, persistent):
     """vitna_hip_moe_step (device routing, one graph): logits within tolerance of the CPU step, replayed at two
     positions through the same graph. Cases: mid-chunk; the last position of the context (q8: 79 of 80, q4km:
     199 of 200); 191 then 192, the last position of a full 64-position attention chunk then the first of the
     next."""
-    say("device step", name, pos, token)
+    say("device step", name, pos, token, "persistent" if persistent else "graph")
     model, dev, kc, vc = prefilled(name, 654, pos + 1)
     try:
+        if persistent:
+            dev.set_step_kernel(True)
         for p in (pos - 1, pos):
             ref_logits, _, ref_tc, _ = oracle.step(model, 0, token, p)
             logits = dev.step(0, token, p)

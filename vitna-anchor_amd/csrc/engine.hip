@@ -17,6 +17,7 @@
  */
 
 #include "vitna_kernels.h"
+#include "step_kernel.h"
 #include "../../include/vitna_hip.h"
 
 #include <stdarg.h>
@@ -74,6 +75,19 @@ struct vitna_cuda_model {
     bool rows_graph_shared;
     hipGraphExec_t step_graph;
     bool graph_ready;
+    /* the persistent decode step (kernels_step.hip): set up on first use when the model's shape takes it */
+    int step_state;             /* 0: not looked at, 1: ready, -1: this model runs the per-layer kernels */
+    const char* step_reason;    /* why not, for -1 */
+    bool step_want;             /* the caller asked for the persistent step (vitna_hip_set_step_kernel) */
+    step_layer* step_L;         /* device: the layer table */
+    float* step_buf;            /* device: every layer's activation buffers */
+    uint32_t* step_flags;       /* device: [NL][phases][256] epochs, then the abort word */
+    uint32_t step_epoch;
+    int step_nb;
+    step_args step_base;        /* the arguments every launch shares */
+    bool last_step_mega;        /* the last decode step ran the persistent kernel */
+    int last_mega_n;            /* and over this many layers */
+    uint64_t* step_trace;       /* device: a traced step's phase timeline */
     bool tiled_ready;           /* the multi-row paths' tiled copies made (ensure_tiled) */
     bool lost;
     size_t fast_rows, long_from;
@@ -650,6 +664,7 @@ extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (!g->attention) return fail(err, err_len, "this model has no attention; use vitna_hip_moe_ffn");
     if (!set_row(g, seq, token, pos, err, err_len)) return false;
+    g->last_step_mega = false;
     hipError_t e = hipSuccess;
     if (layer == 0) e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
     if (e == hipSuccess) e = enqueue_attention(g, (int)layer, 1, false);
@@ -873,6 +888,133 @@ extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_
 
 /* ---- extensions --------------------------------------------------------- */
 
+/* The persistent step's resources, on first use: whether the model's shape takes it, the layer table, the
+   activation buffers and the flags (zeroed: the first launch's epoch is 1). */
+static bool ensure_step(vitna_cuda_model* g, char* err, size_t err_len) {
+    if (g->step_state) return true;
+    const int H = g->H, qd = g->nh * g->hd, kd = g->nkv * g->hd, G = g->nkv ? g->nh / g->nkv : 1;
+    int nb = std::min(256, gemv_device_cus());
+    /* the largest block count the o-projection's split divides */
+    const char* why = nullptr;
+    for (; nb >= 8; nb--)
+        if (!(why = step_unsupported(H, g->I, g->E, g->K, g->nh, g->nkv, g->hd, nb, g->attention ? g->L[0].q.dtype : 0,
+                                     g->attention ? g->L[0].k.dtype : 0, g->attention ? g->L[0].v.dtype : 0,
+                                     g->attention ? g->L[0].o.dtype : 0, g->L[0].gate.dtype, g->L[0].down.dtype)))
+            break;
+    bool same = true;
+    for (int l = 1; l < g->NL; l++)
+        same &= g->L[l].gate.dtype == g->L[0].gate.dtype && g->L[l].down.dtype == g->L[0].down.dtype &&
+                (!g->attention || (g->L[l].o.dtype == g->L[0].o.dtype && g->L[l].q.dtype == g->L[0].q.dtype &&
+                                   g->L[l].k.dtype == g->L[0].k.dtype && g->L[l].v.dtype == g->L[0].v.dtype));
+    if (why || nb < 8 || !same) {
+        g->step_state = -1;
+        g->step_reason = why ? why : "dtypes that differ between layers";
+        return true;
+    }
+    const size_t prec = (size_t)g->hd + 4;
+    step_args& a = g->step_base;
+    memset(&a, 0, sizeof(a));
+    a.s_qkv = (size_t)qd + 2 * kd;
+    a.s_part = (size_t)nb * G * prec;
+    a.s_opart = g->attention ? (size_t)(qd / 256) * H : 0;
+    a.s_att = qd;
+    a.s_xmid = H;
+    a.s_logits = g->E;
+    a.s_act = (size_t)g->K * g->I;
+    auto al4 = [](size_t n) { return (n + 63) & ~(size_t)63; }; /* 256-byte aligned parts */
+    a.s_qkv = al4(a.s_qkv); a.s_part = al4(a.s_part); a.s_opart = al4(a.s_opart); a.s_att = al4(a.s_att);
+    a.s_xmid = al4(a.s_xmid); a.s_logits = al4(a.s_logits); a.s_act = al4(a.s_act);
+    const size_t per_layer = a.s_qkv + a.s_part + a.s_opart + a.s_att + a.s_xmid + a.s_logits + a.s_act + al4(H);
+    if (!dalloc(g, &g->step_buf, per_layer * g->NL * 4, "the step's activation buffers", err, err_len)) return false;
+    const size_t nflags = (size_t)g->NL * STEP_PHASES * 256 + 64;
+    if (!dalloc(g, &g->step_flags, nflags * 4, "the step's flags", err, err_len)) return false;
+    if (!dalloc(g, &g->step_L, g->NL * sizeof(step_layer), "the step's layer table", err, err_len)) return false;
+    HIP_TRY(hipMemset(g->step_flags, 0, nflags * 4), "clearing the step's flags");
+    std::vector<step_layer> lt(g->NL);
+    for (int l = 0; l < g->NL; l++) {
+        const dlayer& d = g->L[l];
+        step_layer& t = lt[l];
+        memset(&t, 0, sizeof(t));
+        t.q = d.q; t.k = d.k; t.v = d.v; t.o = d.o; t.gate = d.gate; t.up = d.up; t.down = d.down;
+        t.attn_norm = d.attn_norm; t.mlp_norm = d.mlp_norm; t.q_norm = d.q_norm; t.k_norm = d.k_norm; t.router = d.router;
+        if (g->attention) {
+            t.k_cache = g->k_cache + (size_t)l * g->layer_kv;
+            t.v_cache = g->v_cache + (size_t)l * g->layer_kv;
+        }
+    }
+    HIP_TRY(hipMemcpy(g->step_L, lt.data(), g->NL * sizeof(step_layer), hipMemcpyHostToDevice), "uploading the layer table");
+    float* p = g->step_buf;
+    a.qkv = p; p += a.s_qkv * g->NL;
+    a.part = p; p += a.s_part * g->NL;
+    a.opart = p; p += a.s_opart * g->NL;
+    a.att = p; p += a.s_att * g->NL;
+    a.xmid = p; p += a.s_xmid * g->NL;
+    a.logits = p; p += a.s_logits * g->NL;
+    a.act = p; p += a.s_act * g->NL;
+    a.xout = p;
+    a.flags = g->step_flags;
+    a.abort_word = g->step_flags + (size_t)g->NL * STEP_PHASES * 256;
+    a.L = g->step_L;
+    a.NL = g->NL;
+    a.embed = g->embed;
+    a.row = g->rows_dev;
+    a.cos_tab = g->cos_tab;
+    a.sin_tab = g->sin_tab;
+    a.seq_stride = (size_t)g->NL * g->layer_kv;
+    a.rt_layers = g->rt_layers;
+    a.rt_last = g->rt;
+    a.x0 = g->x;
+    a.x_final = g->x;
+    a.H = H; a.I = g->I; a.E = g->E; a.K = g->K; a.nh = g->nh; a.nkv = g->nkv; a.hd = g->hd;
+    a.renorm = g->renorm; a.attention = g->attention ? 1 : 0;
+    a.eps = g->eps;
+    a.nb = nb;
+    a.poll_nap = 1;
+    if (const char* v = getenv("VITNA_STEP_NAP")) a.poll_nap = atoi(v);
+    g->step_nb = nb;
+    g->step_epoch = 0;
+    g->step_state = 1;
+    return true;
+}
+
+/* Whether this call runs the persistent step: asked for, and the model's shape takes it. */
+static bool use_step(vitna_cuda_model* g, bool* mega, char* err, size_t err_len) {
+    *mega = false;
+    if (!g->step_want) return true;
+    if (!ensure_step(g, err, err_len)) return false;
+    *mega = g->step_state > 0;
+    return true;
+}
+
+/* One launch of the persistent step over layers first .. first + n - 1 (the whole model, or one layer of a model
+   without attention), on residual row 0. */
+static hipError_t launch_step_layers(vitna_cuda_model* g, int first, int n, uint64_t* trace = nullptr, int trace_block = 0) {
+    step_args a = g->step_base;
+    a.trace = trace;
+    a.trace_block = trace_block;
+    g->last_step_mega = true;
+    g->last_mega_n = n;
+    a.L = g->step_L + first;
+    a.NL = n;
+    a.rt_layers = g->rt_layers + first;
+    a.epoch = ++g->step_epoch;
+    const dlayer& d = g->L[first];
+    const int dts[5] = {d.gate.dtype, d.down.dtype, g->attention ? d.q.dtype : 0, g->attention ? d.v.dtype : 0,
+                        g->attention ? d.o.dtype : 0};
+    return launch_step(a, dts, g->stream);
+}
+
+/* After a synchronized persistent step: its abort word, cleared, as an error. */
+static bool step_check(vitna_cuda_model* g, char* err, size_t err_len) {
+    uint32_t ab = 0;
+    HIP_TRY(hipMemcpy(&ab, g->step_base.abort_word, 4, hipMemcpyDeviceToHost), "reading the step's state");
+    if (ab) {
+        (void)hipMemset(g->step_base.abort_word, 0, 4);
+        return fail(err, err_len, "the persistent step gave up waiting for a block (a block did not run or did not finish)");
+    }
+    return true;
+}
+
 static hipError_t enqueue_step_body(vitna_cuda_model* g) {
     hipError_t e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
     for (int l = 0; e == hipSuccess && l < g->NL; l++) {
@@ -905,9 +1047,19 @@ static bool ensure_graph(vitna_cuda_model* g, char* err, size_t err_len) {
 extern "C" bool vitna_hip_moe_step_async(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (!g->attention) return fail(err, err_len, "this model has no attention; use vitna_hip_moe_ffn");
+    bool mega;
+    if (!use_step(g, &mega, err, err_len)) return false;
+    if (mega) {
+        if (!set_row(g, seq, token, pos, err, err_len)) return false;
+        hipError_t e = launch_step_layers(g, 0, g->NL);
+        if (e == hipSuccess) e = enqueue_head(g);
+        g->last_step_mega = true;
+        return check_launch(g, e, "the step", err, err_len);
+    }
     if (!ensure_graph(g, err, err_len)) return false;
     if (!set_row(g, seq, token, pos, err, err_len)) return false;
     HIP_TRY(hipGraphLaunch(g->step_graph, g->stream), "launching the step");
+    g->last_step_mega = false;
     return true;
 }
 
@@ -916,12 +1068,49 @@ extern "C" bool vitna_hip_moe_step(struct vitna_cuda_model* g, size_t seq, int32
     if (!vitna_hip_moe_step_async(g, seq, token, pos, err, err_len)) return false;
     if (logits) HIP_TRY(hipMemcpyAsync(logits, g->vocab, (size_t)g->V * 4, hipMemcpyDeviceToHost, g->stream), "copying the logits");
     HIP_TRY(hipStreamSynchronize(g->stream), "running the step");
+    return !g->last_step_mega || step_check(g, err, err_len);
+}
+
+extern "C" bool vitna_hip_set_step_kernel(struct vitna_cuda_model* g, int on, int* taken, char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
+    g->step_want = on != 0;
+    bool mega = false;
+    if (!use_step(g, &mega, err, err_len)) return false;
+    if (taken) *taken = mega ? 1 : 0;
+    return true;
+}
+
+extern "C" bool vitna_hip_step_trace(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, int block, uint64_t* out, size_t n,
+                                     char* err, size_t err_len) {
+    if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
+    if (!ensure_step(g, err, err_len)) return false;
+    if (g->step_state < 1) return fail(err, err_len, "this model runs the per-layer kernels (%s)", g->step_reason);
+    if (block < 0 || block >= g->step_nb) return fail(err, err_len, "block %d: the step runs %d", block, g->step_nb);
+    const size_t need = (size_t)g->NL * STEP_TRACE_PER_LAYER;
+    if (n < need) return fail(err, err_len, "the timeline takes %zu words", need);
+    if (!g->step_trace && !dalloc(g, &g->step_trace, need * 8, "the step's timeline", err, err_len)) return false;
+    HIP_TRY(hipMemset(g->step_trace, 0, need * 8), "clearing the timeline");
+    if (g->attention && !set_row(g, seq, token, pos, err, err_len)) return false;
+    if (!check_launch(g, launch_step_layers(g, 0, g->NL, g->step_trace, block), "the traced step", err, err_len)) return false;
+    HIP_TRY(hipStreamSynchronize(g->stream), "running the traced step");
+    if (!step_check(g, err, err_len)) return false;
+    HIP_TRY(hipMemcpy(out, g->step_trace, need * 8, hipMemcpyDeviceToHost), "copying the timeline");
     return true;
 }
 
 extern "C" bool vitna_hip_moe_ffn(struct vitna_cuda_model* g, size_t layer, char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    bool mega = false;
+    if (!g->attention && !use_step(g, &mega, err, err_len)) return false;
+    if (mega) {
+        /* the persistent step, one layer, no attention: route, experts, sum onto row 0 */
+        if (!check_launch(g, launch_step_layers(g, (int)layer, 1), "the mixture of experts", err, err_len)) return false;
+        HIP_TRY(hipStreamSynchronize(g->stream), "running the mixture of experts");
+        return step_check(g, err, err_len);
+    }
+    g->last_step_mega = false;
     hipError_t e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn, true);
     if (e == hipSuccess) e = enqueue_experts(g, (int)layer, g->rlogits, g->x, 1);
     return check_launch(g, e, "the mixture of experts", err, err_len);
@@ -969,7 +1158,10 @@ extern "C" bool vitna_hip_routing(struct vitna_cuda_model* g, size_t row, float*
     HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
     route_out r;
     HIP_TRY(hipMemcpy(&r, g->rt + row, sizeof(r), hipMemcpyDeviceToHost), "copying the routing");
-    if (logits) HIP_TRY(hipMemcpy(logits, g->rlogits + row * g->E, g->E * 4, hipMemcpyDeviceToHost), "copying the router's logits");
+    const float* lsrc = g->rlogits + row * g->E;
+    if (g->last_step_mega && row == 0) /* the persistent step keeps each layer's logits in its own buffer */
+        lsrc = g->step_base.logits + (size_t)(g->last_mega_n - 1) * g->step_base.s_logits;
+    if (logits) HIP_TRY(hipMemcpy(logits, lsrc, g->E * 4, hipMemcpyDeviceToHost), "copying the router's logits");
     for (int k = 0; k < g->K; k++) {
         if (chosen) chosen[k] = r.chosen[k];
         if (ids) ids[k] = r.ids[k];
@@ -999,6 +1191,14 @@ extern "C" bool vitna_hip_attention_io(struct vitna_cuda_model* g, size_t row, f
     if (row >= ROWS_MAX) return fail(err, err_len, "row %zu: at most %d", row, ROWS_MAX);
     const size_t qd = (size_t)g->nh * g->hd;
     HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
+    if (g->last_step_mega && row == 0) {
+        /* the persistent step keeps each layer's q/k/v and attention output in its own buffers */
+        const step_args& a = g->step_base;
+        const size_t l = (size_t)g->NL - 1;
+        if (q) HIP_TRY(hipMemcpy(q, a.qkv + l * a.s_qkv, qd * 4, hipMemcpyDeviceToHost), "copying q");
+        if (att) HIP_TRY(hipMemcpy(att, a.att + l * a.s_att, qd * 4, hipMemcpyDeviceToHost), "copying the attention output");
+        return true;
+    }
     if (q) HIP_TRY(hipMemcpy(q, g->q + row * qd, qd * 4, hipMemcpyDeviceToHost), "copying q");
     if (att) HIP_TRY(hipMemcpy(att, g->att + row * qd, qd * 4, hipMemcpyDeviceToHost), "copying the attention output");
     return true;
@@ -1282,16 +1482,28 @@ extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int
                                      char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (steps < 1) return fail(err, err_len, "at least one step");
-    if (!ensure_graph(g, err, err_len)) return false;
+    bool mega;
+    if (!use_step(g, &mega, err, err_len)) return false;
+    if (!mega && !ensure_graph(g, err, err_len)) return false;
     /* every timed step decodes the same row, copied in once */
     if (!set_row(g, seq, token, pos, err, err_len)) return false;
     event_pair ev;
     HIP_TRY(ev.make(), "events");
     HIP_TRY(hipStreamSynchronize(g->stream), "before timing");
     HIP_TRY(hipEventRecord(ev.t0, g->stream), "events");
-    for (int i = 0; i < steps; i++) HIP_TRY(hipGraphLaunch(g->step_graph, g->stream), "launching the step");
+    for (int i = 0; i < steps; i++) {
+        if (mega) {
+            hipError_t e = launch_step_layers(g, 0, g->NL);
+            if (e == hipSuccess) e = enqueue_head(g);
+            if (!check_launch(g, e, "the step", err, err_len)) return false;
+        } else {
+            HIP_TRY(hipGraphLaunch(g->step_graph, g->stream), "launching the step");
+        }
+    }
     HIP_TRY(hipEventRecord(ev.t1, g->stream), "events");
     HIP_TRY(hipEventSynchronize(ev.t1), "timing the steps");
+    if (mega && !step_check(g, err, err_len)) return false;
+    g->last_step_mega = mega;
     float ms = 0;
     HIP_TRY(hipEventElapsedTime(&ms, ev.t0, ev.t1), "events");
     *ms_per_step = (double)ms / steps;
@@ -1301,6 +1513,25 @@ extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int
 extern "C" bool vitna_hip_time_ffn(struct vitna_cuda_model* g, int reps, double* us_per_layer, char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (reps < 1) return fail(err, err_len, "at least one repetition");
+    bool mega = false;
+    if (!g->attention && !use_step(g, &mega, err, err_len)) return false;
+    if (mega) {
+        /* the persistent step over every layer, without attention: one launch a repetition */
+        event_pair ev;
+        HIP_TRY(ev.make(), "events");
+        for (int i = 0; i < 2; i++)
+            if (!check_launch(g, launch_step_layers(g, 0, g->NL), "warming up", err, err_len)) return false;
+        HIP_TRY(hipEventRecord(ev.t0, g->stream), "events");
+        for (int i = 0; i < reps; i++)
+            if (!check_launch(g, launch_step_layers(g, 0, g->NL), "timing the layers", err, err_len)) return false;
+        HIP_TRY(hipEventRecord(ev.t1, g->stream), "events");
+        HIP_TRY(hipEventSynchronize(ev.t1), "timing the layers");
+        float ms = 0;
+        HIP_TRY(hipEventElapsedTime(&ms, ev.t0, ev.t1), "events");
+        if (!step_check(g, err, err_len)) return false;
+        *us_per_layer = 1000.0 * ms / ((double)reps * g->NL);
+        return true;
+    }
     /* every layer's mixture-of-experts half on residual row 0, one after another, captured once */
     HIP_TRY(hipStreamSynchronize(g->stream), "before capturing the layers");
     HIP_TRY(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "capturing the layers");
@@ -1520,6 +1751,7 @@ extern "C" bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitn
     if (!ensure_tiled(g, err, err_len)) return false;
     if (!g->attention) return fail(err, err_len, "this model has no attention");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    g->last_step_mega = false;
     if (layer == 0) {
         if (!set_rows(g, rows, n, err, err_len)) return false;
         if (!check_launch(g, launch_embed_rows(g->embed, g->rows_dev, (int)n, g->x, g->stream), "the embeddings", err, err_len)) return false;
@@ -1619,6 +1851,7 @@ extern "C" bool vitna_hip_moe_rows_step(struct vitna_cuda_model* g, const vitna_
     if (!set_rows(g, rows, n, err, err_len)) return false;
     if (!ensure_rows_graph(g, (int)n, err, err_len)) return false;
     HIP_TRY(hipGraphLaunch(g->rows_graph, g->stream), "launching the rows step");
+    g->last_step_mega = false;
     for (size_t i = 0; i < n; i++)
         if (logits && logits[i])
             HIP_TRY(hipMemcpyAsync(logits[i], g->vocab + i * g->V, (size_t)g->V * 4, hipMemcpyDeviceToHost, g->stream), "copying logits");

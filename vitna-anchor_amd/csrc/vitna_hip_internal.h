@@ -254,25 +254,37 @@ struct qraw {
     uint32_t d;   /* Q6_K: d */
 };
 
+/* A load from device memory through a global-address-space pointer: a global_load, counted by vmcnt alone (a
+   flat load is counted by lgkmcnt too, so an LDS wait would also wait for it). */
+template <typename T>
+__device__ __forceinline__ T gld(const void* p) {
+    typedef uint32_t w2 __attribute__((ext_vector_type(2)));
+    if constexpr (sizeof(T) == 16) return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) u32x4*)p);
+    else if constexpr (sizeof(T) == 8) return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) w2*)p);
+    else if constexpr (sizeof(T) == 4) return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) uint32_t*)p);
+    else if constexpr (sizeof(T) == 2) return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) uint16_t*)p);
+    else return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) uint8_t*)p);
+}
+
 template <int DT>
 __device__ __forceinline__ void slice_load(const qmat& m, int e, int row, int t, qraw& r) {
     const size_t blk = (size_t)row * m.nb + (t >> (DT == VITNA_DTYPE_Q8_0 ? 0 : 3));
     if (DT == VITNA_DTYPE_Q8_0) {
-        const u32x4* q = reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 32);
-        r.a = *q;
-        r.b = *(q + 1);
-        r.c = *reinterpret_cast<const uint16_t*>(m.p[1] + e * m.estride[1] + blk * 2);
+        const uint8_t* q = m.p[0] + e * m.estride[0] + blk * 32;
+        r.a = gld<u32x4>(q);
+        r.b = gld<u32x4>(q + 16);
+        r.c = gld<uint16_t>(m.p[1] + e * m.estride[1] + blk * 2);
     } else if (DT == VITNA_DTYPE_Q4_K) {
-        r.a = *reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 128 + 16 * (t & 7));
-        r.b = *reinterpret_cast<const u32x4*>(m.p[1] + e * m.estride[1] + blk * 16);
+        r.a = gld<u32x4>(m.p[0] + e * m.estride[0] + blk * 128 + 16 * (t & 7));
+        r.b = gld<u32x4>(m.p[1] + e * m.estride[1] + blk * 16);
     } else if (DT == VITNA_DTYPE_Q6_K) {
         const int u = t & 7, h = u >> 2, r0 = (u >> 1) & 1, s = u & 1;
-        r.a = *reinterpret_cast<const u32x4*>(m.p[0] + e * m.estride[0] + blk * 128 + 64 * h + 32 * r0 + 16 * s);
-        r.b = *reinterpret_cast<const u32x4*>(m.p[1] + e * m.estride[1] + blk * 64 + 32 * h + 16 * s);
+        r.a = gld<u32x4>(m.p[0] + e * m.estride[0] + blk * 128 + 64 * h + 32 * r0 + 16 * s);
+        r.b = gld<u32x4>(m.p[1] + e * m.estride[1] + blk * 64 + 32 * h + 16 * s);
         const uint8_t* sc = m.p[2] + e * m.estride[2] + blk * 16;
         /* scale of weights i: i / 16 = 8h + 2r + s, for r = r0 and r0 + 2 */
-        r.c = (uint32_t)sc[8 * h + 2 * r0 + s] | ((uint32_t)sc[8 * h + 2 * r0 + 4 + s] << 8);
-        r.d = *reinterpret_cast<const uint16_t*>(m.p[3] + e * m.estride[3] + blk * 2);
+        r.c = (uint32_t)gld<uint8_t>(sc + 8 * h + 2 * r0 + s) | ((uint32_t)gld<uint8_t>(sc + 8 * h + 2 * r0 + 4 + s) << 8);
+        r.d = gld<uint16_t>(m.p[3] + e * m.estride[3] + blk * 2);
         r.c |= (uint32_t)(2 * r0) << 16; /* the shift of this slice's high bits */
     }
 }

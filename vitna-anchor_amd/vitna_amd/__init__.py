@@ -350,6 +350,9 @@ def _hip():
         "vitna_hip_gguf_llama": (C.c_bool, [P, C.POINTER(Config), C.c_size_t, C.c_size_t, C.POINTER(Llama), *E]),
         "vitna_hip_gguf_llama_free": (None, [C.POINTER(Llama)]),
         "vitna_hip_gguf_close": (None, [P]),
+        "vitna_hip_set_step_kernel": (C.c_bool, [P, C.c_int, C.POINTER(C.c_int), *E]),
+        "vitna_hip_step_trace": (C.c_bool, [P, C.c_size_t, C.c_int32, C.c_size_t, C.c_int, C.POINTER(C.c_uint64),
+                                             C.c_size_t, *E]),
         "vitna_hip_kv": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, _FP, _FP, C.c_bool, *E]),
         "vitna_hip_kv_fill": (C.c_bool, [P, C.c_uint64, C.POINTER(C.c_size_t), *E]),
         "vitna_hip_sync": (C.c_bool, [P, *E]),
@@ -528,6 +531,21 @@ class Device:
         att = np.empty(qd, np.float32)
         self._ok(self.lib.vitna_hip_attention_io(self.g, row, fptr(q), fptr(att), self.err, 512))
         return q, att
+
+    def set_step_kernel(self, on):
+        """Decode steps on the persistent step kernel (on) or the per-layer graph (off, the default); returns
+        whether the model's shape takes the persistent kernel (vitna_hip_set_step_kernel)."""
+        taken = C.c_int(0)
+        self._ok(self.lib.vitna_hip_set_step_kernel(self.g, 1 if on else 0, C.byref(taken), self.err, 512))
+        return bool(taken.value)
+
+    def step_trace(self, seq, token, pos, block=0):
+        """[layers, 6 phases, 3 stamps] s_memrealtime readings (100 MHz) of one traced step (vitna_hip_step_trace)."""
+        L = self.model.cfg.n_layers
+        out = np.zeros(L * 32, np.uint64)
+        self._ok(self.lib.vitna_hip_step_trace(self.g, seq, token, pos, block, out.ctypes.data_as(C.POINTER(C.c_uint64)),
+                                               out.size, self.err, 512))
+        return out.reshape(L, 32)[:, :18].reshape(L, 6, 3)
 
     def kv(self, seq, layer, pos0, n, k=None, v=None):
         cfg = self.model.cfg
