@@ -221,6 +221,20 @@ const float* vitna_hip_logits_device(struct vitna_cuda_model* g);
     prefill grouping: model_cuda.cu:5151-5176, :2288-2343. Q8_0 experts. */
 bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, int32_t* chosen, char* err, size_t err_len);
 
+/** vitna_hip_moe_prefill without allocating: no reference counterpart; for
+    callers that cannot allocate device memory (code under HIP graph capture,
+    tight serving loops, harnesses that forbid hipMalloc). x (n x hidden fp32)
+    and chosen (n x K int32, or NULL) are DEVICE pointers; x is updated in
+    place. The working buffers come from a static 128 MiB device region
+    that each GPU the library runs on holds until the process ends; a call
+    whose rows need more fails with the most rows of this model it holds.
+    Asynchronous on the model's stream (vitna_hip_stream): the caller
+    synchronizes. Calls that overlap on one GPU share the region and race;
+    nothing in it has to start at zero. Same kernels, same results as
+    vitna_hip_moe_prefill. */
+bool vitna_hip_moe_prefill_noalloc(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, int32_t* chosen, char* err,
+                                   size_t err_len);
+
 /** A prefill of n rows drawn N(0,1) on the device (seed), timed with HIP
     events over reps runs after a warm-up: us_total, and us_phase[5] = norm +
     router, routing + grouping, gate/up GEMM, down GEMM, ordered sum. The

@@ -27,6 +27,7 @@
 #include <vector>
 #include <algorithm>
 #include <type_traits>
+#include <mutex>
 
 #define ROWS_MAX 256
 
@@ -35,6 +36,15 @@ struct dlayer {
     float *attn_norm, *mlp_norm, *q_norm, *k_norm;
     float* router;
     qmat gate, up, down;
+};
+
+/* A prefill's working buffers for n rows (everything but the rows themselves), carved from one region by
+   prefill_layout. Nothing in them has to start at zero: every kernel of the prefill writes what it later reads. */
+struct pf_bufs {
+    float *xn, *logits, *ypart;
+    uint16_t *xb, *act;
+    route_out* rt;
+    int *count, *pairs, *off, *tiles, *ntiles;
 };
 
 struct vitna_cuda_model {
@@ -95,10 +105,8 @@ struct vitna_cuda_model {
     /* prefill through one MoE layer: buffers for pf_cap rows, allocated on first use */
     size_t pf_cap;
     std::vector<void*> pf_allocs;
-    float *pf_x, *pf_x0, *pf_xn, *pf_logits, *pf_ypart;
-    uint16_t *pf_xb, *pf_act;
-    route_out* pf_rt;
-    int *pf_count, *pf_pairs, *pf_off, *pf_tiles, *pf_ntiles;
+    float *pf_x, *pf_x0;
+    pf_bufs pf;
 };
 
 static bool fail(char* err, size_t len, const char* fmt, ...) {
@@ -1347,56 +1355,80 @@ static bool sync_stream(vitna_cuda_model* g, const char* what, char* err, size_t
     return true;
 }
 
+/* The bytes a prefill of n rows needs for its working buffers; with base, the buffers' places in that region
+   (each part 256-byte aligned). */
+static size_t prefill_layout(const vitna_cuda_model* g, size_t n, char* base, pf_bufs* b) {
+    const size_t H = g->H, E = g->E, K = g->K, I = g->I;
+    const size_t tiles = (size_t)prefill_max_tiles((int)n, (int)K, (int)E) + 1;
+    size_t at = 0;
+    auto part = [&](auto** ptr, size_t bytes) {
+        if (base) *ptr = reinterpret_cast<std::remove_reference_t<decltype(*ptr)>>(base + at);
+        at += (bytes + 255) & ~(size_t)255;
+    };
+    pf_bufs dummy;
+    pf_bufs& d = b ? *b : dummy;
+    part(&d.xn, n * H * 4);
+    part(&d.xb, n * H * 2);
+    part(&d.logits, n * E * 4);
+    part(&d.rt, n * sizeof(route_out));
+    part(&d.count, E * 4);
+    part(&d.pairs, E * n * 4);
+    part(&d.off, E * 4);
+    part(&d.tiles, tiles * 4);
+    part(&d.ntiles, 4);
+    part(&d.act, n * K * I * 2);
+    part(&d.ypart, n * K * H * 4);
+    return at;
+}
+
 static bool prefill_reserve(vitna_cuda_model* g, size_t n, char* err, size_t err_len) {
     if (n <= g->pf_cap) return true;
     HIP_TRY(hipStreamSynchronize(g->stream), "waiting before the prefill buffers grow");
     for (void* p : g->pf_allocs) (void)hipFree(p);
     g->pf_allocs.clear();
     g->pf_cap = 0;
-    const size_t H = g->H, E = g->E, K = g->K, I = g->I;
-    const size_t tiles = (size_t)prefill_max_tiles((int)n, (int)K, (int)E) + 1;
-    auto get = [&](auto** ptr, size_t bytes) -> bool {
+    auto get = [&](void** ptr, size_t bytes) -> bool {
         void* p = nullptr;
         const hipError_t e = hipMalloc(&p, bytes ? bytes : 256);
         if (e != hipSuccess) return fail(err, err_len, "device memory for a prefill of %zu rows (%zu bytes): %s", n, bytes, hipGetErrorString(e));
         g->pf_allocs.push_back(p);
-        *ptr = static_cast<std::remove_reference_t<decltype(*ptr)>>(p);
+        *ptr = p;
         return true;
     };
-    if (!(get(&g->pf_x, n * H * 4) && get(&g->pf_x0, n * H * 4) && get(&g->pf_xn, n * H * 4) && get(&g->pf_xb, n * H * 2) &&
-          get(&g->pf_logits, n * E * 4) && get(&g->pf_rt, n * sizeof(route_out)) && get(&g->pf_count, E * 4) &&
-          get(&g->pf_pairs, E * n * 4) && get(&g->pf_off, E * 4) && get(&g->pf_tiles, tiles * 4) && get(&g->pf_ntiles, 4) &&
-          get(&g->pf_act, n * K * I * 2) && get(&g->pf_ypart, n * K * H * 4)))
-        return false;
+    void *x = nullptr, *x0 = nullptr, *region = nullptr;
+    if (!(get(&x, n * g->H * 4) && get(&x0, n * g->H * 4) && get(&region, prefill_layout(g, n, nullptr, nullptr)))) return false;
+    g->pf_x = static_cast<float*>(x);
+    g->pf_x0 = static_cast<float*>(x0);
+    prefill_layout(g, n, static_cast<char*>(region), &g->pf);
     g->pf_cap = n;
     return true;
 }
 
-/* The phases of a prefill of n rows held in pf_x, in place; ev (6 events or NULL) marks their boundaries:
-   norm + router | routing + grouping + plan | gate/up GEMM | down GEMM | ordered sum. */
-static hipError_t enqueue_prefill(vitna_cuda_model* g, int layer, int n, hipEvent_t* ev) {
+/* The phases of a prefill of the n rows at x (device), in place, on the working buffers b; ev (6 events or NULL)
+   marks their boundaries: norm + router | routing + grouping + plan | gate/up GEMM | down GEMM | ordered sum. */
+static hipError_t enqueue_prefill(vitna_cuda_model* g, int layer, int n, float* x, const pf_bufs& b, hipEvent_t* ev) {
     const dlayer& d = g->L[layer];
     hipStream_t s = g->stream;
     hipError_t e = hipSuccess;
     auto mark = [&](int i) { if (ev && e == hipSuccess) e = hipEventRecord(ev[i], s); };
     mark(0);
-    if (e == hipSuccess) e = launch_prefill_norm(g->pf_x, d.mlp_norm, g->pf_xn, g->pf_xb, n, g->H, g->eps, s);
-    if (e == hipSuccess) e = launch_prefill_router(g->pf_xn, d.router, g->pf_logits, n, g->E, g->H, s);
+    if (e == hipSuccess) e = launch_prefill_norm(x, d.mlp_norm, b.xn, b.xb, n, g->H, g->eps, s);
+    if (e == hipSuccess) e = launch_prefill_router(b.xn, d.router, b.logits, n, g->E, g->H, s);
     mark(1);
-    if (e == hipSuccess) e = launch_topk(g->pf_logits, n, g->E, g->K, g->renorm, g->pf_rt, s);
-    if (e == hipSuccess) e = launch_group(g->pf_rt, n, g->E, g->K, n, g->pf_count, g->pf_pairs, s);
-    if (e == hipSuccess) e = launch_prefill_plan(g->pf_count, g->E, g->pf_off, g->pf_tiles, g->pf_ntiles, s);
+    if (e == hipSuccess) e = launch_topk(b.logits, n, g->E, g->K, g->renorm, b.rt, s);
+    if (e == hipSuccess) e = launch_group(b.rt, n, g->E, g->K, n, b.count, b.pairs, s);
+    if (e == hipSuccess) e = launch_prefill_plan(b.count, g->E, b.off, b.tiles, b.ntiles, s);
     mark(2);
     prefill_args a;
     a.gate = d.gate; a.up = d.up; a.down = d.down;
-    a.xb = g->pf_xb; a.rt = g->pf_rt; a.count = g->pf_count; a.pairs = g->pf_pairs; a.off = g->pf_off;
-    a.tiles = g->pf_tiles; a.n_tiles = g->pf_ntiles; a.act = g->pf_act; a.ypart = g->pf_ypart;
+    a.xb = b.xb; a.rt = b.rt; a.count = b.count; a.pairs = b.pairs; a.off = b.off;
+    a.tiles = b.tiles; a.n_tiles = b.ntiles; a.act = b.act; a.ypart = b.ypart;
     a.E = g->E; a.K = g->K; a.cap = n; a.n = n;
     if (e == hipSuccess) e = launch_prefill_gemm(a, true, s);
     mark(3);
     if (e == hipSuccess) e = launch_prefill_gemm(a, false, s);
     mark(4);
-    if (e == hipSuccess) e = launch_reduce_rows(g->pf_ypart, g->pf_x, n, g->K, g->H, s);
+    if (e == hipSuccess) e = launch_reduce_rows(b.ypart, x, n, g->K, g->H, s);
     mark(5);
     return e;
 }
@@ -1421,11 +1453,11 @@ extern "C" bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, 
     HIP_TRY(hipSetDevice(g->device), "selecting the model's device");
     if (!prefill_reserve(g, n, err, err_len)) return false;
     HIP_TRY(hipMemcpyAsync(g->pf_x, x, n * g->H * 4, hipMemcpyHostToDevice, g->stream), "copying the rows to the device");
-    if (!check_launch(g, enqueue_prefill(g, (int)layer, (int)n, nullptr), "the prefill", err, err_len)) return false;
+    if (!check_launch(g, enqueue_prefill(g, (int)layer, (int)n, g->pf_x, g->pf, nullptr), "the prefill", err, err_len)) return false;
     HIP_TRY(hipMemcpyAsync(x, g->pf_x, n * g->H * 4, hipMemcpyDeviceToHost, g->stream), "copying the rows back");
     if (chosen) {
         std::vector<route_out> rt(n);
-        HIP_TRY(hipMemcpyAsync(rt.data(), g->pf_rt, n * sizeof(route_out), hipMemcpyDeviceToHost, g->stream), "copying the routing");
+        HIP_TRY(hipMemcpyAsync(rt.data(), g->pf.rt, n * sizeof(route_out), hipMemcpyDeviceToHost, g->stream), "copying the routing");
         if (!sync_stream(g, "the prefill", err, err_len)) return false;
         for (size_t i = 0; i < n; i++)
             for (int k = 0; k < g->K; k++) chosen[i * g->K + k] = rt[i].chosen[k];
@@ -1447,7 +1479,7 @@ extern "C" bool vitna_hip_time_prefill(struct vitna_cuda_model* g, size_t layer,
     bool ok = true;
     for (int r = -1; r < reps && ok; r++) { /* r = -1: warm-up */
         hipError_t e = hipMemcpyAsync(g->pf_x, g->pf_x0, n * g->H * 4, hipMemcpyDeviceToDevice, g->stream);
-        if (e == hipSuccess) e = enqueue_prefill(g, (int)layer, (int)n, ev);
+        if (e == hipSuccess) e = enqueue_prefill(g, (int)layer, (int)n, g->pf_x, g->pf, ev);
         if (e == hipSuccess) e = hipEventSynchronize(ev[5]);
         if (e != hipSuccess) { ok = fail_hip(err, err_len, "the timed prefill", e); break; }
         for (int i = 0; r >= 0 && i < 5; i++) {
@@ -1463,6 +1495,56 @@ extern "C" bool vitna_hip_time_prefill(struct vitna_cuda_model* g, size_t layer,
     return true;
 }
 
+/* ---- the prefill without allocating ----
+   The working buffers live in scratch, a file-scope device array of PREFILL_SCRATCH_BYTES that every GPU the
+   library runs on holds until the process ends. Host code never passes the array's name to a kernel: on the host
+   that name is a stand-in, not a device address. Its address on each device comes from hipGetSymbolAddress, taken
+   once per device with that device current, and that pointer is what the kernels receive. Every call on one GPU
+   shares the region, so calls that overlap on one GPU (two streams, two models on the same device) race. */
+#define PREFILL_SCRATCH_BYTES ((size_t)128 << 20)
+#define SCRATCH_DEVICES 64
+static __device__ __align__(256) unsigned char scratch[PREFILL_SCRATCH_BYTES];
+static std::mutex scratch_mu;
+static char* scratch_at[SCRATCH_DEVICES];
+
+static bool scratch_address(int device, char** out, char* err, size_t err_len) {
+    if (device < 0 || device >= SCRATCH_DEVICES) return fail(err, err_len, "device %d: the static region serves devices 0..%d", device, SCRATCH_DEVICES - 1);
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_at[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return fail(err, err_len, "the static region's address on device %d: %s", device, hipGetErrorString(e));
+        scratch_at[device] = static_cast<char*>(p);
+    }
+    *out = scratch_at[device];
+    return true;
+}
+
+extern "C" bool vitna_hip_moe_prefill_noalloc(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, int32_t* chosen, char* err,
+                                              size_t err_len) {
+    if (!prefill_check(g, layer, n, err, err_len)) return false;
+    if (!x) return fail(err, err_len, "no rows");
+    const size_t need = prefill_layout(g, n, nullptr, nullptr);
+    if (need > PREFILL_SCRATCH_BYTES) {
+        size_t lo = 0, hi = n; /* the most rows of this model the region holds */
+        while (lo + 1 < hi) {
+            const size_t mid = (lo + hi) / 2;
+            (prefill_layout(g, mid, nullptr, nullptr) <= PREFILL_SCRATCH_BYTES ? lo : hi) = mid;
+        }
+        return fail(err, err_len, "%zu rows need %zu bytes of working memory; the static region holds %zu (%zu rows of this model)", n, need,
+                    PREFILL_SCRATCH_BYTES, lo);
+    }
+    HIP_TRY(hipSetDevice(g->device), "selecting the model's device");
+    char* base = nullptr;
+    if (!scratch_address(g->device, &base, err, err_len)) return false;
+    pf_bufs b;
+    prefill_layout(g, n, base, &b);
+    hipError_t e = enqueue_prefill(g, (int)layer, (int)n, x, b, nullptr);
+    if (e == hipSuccess && chosen) e = launch_prefill_chosen(b.rt, (int)n, g->K, chosen, g->stream);
+    g->last_step_mega = false;
+    return check_launch(g, e, "the prefill", err, err_len);
+}
+
 /* The prefill's routing and output rows of the last timed or served prefill, to the host. */
 extern "C" bool vitna_hip_prefill_rows(struct vitna_cuda_model* g, size_t n, float* x_in, float* x_out, int32_t* chosen, char* err,
                                        size_t err_len) {
@@ -1471,7 +1553,7 @@ extern "C" bool vitna_hip_prefill_rows(struct vitna_cuda_model* g, size_t n, flo
     if (x_in) HIP_TRY(hipMemcpyAsync(x_in, g->pf_x0, n * g->H * 4, hipMemcpyDeviceToHost, g->stream), "copying the input rows");
     if (x_out) HIP_TRY(hipMemcpyAsync(x_out, g->pf_x, n * g->H * 4, hipMemcpyDeviceToHost, g->stream), "copying the output rows");
     std::vector<route_out> rt(chosen ? n : 0);
-    if (chosen) HIP_TRY(hipMemcpyAsync(rt.data(), g->pf_rt, n * sizeof(route_out), hipMemcpyDeviceToHost, g->stream), "copying the routing");
+    if (chosen) HIP_TRY(hipMemcpyAsync(rt.data(), g->pf.rt, n * sizeof(route_out), hipMemcpyDeviceToHost, g->stream), "copying the routing");
     if (!sync_stream(g, "copying the prefill", err, err_len)) return false;
     for (size_t i = 0; chosen && i < n; i++)
         for (int k = 0; k < g->K; k++) chosen[i * g->K + k] = rt[i].chosen[k];

@@ -382,6 +382,17 @@ hipError_t launch_prefill_plan(const int* count, int E, int* off, int* tiles, in
     return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void prefill_chosen_kernel(const route_out* __restrict__ rt, int n, int K, int32_t* __restrict__ chosen) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n * K) chosen[i] = rt[i / K].chosen[i % K];
+}
+
+hipError_t launch_prefill_chosen(const route_out* rt, int n, int K, int32_t* chosen, hipStream_t s) {
+    if (n < 1 || K < 1 || K > ROUTE_K_MAX) return hipErrorInvalidValue;
+    prefill_chosen_kernel<<<(n * K + 255) / 256, 256, 0, s>>>(rt, n, K, chosen);
+    return hipGetLastError();
+}
+
 int prefill_max_tiles(int n, int K, int E) { return (n * K + PF_BM - 1) / PF_BM + E; }
 
 hipError_t launch_prefill_gemm(const prefill_args& a, bool gate_up, hipStream_t s) {

@@ -281,6 +281,8 @@ hipError_t launch_prefill_norm(const float* x, const float* w, float* xn, uint16
 hipError_t launch_prefill_router(const float* xn, const float* R, float* logits, int n, int E, int H, hipStream_t s);
 hipError_t launch_prefill_plan(const int* count, int E, int* off, int* tiles, int* n_tiles, hipStream_t s);
 int prefill_max_tiles(int n, int K, int E);
+/* chosen[i * K + k] = rt[i].chosen[k]: each row's experts, largest logit first, as the caller's int32 array. */
+hipError_t launch_prefill_chosen(const route_out* rt, int n, int K, int32_t* chosen, hipStream_t s);
 hipError_t launch_prefill_gemm(const prefill_args& a, bool gate_up, hipStream_t s);
 
 #endif

@@ -358,6 +358,7 @@ def _hip():
         "vitna_hip_sync": (C.c_bool, [P, *E]),
         "vitna_hip_stream": (P, [P]),
         "vitna_hip_moe_prefill": (C.c_bool, [P, C.c_size_t, _FP, C.c_size_t, C.POINTER(C.c_int32), *E]),
+        "vitna_hip_moe_prefill_noalloc": (C.c_bool, [P, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p, *E]),
         "vitna_hip_time_prefill": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.c_uint64, C.c_int, C.POINTER(C.c_double),
                                               C.POINTER(C.c_double), *E]),
         "vitna_hip_time_rows": (C.c_bool, [P, C.POINTER(RowT), C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
@@ -572,6 +573,11 @@ class Device:
         ch = np.empty((x.shape[0], self.model.cfg.n_experts_used), np.int32)
         self._ok(self.lib.vitna_hip_moe_prefill(self.g, layer, fptr(x), x.shape[0], _i32(ch), self.err, 512))
         return x, ch
+
+    def prefill_noalloc(self, layer, x_dev, n, chosen_dev=None):
+        """vitna_hip_moe_prefill_noalloc on device addresses (x_dev: n x hidden fp32, in place; chosen_dev: n x K
+        int32 or None); asynchronous on the model's stream."""
+        self._ok(self.lib.vitna_hip_moe_prefill_noalloc(self.g, layer, x_dev, n, chosen_dev, self.err, 512))
 
     def time_prefill(self, layer, n, seed=1, reps=10):
         """(total us, [norm + router, routing + grouping, gate/up, down, ordered sum] us) of a prefill of n rows."""
