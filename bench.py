@@ -153,20 +153,15 @@ def main():
             oracle.step(model, 0, token, pos, threads=1, trace=False)
             t_cpu += time.perf_counter() - t1
             n += 1
-        cpu_model = "unknown"
-        try:
-            with open("/proc/cpuinfo") as f:
-                cpu_model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "unknown")
-        except OSError:
-            pass
+        host = host_info()
         cpu = {"value": round(n / t_cpu, 4), "unit": "tok/s", "cores": 1, "kind": "port",
                "sample": "%d whole decode steps of the same model and position (48 layers + head), single thread, "
                          "the reference's CPU arithmetic (AVX2 order) restated in oracle/vitna_oracle.c" % n,
-               "cpu": cpu_model}
+               "host": host}
         log("cpu baseline: %d steps in %.1f s -> %.3f tok/s" % (n, t_cpu, n / t_cpu))
-        # the same arithmetic with each matrix's rows split over the host cores (the reference's pool pattern);
-        # 16 threads: this box's CPU share for one GPU
-        threads = max(1, min(16, os.cpu_count() or 1))
+        # the same arithmetic with each matrix's rows split over the host's cores (the reference's pool pattern),
+        # as many as this process may use up to 16, the CPU share a GPU box grants one GPU
+        threads = max(1, min(16, host["cores_usable"]))
         n2, t2 = 0, 0.0
         while t2 < args.cpu_seconds / 2 and n2 < 40:
             t1 = time.perf_counter()
@@ -175,7 +170,8 @@ def main():
             n2 += 1
         cpu_mt = {"value": round(n2 / t2, 4), "unit": "tok/s", "cores": threads, "kind": "port",
                   "sample": "%d whole decode steps, rows of each matrix split over %d threads (same sums in the same "
-                            "order per row)" % (n2, threads), "cpu": cpu_model}
+                            "order per row); threads = the cores this process may use, capped at 16, the host share of one GPU"
+                            % (n2, threads), "host": host}
         log("cpu baseline, %d threads: %d steps in %.1f s -> %.3f tok/s" % (threads, n2, t2, n2 / t2))
 
     dev.close()
@@ -212,6 +208,28 @@ def main():
     model.free()
 
 
+def host_info():
+    """The host the CPU baseline ran on: CPU model, cores, compiler and C library."""
+    import platform
+    import subprocess
+    info = {"cpu_model": "unknown", "cores_online": os.cpu_count(), "cores_usable": len(os.sched_getaffinity(0)),
+            "gcc": "unknown", "glibc": "-".join(platform.libc_ver()), "oracle_flags": "-O3 -mavx2 -mfma -ffp-contract=off"}
+    try:
+        with open("/proc/cpuinfo") as f:
+            lines = f.read().splitlines()
+        pick = lambda key: next((l.split(":", 1)[1].strip() for l in lines if l.split(":")[0].strip() == key), None)
+        info["cpu_model"] = pick("model name") or "unknown"
+        info["cpu_family_model_stepping"] = "%s/%s/%s" % (pick("cpu family"), pick("model"), pick("stepping"))
+        info["cpu_mhz"] = pick("cpu MHz")
+    except OSError:
+        pass
+    try:
+        info["gcc"] = subprocess.run(["gcc", "--version"], capture_output=True, text=True, timeout=10).stdout.splitlines()[0]
+    except (OSError, IndexError, subprocess.SubprocessError):
+        pass
+    return info
+
+
 def bench_ragged(va, model, dev, steps, reps=None):
     """32 sequences, one new token each, key-value lengths U{128..8192} (seeded), values N(0,1).
     Times max(steps / 5, 5) rows steps, or reps of them."""
@@ -224,17 +242,29 @@ def bench_ragged(va, model, dev, steps, reps=None):
     ms = dev.time_rows(rows, reps if reps else max(steps // 5, 5))
     L, kd = cfg.n_layers, cfg.n_kv_heads * cfg.head_dim
     kv_bytes = float(np.sum(lengths + 1)) * kd * 4 * 2 * L
-    # expected distinct experts a layer when 32 tokens each choose 8 of 128 (uniform routing)
+    # the distinct experts each layer reads: the same rows walked layer by layer through the reference's ABI
+    # (vitna_cuda_moe_rows_route / _rows_experts), each row routed by the device's rule (vitna_hip_route_check)
     E, K = cfg.n_experts, cfg.n_experts_used
-    uniq = E * (1.0 - (1.0 - K / E) ** 32)
-    expert_bytes = L * uniq * (2 * 884736 + 1290240)
+    distinct = []
+    for l in range(L):
+        lg = dev.rows_route(rows, l)
+        ids = np.empty((len(rows), K), np.int32)
+        wts = np.empty((len(rows), K), np.float32)
+        for i in range(len(rows)):
+            _, ids[i], wts[i] = va.route_check(lg[i], K, bool(cfg.renormalize))
+        dev.rows_experts(l, ids, wts)
+        distinct.append(len(np.unique(ids)))
+    uniq = float(np.mean(distinct))
+    expert_bytes = float(np.sum(distinct)) * (2 * 884736 + 1290240)
     log("configs[3]: %d rows, %.3f ms a step, %.1f tok/s (cache filled in %.1f s)" % (len(rows), ms, 32e3 / ms, time.time() - t0))
     return {"workload": "BASELINE configs[3]: 32 sequences, one new token each, key-value lengths U{128..8192}, "
                         "Qwen3-30B-A3B-shaped Q4_K_M, 48 layers",
             "value": round(32e3 / ms, 1), "unit": "tok/s", "ms_per_step": round(ms, 4),
             "kv_positions": int(np.sum(lengths)),
             "est_GBps": round((kv_bytes + expert_bytes + 5.2258e8 + 5.0332e7 + 2.5525e8) / ms / 1e6, 1),
-            "est_note": "key-value bytes exact; expert bytes for the expected %.1f distinct experts a layer" % uniq}
+            "distinct_experts": {"mean": round(uniq, 2), "min": int(min(distinct)), "max": int(max(distinct))},
+            "est_note": "key-value bytes exact; expert bytes for the distinct experts each layer reads, counted "
+                        "(%.1f a layer on average)" % uniq}
 
 
 def bench_layer(va, c, reps=20):

@@ -662,17 +662,17 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     /* several splits: this block's sum of the tile into part[], then the last block of the tile adds them */
     const size_t slot = (size_t)blockIdx.y * a.tiles + tile0 + tile; /* the tile's counter */
     float* part = a.part + slot * a.split_max * 1024;
-    /* The sums are stored as agent-scope atomics, which write through this XCD's L2; every thread waits for
-       their completion before the barrier and the counter moves; the last block reads them back the same way.
-       A device-wide fence would instead write back the whole L2. */
+    /* The sums are stored as agent-scope atomics (written through this XCD's L2 to where every XCD reads);
+       the counter's increment releases them and the last block's acquires them, at agent scope, so the last
+       block reads every split's sums (the workgroup barrier carries thread 0's acquire to the others). */
     for (int r = wv; r < 16; r += KS) {
         float v = 0.0f;
         for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
         __hip_atomic_store(part + (size_t)sp * 1024 + r * 64 + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* every wave's stores complete before the barrier */
     __syncthreads();
-    if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+    if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + slot, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
     __syncthreads();
     if (!last) return;
     for (int r = wv; r < 16; r += KS) {
