@@ -10,8 +10,9 @@ The bar, per row:
     GEMM: for element r, 2^-8 * sum_e |w_e| sum_j |a_ej D_e[r, j]| + 1e-6, with
     the checker's SwiGLU outputs a_e and its own widened down weights D_e
     (oracle.widen). The bound takes a bf16 rounding of each factor of each
-    product (2^-9 each); the error the gate/up GEMM leaves in a_e is of the
-    same kind and size, and a bf16 emulation of the device's arithmetic stays
+    product (2^-9 each); the error the gate/up GEMM leaves in a_e and the bf16
+    rounding of each pair's part are of the same kind and size, and a bf16
+    emulation of the device's arithmetic stays
     under a fifth of the bound at config 4's shape and under a third at the
     small one (tests/test_prefill_bound.py). The bound is 6-14% of the mean
     |sum|, so a wrong scale, a dropped block, a transposed tile or a row given

@@ -28,7 +28,7 @@ def test_bound_holds_for_bf16_and_catches_one_element():
             x = va.normal(7, seed, H)
             ch, proj, bound = moe_bound(model, 0, x)
             assert np.all(bound > 0)
-            # the device's arithmetic: bf16 inputs to each GEMM, fp32 sums, bf16 SwiGLU output
+            # the device's arithmetic: bf16 inputs to each GEMM, fp32 sums, bf16 SwiGLU output, bf16 parts
             xn = oracle.rmsnorm(x, norm, cfg.rms_eps)
             _, _, order, wts, _ = oracle.moe(model, 0, xn)
             y = np.zeros(H, np.float64)
@@ -38,7 +38,7 @@ def test_bound_holds_for_bf16_and_catches_one_element():
                 g = G.astype(np.float32) @ bf16(xn)
                 u = U.astype(np.float32) @ bf16(xn)
                 act = bf16(g / (1.0 + np.exp(-g)) * u)
-                y += float(w) * (D.astype(np.float32) @ act)
+                y += bf16(np.float32(w) * (D.astype(np.float32) @ act))  # each pair's part is kept in bf16
             ratio = np.abs(y - proj) / bound
             worst = max(worst, float(ratio.max()))
             assert ratio.max() <= 1.0

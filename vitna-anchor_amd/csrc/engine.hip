@@ -41,8 +41,8 @@ struct dlayer {
 /* A prefill's working buffers for n rows (everything but the rows themselves), carved from one region by
    prefill_layout. Nothing in them has to start at zero: every kernel of the prefill writes what it later reads. */
 struct pf_bufs {
-    float *xn, *logits, *ypart;
-    uint16_t *xb, *act;
+    float *xn, *logits;
+    uint16_t *xb, *act, *ypart;
     route_out* rt;
     int *count, *pairs, *off, *tiles, *ntiles;
 };
@@ -1377,7 +1377,7 @@ static size_t prefill_layout(const vitna_cuda_model* g, size_t n, char* base, pf
     part(&d.tiles, tiles * 4);
     part(&d.ntiles, 4);
     part(&d.act, n * K * I * 2);
-    part(&d.ypart, n * K * H * 4);
+    part(&d.ypart, n * K * H * 2);
     return at;
 }
 
@@ -1428,7 +1428,7 @@ static hipError_t enqueue_prefill(vitna_cuda_model* g, int layer, int n, float* 
     mark(3);
     if (e == hipSuccess) e = launch_prefill_gemm(a, false, s);
     mark(4);
-    if (e == hipSuccess) e = launch_reduce_rows(b.ypart, x, n, g->K, g->H, s);
+    if (e == hipSuccess) e = launch_prefill_sum(b.ypart, x, n, g->K, g->H, s);
     mark(5);
     return e;
 }

@@ -354,9 +354,9 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
             } else {
                 const int pr = a.pairs[(size_t)e * a.cap + p], row = pr / ROUTE_K_MAX, sl = pr % ROUTE_K_MAX;
                 const float wt = a.rt[row].weights[sl];
-                float* y = a.ypart + ((size_t)row * a.K + sl) * H + nt * PF_BN + wni * 128 + l32;
+                uint16_t* y = a.ypart + ((size_t)row * a.K + sl) * H + nt * PF_BN + wni * 128 + l32;
 #pragma unroll
-                for (int k = 0; k < 4; k++) y[32 * k] = acc[i][k][r] * wt;
+                for (int k = 0; k < 4; k++) y[32 * k] = (uint16_t)bf16_rne(acc[i][k][r] * wt);
             }
         }
 }
@@ -390,6 +390,41 @@ __global__ __launch_bounds__(256) void prefill_chosen_kernel(const route_out* __
 hipError_t launch_prefill_chosen(const route_out* rt, int n, int K, int32_t* chosen, hipStream_t s) {
     if (n < 1 || K < 1 || K > ROUTE_K_MAX) return hipErrorInvalidValue;
     prefill_chosen_kernel<<<(n * K + 255) / 256, 256, 0, s>>>(rt, n, K, chosen);
+    return hipGetLastError();
+}
+
+/* x[row][c] += sum over slots k, in order, of the bf16 parts: eight columns a thread, the K parts all requested
+   before the first add */
+__global__ __launch_bounds__(256) void prefill_sum_kernel(const uint16_t* __restrict__ ypart, float* __restrict__ x, int K, int H) {
+    const int row = blockIdx.y, c8 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c8 >= H / 8) return;
+    const uint4* yp = reinterpret_cast<const uint4*>(ypart + (size_t)row * K * H) + c8;
+    uint4 p[ROUTE_K_MAX];
+#pragma unroll
+    for (int k = 0; k < ROUTE_K_MAX; k++)
+        if (k < K) p[k] = yp[(size_t)k * (H / 8)];
+    float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < ROUTE_K_MAX; k++)
+        if (k < K) {
+            const uint32_t w[4] = {p[k].x, p[k].y, p[k].z, p[k].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                sum[2 * i] = sum[2 * i] + __uint_as_float(w[i] << 16);
+                sum[2 * i + 1] = sum[2 * i + 1] + __uint_as_float(w[i] & 0xffff0000u);
+            }
+        }
+    float4* xp = reinterpret_cast<float4*>(x + (size_t)row * H) + 2 * c8;
+    float4 v0 = xp[0], v1 = xp[1];
+    v0.x = v0.x + sum[0]; v0.y = v0.y + sum[1]; v0.z = v0.z + sum[2]; v0.w = v0.w + sum[3];
+    v1.x = v1.x + sum[4]; v1.y = v1.y + sum[5]; v1.z = v1.z + sum[6]; v1.w = v1.w + sum[7];
+    xp[0] = v0;
+    xp[1] = v1;
+}
+
+hipError_t launch_prefill_sum(const uint16_t* ypart, float* x, int n, int K, int H, hipStream_t s) {
+    if (n < 1 || K < 1 || K > ROUTE_K_MAX || H % 8) return hipErrorInvalidValue;
+    prefill_sum_kernel<<<dim3((H / 8 + 255) / 256, n), 256, 0, s>>>(ypart, x, K, H);
     return hipGetLastError();
 }
 

@@ -274,13 +274,15 @@ struct prefill_args {
     const int* tiles;       /* (expert << 16) | tile of 256 pairs */
     const int* n_tiles;
     uint16_t* act;          /* bf16 [n * K][I], pairs in expert order */
-    float* ypart;           /* [n * K][H], row * K + slot */
+    uint16_t* ypart;        /* bf16 [n * K][H], row * K + slot: each pair's weighted expert output */
     int E, K, cap, n;
 };
 hipError_t launch_prefill_norm(const float* x, const float* w, float* xn, uint16_t* xb, int n, int H, float eps, hipStream_t s);
 hipError_t launch_prefill_router(const float* xn, const float* R, float* logits, int n, int E, int H, hipStream_t s);
 hipError_t launch_prefill_plan(const int* count, int E, int* off, int* tiles, int* n_tiles, hipStream_t s);
 int prefill_max_tiles(int n, int K, int E);
+/* x[row] += the sum over slots k (in order) of the bf16 parts ypart[row * K + k]. */
+hipError_t launch_prefill_sum(const uint16_t* ypart, float* x, int n, int K, int H, hipStream_t s);
 /* chosen[i * K + k] = rt[i].chosen[k]: each row's experts, largest logit first, as the caller's int32 array. */
 hipError_t launch_prefill_chosen(const route_out* rt, int n, int K, int32_t* chosen, hipStream_t s);
 hipError_t launch_prefill_gemm(const prefill_args& a, bool gate_up, hipStream_t s);
