@@ -287,6 +287,16 @@ bool vitna_hip_route_check(const float* logits, int n_experts, int k, bool renor
     bytes fetched and written are the yardstick for the other kernels'. */
 bool vitna_hip_copy_probe(size_t bytes, int reps, double* avg_us, char* err, size_t err_len);
 
+/** For checking the expert cache (vitna_cuda_create with an expert_cache_bytes
+    that holds fewer slots than the model has experts; the reference's
+    expert_cache_t, engine/src/model_cuda.cu:249-290): where[layer * E + e]
+    is the slot holding that expert or -1 (n_places entries, when where is not
+    NULL), and counters[0..9] = slots, slot bytes, acquired, hits, still being
+    copied, misses, copied for a guess, guesses used, copies, bytes copied.
+    False (with a reason) for a model whose experts are all resident. */
+bool vitna_hip_expert_cache_state(const struct vitna_cuda_model* g, int32_t* where, size_t n_places, uint64_t* counters, char* err,
+                                  size_t err_len);
+
 #ifdef __cplusplus
 }
 #endif

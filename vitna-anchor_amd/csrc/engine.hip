@@ -18,6 +18,7 @@
 
 #include "vitna_kernels.h"
 #include "step_kernel.h"
+#include "expert_cache.h"
 #include "../../include/vitna_hip.h"
 
 #include <stdarg.h>
@@ -107,6 +108,8 @@ struct vitna_cuda_model {
     std::vector<void*> pf_allocs;
     float *pf_x, *pf_x0;
     pf_bufs pf;
+    /* the experts through a cache of slots, when expert_cache_bytes leaves fewer slots than experts */
+    expert_cache ec;
 };
 
 static bool fail(char* err, size_t len, const char* fmt, ...) {
@@ -393,13 +396,13 @@ extern "C" void vitna_cuda_free(struct vitna_cuda_model* g) {
     if (g->rows_host) (void)hipHostFree(g->rows_host);
     if (g->h_logits) (void)hipHostFree(g->h_logits);
     if (g->rows_copied) (void)hipEventDestroy(g->rows_copied);
+    ec_destroy(g->ec);
     if (g->stream) (void)hipStreamDestroy(g->stream);
     delete g;
 }
 
 extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, const float* cos_tab, const float* sin_tab,
                                                       size_t expert_cache_bytes, char* err, size_t err_len) {
-    (void)expert_cache_bytes;
     if (!m) { fail(err, err_len, "no model"); return nullptr; }
     if (!check_shapes(m, err, err_len)) return nullptr;
     const vitna_llama_config_t* c = &m->cfg;
@@ -442,7 +445,9 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
     (void)L0;
     uint8_t* staging = nullptr;
     if (hipMalloc(&staging, staging_bytes) != hipSuccess) { fail(err, err_len, "device memory for staging (%zu bytes)", staging_bytes); return bail(); }
-    bool ok = true;
+    /* experts through a cache of slots when expert_cache_bytes holds fewer than all of them (expert_cache.h) */
+    bool ok = ec_create(g->ec, m, expert_cache_bytes, err, err_len);
+    if (!ok) { (void)hipFree(staging); return bail(); }
     g->L.resize(c->n_layers);
     std::vector<const vitna_matrix_t*> mats(c->n_experts);
     for (size_t l = 0; ok && l < c->n_layers; l++) {
@@ -453,20 +458,26 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
              upload_f32(g, &d.router, (const float*)L->router.data, c->n_experts * c->hidden, "the router", err, err_len);
         const vitna_expert_t* x0 = &L->experts[0];
         const size_t E = c->n_experts;
-        const size_t gbytes = set_bytes(x0->gate.dtype, x0->gate.rows, x0->gate.cols, E);
-        const size_t dbytes = set_bytes(x0->down.dtype, x0->down.rows, x0->down.cols, E);
-        uint8_t* mem = nullptr;
-        ok = ok && dalloc(g, &mem, 2 * gbytes + dbytes, "a layer's experts", err, err_len);
-        if (!ok) break;
-        d.gate = place(mem, x0->gate.dtype, x0->gate.rows, x0->gate.cols, E);
-        d.up = place(mem + gbytes, x0->up.dtype, x0->up.rows, x0->up.cols, E);
-        d.down = place(mem + 2 * gbytes, x0->down.dtype, x0->down.rows, x0->down.cols, E);
-        for (size_t e = 0; e < E; e++) mats[e] = &L->experts[e].gate;
-        ok = upload_set(g, mats.data(), E, d.gate, staging, staging_bytes, err, err_len);
-        for (size_t e = 0; ok && e < E; e++) mats[e] = &L->experts[e].up;
-        ok = ok && upload_set(g, mats.data(), E, d.up, staging, staging_bytes, err, err_len);
-        for (size_t e = 0; ok && e < E; e++) mats[e] = &L->experts[e].down;
-        ok = ok && upload_set(g, mats.data(), E, d.down, staging, staging_bytes, err, err_len);
+        if (g->ec.on) {
+            d.gate = ec_view(g->ec, (int)l, 0);
+            d.up = ec_view(g->ec, (int)l, 1);
+            d.down = ec_view(g->ec, (int)l, 2);
+        } else {
+            const size_t gbytes = set_bytes(x0->gate.dtype, x0->gate.rows, x0->gate.cols, E);
+            const size_t dbytes = set_bytes(x0->down.dtype, x0->down.rows, x0->down.cols, E);
+            uint8_t* mem = nullptr;
+            ok = ok && dalloc(g, &mem, 2 * gbytes + dbytes, "a layer's experts", err, err_len);
+            if (!ok) break;
+            d.gate = place(mem, x0->gate.dtype, x0->gate.rows, x0->gate.cols, E);
+            d.up = place(mem + gbytes, x0->up.dtype, x0->up.rows, x0->up.cols, E);
+            d.down = place(mem + 2 * gbytes, x0->down.dtype, x0->down.rows, x0->down.cols, E);
+            for (size_t e = 0; e < E; e++) mats[e] = &L->experts[e].gate;
+            ok = upload_set(g, mats.data(), E, d.gate, staging, staging_bytes, err, err_len);
+            for (size_t e = 0; ok && e < E; e++) mats[e] = &L->experts[e].up;
+            ok = ok && upload_set(g, mats.data(), E, d.up, staging, staging_bytes, err, err_len);
+            for (size_t e = 0; ok && e < E; e++) mats[e] = &L->experts[e].down;
+            ok = ok && upload_set(g, mats.data(), E, d.down, staging, staging_bytes, err, err_len);
+        }
         if (ok && g->attention) {
             ok = upload_matrix(g, &d.q, &L->q, staging, staging_bytes, "q", err, err_len) &&
                  upload_matrix(g, &d.k, &L->k, staging, staging_bytes, "k", err, err_len) &&
@@ -688,7 +699,9 @@ extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int
     return true;
 }
 
-static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const float* weights, size_t k, char* err, size_t err_len) {
+/* slots: where the experts are in the expert cache (the kernels' expert index), or null for resident experts */
+static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const float* weights, size_t k, char* err, size_t err_len,
+                        const int32_t* slots = nullptr) {
     if (k != (size_t)g->K) return fail(err, err_len, "%zu experts given; the model routes to %d", k, g->K);
     std::vector<route_out> ro(n);
     for (size_t t = 0; t < n; t++) {
@@ -700,7 +713,7 @@ static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const
                 if (ids[t * k + j] == e) return fail(err, err_len, "expert %d is named twice", e);
             ro[t].ids[i] = e;
             ro[t].weights[i] = weights[t * k + i];
-            ro[t].chosen[i] = e;
+            ro[t].chosen[i] = slots ? slots[t * k + i] : e;
             ro[t].cw[i] = weights[t * k + i];
         }
     }
@@ -712,11 +725,53 @@ static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const
 
 extern "C" bool vitna_cuda_moe_experts(struct vitna_cuda_model* g, size_t layer, const int32_t* ids, const float* weights, size_t k,
                                        const int32_t* guess, char* err, size_t err_len) {
-    (void)guess;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
-    if (!put_routing(g, 1, ids, weights, k, err, err_len)) return false;
-    return check_launch(g, enqueue_experts(g, (int)layer, nullptr, g->x, 1), "the experts", err, err_len);
+    if (!g->ec.on) {
+        if (!put_routing(g, 1, ids, weights, k, err, err_len)) return false;
+        return check_launch(g, enqueue_experts(g, (int)layer, nullptr, g->x, 1), "the experts", err, err_len);
+    }
+    /* through the expert cache (model_cuda.cu:4757-4913): the slots of this layer's experts, the routing naming the
+       slots, the kernels after the copies into them, then the guess's copies behind the kernels */
+    if (k != (size_t)g->K) return fail(err, err_len, "%zu experts given; the model routes to %d", k, g->K);
+    for (size_t i = 0; i < k; i++) {
+        if (ids[i] < 0 || ids[i] >= g->E) return fail(err, err_len, "expert %d is outside the layer's %d", ids[i], g->E);
+        if (guess && (guess[i] < 0 || guess[i] >= g->E)) return fail(err, err_len, "guessed expert %d is outside the layer's %d", guess[i], g->E);
+    }
+    int32_t slot_of[ROUTE_K_MAX];
+    bool ok = ec_acquire(g->ec, (int)layer, ids, (int)k, g->stream, slot_of, err, err_len) &&
+              put_routing(g, 1, ids, weights, k, err, err_len, slot_of) && ec_wait(g->ec, slot_of, (int)k, g->stream, err, err_len) &&
+              check_launch(g, enqueue_experts(g, (int)layer, nullptr, g->x, 1), "the experts", err, err_len);
+    /* the holds are released whatever happened; the guess only after the kernels */
+    const bool fin = ec_finish(g->ec, (int)layer, ok ? guess : nullptr, (int)k, err, err_len);
+    return ok && fin;
+}
+
+extern "C" bool vitna_hip_expert_cache_state(const struct vitna_cuda_model* g, int32_t* where, size_t n_places, uint64_t* counters,
+                                             char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no model");
+    const expert_cache& c = g->ec;
+    if (!c.on) return fail(err, err_len, "every expert of this model is resident on the device");
+    if (where) {
+        if (n_places != c.n_places) return fail(err, err_len, "%zu places given; the model has %zu", n_places, c.n_places);
+        memcpy(where, c.where.data(), c.n_places * sizeof(int32_t));
+    }
+    if (counters) {
+        const uint64_t v[10] = {(uint64_t)c.n_slots, c.slot_bytes, c.acquired, c.hits, c.in_flight, c.misses, c.prefetched,
+                                c.prefetch_used, c.copies, c.bytes_copied};
+        memcpy(counters, v, sizeof(v));
+    }
+    return true;
+}
+
+/* Paths that read every expert from where it rests on the device refuse a model whose experts pass through the
+   cache. */
+static bool experts_resident(const vitna_cuda_model* g, char* err, size_t err_len) {
+    if (!g->ec.on) return true;
+    return fail(err, err_len,
+                "the experts pass through a cache of %d slots on the device; this path needs every expert resident "
+                "(vitna_cuda_moe_route and vitna_cuda_moe_experts take the cache)",
+                g->ec.n_slots);
 }
 
 extern "C" bool vitna_cuda_moe_head(struct vitna_cuda_model* g, float* logits, char* err, size_t err_len) {
@@ -731,6 +786,10 @@ extern "C" bool vitna_cuda_moe_head(struct vitna_cuda_model* g, float* logits, c
 extern "C" const char* vitna_cuda_moe_report(const struct vitna_cuda_model* g, char* buf, size_t len) {
     if (len == 0) return buf;
     if (!g) { buf[0] = 0; return buf; }
+    if (g->ec.on) {
+        ec_report(g->ec, buf, len);
+        return buf;
+    }
     snprintf(buf, len, "experts: all %d of each of %d layers resident on the device; nothing copied per token", g->E, g->NL);
     return buf;
 }
@@ -1053,6 +1112,7 @@ static bool ensure_graph(vitna_cuda_model* g, char* err, size_t err_len) {
 }
 
 extern "C" bool vitna_hip_moe_step_async(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, char* err, size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (!g->attention) return fail(err, err_len, "this model has no attention; use vitna_hip_moe_ffn");
     bool mega;
@@ -1073,6 +1133,7 @@ extern "C" bool vitna_hip_moe_step_async(struct vitna_cuda_model* g, size_t seq,
 
 extern "C" bool vitna_hip_moe_step(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, float* logits, char* err,
                                    size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!vitna_hip_moe_step_async(g, seq, token, pos, err, err_len)) return false;
     if (logits) HIP_TRY(hipMemcpyAsync(logits, g->vocab, (size_t)g->V * 4, hipMemcpyDeviceToHost, g->stream), "copying the logits");
     HIP_TRY(hipStreamSynchronize(g->stream), "running the step");
@@ -1080,6 +1141,7 @@ extern "C" bool vitna_hip_moe_step(struct vitna_cuda_model* g, size_t seq, int32
 }
 
 extern "C" bool vitna_hip_set_step_kernel(struct vitna_cuda_model* g, int on, int* taken, char* err, size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
     g->step_want = on != 0;
@@ -1091,6 +1153,7 @@ extern "C" bool vitna_hip_set_step_kernel(struct vitna_cuda_model* g, int on, in
 
 extern "C" bool vitna_hip_step_trace(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, int block, uint64_t* out, size_t n,
                                      char* err, size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (!ensure_step(g, err, err_len)) return false;
     if (g->step_state < 1) return fail(err, err_len, "this model runs the per-layer kernels (%s)", g->step_reason);
@@ -1108,6 +1171,7 @@ extern "C" bool vitna_hip_step_trace(struct vitna_cuda_model* g, size_t seq, int
 }
 
 extern "C" bool vitna_hip_moe_ffn(struct vitna_cuda_model* g, size_t layer, char* err, size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     bool mega = false;
@@ -1258,6 +1322,7 @@ static double qmat_bytes(const qmat& q) {
 
 extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int reps, int warmup, double* avg_us, double* bytes, char* err,
                                       size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if ((which >= 3 && which <= 6 && !g->attention) || which < 0 || which > 9)
         return fail(err, err_len, "no such kernel (%d) in this model", which);
@@ -1448,6 +1513,7 @@ static bool prefill_check(vitna_cuda_model* g, size_t layer, size_t n, char* err
 
 extern "C" bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, int32_t* chosen, char* err,
                                       size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!prefill_check(g, layer, n, err, err_len)) return false;
     if (!x) return fail(err, err_len, "no rows");
     HIP_TRY(hipSetDevice(g->device), "selecting the model's device");
@@ -1468,6 +1534,7 @@ extern "C" bool vitna_hip_moe_prefill(struct vitna_cuda_model* g, size_t layer, 
 
 extern "C" bool vitna_hip_time_prefill(struct vitna_cuda_model* g, size_t layer, size_t n, uint64_t seed, int reps, double* us_total,
                                        double* us_phase, char* err, size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!prefill_check(g, layer, n, err, err_len)) return false;
     if (reps < 1) return fail(err, err_len, "reps must be positive");
     HIP_TRY(hipSetDevice(g->device), "selecting the model's device");
@@ -1522,6 +1589,7 @@ static bool scratch_address(int device, char** out, char* err, size_t err_len) {
 
 extern "C" bool vitna_hip_moe_prefill_noalloc(struct vitna_cuda_model* g, size_t layer, float* x, size_t n, int32_t* chosen, char* err,
                                               size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!prefill_check(g, layer, n, err, err_len)) return false;
     if (!x) return fail(err, err_len, "no rows");
     const size_t need = prefill_layout(g, n, nullptr, nullptr);
@@ -1548,6 +1616,7 @@ extern "C" bool vitna_hip_moe_prefill_noalloc(struct vitna_cuda_model* g, size_t
 /* The prefill's routing and output rows of the last timed or served prefill, to the host. */
 extern "C" bool vitna_hip_prefill_rows(struct vitna_cuda_model* g, size_t n, float* x_in, float* x_out, int32_t* chosen, char* err,
                                        size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || n > g->pf_cap) return fail(err, err_len, "%zu rows: the last prefill held %zu", n, g ? g->pf_cap : 0);
     HIP_TRY(hipSetDevice(g->device), "selecting the model's device");
     if (x_in) HIP_TRY(hipMemcpyAsync(x_in, g->pf_x0, n * g->H * 4, hipMemcpyDeviceToHost, g->stream), "copying the input rows");
@@ -1562,6 +1631,7 @@ extern "C" bool vitna_hip_prefill_rows(struct vitna_cuda_model* g, size_t n, flo
 
 extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, int steps, double* ms_per_step,
                                      char* err, size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (steps < 1) return fail(err, err_len, "at least one step");
     bool mega;
@@ -1593,6 +1663,7 @@ extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int
 }
 
 extern "C" bool vitna_hip_time_ffn(struct vitna_cuda_model* g, int reps, double* us_per_layer, char* err, size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (reps < 1) return fail(err, err_len, "at least one repetition");
     bool mega = false;
@@ -1861,6 +1932,7 @@ extern "C" bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitn
 
 extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t layer, size_t n, const int32_t* ids, const float* weights,
                                             size_t k, const int32_t* guess, char* err, size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     (void)guess;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (!ensure_tiled(g, err, err_len)) return false;
@@ -1928,6 +2000,7 @@ static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_
 
 extern "C" bool vitna_hip_moe_rows_step(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, float* const* logits, char* err,
                                         size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (!g->attention) return fail(err, err_len, "this model has no attention");
     if (!set_rows(g, rows, n, err, err_len)) return false;
@@ -1943,6 +2016,7 @@ extern "C" bool vitna_hip_moe_rows_step(struct vitna_cuda_model* g, const vitna_
 
 extern "C" bool vitna_hip_time_rows(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, int steps, double* ms_per_step,
                                     char* err, size_t err_len) {
+    if (g && !experts_resident(g, err, err_len)) return false;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (!g->attention) return fail(err, err_len, "this model has no attention");
     if (steps < 1) return fail(err, err_len, "at least one step");

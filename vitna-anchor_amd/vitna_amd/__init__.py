@@ -363,8 +363,10 @@ def _hip():
                                               C.POINTER(C.c_double), *E]),
         "vitna_hip_time_rows": (C.c_bool, [P, C.POINTER(RowT), C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_prefill_rows": (C.c_bool, [P, C.c_size_t, _FP, _FP, C.POINTER(C.c_int32), *E]),
-"vitna_hip_route_check": (C.c_bool, [_FP, C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
+        "vitna_hip_route_check": (C.c_bool, [_FP, C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                              _FP, *E]),
+        "vitna_hip_expert_cache_state": (C.c_bool, [P, C.POINTER(C.c_int32), C.c_size_t, C.POINTER(C.c_uint64), *E]),
+        "vitna_cuda_moe_report": (C.c_char_p, [P, C.c_char_p, C.c_size_t]),
         "vitna_hip_copy_probe": (C.c_bool, [C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_steps": (C.c_bool, [P, C.c_size_t, C.c_int32, C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_ffn": (C.c_bool, [P, C.c_int, C.POINTER(C.c_double), *E]),
@@ -395,7 +397,9 @@ def _i32(a):
 class Device:
     """A model uploaded to the GPU through vitna_cuda_create."""
 
-    def __init__(self, model):
+    def __init__(self, model, expert_cache_bytes=0):
+        """expert_cache_bytes: 0 keeps every expert resident; fewer bytes than the experts take puts them behind a
+        cache of slots (the reference's expert cache), served by moe_route / moe_experts."""
         self.model = model
         self.lib = hip()
         self.err = C.create_string_buffer(512)
@@ -405,7 +409,7 @@ class Device:
             c, s = fptr(self.cos), fptr(self.sin)
         else:
             c = s = None
-        self.g = self.lib.vitna_cuda_create(model.ptr, c, s, 0, self.err, 512)
+        self.g = self.lib.vitna_cuda_create(model.ptr, c, s, expert_cache_bytes, self.err, 512)
         if not self.g:
             raise VitnaError(self.err.value.decode())
 
@@ -427,10 +431,26 @@ class Device:
                                                self.err, 512))
         return (lg, nx) if want_next else lg
 
-    def moe_experts(self, layer, ids, weights):
+    def moe_experts(self, layer, ids, weights, guess=None):
         ids = np.ascontiguousarray(ids, np.int32)
         w = np.ascontiguousarray(weights, np.float32)
-        self._ok(self.lib.vitna_cuda_moe_experts(self.g, layer, _i32(ids), fptr(w), ids.size, None, self.err, 512))
+        gs = None if guess is None else np.ascontiguousarray(guess, np.int32)
+        self._ok(self.lib.vitna_cuda_moe_experts(self.g, layer, _i32(ids), fptr(w), ids.size, None if gs is None else _i32(gs),
+                                                 self.err, 512))
+
+    def moe_report(self):
+        buf = C.create_string_buffer(1024)
+        return self.lib.vitna_cuda_moe_report(self.g, buf, 1024).decode()
+
+    def expert_cache_state(self):
+        """(where[n_layers * E], counters dict) of the expert cache."""
+        cfg = self.model.cfg
+        where = np.empty(cfg.n_layers * cfg.n_experts, np.int32)
+        cnt = (C.c_uint64 * 10)()
+        self._ok(self.lib.vitna_hip_expert_cache_state(self.g, _i32(where), where.size, cnt, self.err, 512))
+        keys = ("slots", "slot_bytes", "acquired", "hits", "in_flight", "misses", "prefetched", "prefetch_used", "copies",
+                "bytes_copied")
+        return where, dict(zip(keys, [int(v) for v in cnt]))
 
     def moe_head(self):
         out = np.empty(self.model.cfg.vocab, np.float32)
