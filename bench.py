@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
     python bench.py --only 0|1|3|4 [--steps K] one of the other configs alone (profiling)
+    python bench.py --only cache [--cache-frac F] configs[2]'s decode through the expert cache
 
 Workload: a full 48-layer Qwen3-30B-A3B-shaped model
 with seeded random weights (Q4_K gate/up/q/k/o, Q6_K down/v/LM head, Q4_K
@@ -24,7 +25,11 @@ Prints one JSON line. Besides the step throughput it carries:
             key-value lengths drawn from U{128..8192}, one rows step (device
             routing, experts grouped so each chosen expert is read once a
             layer); configs[4], a prefill of 4096 rows through one
-            Qwen3-shaped MoE layer with Q8_0 experts (bf16 MFMA grouped GEMM).
+            Qwen3-shaped MoE layer with Q8_0 experts (bf16 MFMA grouped GEMM);
+            configs[0] and [1], one MoE layer of one token; expert_cache,
+            configs[2]'s model decoded a layer at a time through the
+            reference's ABI with every expert resident and with a cache
+            holding half of them (copied in from host memory).
 """
 import argparse
 import json
@@ -62,7 +67,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-extra", action="store_true", help="measure configs[2] only")
-    ap.add_argument("--only", choices=["0", "1", "3", "4"], help="run one of the other configs alone (profiling) and print its object")
+    ap.add_argument("--only", choices=["0", "1", "3", "4", "cache"],
+                    help="run one of the other configs alone (profiling), or the expert cache's decode, and print its object")
+    ap.add_argument("--cache-frac", type=float, default=0.5, help="--only cache: the share of the experts the cache holds")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every GPU box here has one GPU). "
@@ -76,6 +83,8 @@ def main():
             res = bench_layer(va, int(args.only), reps=args.steps)
         elif args.only == "4":
             res = bench_prefill(va, reps=args.steps)
+        elif args.only == "cache":
+            res = bench_cache(va, args.steps, args.warmup, args.cache_frac, args.layers)
         else:
             model = va.Model(va.shape(n_layers=args.layers, ctx=8193, seqs=32, kv_host=0), 20260101, threads=16)
             dev = va.Device(model)
@@ -185,6 +194,7 @@ def main():
         extra["4"] = bench_prefill(va)
         extra["0"] = bench_layer(va, 0)
         extra["1"] = bench_layer(va, 1)
+        extra["expert_cache"] = bench_cache(va, 8, 2, 0.5, L, model, kc, vc)
 
     out = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -265,6 +275,86 @@ def bench_ragged(va, model, dev, steps, reps=None):
             "distinct_experts": {"mean": round(uniq, 2), "min": int(min(distinct)), "max": int(max(distinct))},
             "est_note": "key-value bytes exact; expert bytes for the distinct experts each layer reads, counted "
                         "(%.1f a layer on average)" % uniq}
+
+
+def bench_cache(va, tokens, warmup, frac, layers, model=None, kc=None, vc=None):
+    """configs[2]'s model decoded a layer at a time through the reference's ABI (vitna_cuda_moe_route, the host's
+    routing, vitna_cuda_moe_experts with the next layer's guess, vitna_cuda_moe_head), once with every expert
+    resident and once with an expert cache holding `frac` of them, copied in from page-locked host memory as the
+    layers ask. Wall-clock per token (the ABI waits for the device every layer). model, kc, vc: the main bench's
+    model and its sequence 0's cache (positions 0..2047 filled), or None to make them."""
+    pos0 = 2048
+    own = model is None
+    if own:
+        model = va.Model(va.shape(n_layers=layers, ctx=pos0 + warmup + tokens + 1, seqs=1, kv_host=1), 20260101, threads=16)
+    cfg = model.cfg
+    L, K, E = cfg.n_layers, cfg.n_experts_used, cfg.n_experts
+    kd = cfg.n_kv_heads * cfg.head_dim
+    if own:
+        kc = np.ctypeslib.as_array(model.m.k_cache, shape=(L, model.m.ctx, kd))
+        vc = np.ctypeslib.as_array(model.m.v_cache, shape=(L, model.m.ctx, kd))
+        for l in range(L):
+            kc[l, :pos0] = va.normal(7, 2 * l, pos0 * kd).reshape(pos0, kd)
+            vc[l, :pos0] = va.normal(7, 2 * l + 1, pos0 * kd).reshape(pos0, kd)
+    e0 = model.m.layers[0].experts[0]
+    expert_bytes = sum(va.row_bytes(m.dtype, m.cols) * m.rows for m in (e0.gate, e0.up, e0.down))
+    renorm = bool(cfg.renormalize)
+    out = {}
+    for name, cache in (("resident", 0), ("cached", int(frac * L * E * expert_bytes * 1.02))):
+        t0 = time.time()
+        # the device holds one sequence of the positions decoded here
+        saved = (model.m.ctx, model.m.seqs)
+        model.m.ctx, model.m.seqs = pos0 + warmup + tokens + 1, 1
+        try:
+            dev = va.Device(model, expert_cache_bytes=cache)
+        finally:
+            model.m.ctx, model.m.seqs = saved
+        for l in range(L):
+            dev.kv(0, l, 0, pos0, kc[l, :pos0], vc[l, :pos0])
+        log("%s: uploaded in %.1f s" % (name, time.time() - t0))
+        try:
+            def token(t):
+                pos = pos0 + t
+                tok = (1234 + 7919 * t) % cfg.vocab
+                for l in range(L):
+                    lg, nx = dev.moe_route(0, tok, pos, l, want_next=True)
+                    _, order, w = va.host_route(lg, K, renorm)
+                    guess = va.host_route(nx, K, renorm)[0] if l + 1 < L else None
+                    dev.moe_experts(l, order, w, guess)
+                dev.moe_head()
+            for t in range(warmup):
+                token(t)
+            c0 = dev.expert_cache_state()[1] if cache else None
+            t1 = time.perf_counter()
+            for t in range(warmup, warmup + tokens):
+                token(t)
+            ms = (time.perf_counter() - t1) * 1000.0 / tokens
+            res = {"ms_per_token": round(ms, 3), "tok_s": round(1000.0 / ms, 2)}
+            if cache:
+                c1 = dev.expert_cache_state()[1]
+                d = {k: c1[k] - c0[k] for k in c1 if k not in ("slots", "slot_bytes")}
+                res.update({"slots": c1["slots"], "slot_bytes": c1["slot_bytes"],
+                            "misses_per_token": round(d["misses"] / tokens, 2),
+                            "present_per_token": round((d["hits"] + d["in_flight"]) / tokens, 2),
+                            "guess_copies_per_token": round(d["prefetched"] / tokens, 2),
+                            "guesses_used_per_token": round(d["prefetch_used"] / tokens, 2),
+                            "MB_copied_per_token": round(d["bytes_copied"] / tokens / 1e6, 2)})
+                res["report"] = dev.moe_report()
+            out[name] = res
+            log("%s: %.3f ms a token" % (name, ms))
+        finally:
+            dev.close()
+    if own:
+        model.free()
+    r, c = out["resident"], out["cached"]
+    extra_ms = c["ms_per_token"] - r["ms_per_token"]
+    c["copy_GBps_est"] = round(c["MB_copied_per_token"] / extra_ms, 2) if extra_ms > 0 else None
+    return {"workload": "BASELINE configs[2]'s model (Qwen3-30B-A3B-shaped Q4_K_M, 48 layers), batch 1 from position %d, "
+                        "decoded a layer at a time through the reference's ABI with the host routing; the expert cache "
+                        "holding %.0f%% of the %d experts" % (pos0, 100 * frac, L * E),
+            "tokens": tokens, "warmup_tokens": warmup, "expert_bytes": expert_bytes, "resident": r, "cached": c,
+            "note": "synthetic routing spreads over every expert, so hits follow the cache's share; copy_GBps_est is "
+                    "the bytes copied a token over the extra time a token takes"}
 
 
 def bench_layer(va, c, reps=20):

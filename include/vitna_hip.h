@@ -282,6 +282,13 @@ bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int32_t token,
 bool vitna_hip_route_check(const float* logits, int n_experts, int k, bool renormalize, int32_t* chosen, int32_t* ids, float* weights,
                            char* err, size_t err_len);
 
+/** The reference's host routing (engine/src/model.c:626-703, top_k and
+    route) on the host, for callers of the layer-at-a-time ABI that have
+    none of their own: chosen largest first, order the chosen sorted by id,
+    weights aligned with order. Runs no device code. */
+bool vitna_hip_host_route(const float* logits, int n_experts, int k, bool renormalize, int32_t* chosen, int32_t* order, float* weights,
+                          char* err, size_t err_len);
+
 /** A plain device copy of bytes (a multiple of 16), reps times, on a buffer
     of its own: the average microseconds a copy. Its hardware counters of
     bytes fetched and written are the yardstick for the other kernels'. */

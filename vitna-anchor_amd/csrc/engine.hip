@@ -1738,6 +1738,49 @@ extern "C" bool vitna_hip_route_check(const float* logits, int n_experts, int k,
     return true;
 }
 
+/* The reference's host routing (engine/src/model.c:626-703, top_k and route), for callers of the layer-at-a-time ABI
+   that have none of their own: K passes of argmax (strict >, so the first of equals; a NaN where a pass starts is
+   kept), the chosen sorted by id, softmax in float32 (the max as scanned, the sum of expf(l - max) in index
+   order), renormalized over the chosen with their total summed largest first. */
+extern "C" bool vitna_hip_host_route(const float* logits, int n_experts, int k, bool renormalize, int32_t* chosen, int32_t* order,
+                                     float* weights, char* err, size_t err_len) {
+    if (!logits || n_experts < 1 || k < 1 || k > ROUTE_K_MAX || k > n_experts)
+        return fail(err, err_len, "%d experts, %d a token: 1 to %d a token, no more than the experts", n_experts, k, ROUTE_K_MAX);
+    int32_t ch[ROUTE_K_MAX], ord[ROUTE_K_MAX];
+    float w[ROUTE_K_MAX];
+    for (int i = 0; i < k; i++) {
+        int best = -1;
+        for (int e = 0; e < n_experts; e++) {
+            bool taken = false;
+            for (int j = 0; j < i; j++) taken |= ch[j] == e;
+            if (!taken && (best < 0 || logits[e] > logits[best])) best = e;
+        }
+        ch[i] = best;
+    }
+    for (int i = 0; i < k; i++) ord[i] = ch[i];
+    std::sort(ord, ord + k);
+    float mx = logits[0];
+    for (int e = 1; e < n_experts; e++)
+        if (logits[e] > mx) mx = logits[e];
+    float sum = 0.0f;
+    for (int e = 0; e < n_experts; e++) sum += expf(logits[e] - mx);
+    for (int i = 0; i < k; i++) w[i] = expf(logits[ord[i]] - mx) / sum;
+    if (renormalize) {
+        float share[ROUTE_K_MAX];
+        for (int i = 0; i < k; i++) share[i] = w[i];
+        std::stable_sort(share, share + k, [](float a, float b) { return a > b; });
+        float total = 0.0f;
+        for (int i = 0; i < k; i++) total += share[i];
+        for (int i = 0; i < k; i++) w[i] /= total;
+    }
+    for (int i = 0; i < k; i++) {
+        if (chosen) chosen[i] = ch[i];
+        if (order) order[i] = ord[i];
+        if (weights) weights[i] = w[i];
+    }
+    return true;
+}
+
 extern "C" bool vitna_hip_copy_probe(size_t bytes, int reps, double* avg_us, char* err, size_t err_len) {
     if (bytes % 16 || bytes == 0 || reps < 1) return fail(err, err_len, "a positive multiple of 16 bytes, at least one repetition");
     void *a = nullptr, *b = nullptr;

@@ -365,6 +365,8 @@ def _hip():
         "vitna_hip_prefill_rows": (C.c_bool, [P, C.c_size_t, _FP, _FP, C.POINTER(C.c_int32), *E]),
         "vitna_hip_route_check": (C.c_bool, [_FP, C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                              _FP, *E]),
+        "vitna_hip_host_route": (C.c_bool, [_FP, C.c_int, C.c_int, C.c_bool, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
+                                            _FP, *E]),
         "vitna_hip_expert_cache_state": (C.c_bool, [P, C.POINTER(C.c_int32), C.c_size_t, C.POINTER(C.c_uint64), *E]),
         "vitna_cuda_moe_report": (C.c_char_p, [P, C.c_char_p, C.c_size_t]),
         "vitna_hip_copy_probe": (C.c_bool, [C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
@@ -674,6 +676,18 @@ def copy_probe(nbytes, reps=10):
     if not hip().vitna_hip_copy_probe(nbytes, reps, C.byref(us), err, 512):
         raise VitnaError(err.value.decode())
     return us.value
+
+
+def host_route(logits, k, renormalize):
+    """vitna_hip_host_route: the reference's host routing of the given logits -> (chosen, order, weights)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    ch = np.empty(k, np.int32)
+    order = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    err = C.create_string_buffer(512)
+    if not hip().vitna_hip_host_route(fptr(lg), lg.size, k, renormalize, _i32(ch), _i32(order), fptr(w), err, 512):
+        raise VitnaError(err.value.decode())
+    return ch, order, w
 
 
 def route_check(logits, k, renormalize):
