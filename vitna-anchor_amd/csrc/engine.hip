@@ -69,6 +69,10 @@ struct vitna_cuda_model {
     row_rec* rows_dev;
     row_rec* rows_host; /* pinned */
     hipEvent_t rows_copied;
+    bool row_set;       /* rows_dev[0] holds row_last (set_row); another pass of rows clears it */
+    row_rec row_last;
+    route_out* rt_host; /* pinned, ROWS_MAX: the routing a caller gives, on its way to rt */
+    hipEvent_t rt_copied;
     float* h_logits;    /* pinned, 2 * ROWS_MAX * E */
     hipGraph_t step_graph_src; /* kept until free: graph tools may refer to its nodes */
     int *grp_count, *grp_pairs; /* expert grouping of a pass of rows: [E], [E][ROWS_MAX] */
@@ -396,6 +400,8 @@ extern "C" void vitna_cuda_free(struct vitna_cuda_model* g) {
     if (g->rows_host) (void)hipHostFree(g->rows_host);
     if (g->h_logits) (void)hipHostFree(g->h_logits);
     if (g->rows_copied) (void)hipEventDestroy(g->rows_copied);
+    if (g->rt_host) (void)hipHostFree(g->rt_host);
+    if (g->rt_copied) (void)hipEventDestroy(g->rt_copied);
     ec_destroy(g->ec);
     if (g->stream) (void)hipStreamDestroy(g->stream);
     delete g;
@@ -427,7 +433,11 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
     hipDeviceProp_t p;
     if (hipGetDeviceProperties(&p, 0) == hipSuccess) snprintf(g->name, sizeof(g->name), "%s (%s)", p.name, p.gcnArchName);
     if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess) { fail(err, err_len, "cannot create a stream"); return bail(); }
-    if (hipEventCreateWithFlags(&g->rows_copied, hipEventDisableTiming) != hipSuccess) { fail(err, err_len, "cannot create an event"); return bail(); }
+    if (hipEventCreateWithFlags(&g->rows_copied, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&g->rt_copied, hipEventDisableTiming) != hipSuccess) {
+        fail(err, err_len, "cannot create an event");
+        return bail();
+    }
 
     /* staging for the largest set of one layer's experts of one part */
     const vitna_llama_layer_t* L0 = &m->layers[0];
@@ -559,7 +569,8 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
         return bail();
     }
     if (hipHostMalloc((void**)&g->rows_host, R * sizeof(row_rec), 0) != hipSuccess ||
-        hipHostMalloc((void**)&g->h_logits, 2 * R * E * 4, 0) != hipSuccess) {
+        hipHostMalloc((void**)&g->h_logits, 2 * R * E * 4, 0) != hipSuccess ||
+        hipHostMalloc((void**)&g->rt_host, R * sizeof(route_out), 0) != hipSuccess) {
         fail(err, err_len, "page-locked host memory for the rows and logits");
         return bail();
     }
@@ -667,11 +678,16 @@ static bool set_row(vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, 
     if (seq >= (size_t)g->seqs) return fail(err, err_len, "sequence %zu: the cache holds %d", seq, g->seqs);
     if (pos >= (size_t)g->ctx) return fail(err, err_len, "position %zu: the cache holds %d", pos, g->ctx);
     if (g->attention && (token < 0 || token >= g->V)) return fail(err, err_len, "token %d is outside the vocabulary of %d", token, g->V);
+    const row_rec r = {token, (int32_t)pos, (int32_t)seq};
+    /* the layers of one token after the first find their row in place */
+    if (g->row_set && g->row_last.token == r.token && g->row_last.pos == r.pos && g->row_last.seq == r.seq) return true;
     /* the previous copy out of the page-locked row must have run */
     HIP_TRY(hipEventSynchronize(g->rows_copied), "waiting for the previous row copy");
-    g->rows_host[0] = {token, (int32_t)pos, (int32_t)seq};
+    g->rows_host[0] = r;
     HIP_TRY(hipMemcpyAsync(g->rows_dev, g->rows_host, sizeof(row_rec), hipMemcpyHostToDevice, g->stream), "copying the row");
     HIP_TRY(hipEventRecord(g->rows_copied, g->stream), "recording the row copy");
+    g->row_last = r;
+    g->row_set = true;
     return true;
 }
 
@@ -684,12 +700,14 @@ extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int
     if (!g->attention) return fail(err, err_len, "this model has no attention; use vitna_hip_moe_ffn");
     if (!set_row(g, seq, token, pos, err, err_len)) return false;
     g->last_step_mega = false;
+    const bool nx = next && layer + 1 < (size_t)g->NL;
+    /* embedding (layer 0), attention, router (and the next layer's router on the same residual, whose norm must
+       not replace this layer's), the logits to the page-locked buffer. Launched one by one: a graph a layer was
+       slower here (5.3-5.4 against 4.5-4.7 ms a token for configs[2]'s model). */
     hipError_t e = hipSuccess;
     if (layer == 0) e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
     if (e == hipSuccess) e = enqueue_attention(g, (int)layer, 1, false);
     if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn, false);
-    const bool nx = next && layer + 1 < (size_t)g->NL;
-    /* the next layer's router on the same residual; its norm must not replace this layer's */
     if (e == hipSuccess && nx) e = enqueue_route(g, (int)layer + 1, g->rlogits + g->E, 1, g->x, nullptr, false);
     if (!check_launch(g, e, "the layer up to its router", err, err_len)) return false;
     HIP_TRY(hipMemcpyAsync(g->h_logits, g->rlogits, (nx ? 2 : 1) * g->E * 4, hipMemcpyDeviceToHost, g->stream), "copying the router's logits");
@@ -703,7 +721,9 @@ extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int
 static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const float* weights, size_t k, char* err, size_t err_len,
                         const int32_t* slots = nullptr) {
     if (k != (size_t)g->K) return fail(err, err_len, "%zu experts given; the model routes to %d", k, g->K);
-    std::vector<route_out> ro(n);
+    /* the previous routing's copy out of the page-locked buffer must have run */
+    HIP_TRY(hipEventSynchronize(g->rt_copied), "waiting for the previous routing copy");
+    route_out* ro = g->rt_host;
     for (size_t t = 0; t < n; t++) {
         memset(&ro[t], 0, sizeof(route_out));
         for (size_t i = 0; i < k; i++) {
@@ -717,20 +737,22 @@ static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const
             ro[t].cw[i] = weights[t * k + i];
         }
     }
-    /* pageable source: the copy has taken the bytes when this returns */
-    HIP_TRY(hipMemcpyAsync(g->rt, ro.data(), n * sizeof(route_out), hipMemcpyHostToDevice, g->stream), "copying the routing");
-    HIP_TRY(hipStreamSynchronize(g->stream), "copying the routing");
+    /* from page-locked memory, in stream order: the kernels after it read it, nothing waits on the host */
+    HIP_TRY(hipMemcpyAsync(g->rt, ro, n * sizeof(route_out), hipMemcpyHostToDevice, g->stream), "copying the routing");
+    HIP_TRY(hipEventRecord(g->rt_copied, g->stream), "recording the routing copy");
     return true;
+}
+
+/* One token's experts of layer as g->rt routes them, added into the residual. */
+static bool run_experts(vitna_cuda_model* g, int layer, char* err, size_t err_len) {
+    return check_launch(g, enqueue_experts(g, layer, nullptr, g->x, 1), "the experts", err, err_len);
 }
 
 extern "C" bool vitna_cuda_moe_experts(struct vitna_cuda_model* g, size_t layer, const int32_t* ids, const float* weights, size_t k,
                                        const int32_t* guess, char* err, size_t err_len) {
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
-    if (!g->ec.on) {
-        if (!put_routing(g, 1, ids, weights, k, err, err_len)) return false;
-        return check_launch(g, enqueue_experts(g, (int)layer, nullptr, g->x, 1), "the experts", err, err_len);
-    }
+    if (!g->ec.on) return put_routing(g, 1, ids, weights, k, err, err_len) && run_experts(g, (int)layer, err, err_len);
     /* through the expert cache (model_cuda.cu:4757-4913): the slots of this layer's experts, the routing naming the
        slots, the kernels after the copies into them, then the guess's copies behind the kernels */
     if (k != (size_t)g->K) return fail(err, err_len, "%zu experts given; the model routes to %d", k, g->K);
@@ -741,7 +763,7 @@ extern "C" bool vitna_cuda_moe_experts(struct vitna_cuda_model* g, size_t layer,
     int32_t slot_of[ROUTE_K_MAX];
     bool ok = ec_acquire(g->ec, (int)layer, ids, (int)k, g->stream, slot_of, err, err_len) &&
               put_routing(g, 1, ids, weights, k, err, err_len, slot_of) && ec_wait(g->ec, slot_of, (int)k, g->stream, err, err_len) &&
-              check_launch(g, enqueue_experts(g, (int)layer, nullptr, g->x, 1), "the experts", err, err_len);
+              run_experts(g, (int)layer, err, err_len);
     /* the holds are released whatever happened; the guess only after the kernels */
     const bool fin = ec_finish(g->ec, (int)layer, ok ? guess : nullptr, (int)k, err, err_len);
     return ok && fin;
@@ -1933,6 +1955,7 @@ static bool set_rows(vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n
         for (size_t j = 0; j < i; j++) shared |= rows[j].seq == r.seq;
     }
     HIP_TRY(hipEventSynchronize(g->rows_copied), "waiting for the previous row copy");
+    g->row_set = false;
     for (size_t i = 0; i < n; i++) g->rows_host[i] = {rows[i].token, rows[i].pos, rows[i].seq};
     HIP_TRY(hipMemcpyAsync(g->rows_dev, g->rows_host, n * sizeof(row_rec), hipMemcpyHostToDevice, g->stream), "copying the rows");
     HIP_TRY(hipEventRecord(g->rows_copied, g->stream), "recording the row copy");
