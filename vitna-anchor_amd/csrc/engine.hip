@@ -1469,6 +1469,8 @@ static size_t prefill_layout(const vitna_cuda_model* g, size_t n, char* base, pf
 }
 
 static bool prefill_reserve(vitna_cuda_model* g, size_t n, char* err, size_t err_len) {
+    /* the experts' tiled copy the prefill GEMM reads (made once) */
+    if (!ensure_tiled(g, err, err_len)) return false;
     if (n <= g->pf_cap) return true;
     HIP_TRY(hipStreamSynchronize(g->stream), "waiting before the prefill buffers grow");
     for (void* p : g->pf_allocs) (void)hipFree(p);

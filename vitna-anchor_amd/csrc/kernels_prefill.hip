@@ -40,6 +40,11 @@
 
 #include "vitna_kernels.h"
 
+#include <type_traits>
+#ifndef PF_DIAG_MODE
+#define PF_DIAG_MODE 0
+#endif
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -47,6 +52,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 #define PF_BN 256 /* weight rows a workgroup */
 #define PF_THREADS 512
 #define PF_BK 64  /* contraction a stage: two Q8_0 blocks */
+
+/* The SwiGLU of the prefill GEMM, rounded to bf16 right after: silu(g) u with a hardware reciprocal (1 ulp),
+   which the bf16 rounding dwarfs. Both GEMM kernels use this one form, so they give the same bits. */
+__device__ __forceinline__ float pf_swiglu(float g, float u) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u; }
 
 __device__ __forceinline__ uint32_t bf16_rne(float f) {
     const uint32_t b = __float_as_uint(f);
@@ -348,7 +357,7 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
 #pragma unroll
                 for (int k = 0; k < 2; k++) {
                     const float gt = acc[i][k][r], up = acc[i][k + 2][r];
-                    const float v = gt / (1.0f + __expf(-gt)) * up;
+                    const float v = pf_swiglu(gt, up);
                     a.act[(size_t)(pbase + p) * I + nt * (PF_BN / 2) + wni * 64 + k * 32 + l32] = (uint16_t)bf16_rne(v);
                 }
             } else {
@@ -359,6 +368,257 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
                 for (int k = 0; k < 4; k++) y[32 * k] = (uint16_t)bf16_rne(acc[i][k][r] * wt);
             }
         }
+}
+
+/* ---- the grouped GEMM, each wave converting its own weights ------------------------------------------
+
+   A 256-thread workgroup (one wave a SIMD) owns one tile (up to 256 pairs) and 256 weight rows; wave w owns 64 of
+   them (gate/up: 32 gate rows and the 32 up rows of the same columns, so SwiGLU stays in a lane; down: 64 rows)
+   against every pair of the tile, as ML x 2 tiles of v_mfma_f32_32x32x16_bf16. The waves share only the
+   activations, which arrive in an LDS ring (three stages of K = 64, 256 rows x 128 bytes) by global-to-LDS
+   loads two stages ahead; one barrier a stage. The weights never pass through LDS: each lane loads the Q8_0
+   bytes its own B fragments need, three stages ahead, and widens them itself (q * d exact in fp32, rounded to
+   bf16, as before) just before its MFMAs, on the VALU while the matrix core works. Every weight is read and
+   widened once a workgroup, by the one wave that uses it.
+
+   A lane (l32, kq) of a 32-row weight tile needs, for K step j (16 columns), row l32's 8 quants at 16 j + 8 kq;
+   the experts' tiled copy holds each K step's 16 bytes of 64 rows together, so each weight load of a wave is
+   512 contiguous bytes (a wave's loads of the row-major planes, 32 rows 2 KB apart, ran at a fraction of that).
+
+   Loads a stage, in this order: the activations of stage s + 2 (NA a lane), the weights of stage s + 3 (NB a
+   lane: eight 8-byte quant loads, two scale loads), every stage past the end a repeat of the last. At the top of
+   stage s the youngest NA + 2 NB loads may still run; the activations stage s reads are older. */
+
+/* The workgroup barrier of the pipeline: this wave's LDS accesses done, then s_barrier. Not a fence: a
+   workgroup release fence would also wait for every global-to-LDS load in flight (vmcnt(0)), which the
+   pipeline keeps in flight across barriers on purpose. The memory clobber keeps the compiler from moving
+   memory accesses across it. */
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void vm_wait() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)p;
+}
+
+/* A global-to-LDS load of 16 bytes a lane: lane L's bytes land at lds + 16 L. M0 is set here and nowhere else
+   in these kernels. */
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+
+#define PW_THREADS 256
+#define PW_NA 8 /* 16-byte activation loads a lane a stage: 256 rows x 128 bytes over 256 lanes */
+#define PW_NB 10
+
+typedef __attribute__((ext_vector_type(2))) uint32_t pw_u32x2;
+
+/* eight int8 quants (lo, hi) times d, rounded to bf16: (u - 128) d with u = q + 128 as a byte, exact in fp32 */
+__device__ __forceinline__ u32x4 pw_widen8(uint32_t lo, uint32_t hi, float d, float nd128) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const uint32_t v[2] = {lo ^ 0x80808080u, hi ^ 0x80808080u};
+    uint32_t o[4];
+#pragma unroll
+    for (int w = 0; w < 2; w++) {
+        const float f0 = fmaf((float)(v[w] & 0xffu), d, nd128), f1 = fmaf((float)((v[w] >> 8) & 0xffu), d, nd128);
+        const float f2 = fmaf((float)((v[w] >> 16) & 0xffu), d, nd128), f3 = fmaf((float)(v[w] >> 24), d, nd128);
+        const bf16x2 p0 = {(__bf16)f0, (__bf16)f1}, p1 = {(__bf16)f2, (__bf16)f3};
+        o[2 * w] = __builtin_bit_cast(uint32_t, p0);
+        o[2 * w + 1] = __builtin_bit_cast(uint32_t, p1);
+    }
+    return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+/* A stage's weights of one lane: quants q[t][j] (tile t, K step j: its 8 bytes), scales d[t] (the stage's two
+   blocks, f16) */
+struct pw_bset {
+    pw_u32x2 q[2][4];
+    uint32_t d[2];
+};
+
+template <bool GU, int ML>
+__device__ __forceinline__ void pw_body(const prefill_args& a, int e, int m0, int nt, int cnt, uint8_t* lds, int* yrow, float* ywt) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, l32 = lane & 31, kq = lane >> 5;
+    const int H = a.gate.cols, I = a.gate.rows;
+    const int KD = GU ? H : I, nb = KD / 32, S = KD / PF_BK;
+    const int pbase = a.off[e];
+
+    /* activations: DMA i of this lane fills 16-byte slot (wv * PW_NA + i) * 64 + lane of a stage: row slot / 8,
+       position slot % 8, which holds chunk position ^ ((row >> 1) & 7) */
+    const uint8_t* abase = reinterpret_cast<const uint8_t*>(GU ? a.xb : a.act);
+    uint32_t aoff[PW_NA]; /* byte offsets from abase: the activations are under 4 GiB (launch_prefill_gemm) */
+#pragma unroll
+    for (int i = 0; i < PW_NA; i++) {
+        const int sl = (wv * PW_NA + i) * 64 + lane, r = sl >> 3, c = chunk_pos(r, sl & 7);
+        const int pa = min(m0 + r, cnt - 1);
+        const size_t row = GU ? (size_t)(a.pairs[(size_t)e * a.cap + pa] / ROUTE_K_MAX) * H : (size_t)(pbase + pa) * I;
+        aoff[i] = (uint32_t)(row * 2 + 16 * c);
+    }
+    /* weights from the experts' tiled copy (gtile_kernel): per 64-row group and 128-column unit, eight 1 KB
+       chunks [64 rows][16 columns], then the rows' four scales each. Tile t of this wave is a 32-row half of a
+       group. */
+    const uint8_t *wq[2], *wd[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const qmat& W = GU ? (t ? a.up : a.gate) : a.down;
+        const int r0 = GU ? nt * 128 + wv * 32 : nt * 256 + wv * 64 + t * 32;
+        const size_t units = (size_t)W.cols / 128, stride = (size_t)(W.rows / 64) * units * 8704;
+        const uint8_t* g0 = W.tiled + (size_t)e * stride + (size_t)(r0 >> 6) * units * 8704;
+        const int rin = (r0 & 32) + l32; /* row in the 64-row group */
+        wq[t] = g0 + rin * 16 + 8 * kq;
+        wd[t] = g0 + 8192 + rin * 8;
+    }
+    const uint32_t lds0 = lds_addr(lds);
+    if (!GU && tid < PF_BM && m0 + tid < cnt) {
+        /* the tile's pairs: where each one's part goes and its weight (read by the epilogue, after the barriers) */
+        const int pr = a.pairs[(size_t)e * a.cap + m0 + tid], row = pr / ROUTE_K_MAX, sl = pr % ROUTE_K_MAX;
+        yrow[tid] = row * a.K + sl;
+        ywt[tid] = a.rt[row].weights[sl];
+    }
+
+    auto issue_a = [&](int x) {
+        x = min(x, S - 1);
+        const uint32_t base = lds0 + (uint32_t)(x % PF_A_STAGES) * PF_TILE_BYTES + (uint32_t)wv * PW_NA * 1024;
+#pragma unroll
+        for (int i = 0; i < PW_NA; i++) dma16(abase + aoff[i] + (size_t)((PF_DIAG_MODE & 4) ? 0 : x) * 128, __builtin_amdgcn_readfirstlane(base + i * 1024));
+    };
+    /* ordinary loads: the compiler waits for them where they are used (counting only its own loads, so it also
+       waits for some younger global-to-LDS loads: the weights land about two stages ahead) */
+    auto issue_b = [&](int x, pw_bset& b) {
+        x = min(x, S - 1);
+        const size_t u = (size_t)(x >> 1) * 8704;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) b.q[t][j] = *reinterpret_cast<const pw_u32x2*>(wq[t] + u + (4 * (x & 1) + j) * 1024);
+            /* the scales of the stage's two blocks */
+            b.d[t] = *reinterpret_cast<const uint32_t*>(wd[t] + u + 4 * (x & 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    f32x16 acc[ML][2];
+#pragma unroll
+    for (int m = 0; m < ML; m++)
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[m][t][r] = 0.0f;
+
+    /* fragment reads: row 32 m + l32 of the stage, chunk 2 j + kq */
+    const int swz = (l32 >> 1) & 7;
+    auto read_a = [&](uint32_t base, int j, u32x4 (&f)[ML]) {
+        const uint32_t p = base + (uint32_t)l32 * 128 + (uint32_t)(((2 * j + kq) ^ swz) << 4);
+#pragma unroll
+        for (int m = 0; m < ML; m++) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(f[m]) : "v"(p), "n"(m * 4096) : "memory");
+    };
+    auto wait_a = [&](u32x4 (&f)[ML], auto n) {
+        constexpr int N = decltype(n)::value;
+#pragma unroll
+        for (int m = 0; m < ML; m++) asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(f[m]) : "n"(N));
+    };
+
+    pw_bset bs[4];
+    auto stage = [&](int s, pw_bset& b) {
+        /* the activations of stage s in LDS (every wave's own loads, then the barrier), this lane's weights */
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PW_NA + 2 * PW_NB) : "memory");
+        wg_barrier();
+        issue_a(s + 2);
+        const uint32_t abase = lds0 + (uint32_t)(s % PF_A_STAGES) * PF_TILE_BYTES;
+        u32x4 fa[2][ML];
+        read_a(abase, 0, fa[0]);
+        float dd[2][2], nd[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                dd[t][h] = f16_bits_to_f32(h ? b.d[t] >> 16 : b.d[t] & 0xffffu);
+                nd[t][h] = -128.0f * dd[t][h];
+            }
+        /* the next stage's weight set is free once this stage has widened its own: issue it at the end */
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (j < 3) read_a(abase, j + 1, fa[(j + 1) & 1]);
+            u32x4 bw[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) bw[t] = pw_widen8(b.q[t][j].x, b.q[t][j].y, dd[t][j >> 1], nd[t][j >> 1]);
+            if (j < 3) wait_a(fa[j & 1], std::integral_constant<int, ML>{});
+            else wait_a(fa[j & 1], std::integral_constant<int, 0>{});
+            if constexpr ((PF_DIAG_MODE & 1) != 0) {
+#pragma unroll
+                for (int m = 0; m < ML; m++) acc[m][0][0] += __builtin_bit_cast(float, fa[j & 1][m].x) + __builtin_bit_cast(float, bw[0].x ^ bw[1].y);
+                continue;
+            }
+#pragma unroll
+            for (int m = 0; m < ML; m++)
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+                    acc[m][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fa[j & 1][m]),
+                                                                       __builtin_bit_cast(bf16x8, bw[t]), acc[m][t], 0, 0, 0);
+        }
+    };
+
+    /* prologue: A(0) B(0) A(1) B(1) B(2); stage s then issues A(s + 2) and B(s + 3) */
+    vm_wait<0>();
+    issue_a(0);
+    issue_b(0, bs[0]);
+    issue_a(1);
+    issue_b(1, bs[1]);
+    issue_b(2, bs[2]);
+    /* S is a multiple of 4 (launch_prefill_gemm): the body has no branch, so the compiler's waits for the
+       weight registers count the loads of the straight line */
+    for (int s0 = 0; s0 < S; s0 += 4) {
+        stage(s0, bs[0]);
+        issue_b(s0 + 3, bs[3]);
+        stage(s0 + 1, bs[1]);
+        issue_b(s0 + 4, bs[0]);
+        stage(s0 + 2, bs[2]);
+        issue_b(s0 + 5, bs[1]);
+        stage(s0 + 3, bs[3]);
+        issue_b(s0 + 6, bs[2]);
+    }
+    vm_wait<0>(); /* no load into LDS outlives the workgroup */
+
+    /* accumulator r of a lane: row 8 (r / 4) + 4 kq + r % 4 of the 32 x 32 tile, column l32 */
+#pragma unroll
+    for (int m = 0; m < ML; m++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int p = m0 + 32 * m + 8 * (r >> 2) + 4 * kq + (r & 3);
+            if (p >= cnt) continue;
+            if (GU) {
+                const float gt = acc[m][0][r], up = acc[m][1][r];
+                const float v = pf_swiglu(gt, up);
+                a.act[(size_t)(pbase + p) * I + nt * 128 + wv * 32 + l32] = (uint16_t)bf16_rne(v);
+            } else {
+                const int q = p - m0;
+                const float wt = ywt[q];
+                uint16_t* y = a.ypart + (size_t)yrow[q] * H + nt * 256 + wv * 64 + l32;
+#pragma unroll
+                for (int t = 0; t < 2; t++) y[32 * t] = (uint16_t)bf16_rne(acc[m][t][r] * wt);
+            }
+        }
+}
+
+template <bool GU>
+__global__ __launch_bounds__(PW_THREADS, 1) void prefill_wgemm_kernel(prefill_args a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[PF_A_STAGES * PF_TILE_BYTES];
+    __shared__ int yrow[PF_BM];
+    __shared__ float ywt[PF_BM];
+    const int H = a.gate.cols, I = a.gate.rows;
+    const int NT = GU ? I / 128 : H / 256;
+    const int nwork = *a.n_tiles * NT;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, per = (nwork + 7) >> 3;
+    const int w = xcd * per + slot;
+    if (slot >= per || w >= nwork) return;
+    const int tl = a.tiles[w / NT], nt = w - (w / NT) * NT;
+    const int e = tl >> 16, m0 = (tl & 0xffff) * PF_BM;
+    const int cnt = a.count[e];
+    const int rows = cnt - m0;
+    if (rows > 128) pw_body<GU, 8>(a, e, m0, nt, cnt, lds, yrow, ywt);
+    else if (rows > 64) pw_body<GU, 4>(a, e, m0, nt, cnt, lds, yrow, ywt);
+    else pw_body<GU, 2>(a, e, m0, nt, cnt, lds, yrow, ywt);
 }
 
 /* ---- launches ----------------------------------------------------------- */
@@ -440,7 +700,14 @@ hipError_t launch_prefill_gemm(const prefill_args& a, bool gate_up, hipStream_t 
     const int NT = gate_up ? I / (PF_BN / 2) : H / PF_BN;
     const size_t blocks = ((size_t)NT * prefill_max_tiles(a.n, a.K, a.E) + 7) / 8 * 8;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    if (gate_up) prefill_gemm_kernel<true><<<(unsigned)blocks, PF_THREADS, 0, s>>>(a);
+    /* the kernel that widens each wave's own weights reads the experts' tiled copy, made by the allocating entry
+       points; without it (the no-allocation entry point before any of them ran) the shared-stage kernel reads
+       the planes. Both give the same bits: the same products, summed in the same order. */
+    const bool wide = a.gate.tiled && a.up.tiled && a.down.tiled && H % 256 == 0 && I % 256 == 0 &&
+                      (size_t)a.n * a.K * I * 2 < ((size_t)1 << 32) && (size_t)a.n * H * 2 < ((size_t)1 << 32);
+    if (wide && gate_up) prefill_wgemm_kernel<true><<<(unsigned)blocks, PW_THREADS, 0, s>>>(a);
+    else if (wide) prefill_wgemm_kernel<false><<<(unsigned)blocks, PW_THREADS, 0, s>>>(a);
+    else if (gate_up) prefill_gemm_kernel<true><<<(unsigned)blocks, PF_THREADS, 0, s>>>(a);
     else prefill_gemm_kernel<false><<<(unsigned)blocks, PF_THREADS, 0, s>>>(a);
     return hipGetLastError();
 }
