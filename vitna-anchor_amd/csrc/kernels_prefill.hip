@@ -41,9 +41,6 @@
 #include "vitna_kernels.h"
 
 #include <type_traits>
-#ifndef PF_DIAG_MODE
-#define PF_DIAG_MODE 0
-#endif
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -375,8 +372,8 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
    A 256-thread workgroup (one wave a SIMD) owns one tile (up to 256 pairs) and 256 weight rows; wave w owns 64 of
    them (gate/up: 32 gate rows and the 32 up rows of the same columns, so SwiGLU stays in a lane; down: 64 rows)
    against every pair of the tile, as ML x 2 tiles of v_mfma_f32_32x32x16_bf16. The waves share only the
-   activations, which arrive in an LDS ring (three stages of K = 64, 256 rows x 128 bytes) by global-to-LDS
-   loads two stages ahead; one barrier a stage. The weights never pass through LDS: each lane loads the Q8_0
+   activations, which arrive in an LDS ring (four stages of K = 64, 256 rows x 128 bytes) by global-to-LDS
+   loads three stages ahead; one barrier a stage. The weights never pass through LDS: each lane loads the Q8_0
    bytes its own B fragments need, three stages ahead, and widens them itself (q * d exact in fp32, rounded to
    bf16, as before) just before its MFMAs, on the VALU while the matrix core works. Every weight is read and
    widened once a workgroup, by the one wave that uses it.
@@ -385,9 +382,11 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
    the experts' tiled copy holds each K step's 16 bytes of 64 rows together, so each weight load of a wave is
    512 contiguous bytes (a wave's loads of the row-major planes, 32 rows 2 KB apart, ran at a fraction of that).
 
-   Loads a stage, in this order: the activations of stage s + 2 (NA a lane), the weights of stage s + 3 (NB a
-   lane: eight 8-byte quant loads, two scale loads), every stage past the end a repeat of the last. At the top of
-   stage s the youngest NA + 2 NB loads may still run; the activations stage s reads are older. */
+   Loads a stage, in this order: the activations of stage s + 3 (NA = ML a lane: the live rows) after the barrier, the weights of
+   stage s + 3 (NB a lane: eight 8-byte quant loads, two scale loads) after the MFMAs, every stage past the end a
+   repeat of the last. At the top of stage s the youngest 2 NA + 2 NB loads may still run: those of stages s + 1
+   and s + 2; everything stage s reads is older. The loads stay in flight for about three stages, which the
+   activation and weight streams need: with two, the stage time was the memory latency over two. */
 
 /* The workgroup barrier of the pipeline: this wave's LDS accesses done, then s_barrier. Not a fence: a
    workgroup release fence would also wait for every global-to-LDS load in flight (vmcnt(0)), which the
@@ -409,8 +408,8 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
 }
 
 #define PW_THREADS 256
-#define PW_NA 8 /* 16-byte activation loads a lane a stage: 256 rows x 128 bytes over 256 lanes */
 #define PW_NB 10
+#define PW_AST 4 /* activation stages in the LDS ring */
 
 typedef __attribute__((ext_vector_type(2))) uint32_t pw_u32x2;
 
@@ -444,13 +443,14 @@ __device__ __forceinline__ void pw_body(const prefill_args& a, int e, int m0, in
     const int KD = GU ? H : I, nb = KD / 32, S = KD / PF_BK;
     const int pbase = a.off[e];
 
-    /* activations: DMA i of this lane fills 16-byte slot (wv * PW_NA + i) * 64 + lane of a stage: row slot / 8,
-       position slot % 8, which holds chunk position ^ ((row >> 1) & 7) */
+    /* activations, only the tile's 32 ML live rows: DMA i of this lane fills 16-byte slot (wv * NA + i) * 64 + lane
+       of a stage: row slot / 8, position slot % 8, which holds chunk position ^ ((row >> 1) & 7) */
+    constexpr int NA = ML;
     const uint8_t* abase = reinterpret_cast<const uint8_t*>(GU ? a.xb : a.act);
-    uint32_t aoff[PW_NA]; /* byte offsets from abase: the activations are under 4 GiB (launch_prefill_gemm) */
+    uint32_t aoff[NA]; /* byte offsets from abase: the activations are under 4 GiB (launch_prefill_gemm) */
 #pragma unroll
-    for (int i = 0; i < PW_NA; i++) {
-        const int sl = (wv * PW_NA + i) * 64 + lane, r = sl >> 3, c = chunk_pos(r, sl & 7);
+    for (int i = 0; i < NA; i++) {
+        const int sl = (wv * NA + i) * 64 + lane, r = sl >> 3, c = chunk_pos(r, sl & 7);
         const int pa = min(m0 + r, cnt - 1);
         const size_t row = GU ? (size_t)(a.pairs[(size_t)e * a.cap + pa] / ROUTE_K_MAX) * H : (size_t)(pbase + pa) * I;
         aoff[i] = (uint32_t)(row * 2 + 16 * c);
@@ -479,23 +479,23 @@ __device__ __forceinline__ void pw_body(const prefill_args& a, int e, int m0, in
 
     auto issue_a = [&](int x) {
         x = min(x, S - 1);
-        const uint32_t base = lds0 + (uint32_t)(x % PF_A_STAGES) * PF_TILE_BYTES + (uint32_t)wv * PW_NA * 1024;
+        const uint32_t base = lds0 + (uint32_t)(x % PW_AST) * PF_TILE_BYTES + (uint32_t)wv * NA * 1024;
 #pragma unroll
-        for (int i = 0; i < PW_NA; i++) dma16(abase + aoff[i] + (size_t)((PF_DIAG_MODE & 4) ? 0 : x) * 128, __builtin_amdgcn_readfirstlane(base + i * 1024));
+        for (int i = 0; i < NA; i++) dma16(abase + aoff[i] + (size_t)x * 128, __builtin_amdgcn_readfirstlane(base + i * 1024));
     };
-    /* ordinary loads: the compiler waits for them where they are used (counting only its own loads, so it also
-       waits for some younger global-to-LDS loads: the weights land about two stages ahead) */
+    /* The weight loads are asm of our own, like the activations', and waited for by count: the compiler would
+       count only its own loads and so wait for younger global-to-LDS loads too. Nothing touches a set's
+       registers between its loads and the wait that names them (the stage's "+v" wait below). */
     auto issue_b = [&](int x, pw_bset& b) {
         x = min(x, S - 1);
         const size_t u = (size_t)(x >> 1) * 8704;
 #pragma unroll
         for (int t = 0; t < 2; t++) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) b.q[t][j] = *reinterpret_cast<const pw_u32x2*>(wq[t] + u + (4 * (x & 1) + j) * 1024);
-            /* the scales of the stage's two blocks */
-            b.d[t] = *reinterpret_cast<const uint32_t*>(wd[t] + u + 4 * (x & 1));
+            for (int j = 0; j < 4; j++)
+                asm volatile("global_load_dwordx2 %0, %1, off" : "=&v"(b.q[t][j]) : "v"(wq[t] + u + (4 * (x & 1) + j) * 1024) : "memory");
+            asm volatile("global_load_dword %0, %1, off" : "=&v"(b.d[t]) : "v"(wd[t] + u + 4 * (x & 1)) : "memory");
         }
-        __builtin_amdgcn_sched_barrier(0);
     };
 
     f32x16 acc[ML][2];
@@ -508,24 +508,27 @@ __device__ __forceinline__ void pw_body(const prefill_args& a, int e, int m0, in
 
     /* fragment reads: row 32 m + l32 of the stage, chunk 2 j + kq */
     const int swz = (l32 >> 1) & 7;
+    /* Fragment reads are plain LDS loads: the compiler sees no global-to-LDS load (they are asm of our own), so it
+       waits only for its LDS reads, and it can interleave them, the widening and the MFMAs. The barrier's memory
+       clobber keeps them inside their stage. */
+    typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
     auto read_a = [&](uint32_t base, int j, u32x4 (&f)[ML]) {
         const uint32_t p = base + (uint32_t)l32 * 128 + (uint32_t)(((2 * j + kq) ^ swz) << 4);
 #pragma unroll
-        for (int m = 0; m < ML; m++) asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(f[m]) : "v"(p), "n"(m * 4096) : "memory");
-    };
-    auto wait_a = [&](u32x4 (&f)[ML], auto n) {
-        constexpr int N = decltype(n)::value;
-#pragma unroll
-        for (int m = 0; m < ML; m++) asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(f[m]) : "n"(N));
+        for (int m = 0; m < ML; m++) f[m] = *(lds_u32x4*)(uintptr_t)(p + m * 4096);
     };
 
     pw_bset bs[4];
     auto stage = [&](int s, pw_bset& b) {
         /* the activations of stage s in LDS (every wave's own loads, then the barrier), this lane's weights */
-        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PW_NA + 2 * PW_NB) : "memory");
+        asm volatile("s_waitcnt vmcnt(%10)"
+                     : "+v"(b.q[0][0]), "+v"(b.q[0][1]), "+v"(b.q[0][2]), "+v"(b.q[0][3]), "+v"(b.q[1][0]), "+v"(b.q[1][1]),
+                       "+v"(b.q[1][2]), "+v"(b.q[1][3]), "+v"(b.d[0]), "+v"(b.d[1])
+                     : "n"(2 * NA + 2 * PW_NB)
+                     : "memory");
         wg_barrier();
-        issue_a(s + 2);
-        const uint32_t abase = lds0 + (uint32_t)(s % PF_A_STAGES) * PF_TILE_BYTES;
+        issue_a(s + 3);
+        const uint32_t abase = lds0 + (uint32_t)(s % PW_AST) * PF_TILE_BYTES;
         u32x4 fa[2][ML];
         read_a(abase, 0, fa[0]);
         float dd[2][2], nd[2][2];
@@ -543,13 +546,6 @@ __device__ __forceinline__ void pw_body(const prefill_args& a, int e, int m0, in
             u32x4 bw[2];
 #pragma unroll
             for (int t = 0; t < 2; t++) bw[t] = pw_widen8(b.q[t][j].x, b.q[t][j].y, dd[t][j >> 1], nd[t][j >> 1]);
-            if (j < 3) wait_a(fa[j & 1], std::integral_constant<int, ML>{});
-            else wait_a(fa[j & 1], std::integral_constant<int, 0>{});
-            if constexpr ((PF_DIAG_MODE & 1) != 0) {
-#pragma unroll
-                for (int m = 0; m < ML; m++) acc[m][0][0] += __builtin_bit_cast(float, fa[j & 1][m].x) + __builtin_bit_cast(float, bw[0].x ^ bw[1].y);
-                continue;
-            }
 #pragma unroll
             for (int m = 0; m < ML; m++)
 #pragma unroll
@@ -565,6 +561,7 @@ __device__ __forceinline__ void pw_body(const prefill_args& a, int e, int m0, in
     issue_b(0, bs[0]);
     issue_a(1);
     issue_b(1, bs[1]);
+    issue_a(2);
     issue_b(2, bs[2]);
     /* S is a multiple of 4 (launch_prefill_gemm): the body has no branch, so the compiler's waits for the
        weight registers count the loads of the straight line */
@@ -578,7 +575,15 @@ __device__ __forceinline__ void pw_body(const prefill_args& a, int e, int m0, in
         stage(s0 + 3, bs[3]);
         issue_b(s0 + 6, bs[2]);
     }
-    vm_wait<0>(); /* no load into LDS outlives the workgroup */
+    /* every load done: none into LDS outlives the workgroup, and the weight sets loaded past the end stay live
+       until here, so the compiler gives their registers to nothing else while their loads may still land */
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        asm volatile("s_waitcnt vmcnt(0)"
+                     : "+v"(bs[i].q[0][0]), "+v"(bs[i].q[0][1]), "+v"(bs[i].q[0][2]), "+v"(bs[i].q[0][3]), "+v"(bs[i].q[1][0]),
+                       "+v"(bs[i].q[1][1]), "+v"(bs[i].q[1][2]), "+v"(bs[i].q[1][3]), "+v"(bs[i].d[0]), "+v"(bs[i].d[1])
+                     :
+                     : "memory");
 
     /* accumulator r of a lane: row 8 (r / 4) + 4 kq + r % 4 of the 32 x 32 tile, column l32 */
 #pragma unroll
@@ -601,9 +606,11 @@ __device__ __forceinline__ void pw_body(const prefill_args& a, int e, int m0, in
         }
 }
 
+
 template <bool GU>
 __global__ __launch_bounds__(PW_THREADS, 1) void prefill_wgemm_kernel(prefill_args a) {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[PF_A_STAGES * PF_TILE_BYTES];
+
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[PW_AST * PF_TILE_BYTES];
     __shared__ int yrow[PF_BM];
     __shared__ float ywt[PF_BM];
     const int H = a.gate.cols, I = a.gate.rows;
