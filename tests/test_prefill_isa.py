@@ -104,3 +104,25 @@ def test_weight_registers_untouched_until_waited():
             assert not problems, problems[:5]
     finally:
         shutil.rmtree(tmp)
+
+
+def test_checker_catches_an_early_touch():
+    """The checker itself: a loop whose weight register is copied before its third stage-top wait is caught, the
+    same loop without the copy passes."""
+    good = [
+        "s_waitcnt vmcnt(0)",
+        ".LBB0_1:                                ; =>This Inner Loop Header: Depth=1",
+        "s_waitcnt vmcnt(36)",
+        "global_load_dwordx2 v[10:11], v[4:5], off",
+        "s_waitcnt vmcnt(36)",
+        "v_add_u32_e32 v1, v2, v3",
+        "s_waitcnt vmcnt(36)",
+        "s_waitcnt vmcnt(36)",
+        "v_add_u32_e32 v1, v10, v3",
+        "s_cbranch_scc0 .LBB0_1",
+    ]
+    assert check_kernel(good) == (1, [])
+    bad = list(good)
+    bad.insert(5, "v_mov_b32_e32 v20, v11")
+    loops, problems = check_kernel(bad)
+    assert loops == 1 and len(problems) == 1 and "v_mov_b32_e32 v20, v11" in problems[0]
