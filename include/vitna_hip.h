@@ -82,7 +82,8 @@ size_t vitna_cuda_moe_rows_max(const struct vitna_cuda_model* g);
 /* model_cuda.h:145-146 */
 bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, size_t layer, float* logits, float* next,
                                char* err, size_t err_len);
-/* model_cuda.h:157-158 */
+/* model_cuda.h:157-158. With an expert cache the experts go in waves through the slots, and guess (n x k) starts
+   the next layer's copies, as model_cuda.cu:5134-5386 does. */
 bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t layer, size_t n, const int32_t* ids, const float* weights, size_t k,
                                  const int32_t* guess, char* err, size_t err_len);
 /* model_cuda.h:161 */

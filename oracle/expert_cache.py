@@ -16,6 +16,15 @@ Reference: engine/src/model_cuda.cu
     are filled in request order; after the kernels, the first ceil(k / 2)
     places of the guess that the device lacks are filled while a slot is free;
     then every hold is released.
+  - vitna_cuda_moe_rows_experts :5134-5386, the same without the expert
+    stream: each wanted expert counts one use per row that wants it (the
+    halving when the count crosses a multiple of 65,536); the wanted experts,
+    in order of expert, go in waves of at most n_slots - k: a wave releases
+    the previous wave's holds, holds the experts present (hits, or in flight,
+    counted once per row) and fills those lacking k at a time, a miss for the
+    first row and hits for the others; after the last wave, of each row's
+    guess the first ceil(k / 2) experts, each once, are filled while a slot is
+    free; then every hold is released.
 """
 
 
@@ -106,6 +115,74 @@ class ExpertCache:
                     break
                 self.fill(s, place, True)
                 self.prefetched += 1
+        self.held = [False] * self.n_slots
+        return slot_of
+
+    def rows_experts(self, layer, ids, guess=None):
+        """One vitna_cuda_moe_rows_experts call over n rows (ids, guess: n lists of k); returns {expert: slot}."""
+        k = len(ids[0])
+        cnt = {}
+        for row in ids:
+            for e in row:
+                cnt[int(e)] = cnt.get(int(e), 0) + 1
+        want = sorted(cnt)
+        for x in want:
+            self.uses[layer * self.E + x] += cnt[x]
+            before = self.acquired
+            self.acquired += cnt[x]
+            if before // 65536 != self.acquired // 65536:
+                self.uses = [u // 2 for u in self.uses]
+        slot_of = {}
+        W = self.n_slots - k
+        for w0 in range(0, len(want), W):
+            self.held = [False] * self.n_slots
+            batch = []
+            wave = want[w0:w0 + W]
+            for i in range(len(wave) + 1):
+                if i < len(wave):
+                    x = wave[i]
+                    s = self.where[layer * self.E + x]
+                    if s >= 0:
+                        self.held[s] = True
+                        self.clock += 1
+                        self.last_use[s] = self.clock
+                        self.present += cnt[x]
+                        if self.guessed[s]:
+                            self.prefetch_used += 1
+                            self.guessed[s] = False
+                        slot_of[x] = s
+                        continue
+                    self.misses += 1
+                    self.present += cnt[x] - 1
+                    batch.append(x)
+                    if len(batch) < k:
+                        continue
+                for x in batch:
+                    s = self.free_slot()
+                    assert s >= 0
+                    self.fill(s, layer * self.E + x, False)
+                    slot_of[x] = s
+                batch = []
+        if guess is not None and (layer + 1) * self.E < self.n_places:
+            mark = set()
+            room = True
+            for row in guess:
+                if not room:
+                    break
+                for j in range((k + 1) // 2):
+                    x = int(row[j])
+                    if x in mark:
+                        continue
+                    mark.add(x)
+                    place = (layer + 1) * self.E + x
+                    if self.where[place] >= 0:
+                        continue
+                    s = self.free_slot()
+                    if s < 0:
+                        room = False
+                        break
+                    self.fill(s, place, True)
+                    self.prefetched += 1
         self.held = [False] * self.n_slots
         return slot_of
 

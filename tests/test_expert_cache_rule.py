@@ -79,3 +79,51 @@ def test_counters_add_up():
         if p >= 0:
             assert c.where[p] == s
     assert sum(1 for w in c.where if w >= 0) == sum(1 for p in c.place if p >= 0)
+
+
+def test_rows_worked_sequence():
+    # a pass of rows (model_cuda.cu:5134-5386): 2 layers of 8 experts, k = 2, 4 slots, so waves of 2 experts
+    c = ExpertCache(2, 8, 4, [100, 150])
+    # three rows want {0, 1}, {1, 3}, {5, 1}: experts 0, 1, 3, 5 in order; wave (0, 1) misses both, expert 1's other
+    # two rows are hits; the pair fills slots 0 and 1 (clock 1, 2); wave (3, 5) fills slots 2 and 3 (clock 3, 4)
+    slots = c.rows_experts(0, [[0, 1], [1, 3], [5, 1]], guess=[[2, 4], [2, 6], [7, 2]])
+    assert slots == {0: 0, 1: 1, 3: 2, 5: 3}
+    # the guess's upper half per row: 2 (then 2 again, once), 7. The last wave's slots 2, 3 are still held; of 0 and 1,
+    # slot 0's expert was used once, slot 1's three times: 2 goes to slot 0 (clock 5), 7 to slot 1 (clock 6)
+    assert c.where[:8] == [-1, -1, -1, 2, -1, 3, -1, -1]
+    assert c.where[8:] == [-1, -1, 0, -1, -1, -1, -1, 1]
+    assert c.counters() == dict(acquired=6, present=2, misses=4, prefetched=2, prefetch_used=0, copies=6,
+                                bytes_copied=4 * 100 + 2 * 150)
+    # layer 1, rows {2, 7}, {2, 4}: wave (2, 4): 2 present twice (a used guess, clock 7), 4 a miss; of the slots not
+    # held, 1 (expert 7 of layer 1), 2 and 3 were each used once, slot 2 least recently (clock 3): 4 goes there
+    # (clock 8). Wave (7): present in slot 1 (a used guess)
+    slots = c.rows_experts(1, [[2, 7], [2, 4]])
+    assert slots == {2: 0, 4: 2, 7: 1}
+    assert c.where[3] == -1 and c.where[8 + 4] == 2
+    assert c.counters() == dict(acquired=10, present=5, misses=5, prefetched=2, prefetch_used=2, copies=7,
+                                bytes_copied=4 * 100 + 3 * 150)
+
+
+def test_rows_halving_on_crossing():
+    # the counts are halved when a pass's requests cross a multiple of 65,536, not only when they land on one
+    c = ExpertCache(1, 4, 2, [1])
+    c.rows_experts(0, [[0]] * 65534)
+    assert c.uses[0] == 65534
+    c.rows_experts(0, [[1]] * 3)
+    assert c.acquired == 65537 and c.uses[0] == 32767 and c.uses[1] == 1
+
+
+def test_rows_match_single_rows():
+    # a pass of one row asks for what a step asks for: same slots, same counts as the step's rule
+    import random
+    rnd = random.Random(9)
+    a = ExpertCache(3, 16, 9, [7, 8, 9])
+    b = ExpertCache(3, 16, 9, [7, 8, 9])
+    for t in range(300):
+        for l in range(3):
+            ids = sorted(rnd.sample(range(16), 4))
+            guess = rnd.sample(range(16), 4) if l < 2 else None
+            sa = a.experts(l, ids, guess)
+            sb = b.rows_experts(l, [ids], [guess] if guess else None)
+            assert [sb[e] for e in ids] == sa
+    assert a.counters() == b.counters() and a.where == b.where

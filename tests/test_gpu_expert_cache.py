@@ -132,3 +132,78 @@ def test_cache_limits():
             dev.close()
     finally:
         model.free()
+
+
+@pytest.mark.parametrize("extra_slots", [0, 20])
+def test_cached_rows_match_resident(extra_slots):
+    """Passes of rows through the cache (vitna_cuda_moe_rows_experts, model_cuda.cu:5134-5386): at 2K slots the
+    rows' experts go in several waves, at 2K + 20 in one. Interleaved with single-token steps, which move experts
+    between slots under the rows' tiled copies. Bits as with every expert resident; slots and counts as the rule."""
+    say("expert cache rows, slots 2K +", extra_slots)
+    model = va.Model(va.shape(**SHAPE), 779)
+    cfg = model.cfg
+    kd = cfg.n_kv_heads * cfg.head_dim
+    kc = np.ctypeslib.as_array(model.m.k_cache, shape=(model.m.seqs, cfg.n_layers, model.m.ctx, kd))
+    vc = np.ctypeslib.as_array(model.m.v_cache, shape=(model.m.seqs, cfg.n_layers, model.m.ctx, kd))
+    kc[:] = va.normal(779, 101, kc.size).reshape(kc.shape)
+    vc[:] = va.normal(779, 102, vc.size).reshape(vc.shape)
+    K, E, L = cfg.n_experts_used, cfg.n_experts, cfg.n_layers
+    sb = slot_bytes(cfg)
+    n_slots = 2 * K + extra_slots
+    res = va.Device(model)
+    cac = va.Device(model, expert_cache_bytes=n_slots * sb)
+    try:
+        sim = ExpertCache(L, E, n_slots, [sb] * L)
+        pos0 = 50
+        fill_kv(model, res, pos0)
+        fill_kv(model, cac, pos0)
+        passes = [[(5, pos0, 0), (17, pos0, 1), (999, pos0 + 1, 1), (300, pos0 + 1, 0), (42, pos0 + 2, 0), (7, pos0 + 2, 1)],
+                  "step",
+                  [(11, pos0 + 3, 1), (12, pos0 + 4, 0), (13, pos0 + 4, 1)]]
+        for pi, rows in enumerate(passes):
+            if rows == "step":
+                # one token through the single-token path: it moves experts between slots
+                for l in range(L):
+                    outs = []
+                    for dev in (res, cac):
+                        lg, nx = dev.moe_route(0, 77, pos0 + 3, l, want_next=True)
+                        ch, order, w = oracle.route(lg, K, bool(cfg.renormalize))
+                        guess = oracle.route(nx, K, bool(cfg.renormalize))[0] if l + 1 < L else None
+                        dev.moe_experts(l, order, w, guess)
+                        outs.append(dev.residual())
+                        if dev is cac:
+                            sim.experts(l, order, guess)
+                    assert same_bits(outs[0], outs[1]), "step layer %d" % l
+                continue
+            n = len(rows)
+            for l in range(L):
+                outs = []
+                for dev in (res, cac):
+                    lg, nx = dev.rows_route(rows, l, want_next=True)
+                    ids, ws, gs = [], [], []
+                    for i in range(n):
+                        ch, order, w = oracle.route(lg[i], K, bool(cfg.renormalize))
+                        ids.append(order)
+                        ws.append(w)
+                        if l + 1 < L:
+                            gs.append(oracle.route(nx[i], K, bool(cfg.renormalize))[0])
+                    dev.rows_experts(l, np.array(ids), np.array(ws), np.array(gs) if gs else None)
+                    outs.append((np.array(ids), [dev.residual(i) for i in range(n)]))
+                    if dev is cac:
+                        sim.rows_experts(l, ids, gs if gs else None)
+                assert np.array_equal(outs[0][0], outs[1][0]), "pass %d layer %d choice" % (pi, l)
+                for i in range(n):
+                    assert same_bits(outs[0][1][i], outs[1][1][i]), "pass %d layer %d row %d residual" % (pi, l, i)
+            assert same_bits(res.rows_head(n), cac.rows_head(n)), "pass %d logits" % pi
+            where, cnt = cac.expert_cache_state()
+            ref = sim.counters()
+            say("  pass", pi, "device", cnt)
+            say("  pass", pi, "rule  ", ref)
+            assert where.tolist() == sim.where, "pass %d slots" % pi
+            assert cnt["acquired"] == ref["acquired"] and cnt["hits"] + cnt["in_flight"] == ref["present"]
+            for k in ("misses", "prefetched", "prefetch_used", "copies", "bytes_copied"):
+                assert cnt[k] == ref[k], (pi, k)
+    finally:
+        cac.close()
+        res.close()
+        model.free()

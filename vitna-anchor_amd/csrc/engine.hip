@@ -114,6 +114,11 @@ struct vitna_cuda_model {
     pf_bufs pf;
     /* the experts through a cache of slots, when expert_cache_bytes leaves fewer slots than experts */
     expert_cache ec;
+    /* a cached model's passes of rows: the grouped experts' tiled copy of each slot (gate, up, down areas, made on
+       the first pass), the place each slot's copy was made from (-1: none), and the tile strides it was made with */
+    uint8_t* st_area[3];
+    size_t st_stride[3];
+    std::vector<int64_t> st_place;
 };
 
 static bool fail(char* err, size_t len, const char* fmt, ...) {
@@ -340,7 +345,8 @@ static bool ensure_tiled(vitna_cuda_model* g, char* err, size_t err_len) {
         if (g->attention && !(make_tiled(g, &d.q, "q", err, err_len) && make_tiled(g, &d.k, "k", err, err_len) &&
                               make_tiled(g, &d.v, "v", err, err_len) && make_tiled(g, &d.o, "o", err, err_len)))
             return false;
-        if (gmma_fits(d.gate, d.up, d.down)) {
+        /* (the experts' copy only where they are resident: a cached model's views hold slots, not experts) */
+        if (!g->ec.on && gmma_fits(d.gate, d.up, d.down)) {
             qmat* sets[3] = {&d.gate, &d.up, &d.down};
             for (int i = 0; i < 3; i++) {
                 uint8_t* t;
@@ -533,8 +539,9 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
          dalloc(g, &g->rlogits, 2 * R * E * 4, "scratch", err, err_len) && dalloc(g, &g->rt, R * sizeof(route_out), "scratch", err, err_len) &&
          dalloc(g, &g->rt_layers, c->n_layers * sizeof(route_out), "scratch", err, err_len) &&
          dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len) &&
-         dalloc(g, &g->grp_count, E * sizeof(int), "scratch", err, err_len) &&
-         dalloc(g, &g->grp_pairs, E * R * sizeof(int), "scratch", err, err_len);
+         /* grouped by expert, or by slot when the experts pass through the cache */
+         dalloc(g, &g->grp_count, std::max<size_t>(E, g->ec.n_slots) * sizeof(int), "scratch", err, err_len) &&
+         dalloc(g, &g->grp_pairs, std::max<size_t>(E, g->ec.n_slots) * R * sizeof(int), "scratch", err, err_len);
     if (ok && g->attention) {
         ok = dalloc(g, &g->q, R * qd * 4, "scratch", err, err_len) && dalloc(g, &g->qp, R * qd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->k, R * kd * 4, "scratch", err, err_len) && dalloc(g, &g->v, R * kd * 4, "scratch", err, err_len) &&
@@ -1998,14 +2005,119 @@ extern "C" bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitn
     return true;
 }
 
+/* The slots' tiled copies for layer's expert shapes: the areas made on the first pass of rows (each the largest
+   any layer needs for every slot), and every copy forgotten when the layer's tile strides differ from those the
+   copies were made with (the copies sit at slot * stride). */
+static bool slot_tiles_for(vitna_cuda_model* g, const dlayer& d, char* err, size_t err_len) {
+    const expert_cache& c = g->ec;
+    if (!g->st_area[0]) {
+        for (int p = 0; p < 3; p++) {
+            size_t most = 0;
+            for (int l = 0; l < g->NL; l++) {
+                const qmat& m = p == 0 ? g->L[l].gate : p == 1 ? g->L[l].up : g->L[l].down;
+                most = std::max(most, gmma_tiled_bytes(m, 1));
+            }
+            if (!dalloc(g, &g->st_area[p], most * c.n_slots, "the expert slots' tiled copy", err, err_len)) return false;
+        }
+        g->st_place.assign(c.n_slots, -1);
+    }
+    const size_t st[3] = {gmma_tiled_bytes(d.gate, 1), gmma_tiled_bytes(d.up, 1), gmma_tiled_bytes(d.down, 1)};
+    if (st[0] != g->st_stride[0] || st[1] != g->st_stride[1] || st[2] != g->st_stride[2]) {
+        for (int p = 0; p < 3; p++) g->st_stride[p] = st[p];
+        std::fill(g->st_place.begin(), g->st_place.end(), -1);
+    }
+    return true;
+}
+
+/* A pass of rows through the expert cache (model_cuda.cu:5134-5386): the experts the rows want, in order of expert,
+   in waves of at most n_slots - k; a wave's slots held, those lacking copied in, their tiled copies made where the
+   slot's differs, then the grouped experts over the wave's (row, expert) pairs with the slots for experts. Each row's
+   K outputs are summed once after the last wave, in the order of ids, as a resident pass sums them. Then the guess. */
+static bool cached_rows_experts(vitna_cuda_model* g, int layer, int n, const int32_t* ids, const float* weights, int k,
+                                const int32_t* guess, char* err, size_t err_len) {
+    expert_cache& c = g->ec;
+    const dlayer& d = g->L[layer];
+    if (k != g->K) return fail(err, err_len, "%d experts given; the model routes to %d", k, g->K);
+    if (!gmma_fits(d.gate, d.up, d.down)) return fail(err, err_len, "layer %d's experts do not fit the grouped kernels", layer);
+    std::vector<int32_t> cnt(g->E, 0);
+    for (int t = 0; t < n; t++)
+        for (int i = 0; i < k; i++) {
+            const int32_t e = ids[(size_t)t * k + i];
+            if (e < 0 || e >= g->E) return fail(err, err_len, "expert %d is outside the layer's %d", e, g->E);
+            for (int j = 0; j < i; j++)
+                if (ids[(size_t)t * k + j] == e) return fail(err, err_len, "expert %d is named twice", e);
+            if (guess && (guess[(size_t)t * k + i] < 0 || guess[(size_t)t * k + i] >= g->E))
+                return fail(err, err_len, "guessed expert %d is outside the layer's %d", guess[(size_t)t * k + i], g->E);
+            cnt[e]++;
+        }
+    if (!slot_tiles_for(g, d, err, err_len)) return false;
+    std::vector<int32_t> want, slot_of(g->E, -1);
+    for (int x = 0; x < g->E; x++)
+        if (cnt[x]) want.push_back(x);
+    ec_rows_count(c, layer, cnt.data());
+    gmma_args m;
+    m.gate = d.gate; m.up = d.up; m.down = d.down;
+    m.gate.tiled = g->st_area[0]; m.up.tiled = g->st_area[1]; m.down.tiled = g->st_area[2];
+    m.xs = g->gm_xs; m.xsum = g->gm_xsum; m.as = g->gm_as; m.asum = g->gm_asum; m.rt = g->rt; m.count = g->grp_count; m.pairs = g->grp_pairs;
+    m.E = c.n_slots; m.K = g->K; m.cap = ROWS_MAX; m.ypart = g->ypart;
+    hipError_t e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
+    bool ok = check_launch(g, e, "the rows' split", err, err_len);
+    const int W = c.n_slots - c.K;
+    std::vector<uint8_t> in_wave(g->E, 0);
+    for (size_t w0 = 0; ok && w0 < want.size(); w0 += W) {
+        const int nw = (int)std::min<size_t>(W, want.size() - w0);
+        ok = ec_rows_wave(c, layer, want.data() + w0, nw, cnt.data(), g->stream, slot_of.data(), err, err_len);
+        std::fill(in_wave.begin(), in_wave.end(), 0);
+        for (int i = 0; ok && i < nw; i++) {
+            const int x = want[w0 + i], s = slot_of[x];
+            in_wave[x] = 1;
+            const ec_slot& sl = c.slots[s];
+            if (sl.filling && hipStreamWaitEvent(g->stream, sl.filled, 0) != hipSuccess) ok = fail(err, err_len, "waiting for an expert's copy");
+            if (!ok || g->st_place[s] == sl.place) continue;
+            /* the slot's tiled copy, on the compute stream: after the kernels that read the copy it replaces */
+            const qmat* src[3] = {&d.gate, &d.up, &d.down};
+            for (int p = 0; ok && p < 3; p++) {
+                qmat one = *src[p];
+                for (int q = 0; q < 4; q++)
+                    if (one.p[q]) one.p[q] += (size_t)s * one.estride[q];
+                e = launch_gmma_tile(one, 1, g->st_area[p] + (size_t)s * g->st_stride[p], g->stream);
+                ok = check_launch(g, e, "tiling an expert slot", err, err_len);
+            }
+            if (ok) g->st_place[s] = sl.place;
+        }
+        if (!ok) break;
+        /* the wave's routing: each pair's slot, or -1 for the experts of other waves */
+        if (hipEventSynchronize(g->rt_copied) != hipSuccess) { ok = fail(err, err_len, "waiting for the previous routing copy"); break; }
+        route_out* ro = g->rt_host;
+        for (int t = 0; t < n; t++) {
+            memset(&ro[t], 0, sizeof(route_out));
+            for (int i = 0; i < k; i++) {
+                const int32_t x = ids[(size_t)t * k + i];
+                ro[t].ids[i] = in_wave[x] ? slot_of[x] : -1;
+                ro[t].weights[i] = ro[t].cw[i] = weights[(size_t)t * k + i];
+                ro[t].chosen[i] = ro[t].ids[i];
+            }
+        }
+        e = hipMemcpyAsync(g->rt, ro, (size_t)n * sizeof(route_out), hipMemcpyHostToDevice, g->stream);
+        if (e == hipSuccess) e = hipEventRecord(g->rt_copied, g->stream);
+        if (e == hipSuccess) e = launch_group(g->rt, n, c.n_slots, g->K, ROWS_MAX, g->grp_count, g->grp_pairs, g->stream);
+        if (e == hipSuccess) e = launch_gmma_in(m, g->stream);
+        if (e == hipSuccess) e = launch_gmma_down(m, g->stream);
+        ok = check_launch(g, e, "the rows' experts", err, err_len);
+    }
+    if (ok) ok = check_launch(g, launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream), "the rows' sums", err, err_len);
+    /* the holds are released whatever happened; the guess only after the kernels */
+    const bool fin = ec_rows_finish(c, layer, ok ? guess : nullptr, n, k, err, err_len);
+    return ok && fin;
+}
+
 extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t layer, size_t n, const int32_t* ids, const float* weights,
                                             size_t k, const int32_t* guess, char* err, size_t err_len) {
-    if (g && !experts_resident(g, err, err_len)) return false;
-    (void)guess;
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (!ensure_tiled(g, err, err_len)) return false;
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
+    if (g->ec.on) return cached_rows_experts(g, (int)layer, (int)n, ids, weights, (int)k, guess, err, err_len);
     if (!put_routing(g, n, ids, weights, k, err, err_len)) return false;
     return check_launch(g, enqueue_rows_experts(g, (int)layer, (int)n, false), "the rows' experts", err, err_len);
 }

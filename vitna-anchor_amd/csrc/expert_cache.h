@@ -6,7 +6,8 @@
  *
  * Reference counterpart: expert_cache_t (engine/src/model_cuda.cu:249-290),
  * create_experts (:3633), free_slot (:4334), fill (:4355), and the cache's part
- * of vitna_cuda_moe_experts (:4757-4913) and vitna_cuda_moe_report (:4929).
+ * of vitna_cuda_moe_experts (:4757-4913), vitna_cuda_moe_rows_experts (:5134-5386)
+ * and vitna_cuda_moe_report (:4929).
  *
  * The rule the reference keeps:
  *   - a place is (layer, expert); each request of a place counts one use, and
@@ -78,6 +79,18 @@ bool ec_acquire(expert_cache& c, int layer, const int32_t* ids, int k, hipStream
 bool ec_wait(expert_cache& c, const int32_t* slot_of, int k, hipStream_t compute, char* err, size_t err_len);
 /* After the layer's kernels are queued on compute: the guess's copies, then every hold released. */
 bool ec_finish(expert_cache& c, int layer, const int32_t* guess, int k, char* err, size_t err_len);
+
+/* A pass of rows (model_cuda.cu:5134-5386). ec_rows_count: every row's request of layer's expert x counts a use,
+   cnt[x] of them; the halving of every count when the requests cross a multiple of 65,536. */
+void ec_rows_count(expert_cache& c, int layer, const int32_t* cnt);
+/* One wave of the pass: the experts xs[0..nx) (in order of expert, nx at most n_slots - k), each wanted by cnt[x]
+   rows. The holds of the previous wave are released (first: none), copies are ordered after every kernel queued
+   on compute so far, the experts present are held, those lacking copied in k at a time; slot_of[x] set. */
+bool ec_rows_wave(expert_cache& c, int layer, const int32_t* xs, int nx, const int32_t* cnt, hipStream_t compute,
+                  int32_t* slot_of, char* err, size_t err_len);
+/* After the pass's kernels: of each row's guess (n x k, the next layer's experts by rank) the upper half the
+   device lacks, each expert once, copied while slots are free; then every hold released. */
+bool ec_rows_finish(expert_cache& c, int layer, const int32_t* guess, int n, int k, char* err, size_t err_len);
 
 /* The reference's summary line (model_cuda.cu:4946-4953). */
 void ec_report(const expert_cache& c, char* buf, size_t len);

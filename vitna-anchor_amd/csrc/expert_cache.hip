@@ -260,6 +260,91 @@ bool ec_finish(expert_cache& c, int layer, const int32_t* guess, int k, char* er
     return ok;
 }
 
+void ec_rows_count(expert_cache& c, int layer, const int32_t* cnt) {
+    for (int x = 0; x < c.E; x++) {
+        if (!cnt[x]) continue;
+        c.uses[(size_t)layer * c.E + x] += (uint32_t)cnt[x];
+        const uint64_t before = c.acquired;
+        c.acquired += (uint64_t)cnt[x];
+        if (before / 65536 != c.acquired / 65536)
+            for (uint32_t& u : c.uses) u /= 2;
+    }
+}
+
+bool ec_rows_wave(expert_cache& c, int layer, const int32_t* xs, int nx, const int32_t* cnt, hipStream_t compute,
+                  int32_t* slot_of, char* err, size_t err_len) {
+    if (nx < 1 || nx > c.n_slots - c.K) return ec_fail(err, err_len, "internal: a wave of %d experts", nx);
+    /* the previous wave's slots are free to give up: its kernels are queued before the copies that may replace them */
+    for (ec_slot& x : c.slots) x.held = false;
+    EC_TRY(hipEventRecord(c.queued, compute), "ordering the expert copies");
+    EC_TRY(hipStreamWaitEvent(c.copy, c.queued, 0), "ordering the expert copies");
+    int batch[ROUTE_K_MAX], nb = 0;
+    for (int i = 0; i <= nx; i++) {
+        if (i < nx) {
+            const int x = xs[i];
+            const size_t place = (size_t)layer * c.E + x;
+            const int s = c.where[place];
+            if (s >= 0) {
+                ec_slot& sl = c.slots[s];
+                sl.held = true;
+                sl.last_use = ++c.clock;
+                if (sl.filling) {
+                    const hipError_t q = hipEventQuery(sl.filled);
+                    if (q == hipSuccess) sl.filling = false;
+                    else if (q != hipErrorNotReady) return ec_fail(err, err_len, "an expert copy failed: %s", hipGetErrorString(q));
+                }
+                if (sl.filling) c.in_flight += (uint64_t)cnt[x];
+                else c.hits += (uint64_t)cnt[x];
+                if (sl.guessed) {
+                    c.prefetch_used++;
+                    sl.guessed = false;
+                }
+                slot_of[x] = s;
+                continue;
+            }
+            /* copied once for all its rows: the first row's request a miss, the others' hits */
+            c.misses++;
+            c.hits += (uint64_t)cnt[x] - 1;
+            batch[nb++] = x;
+            if (nb < c.K) continue;
+        }
+        for (int j = 0; j < nb; j++) {
+            const int s = free_slot(c); /* at most n_slots - k are held */
+            if (s < 0) return ec_fail(err, err_len, "internal: no expert slot free");
+            if (!fill(c, s, (size_t)layer * c.E + batch[j], false, err, err_len)) return false;
+            slot_of[batch[j]] = s;
+        }
+        nb = 0;
+    }
+    return true;
+}
+
+bool ec_rows_finish(expert_cache& c, int layer, const int32_t* guess, int n, int k, char* err, size_t err_len) {
+    bool ok = true;
+    if (guess && layer + 1 < c.n_layers) {
+        std::vector<uint8_t> mark(c.E, 0);
+        bool room = true;
+        for (int t = 0; ok && room && t < n; t++) {
+            for (int j = 0; ok && j < (k + 1) / 2; j++) {
+                const int x = guess[(size_t)t * k + j];
+                if (mark[x]) continue;
+                mark[x] = 1;
+                const size_t place = (size_t)(layer + 1) * c.E + x;
+                if (c.where[place] >= 0) continue;
+                const int s = free_slot(c);
+                if (s < 0) {
+                    room = false;
+                    break;
+                }
+                ok = fill(c, s, place, true, err, err_len);
+                c.prefetched++;
+            }
+        }
+    }
+    for (ec_slot& x : c.slots) x.held = false;
+    return ok;
+}
+
 void ec_report(const expert_cache& c, char* buf, size_t len) {
     snprintf(buf, len,
              "experts on the GPU: %d slots, %.0f MiB, copied from %s, %s. %llu acquired: %llu already on the GPU, %llu still being copied "

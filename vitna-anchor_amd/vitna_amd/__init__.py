@@ -482,11 +482,17 @@ class Device:
                                                     fptr(nx) if want_next else None, self.err, 512))
         return (lg, nx) if want_next else lg
 
-    def rows_experts(self, layer, ids, weights):
+    def rows_experts(self, layer, ids, weights, guess=None):
         ids = np.ascontiguousarray(ids, np.int32)
         w = np.ascontiguousarray(weights, np.float32)
         n, k = ids.shape
-        self._ok(self.lib.vitna_cuda_moe_rows_experts(self.g, layer, n, _i32(ids), fptr(w), k, None, self.err, 512))
+        g = None
+        if guess is not None:
+            g = np.ascontiguousarray(guess, np.int32)
+            if g.shape != ids.shape:
+                raise ValueError("a guess of %d experts for each of %d rows" % (k, n))
+        self._ok(self.lib.vitna_cuda_moe_rows_experts(self.g, layer, n, _i32(ids), fptr(w), k,
+                                                      _i32(g) if g is not None else None, self.err, 512))
 
     def rows_head(self, n):
         V = self.model.cfg.vocab
