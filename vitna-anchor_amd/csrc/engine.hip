@@ -1931,10 +1931,10 @@ static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n, bo
     /* every expert set check_shapes accepts (quantized, widths multiples of 256) fits the matrix-core kernels */
     if (!gmma_fits(d.gate, d.up, d.down)) return hipErrorInvalidValue;
     if (!split_done) e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
-    gmma_args m;
+    gmma_args m{};
     m.gate = d.gate; m.up = d.up; m.down = d.down;
     m.xs = g->gm_xs; m.xsum = g->gm_xsum; m.as = g->gm_as; m.asum = g->gm_asum; m.rt = g->rt; m.count = g->grp_count; m.pairs = g->grp_pairs;
-    m.E = g->E; m.K = g->K; m.cap = ROWS_MAX; m.ypart = g->ypart;
+    m.E = g->E; m.K = g->K; m.cap = ROWS_MAX; m.n = n; m.ypart = g->ypart;
     if (e == hipSuccess) e = launch_gmma_in(m, g->stream);
     if (e == hipSuccess) e = launch_gmma_down(m, g->stream);
     if (e == hipSuccess && !defer_sum) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
@@ -2055,11 +2055,11 @@ static bool cached_rows_experts(vitna_cuda_model* g, int layer, int n, const int
     for (int x = 0; x < g->E; x++)
         if (cnt[x]) want.push_back(x);
     ec_rows_count(c, layer, cnt.data());
-    gmma_args m;
+    gmma_args m{};
     m.gate = d.gate; m.up = d.up; m.down = d.down;
     m.gate.tiled = g->st_area[0]; m.up.tiled = g->st_area[1]; m.down.tiled = g->st_area[2];
     m.xs = g->gm_xs; m.xsum = g->gm_xsum; m.as = g->gm_as; m.asum = g->gm_asum; m.rt = g->rt; m.count = g->grp_count; m.pairs = g->grp_pairs;
-    m.E = c.n_slots; m.K = g->K; m.cap = ROWS_MAX; m.ypart = g->ypart;
+    m.E = c.n_slots; m.K = g->K; m.cap = ROWS_MAX; m.n = n; m.ypart = g->ypart;
     hipError_t e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
     bool ok = check_launch(g, e, "the rows' split", err, err_len);
     const int W = c.n_slots - c.K;

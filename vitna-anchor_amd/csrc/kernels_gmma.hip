@@ -416,17 +416,18 @@ __device__ __forceinline__ int pick(gm_int4 v, int i) { return i == 0 ? v.x : i 
    runs of GO rows. A block: KS waves over one group of 64 weight rows of one expert, wave w taking the w-th
    of KS contiguous ranges of the columns; wave 0 writes. */
 template <int DT, int GO, int KS>
-__global__ __launch_bounds__(64 * KS, 8 / KS) void gmma_in_kernel(gmma_args a, int wpe) {
+__global__ __launch_bounds__(64 * KS, 8 / KS) void gmma_in_kernel(gmma_args a, int wpe, int ts_n) {
     __shared__ float red[KS > 1 ? KS * 2 * 4 * 64 : 1];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int e = blockIdx.x / wpe, rw = blockIdx.x - e * wpe;
+    const int per = a.E * wpe, ts = blockIdx.x / per, eb = blockIdx.x - ts * per;
+    const int e = eb / wpe, rw = eb - e * wpe;
     const int c = sload(a.count + e);
-    if (c == 0) return;
+    if (c <= ts * GM_TT) return;
     const int I = a.gate.rows, H = a.gate.cols;
     constexpr int GI = ggran<DT>::g;
     const int n = rw * 64 + lane;
     const int* pr = a.pairs + (size_t)e * a.cap;
-    for (int t0 = 0; t0 < c; t0 += GM_TT) {
+    for (int t0 = ts * GM_TT; t0 < c; t0 += ts_n * GM_TT) {
         const int nt = min(GM_TT, c - t0);
         const gm_int4 pv = tile_pairs(pr, t0, nt);
         const u32x4* arow = reinterpret_cast<const u32x4*>(a.xs + (size_t)(pick(pv, lane & 3) / ROUTE_K_MAX) * 2 * H);
@@ -457,17 +458,18 @@ __global__ __launch_bounds__(64 * KS, 8 / KS) void gmma_in_kernel(gmma_args a, i
 
 /* ypart[row * K + slot][n] = w_slot * (down_e[n] . act[row * K + slot]) */
 template <int DT, int KS>
-__global__ __launch_bounds__(64 * KS, 8 / KS) void gmma_down_kernel(gmma_args a, int wpe) {
+__global__ __launch_bounds__(64 * KS, 8 / KS) void gmma_down_kernel(gmma_args a, int wpe, int ts_n) {
     __shared__ float red[KS > 1 ? KS * 1 * 4 * 64 : 1];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int e = blockIdx.x / wpe, rw = blockIdx.x - e * wpe;
+    const int per = a.E * wpe, ts = blockIdx.x / per, eb = blockIdx.x - ts * per;
+    const int e = eb / wpe, rw = eb - e * wpe;
     const int c = sload(a.count + e);
-    if (c == 0) return;
+    if (c <= ts * GM_TT) return;
     const int H = a.down.rows, I = a.down.cols;
     constexpr int GI = ggran<DT>::g;
     const int n = rw * 64 + lane;
     const int* pr = a.pairs + (size_t)e * a.cap;
-    for (int t0 = 0; t0 < c; t0 += GM_TT) {
+    for (int t0 = ts * GM_TT; t0 < c; t0 += ts_n * GM_TT) {
         const int nt = min(GM_TT, c - t0);
         const gm_int4 pv = tile_pairs(pr, t0, nt);
         const int pl = pick(pv, lane & 3);
@@ -516,16 +518,28 @@ hipError_t launch_gmma_split(const float* x, int n, int K, int xstride, int gran
     return hipGetLastError();
 }
 
+/* Blocks a (expert, row group): the expert's token tiles t, t + ts, ... go to block t of ts, so that an expert
+   with more tiles than the average runs them side by side instead of one after another. Blocks past an expert's
+   tiles return at once; they are dispatched after every first tile. Measured on 32 rows of top-8 over 128
+   experts: gate/up gains from splitting even at two pairs an expert on average (its stragglers of five to eight
+   pairs), down only when the experts are crowded (at two pairs an expert its extra blocks cost more). */
+static int gmma_tile_split(const gmma_args& a, bool down) {
+    const int pairs = a.n * a.K, tiles = (pairs + a.E * GM_TT - 1) / (a.E * GM_TT); /* tiles an expert on average */
+    if (a.n <= GM_TT) return 1;
+    if (down) return tiles <= 1 ? 1 : tiles < 4 ? tiles : 4;
+    return tiles <= 1 ? 2 : 4;
+}
+
 hipError_t launch_gmma_in(const gmma_args& a, hipStream_t s) {
-    if (!gmma_fits(a.gate, a.up, a.down) || !a.gate.tiled || !a.up.tiled || a.K < 1 || a.K > ROUTE_K_MAX || a.cap % 4)
+    if (!gmma_fits(a.gate, a.up, a.down) || !a.gate.tiled || !a.up.tiled || a.K < 1 || a.K > ROUTE_K_MAX || a.cap % 4 || a.n < 1)
         return hipErrorInvalidValue;
     /* KS waves split each row group's columns: enough waves to fill the SIMDs */
-    const int wpe = a.gate.rows / 64, blocks = a.E * wpe;
+    const int wpe = a.gate.rows / 64, ts = gmma_tile_split(a, false), blocks = a.E * wpe * ts;
     const bool g16 = gmma_gran(a.down.dtype) == 16;
 #define GI(D)                                                                                      \
     case D:                                                                                        \
-        if (g16) gmma_in_kernel<D, 16, GIN_KS><<<blocks, 64 * GIN_KS, 0, s>>>(a, wpe);             \
-        else gmma_in_kernel<D, 32, GIN_KS><<<blocks, 64 * GIN_KS, 0, s>>>(a, wpe);                 \
+        if (g16) gmma_in_kernel<D, 16, GIN_KS><<<blocks, 64 * GIN_KS, 0, s>>>(a, wpe, ts);             \
+        else gmma_in_kernel<D, 32, GIN_KS><<<blocks, 64 * GIN_KS, 0, s>>>(a, wpe, ts);                 \
         return hipGetLastError();
     switch (a.gate.dtype) { GI(VITNA_DTYPE_Q4_K) GI(VITNA_DTYPE_Q6_K) GI(VITNA_DTYPE_Q8_0) }
 #undef GI
@@ -533,12 +547,13 @@ hipError_t launch_gmma_in(const gmma_args& a, hipStream_t s) {
 }
 
 hipError_t launch_gmma_down(const gmma_args& a, hipStream_t s) {
-    if (!gmma_fits(a.gate, a.up, a.down) || !a.down.tiled || a.K < 1 || a.K > ROUTE_K_MAX || a.cap % 4) return hipErrorInvalidValue;
-    const int wpe = a.down.rows / 64, blocks = a.E * wpe;
+    if (!gmma_fits(a.gate, a.up, a.down) || !a.down.tiled || a.K < 1 || a.K > ROUTE_K_MAX || a.cap % 4 || a.n < 1)
+        return hipErrorInvalidValue;
+    const int wpe = a.down.rows / 64, ts = gmma_tile_split(a, true), blocks = a.E * wpe * ts;
     switch (a.down.dtype) {
-    case VITNA_DTYPE_Q4_K: gmma_down_kernel<VITNA_DTYPE_Q4_K, GDN_KS><<<blocks, 64 * GDN_KS, 0, s>>>(a, wpe); return hipGetLastError();
-    case VITNA_DTYPE_Q6_K: gmma_down_kernel<VITNA_DTYPE_Q6_K, GDN_KS><<<blocks, 64 * GDN_KS, 0, s>>>(a, wpe); return hipGetLastError();
-    case VITNA_DTYPE_Q8_0: gmma_down_kernel<VITNA_DTYPE_Q8_0, GDN_KS><<<blocks, 64 * GDN_KS, 0, s>>>(a, wpe); return hipGetLastError();
+    case VITNA_DTYPE_Q4_K: gmma_down_kernel<VITNA_DTYPE_Q4_K, GDN_KS><<<blocks, 64 * GDN_KS, 0, s>>>(a, wpe, ts); return hipGetLastError();
+    case VITNA_DTYPE_Q6_K: gmma_down_kernel<VITNA_DTYPE_Q6_K, GDN_KS><<<blocks, 64 * GDN_KS, 0, s>>>(a, wpe, ts); return hipGetLastError();
+    case VITNA_DTYPE_Q8_0: gmma_down_kernel<VITNA_DTYPE_Q8_0, GDN_KS><<<blocks, 64 * GDN_KS, 0, s>>>(a, wpe, ts); return hipGetLastError();
     }
     return hipErrorInvalidValue;
 }

@@ -243,6 +243,7 @@ struct gmma_args {
     const int* count;      /* [E] */
     const int* pairs;      /* [E][cap] */
     int E, K, cap;
+    int n;                 /* rows of the pass */
     float* ypart;          /* [n][K][H] */
 };
 /* The grouped experts' tiled copy of an expert set (kernels_gmma.hip): its size, and making it from the planes. */
