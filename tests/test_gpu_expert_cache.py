@@ -29,15 +29,17 @@ def same_bits(a, b):
     return np.array_equal(np.ascontiguousarray(a, np.float32).view(np.uint32), np.ascontiguousarray(b, np.float32).view(np.uint32))
 
 
-def slot_bytes(cfg):
-    """A slot: gate, up and down, each matrix's planes 256-byte aligned (Q4_K: 128 + 16 bytes a block, Q6_K: 128 +
-    64 + 16 + 2)."""
+def slot_bytes(cfg, spec=SHAPE):
+    """A slot: gate, up and down, each matrix's planes 256-byte aligned (Q4_K: 128 + 16 bytes a 256-column block,
+    Q6_K: 128 + 64 + 16 + 2, Q8_0: 32 + 2 a 32-column block)."""
     a = lambda x: (x + 255) // 256 * 256
-    nb_gu = cfg.hidden // 256
-    gu = a(cfg.intermediate * nb_gu * 128) + a(cfg.intermediate * nb_gu * 16)
-    nb_d = cfg.intermediate // 256
-    d = sum(a(cfg.hidden * nb_d * b) for b in (128, 64, 16, 2))
-    return 2 * gu + d
+    planes = {va.Q4_K: (256, (128, 16)), va.Q6_K: (256, (128, 64, 16, 2)), va.Q8_0: (32, (32, 2))}
+
+    def mat(dt, rows, cols):
+        width, fields = planes[dt]
+        return sum(a(rows * (cols // width) * b) for b in fields)
+    gu = mat(spec["dt_gate_up"], cfg.intermediate, cfg.hidden)
+    return 2 * gu + mat(spec["dt_down"], cfg.hidden, cfg.intermediate)
 
 
 def fill_kv(model, dev, pos):
@@ -134,13 +136,14 @@ def test_cache_limits():
         model.free()
 
 
-@pytest.mark.parametrize("extra_slots", [0, 20])
-def test_cached_rows_match_resident(extra_slots):
+@pytest.mark.parametrize("extra_slots,q8", [(0, False), (20, False), (0, True)])
+def test_cached_rows_match_resident(extra_slots, q8):
     """Passes of rows through the cache (vitna_cuda_moe_rows_experts, model_cuda.cu:5134-5386): at 2K slots the
     rows' experts go in several waves, at 2K + 20 in one. Interleaved with single-token steps, which move experts
     between slots under the rows' tiled copies. Bits as with every expert resident; slots and counts as the rule."""
-    say("expert cache rows, slots 2K +", extra_slots)
-    model = va.Model(va.shape(**SHAPE), 779)
+    say("expert cache rows, slots 2K +", extra_slots, "Q8_0 experts" if q8 else "")
+    spec = dict(SHAPE, dt_gate_up=va.Q8_0, dt_down=va.Q8_0) if q8 else SHAPE
+    model = va.Model(va.shape(**spec), 779)
     cfg = model.cfg
     kd = cfg.n_kv_heads * cfg.head_dim
     kc = np.ctypeslib.as_array(model.m.k_cache, shape=(model.m.seqs, cfg.n_layers, model.m.ctx, kd))
@@ -148,7 +151,7 @@ def test_cached_rows_match_resident(extra_slots):
     kc[:] = va.normal(779, 101, kc.size).reshape(kc.shape)
     vc[:] = va.normal(779, 102, vc.size).reshape(vc.shape)
     K, E, L = cfg.n_experts_used, cfg.n_experts, cfg.n_layers
-    sb = slot_bytes(cfg)
+    sb = slot_bytes(cfg, spec)
     n_slots = 2 * K + extra_slots
     res = va.Device(model)
     cac = va.Device(model, expert_cache_bytes=n_slots * sb)
