@@ -130,6 +130,31 @@ def test_cache_limits():
         try:
             with pytest.raises(va.VitnaError, match="cache of 16 slots"):
                 dev.step(0, 3, 0)
+            rows = [(3, 0, 0), (4, 0, 1)]
+            with pytest.raises(va.VitnaError, match="cache of 16 slots"):
+                dev.rows_step(rows)
+            # a pass of rows through the cache checks its requests before it touches the cache
+            dev.rows_route(rows, 0)
+            K = cfg.n_experts_used
+            ok = np.tile(np.arange(K, dtype=np.int32), (2, 1))
+            w = np.full((2, K), 1.0 / K, np.float32)
+            twice = ok.copy()
+            twice[1, 1] = twice[1, 0]
+            with pytest.raises(va.VitnaError, match="named twice"):
+                dev.rows_experts(0, twice, w)
+            outside = ok.copy()
+            outside[0, 3] = cfg.n_experts
+            with pytest.raises(va.VitnaError, match="outside"):
+                dev.rows_experts(0, outside, w)
+            with pytest.raises(va.VitnaError, match="outside"):
+                dev.rows_experts(0, ok, w, guess=outside)
+            with pytest.raises(va.VitnaError, match="routes to"):
+                dev.rows_experts(0, ok[:, :K - 1], w[:, :K - 1])
+            _, cnt = dev.expert_cache_state()
+            assert cnt["acquired"] == 0 and cnt["copies"] == 0
+            dev.rows_experts(0, ok, w, guess=ok)
+            _, cnt = dev.expert_cache_state()
+            assert cnt["acquired"] == 2 * K and cnt["misses"] == K and cnt["prefetched"] == (K + 1) // 2
         finally:
             dev.close()
     finally:
