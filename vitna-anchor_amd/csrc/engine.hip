@@ -1508,8 +1508,13 @@ static hipError_t enqueue_prefill(vitna_cuda_model* g, int layer, int n, float* 
     hipError_t e = hipSuccess;
     auto mark = [&](int i) { if (ev && e == hipSuccess) e = hipEventRecord(ev[i], s); };
     mark(0);
-    if (e == hipSuccess) e = launch_prefill_norm(x, d.mlp_norm, b.xn, b.xb, n, g->H, g->eps, s);
-    if (e == hipSuccess) e = launch_prefill_router(b.xn, d.router, b.logits, n, g->E, g->H, s);
+    if (e == hipSuccess) {
+        e = launch_prefill_norm_router(x, d.mlp_norm, d.router, b.logits, b.xb, n, g->E, g->H, g->eps, s);
+        if (e == hipErrorNotSupported) {
+            e = launch_prefill_norm(x, d.mlp_norm, b.xn, b.xb, n, g->H, g->eps, s);
+            if (e == hipSuccess) e = launch_prefill_router(b.xn, d.router, b.logits, n, g->E, g->H, s);
+        }
+    }
     mark(1);
     if (e == hipSuccess) e = launch_topk(b.logits, n, g->E, g->K, g->renorm, b.rt, s);
     if (e == hipSuccess) e = launch_group(b.rt, n, g->E, g->K, n, b.count, b.pairs, s);

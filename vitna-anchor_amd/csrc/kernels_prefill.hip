@@ -13,29 +13,28 @@
  * row chooses the experts the CPU chooses, with the same weights.
  *
  * The experts: each Q8_0 weight q * d (exact in fp32) is rounded to bf16 once a
- * workgroup, into a bf16 stage in LDS; the normed rows and the SwiGLU output are
- * rounded to bf16 too; products accumulate in fp32 on the matrix cores.
+ * workgroup (by the one wave that uses it, in registers, or into a bf16 stage in
+ * LDS in the two-phase kernel); the normed rows and the SwiGLU output are rounded
+ * to bf16 too; products accumulate in fp32 on the matrix cores.
  *
  * Pipeline, one stream:
- *   prefill_norm_kernel     exact RMSNorm; fp32 rows for the router, bf16 for the GEMM
- *   prefill_router_kernel   exact router logits, 8 rows x 8 experts a thread
- *   topk_kernel             the routing rule on every row (kernels_decode.hip)
- *   group_kernel            (row, slot) pairs of each expert in row order (kernels_rows.hip)
- *   prefill_plan_kernel     pair offsets of each expert; the list of 256-pair tiles
- *   prefill_gemm_kernel<1>  act = silu(X_e G_e^T) * (X_e U_e^T), bf16, pairs in expert order
- *   prefill_gemm_kernel<0>  ypart[row * K + slot] = w * (act_e D_e^T)
- *   reduce_rows_kernel      x += the K parts of a row in slot order (kernels_rows.hip)
+ *   prefill_norm_router_kernel  exact RMSNorm and router logits in one pass (hidden up to 2048; wider rows
+ *                               take prefill_norm_kernel, then prefill_router_kernel); bf16 rows for the GEMM
+ *   topk_kernel                 the routing rule on every row (kernels_decode.hip)
+ *   group_kernel                (row, slot) pairs of each expert in row order (kernels_rows.hip)
+ *   prefill_plan_kernel         pair offsets of each expert; the list of 256-pair tiles
+ *   prefill_wgemm_kernel<1>     act = silu(X_e G_e^T) * (X_e U_e^T), bf16, pairs in expert order
+ *   prefill_wgemm_kernel<0>     ypart[row * K + slot] = w * (act_e D_e^T), bf16
+ *   prefill_sum_kernel          x += the K parts of a row in slot order, summed in fp32
  *
- * GEMM tiling: a 512-thread workgroup owns 256 pairs x 256 weight rows (for
- * gate/up: 128 gate rows and the 128 up rows of the same columns, so SwiGLU is
- * local to a lane). Each wave owns 64 x 128 as 2 x 4 tiles of
- * v_mfma_f32_32x32x16_bf16. K advances 64 a stage (two Q8_0 blocks); the
- * activations come through a three-stage LDS ring filled by global-to-LDS
- * loads two stages ahead. Work items (tile, column block) are split into eight
- * contiguous ranges, one per XCD (workgroup i runs on XCD i mod 8), so the
- * column blocks of one tile and the tiles of one expert share an L2. A stage
- * has two phases: waves 0-3 run their MFMAs while waves 4-7 dequantize and
- * load, then the other way round.
+ * The per-wave GEMM (prefill_wgemm_kernel, below) reads the experts' tiled copy; an expert set without it, or
+ * with widths that are not multiples of 256, takes the two-phase prefill_gemm_kernel: a 512-thread workgroup
+ * owns 256 pairs x 256 weight rows (for gate/up: 128 gate rows and the 128 up rows of the same columns, so
+ * SwiGLU is local to a lane), each wave 64 x 128 as 2 x 4 tiles of v_mfma_f32_32x32x16_bf16, K advancing 64 a
+ * stage (two Q8_0 blocks), the activations through a three-stage LDS ring filled by global-to-LDS loads two
+ * stages ahead; waves 0-3 run their MFMAs while waves 4-7 dequantize and load, then the other way round. In
+ * both, work items (tile, column block) are split into eight contiguous ranges, one per XCD (workgroup i runs
+ * on XCD i mod 8), so the column blocks of one tile and the tiles of one expert share an L2.
  */
 
 #include "vitna_kernels.h"
@@ -126,6 +125,83 @@ __global__ __launch_bounds__(256) void prefill_router_kernel(const float* __rest
         for (int i = 0; i < RE; i++) rv[i] = rp[i][16 * m];
 #pragma unroll
         for (int t = 0; t < RT; t++) xv[t] = xp[t][16 * m];
+#pragma unroll
+        for (int i = 0; i < RE; i++)
+#pragma unroll
+            for (int t = 0; t < RT; t++) acc[i][t] = fmaf(rv[i], xv[t], acc[i][t]);
+    }
+#pragma unroll
+    for (int i = 0; i < RE; i++)
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+            const float v = fold16_lanes(acc[i][t]);
+            if (j == 0 && e0 + i < E && t0 + t < n) logits[(size_t)(t0 + t) * E + e0 + i] = v;
+        }
+}
+
+/* The norm and the router in one pass, for rows of up to NR_HMAX columns: a workgroup's RT rows are loaded into
+   LDS once, normalized there exactly as prefill_norm_kernel does (sixteen lanes a row for the sum of squares),
+   written out in bf16 for the GEMM, and read by the router's chains from LDS, so that the fp32 normalized rows
+   never go to memory. The same arithmetic as the two kernels, so the same bits. */
+#define NR_HMAX 2048
+template <int RT, int RE>
+__global__ __launch_bounds__(256) void prefill_norm_router_kernel(const float* __restrict__ x, const float* __restrict__ nw,
+                                                                 const float* __restrict__ R, float* __restrict__ logits,
+                                                                 uint16_t* __restrict__ xb, int n, int E, int H, float eps) {
+    __shared__ __attribute__((aligned(16))) float sxn[RT * NR_HMAX];
+    __shared__ float inv_s[RT];
+    const int tid = threadIdx.x, j = tid & 15, grp = tid >> 4;
+    const int t0 = blockIdx.y * RT, H4 = H / 4;
+    for (int i = tid; i < RT * H4; i += 256) {
+        const int t = i / H4, c = i - t * H4;
+        reinterpret_cast<float4*>(sxn + t * H)[c] = reinterpret_cast<const float4*>(x + (size_t)min(t0 + t, n - 1) * H)[c];
+    }
+    __syncthreads();
+    if (grp < RT) {
+        /* engine/src/kernels.c:115-146: sixteen chains of squares, the fold, 1 / sqrtf(ss / n + eps) */
+        const float* sr = sxn + grp * H;
+        float acc = 0.0f;
+        for (int m = 0; m < H / 16; m++) acc = fmaf(sr[16 * m + j], sr[16 * m + j], acc);
+        const float ss = fold16_lanes(acc);
+        if (j == 0) inv_s[grp] = 1.0f / sqrtf(ss / (float)H + eps);
+    }
+    __syncthreads();
+    const float4* w4 = reinterpret_cast<const float4*>(nw);
+    for (int i = tid; i < RT * H4; i += 256) {
+        const int t = i / H4, c = i - t * H4;
+        const float inv = inv_s[t];
+        float4* p = reinterpret_cast<float4*>(sxn + t * H) + c;
+        const float4 v = *p, w = w4[c];
+        float4 o;
+        o.x = (v.x * inv) * w.x; o.y = (v.y * inv) * w.y;
+        o.z = (v.z * inv) * w.z; o.w = (v.w * inv) * w.w;
+        *p = o;
+        if (blockIdx.x == 0 && t0 + t < n) {
+            uint2 b;
+            b.x = bf16_rne(o.x) | (bf16_rne(o.y) << 16);
+            b.y = bf16_rne(o.z) | (bf16_rne(o.w) << 16);
+            reinterpret_cast<uint2*>(xb + (size_t)(t0 + t) * H)[c] = b;
+        }
+    }
+    __syncthreads();
+    const int e0 = (blockIdx.x * 16 + grp) * RE;
+    if (e0 >= E) return; /* whole groups only: the fold stays within a group */
+    const float* rp[RE];
+#pragma unroll
+    for (int i = 0; i < RE; i++) rp[i] = R + (size_t)min(e0 + i, E - 1) * H + j;
+    float acc[RE][RT];
+#pragma unroll
+    for (int i = 0; i < RE; i++)
+#pragma unroll
+        for (int t = 0; t < RT; t++) acc[i][t] = 0.0f;
+    const int M = H / 16;
+#pragma unroll 2
+    for (int m = 0; m < M; m++) {
+        float rv[RE], xv[RT];
+#pragma unroll
+        for (int i = 0; i < RE; i++) rv[i] = rp[i][16 * m];
+#pragma unroll
+        for (int t = 0; t < RT; t++) xv[t] = sxn[t * H + 16 * m + j];
 #pragma unroll
         for (int i = 0; i < RE; i++)
 #pragma unroll
@@ -640,6 +716,15 @@ hipError_t launch_prefill_router(const float* xn, const float* R, float* logits,
     if (n < 1 || E < 1 || H % 16) return hipErrorInvalidValue;
     constexpr int RT = 8, RE = 8;
     prefill_router_kernel<RT, RE><<<dim3((E + 16 * RE - 1) / (16 * RE), (n + RT - 1) / RT), 256, 0, s>>>(xn, R, logits, n, E, H);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_norm_router(const float* x, const float* nw, const float* R, float* logits, uint16_t* xb, int n, int E,
+                                     int H, float eps, hipStream_t s) {
+    if (n < 1 || E < 1 || H % 16) return hipErrorInvalidValue;
+    if (H > NR_HMAX) return hipErrorNotSupported; /* the two-kernel form */
+    constexpr int RT = 8, RE = 8;
+    prefill_norm_router_kernel<RT, RE><<<dim3((E + 16 * RE - 1) / (16 * RE), (n + RT - 1) / RT), 256, 0, s>>>(x, nw, R, logits, xb, n, E, H, eps);
     return hipGetLastError();
 }
 
