@@ -104,6 +104,22 @@ def test_prefill_small(n):
         model.free()
 
 
+def test_prefill_wide_hidden():
+    """A hidden size past the fused norm-and-router kernel's 2048 (4096): the separate norm and router kernels."""
+    say("prefill hidden 4096")
+    model = va.Model(va.shape(**dict(SMALL_Q8, n_layers=1, hidden=4096)), 4243)
+    dev = va.Device(model)
+    try:
+        n = 37
+        x = va.normal(77, 0, n * model.cfg.hidden).reshape(n, model.cfg.hidden)
+        out, chosen = dev.prefill(0, x)
+        worst = check_rows(model, 0, x, out, chosen, range(n))
+        say("  rows", n, "largest error / bound", worst)
+    finally:
+        dev.close()
+        model.free()
+
+
 def test_prefill_config4_full():
     """BASELINE config 4 at full size: 4096 rows N(0,1) drawn on the device, 128 Q8_0 experts, top-8.
     Every row's choice is checked; the sums of 96 rows spread over the batch."""
