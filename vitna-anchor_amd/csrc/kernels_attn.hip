@@ -561,63 +561,87 @@ hipError_t launch_attention(const attn_args& a, hipStream_t s) {
 }
 
 
-/* One block per (query head, row), a thread per dimension: the chunks'
-   maxima and sums read in parallel, each chunk's scale exp(m_s - M) computed
-   once, then each dimension's weighted values summed, eight chunks' loads in
-   flight at a time. */
+/* One block per (query head, row): the chunks' maxima and sums read in parallel, each chunk's scale
+   exp(m_s - M) computed once; then SP threads a dimension, thread (d, sp) summing the weighted values of chunks
+   sp, sp + SP, ... (up to MERGE_PRE of them requested at once), and the SP partial sums added in sp order. SP
+   grows with the chunks a row may have, so a long context is read in one or two rounds of loads rather than
+   one round per eight chunks. */
 #define MERGE_MAX ATTN_SPLITS_MAX
-#define MERGE_PRE 32 /* chunks whose values are requested with their maxima and sums */
-__global__ void attention_merge_kernel(attn_args a) {
-    const int hq = blockIdx.x, row = blockIdx.y, d = threadIdx.x;
-    const int G = a.n_heads / a.n_kv, h = hq / G, g = hq % G, HD = a.hd;
+#define MERGE_PRE 32 /* chunks a thread requests before its first add */
+template <int SP>
+__global__ __launch_bounds__(SP > 1 ? 128 * SP : 1024) void attention_merge_kernel(attn_args a) {
+    const int hq = blockIdx.x, row = blockIdx.y, tid = threadIdx.x, HD = a.hd;
+    /* (one thread a dimension: the block is the head's HD threads) */
+    const int d = SP > 1 ? tid % HD : tid, sp = SP > 1 ? tid / HD : 0, nt = SP > 1 ? HD * SP : (int)blockDim.x;
+    const int G = a.n_heads / a.n_kv, h = hq / G, g = hq % G;
     const int n_act = a.rows[row].pos / ATTN_CHUNK + 1;
     const float* base = a.partial + (((size_t)row * a.n_kv + h) * a.splits_max * G + g) * (HD + 4);
     const size_t stride = (size_t)G * (HD + 4);
     __shared__ float fm[MERGE_MAX], fl[MERGE_MAX];
-    __shared__ float red[4];
-    /* the first MERGE_PRE chunks' values, loaded alongside the maxima: one round trip for most rows */
+    __shared__ float red[8];
+    __shared__ float po[SP > 1 ? SP - 1 : 1][128], pl[SP > 1 ? SP - 1 : 1];
+    /* this thread's first MERGE_PRE chunks' values, requested alongside the maxima */
     float v0[MERGE_PRE];
 #pragma unroll
-    for (int i = 0; i < MERGE_PRE; i++) v0[i] = i < n_act ? base[i * stride + d] : 0.0f;
+    for (int i = 0; i < MERGE_PRE; i++) {
+        const int s = sp + SP * i;
+        v0[i] = s < n_act ? base[s * stride + d] : 0.0f;
+    }
     float m = -INFINITY;
-    for (int s = d; s < n_act; s += blockDim.x) {
+    for (int s = tid; s < n_act; s += nt) {
         fm[s] = base[s * stride + HD];
         fl[s] = base[s * stride + HD + 1];
         m = fmaxf(m, fm[s]);
     }
     m = wave_max_dpp(m);
-    if ((d & 63) == 0) red[d >> 6] = m;
+    if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
     float M = red[0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); w++) M = fmaxf(M, red[w]);
-    for (int s = d; s < n_act; s += blockDim.x) fm[s] = expf(fm[s] - M);
+    for (int w = 1; w < nt / 64; w++) M = fmaxf(M, red[w]);
+    for (int s = tid; s < n_act; s += nt) fm[s] = expf(fm[s] - M);
     __syncthreads();
     float L = 0.f, o = 0.f;
 #pragma unroll
-    for (int i = 0; i < MERGE_PRE; i++)
-        if (i < n_act) {
-            L = fmaf(fl[i], fm[i], L);
-            o = fmaf(v0[i], fm[i], o);
-        }
-    int s = MERGE_PRE;
-    for (; s + 8 <= n_act; s += 8) {
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = base[(s + i) * stride + d];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            L = fmaf(fl[s + i], fm[s + i], L);
-            o = fmaf(v[i], fm[s + i], o);
+    for (int i = 0; i < MERGE_PRE; i++) {
+        const int s = sp + SP * i;
+        if (s < n_act) {
+            L = fmaf(fl[s], fm[s], L);
+            o = fmaf(v0[i], fm[s], o);
         }
     }
-    for (; s < n_act; s++) {
+    int s = sp + SP * MERGE_PRE;
+    for (; s + 7 * SP < n_act; s += 8 * SP) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = base[(s + SP * i) * stride + d];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            L = fmaf(fl[s + SP * i], fm[s + SP * i], L);
+            o = fmaf(v[i], fm[s + SP * i], o);
+        }
+    }
+    for (; s < n_act; s += SP) {
         L = fmaf(fl[s], fm[s], L);
         o = fmaf(base[s * stride + d], fm[s], o);
+    }
+    if constexpr (SP > 1) {
+        if (sp > 0) {
+            po[sp - 1][d] = o;
+            if (d == 0) pl[sp - 1] = L;
+        }
+        __syncthreads();
+        if (sp > 0) return;
+#pragma unroll
+        for (int i = 0; i < SP - 1; i++) {
+            o += po[i][d];
+            L += pl[i];
+        }
     }
     const float val = o / L;
     a.att[(size_t)row * a.n_heads * HD + (size_t)hq * HD + d] = val;
     if (a.img.a) {
-        /* the head's HD columns of the row into the o-projection's operand images: 8 columns a thread */
+        /* the head's HD columns of the row into the o-projection's operand images: 8 columns a thread. Only the
+           waves of sp = 0 are left (whole waves returned above), and a barrier counts the waves still running. */
         __shared__ float sv[128];
         sv[d] = val;
         __syncthreads();
@@ -642,7 +666,12 @@ hipError_t launch_attention_merge(const attn_args& a, hipStream_t s) {
     if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_rows < 1 || (a.hd != 64 && a.hd != 128) || a.splits_max > MERGE_MAX)
         return hipErrorInvalidValue;
     if (a.img.a && ((a.n_heads * a.hd) % 256 || !a.img.b || !a.img.s32 || !a.img.s16)) return hipErrorInvalidValue;
-    attention_merge_kernel<<<dim3(a.n_heads, a.n_rows), a.hd, 0, s>>>(a);
+    const dim3 grid(a.n_heads, a.n_rows);
+    /* threads a dimension: enough that a thread sums at most about MERGE_PRE chunks. A single row (batch-1
+       decode) keeps one: its few blocks leave the device idle either way, and the wider form measured slower there. */
+    if (a.n_rows > 1 && a.splits_max > 4 * MERGE_PRE) attention_merge_kernel<4><<<grid, 4 * a.hd, 0, s>>>(a);
+    else if (a.n_rows > 1 && a.splits_max > 2 * MERGE_PRE) attention_merge_kernel<2><<<grid, 2 * a.hd, 0, s>>>(a);
+    else attention_merge_kernel<1><<<grid, a.hd, 0, s>>>(a);
     return hipGetLastError();
 }
 
