@@ -399,6 +399,9 @@ def bench_prefill(va, reps=10):
         gemm_us = ph[2] + ph[3]
         log("configs[4]: prefill of %d rows %.1f us (norm+router %.1f, routing %.1f, gate/up %.1f, down %.1f, sum %.1f)"
             % (n, tot, *ph))
+        # the yardstick: what back-to-back MFMAs sustain on this box, as the copy probe is for streaming
+        probe = va.mfma_probe()
+        log("MFMA probe: %.1f TFLOP/s dense bf16" % probe)
         return {"workload": "BASELINE configs[4]: prefill of 4096 rows through one Qwen3-shaped MoE layer, Q8_0 experts, "
                             "bf16 MFMA grouped GEMM", "value": round(n / tot * 1e6, 1), "unit": "tok/s",
                 "us": round(tot, 1), "phases_us": {k: round(v, 1) for k, v in zip(
@@ -406,7 +409,8 @@ def bench_prefill(va, reps=10):
                 "roofline": {"bound": "mfma", "achieved": round(flops / gemm_us / 1e6, 1), "peak": 2500.0,
                              "unit": "TFLOP/s", "frac": round(flops / gemm_us / 1e6 / 2500.0, 4),
                              "note": "both GEMMs: 2 n K (3 I H) flops over their summed duration"},
-                "tflops_whole": round(flops / tot / 1e6, 1)}
+                "tflops_whole": round(flops / tot / 1e6, 1),
+                "mfma_probe_TFLOPs": round(probe, 1), "frac_of_probe": round(flops / gemm_us / 1e6 / probe, 4)}
     finally:
         dev.close()
         model.free()

@@ -295,6 +295,12 @@ bool vitna_hip_host_route(const float* logits, int n_experts, int k, bool renorm
     bytes fetched and written are the yardstick for the other kernels'. */
 bool vitna_hip_copy_probe(size_t bytes, int reps, double* avg_us, char* err, size_t err_len);
 
+/** blocks workgroups of one wave a SIMD doing nothing but back-to-back bf16
+    MFMAs (32x32x16, eight independent accumulators), iters each, reps
+    launches: the dense bf16 TFLOP/s the matrix cores sustain on this device,
+    the yardstick for the prefill GEMMs beside the published peak. */
+bool vitna_hip_mfma_probe(int blocks, int iters, int reps, double* tflops, char* err, size_t err_len);
+
 /** For checking the expert cache (vitna_cuda_create with an expert_cache_bytes
     that holds fewer slots than the model has experts; the reference's
     expert_cache_t, engine/src/model_cuda.cu:249-290): where[layer * E + e]

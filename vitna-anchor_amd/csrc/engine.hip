@@ -1836,6 +1836,24 @@ extern "C" bool vitna_hip_copy_probe(size_t bytes, int reps, double* avg_us, cha
     return true;
 }
 
+extern "C" bool vitna_hip_mfma_probe(int blocks, int iters, int reps, double* tflops, char* err, size_t err_len) {
+    if (blocks < 1 || iters < 1 || reps < 1) return fail(err, err_len, "positive blocks, iterations and repetitions");
+    float* out = nullptr;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    bool ok = hipMalloc(&out, (size_t)blocks * 256 * sizeof(float)) == hipSuccess && hipEventCreate(&t0) == hipSuccess &&
+              hipEventCreate(&t1) == hipSuccess && launch_mfma_probe(out, blocks, iters, 0) == hipSuccess &&
+              hipEventRecord(t0, 0) == hipSuccess;
+    for (int i = 0; ok && i < reps; i++) ok = launch_mfma_probe(out, blocks, iters, 0) == hipSuccess;
+    float ms = 0;
+    ok = ok && hipEventRecord(t1, 0) == hipSuccess && hipEventSynchronize(t1) == hipSuccess && hipEventElapsedTime(&ms, t0, t1) == hipSuccess;
+    if (t0) (void)hipEventDestroy(t0);
+    if (t1) (void)hipEventDestroy(t1);
+    (void)hipFree(out);
+    if (!ok) return fail(err, err_len, "the matrix-core probe failed");
+    if (tflops) *tflops = mfma_probe_flops(blocks, iters) * reps / (ms * 1e-3) / 1e12;
+    return true;
+}
+
 /* ---- several rows a layer at a time (model_cuda.h:124-161) -------------- */
 
 extern "C" size_t vitna_cuda_moe_rows_max(const struct vitna_cuda_model* g) { return g ? ROWS_MAX : 0; }

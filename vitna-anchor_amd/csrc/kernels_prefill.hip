@@ -704,6 +704,42 @@ __global__ __launch_bounds__(PW_THREADS, 1) void prefill_wgemm_kernel(prefill_ar
     else pw_body<GU, 2>(a, e, m0, nt, cnt, lds, yrow, ywt);
 }
 
+/* ---- the matrix cores' yardstick ------------------------------------------ */
+
+/* Nothing but v_mfma_f32_32x32x16_bf16 on eight independent accumulators a wave, one wave a SIMD: what the
+   matrix cores of this device sustain, as the copy probe is what its memory streams. */
+__global__ __launch_bounds__(256, 1) void mfma_probe_kernel(float* __restrict__ out, int iters, float seed) {
+    f32x16 acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
+    bf16x8 x, w;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        x[k] = (__bf16)(seed * (float)(threadIdx.x + k));
+        w[k] = (__bf16)(seed * (float)(k + 1));
+    }
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x, w, acc[i], 0, 0, 0);
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) sum += acc[i][r];
+    out[blockIdx.x * 256 + threadIdx.x] = sum; /* kept, so the products are not optimized away */
+}
+
+hipError_t launch_mfma_probe(float* out, int blocks, int iters, hipStream_t s) {
+    if (blocks < 1 || iters < 1) return hipErrorInvalidValue;
+    mfma_probe_kernel<<<blocks, 256, 0, s>>>(out, iters, 1e-3f);
+    return hipGetLastError();
+}
+
+double mfma_probe_flops(int blocks, int iters) { return (double)blocks * 4 * iters * 8 * (2.0 * 32 * 32 * 16); }
+
 /* ---- launches ----------------------------------------------------------- */
 
 hipError_t launch_prefill_norm(const float* x, const float* w, float* xn, uint16_t* xb, int n, int H, float eps, hipStream_t s) {

@@ -261,6 +261,9 @@ hipError_t launch_reduce_rows(const float* ypart, float* x, int n, int K, int H,
 /* compute units of the current device (cached) */
 int gemv_device_cus();
 hipError_t launch_copy_probe(const void* src, void* dst, size_t bytes, hipStream_t s);
+/* blocks x 256 threads of back-to-back bf16 MFMAs (out: blocks x 256 floats); the flops they do */
+hipError_t launch_mfma_probe(float* out, int blocks, int iters, hipStream_t s);
+double mfma_probe_flops(int blocks, int iters);
 hipError_t launch_fill_normal(float* out, size_t n, uint64_t seed, hipStream_t s);
 
 

@@ -370,6 +370,7 @@ def _hip():
         "vitna_hip_expert_cache_state": (C.c_bool, [P, C.POINTER(C.c_int32), C.c_size_t, C.POINTER(C.c_uint64), *E]),
         "vitna_cuda_moe_report": (C.c_char_p, [P, C.c_char_p, C.c_size_t]),
         "vitna_hip_copy_probe": (C.c_bool, [C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
+        "vitna_hip_mfma_probe": (C.c_bool, [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_steps": (C.c_bool, [P, C.c_size_t, C.c_int32, C.c_size_t, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_ffn": (C.c_bool, [P, C.c_int, C.POINTER(C.c_double), *E]),
         "vitna_hip_time_kernel": (C.c_bool, [P, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double),
@@ -682,6 +683,15 @@ def copy_probe(nbytes, reps=10):
     if not hip().vitna_hip_copy_probe(nbytes, reps, C.byref(us), err, 512):
         raise VitnaError(err.value.decode())
     return us.value
+
+
+def mfma_probe(blocks=1024, iters=2000, reps=3):
+    """vitna_hip_mfma_probe: dense bf16 TFLOP/s of back-to-back 32x32x16 MFMAs on this device."""
+    tf = C.c_double()
+    err = C.create_string_buffer(512)
+    if not hip().vitna_hip_mfma_probe(blocks, iters, reps, C.byref(tf), err, 512):
+        raise VitnaError(err.value.decode())
+    return tf.value
 
 
 def host_route(logits, k, renormalize):
