@@ -59,3 +59,41 @@ def test_gguf_model_on_device(tmp_path, norm_dtype):
     finally:
         g.free()
         model.free()
+
+
+def test_gguf_model_through_expert_cache(tmp_path):
+    """The GGUF model's experts through a cache of 2K slots (the experts are views into the file's stacked
+    tensors): the layer-at-a-time ABI gives the same bits as the same file with every expert resident."""
+    from test_gpu_expert_cache import slot_bytes
+    say("gguf model through the expert cache")
+    model = va.Model(va.shape(**SPEC), 98)
+    path = va.write_gguf(model, str(tmp_path), va.F32, 32)
+    g = va.GgufModel(path, ctx=96, seqs=1)
+    cfg = g.cfg
+    K, L = cfg.n_experts_used, cfg.n_layers
+    try:
+        res = va.Device(g)
+        cac = va.Device(g, expert_cache_bytes=2 * K * slot_bytes(cfg, SPEC))
+        try:
+            pos = 5
+            prefill(g, res, pos)
+            prefill(g, cac, pos)
+            for t, token in enumerate([123, 7, 999]):
+                outs = []
+                for dev in (res, cac):
+                    for l in range(L):
+                        lg, nx = dev.moe_route(0, token, pos + t, l, want_next=True)
+                        _, order, w = oracle.route(lg, K, bool(cfg.renormalize))
+                        guess = oracle.route(nx, K, bool(cfg.renormalize))[0] if l + 1 < L else None
+                        dev.moe_experts(l, order, w, guess)
+                    outs.append(dev.moe_head())
+                assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), "token %d" % t
+            _, cnt = cac.expert_cache_state()
+            say("  cache counts", cnt)
+            assert cnt["acquired"] == 3 * L * K and cnt["misses"] > 0
+        finally:
+            cac.close()
+            res.close()
+    finally:
+        g.free()
+        model.free()
