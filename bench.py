@@ -16,6 +16,7 @@ Prints one JSON line. Besides the step throughput it carries:
   roofline: the dominant kernel (the experts' gate/up GEMV) timed with HIP
             events on the model's stream, its algorithmic bytes per launch, the
             achieved GB/s against the 8 TB/s HBM peak;
+  copy_probe_GBps: a plain device copy, what streaming reaches on this box;
   cpu_baseline: the CPU checker's decode step (the reference's CPU arithmetic
             restated, oracle/) on this host, single-threaded, over a bounded
             number of tokens; cpu_baseline_mt the same with each matrix's rows
@@ -25,7 +26,8 @@ Prints one JSON line. Besides the step throughput it carries:
             key-value lengths drawn from U{128..8192}, one rows step (device
             routing, experts grouped so each chosen expert is read once a
             layer); configs[4], a prefill of 4096 rows through one
-            Qwen3-shaped MoE layer with Q8_0 experts (bf16 MFMA grouped GEMM);
+            Qwen3-shaped MoE layer with Q8_0 experts (bf16 MFMA grouped GEMM),
+            with the matrix cores' yardstick (back-to-back MFMAs) beside it;
             configs[0] and [1], one MoE layer of one token; expert_cache,
             configs[2]'s model decoded a layer at a time through the
             reference's ABI with every expert resident and with a cache
