@@ -47,10 +47,9 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "Qwen3-30B-A3B Q4_K_M decode tok/s @1 GPU; expert GEMV HBM GB/s (% of peak)"
-# HBM bytes a launch of experts_in_kernel<Q4_K> moves at this workload, from two rocprofv3 --pmc passes
-# (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, each factor calibrated on copy_probe_kernel):
-# profiles/decode_step_qwen3_hbm_traffic.md
-EXPERTS_IN_TRAFFIC = 14405141 + 24704
+# The committed rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by its factor calibrated on
+# copy_probe_kernel) that roofline.traffic is read from.
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_step_qwen3_hbm_traffic.md")
 KERNELS = {0: "experts_in (gate/up + SiLU)", 1: "experts_down (+ weighted sum)", 2: "route (norm + router + top-k)",
            3: "q/k/v projections", 4: "attention (+ merge)", 5: "o-projection", 6: "LM head",
            7: "route without top-k", 8: "routing rule alone (1 block)", 9: "tiny launch (floor)"}
@@ -206,7 +205,7 @@ def main():
                                "48 layers, KV 2048 positions fp32, LM head Q6_K 151936x2048",
                    "layers": L, "position": pos, "global_batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": EXPERTS_IN_TRAFFIC,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profile_traffic(TRAFFIC_PROFILE, "experts_in_kernel<17,"),
                      "kernel": "experts_in_kernel<Q4_K> (8 experts x (gate + up) 768 x 2048)",
                      "bytes_per_launch": b0, "avg_us": round(us0, 3)},
         "kernels_us": {KERNELS[w]: round(per_kernel[w][0], 3) for w in per_kernel},
@@ -218,6 +217,31 @@ def main():
     }
     print(json.dumps(out), flush=True)
     model.free()
+
+
+def profile_traffic(path, kernel):
+    """HBM bytes a launch of the kernel whose name contains `kernel` moves, from a committed --pmc summary: the
+    table row's scaled bytes read plus bytes written (columns 'bytes read (scaled)', 'bytes written (scaled)').
+    None when the file or the row is missing."""
+    try:
+        with open(path) as f:
+            lines = f.read().splitlines()
+    except OSError:
+        return None
+    head = None
+    for ln in lines:
+        if not ln.startswith("|"):
+            continue
+        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+        if head is None and "bytes read (scaled)" in cells:
+            head = cells
+            continue
+        if head and cells and kernel in cells[0].replace(" ", ""):
+            try:
+                return int(cells[head.index("bytes read (scaled)")]) + int(cells[head.index("bytes written (scaled)")])
+            except (ValueError, IndexError):
+                return None
+    return None
 
 
 def host_info():

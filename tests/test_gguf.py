@@ -191,7 +191,7 @@ def _find(path, needle):
 @pytest.mark.parametrize("case,needle", [("magic", "not a GGUF file"), ("version", "GGUF version 4"),
                                          ("name", "is not one this engine knows"), ("llama", "permuted"),
                                          ("offset", "off its alignment"), ("dtype", "ggml type 2;"),
-                                         ("truncated", "runs past the end")])
+                                         ("truncated", "runs past the end"), ("wide", "rows too wide")])
 def test_reader_refuses(tmp_path, case, needle):
     """The refusals the reference makes (engine/src/gguf.c:239-440), each on a damaged copy of a good file."""
     path = make(tmp_path, SMALL, 5, va.F32, 32)
@@ -218,6 +218,10 @@ def test_reader_refuses(tmp_path, case, needle):
     elif case == "truncated":
         with open(path, "r+b") as f:
             f.truncate(1000)
+    elif case == "wide":
+        # a row width of 2^62 Q6_K weights: its byte count (2^54 * 210) wraps a 64-bit product to a small number
+        i = _find(path, b"output.weight")
+        _patch(path, i + len(b"output.weight") + 4, struct.pack("<Q", 1 << 62))
     with pytest.raises(va.VitnaError, match=needle):
         g = va.GgufModel(path)
         g.free()

@@ -786,8 +786,8 @@ extern "C" bool vitna_hip_expert_cache_state(const struct vitna_cuda_model* g, i
         memcpy(where, c.where.data(), c.n_places * sizeof(int32_t));
     }
     if (counters) {
-        const uint64_t v[10] = {(uint64_t)c.n_slots, c.slot_bytes, c.acquired, c.hits, c.in_flight, c.misses, c.prefetched,
-                                c.prefetch_used, c.copies, c.bytes_copied};
+        const uint64_t v[10] = {(uint64_t)c.n_slots, c.slot_bytes, c.n.acquired, c.n.hits, c.n.in_flight, c.n.misses, c.n.prefetched,
+                                c.n.prefetch_used, c.n.copies, c.n.bytes_copied};
         memcpy(counters, v, sizeof(v));
     }
     return true;
@@ -2095,7 +2095,7 @@ static bool cached_rows_experts(vitna_cuda_model* g, int layer, int n, const int
             const int x = want[w0 + i], s = slot_of[x];
             in_wave[x] = 1;
             const ec_slot& sl = c.slots[s];
-            if (sl.filling && hipStreamWaitEvent(g->stream, sl.filled, 0) != hipSuccess) ok = fail(err, err_len, "waiting for an expert's copy");
+            if (sl.copying && hipStreamWaitEvent(g->stream, sl.landed, 0) != hipSuccess) ok = fail(err, err_len, "waiting for an expert's copy");
             if (!ok || g->st_place[s] == sl.place) continue;
             /* the slot's tiled copy, on the compute stream: after the kernels that read the copy it replaces */
             const qmat* src[3] = {&d.gate, &d.up, &d.down};

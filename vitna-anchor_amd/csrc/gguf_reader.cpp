@@ -197,7 +197,10 @@ bool map_name(const std::string& name, std::string* hf, bool* stack, size_t* lay
     return false;
 }
 
+/* Bytes of one row of cols weights, or 0 for a width the dtype does not take. Widths of 2^40 weights and more
+   are refused before any multiplication, so a hostile shape cannot wrap the product to a small row. */
 uint64_t row_bytes_of(vitna_dtype_t t, uint64_t cols) {
+    if (cols >= ((uint64_t)1 << 40)) return 0;
     switch (t) {
         case VITNA_DTYPE_F32: return cols * 4;
         case VITNA_DTYPE_F16: case VITNA_DTYPE_BF16: return cols * 2;
@@ -398,7 +401,7 @@ extern "C" vitna_hip_gguf_t* vitna_hip_gguf_open(const char* path, vitna_hip_ggu
         const uint64_t cols = t.ne[0], rows = t.dims >= 2 ? t.ne[1] : 1, count = t.dims == 3 ? t.ne[2] : 1;
         const uint64_t rb = row_bytes_of(dt, cols);
         if (!rb || rows == 0 || count == 0 || count > 65536)
-            return bad("tensor %s has rows that are not whole %s blocks, or no rows", t.name.c_str(), dtype_text(dt));
+            return bad("tensor %s has rows that are not whole %s blocks, rows too wide, or no rows", t.name.c_str(), dtype_text(dt));
         if (rows > UINT64_MAX / rb || rows * rb > UINT64_MAX / count) return bad("tensor %s overflows", t.name.c_str());
         const uint64_t slice = rows * rb, bytes = slice * count;
         if (t.offset % info.alignment || t.offset > data_size || bytes > data_size - t.offset)

@@ -43,6 +43,8 @@
 #include "route_impl.h"
 #include "step_kernel.h"
 
+#include <mutex>
+
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
@@ -915,8 +917,12 @@ hipError_t launch_step(const step_args& a, const int* dts, hipStream_t s) {
     const void* fn = step_fn(a.H, dts[0], dts[1], a.K, a.I, a.attention != 0, dts[2], dts[3], dts[4]);
     if (!fn) return hipErrorInvalidValue;
     const size_t lds = step_lds_bytes(a.H, a.hd, a.nh, a.nkv, a.K, a.I, a.nb);
+    /* the functions whose dynamic LDS limit is already raised: shared by every model of the process, so
+       guarded against two host threads launching at once */
+    static std::mutex attr_mu;
     static const void* attr_done[8];
     static size_t attr_lds[8];
+    std::lock_guard<std::mutex> lock(attr_mu);
     int slot = 0;
     while (slot < 8 && attr_done[slot] && attr_done[slot] != fn) slot++;
     if (slot == 8 || attr_done[slot] != fn || attr_lds[slot] < lds) {
