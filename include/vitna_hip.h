@@ -188,6 +188,11 @@ bool vitna_hip_attention_io(struct vitna_cuda_model* g, size_t row, float* q, fl
 bool vitna_hip_step_routing(struct vitna_cuda_model* g, size_t layer, int32_t* chosen, int32_t* ids, float* weights, char* err,
                             size_t err_len);
 
+/* The routing of row `row` at `layer` in the last device-routed rows step (vitna_hip_moe_rows_step): each row's
+   chosen experts (largest logit first), ids (ascending) and weights. No counterpart in the reference: a checker. */
+bool vitna_hip_rows_routing(struct vitna_cuda_model* g, size_t layer, size_t row, int32_t* chosen, int32_t* ids, float* weights,
+                            char* err, size_t err_len);
+
 /** One projection of a pass of n rows (1 <= n <= the rows maximum) as the
     rows step runs it: y[t] = W x[t] for W = layer's q, k, v, o (which = 0..3)
     or the LM head (which = 4, layer ignored); x is n x W's columns, y n x W's

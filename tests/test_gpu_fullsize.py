@@ -7,8 +7,9 @@ attention at long contexts, against the CPU checker (oracle/) on the GPU.
     within 1e-3 of max |cpu| and the reference's LOGIT_ATOL 1e-2
     (reference/compare.mjs:84).
   * configs[3]: 32 sequences at key-value lengths drawn from U{128..8192}
-    (one forced to 8192: 129 chunks), one rows step; the shortest, the
-    longest and two rows between against the checker's step of each.
+    (one forced to 8192: 129 chunks), one rows step; every row's logits
+    against the checker's step of that row, and every layer's chosen experts
+    of the shortest, the longest and two rows between.
   * The attention and its merge alone at 33, 34 and 129 chunks, on the
     batch-1 matrix-core path (8 query heads a key-value head), the rows'
     matrix-core path and the one-row vector path: the device's attention
@@ -78,7 +79,8 @@ def test_config2_full_step():
 
 def test_config3_rows_full():
     """32 sequences, one new token each, key-value lengths U{128..8192} with 8192 among them, the
-    full 48-layer model, one device-routed rows step; four rows against the checker."""
+    full 48-layer model, one device-routed rows step. Every row's logits against the checker's step of that row;
+    for four rows (the shortest, the longest and two between), every layer's chosen experts too."""
     seed = 20260103
     say("configs[3] rows: building the model")
     model = va.Model(va.shape(ctx=8193, seqs=32, kv_host=1), seed, threads=16)
@@ -96,13 +98,12 @@ def test_config3_rows_full():
             say("  device rows step")
             logits = dev.rows_step(rows)
             order = np.argsort(lengths)
-            pick = [int(order[0]), int(order[10]), int(order[21]), int(order[-1])]
+            pick = {int(order[0]), int(order[10]), int(order[21]), int(order[-1])}
             kc = np.ctypeslib.as_array(model.m.k_cache, shape=(32, L, model.m.ctx, kd))
             vc = np.ctypeslib.as_array(model.m.v_cache, shape=(32, L, model.m.ctx, kd))
-            last = {}
-            for s in pick:
-                last[s] = dev.routing(s)[1]
-            for s in pick:
+            per_layer = {s: np.stack([dev.rows_routing(l, s)[0] for l in range(L)]) for s in pick}
+            worst = 0.0
+            for s in range(32):
                 n = int(lengths[s])
                 # the cache the device step read (positions before the row's own), copied to the host model
                 for l in range(L):
@@ -113,10 +114,14 @@ def test_config3_rows_full():
                 ref, tl, tc, _ = oracle.step(model, seq, tok, pos, threads=16)
                 r = rel(logits[s], ref)
                 a = float(np.max(np.abs(logits[s] - ref)))
+                worst = max(worst, r)
                 say("  row %d (kv length %d): logits rel err %.3g, max abs %.3g, smallest margin %.3g"
                     % (s, n, r, a, margins(tl, K).min()))
-                assert np.array_equal(last[s], tc[-1]), ("row", s, last[s], tc[-1])
+                if s in pick:
+                    for l in range(L):
+                        assert np.array_equal(per_layer[s][l], tc[l]), ("row", s, "layer", l, per_layer[s][l], tc[l])
                 assert r <= REL and a <= 1e-2
+            say("  all 32 rows: worst logits rel err %.3g; every layer's choice identical for rows %s" % (worst, sorted(pick)))
         finally:
             dev.close()
     finally:

@@ -4,6 +4,12 @@ against vitna_hip_moe_prefill (same kernels, allocated buffers) on the same
 rows. Bit-exact: the same kernels in the same order on the same inputs give
 the same bits, and the chosen experts are identical.
 
+On a fresh model, before any allocating entry point has made the experts'
+tiled copy, the no-allocation prefill runs the shared-stage GEMM kernel
+(widening from the planes); the allocating prefill afterwards runs the kernel
+that widens each wave's own weights from the tiled copy. The two must give
+the same bits.
+
 Two calls in a row, the second with fewer rows (the region keeps the first
 call's contents), then a call with more rows than the region holds, which
 must fail with a message and leave the device usable. Config 4's shape
@@ -85,6 +91,41 @@ def test_prefill_noalloc_matches_allocating_entry():
             dev.prefill_noalloc(0, xb.p.value, 65536, None)
         dev.prefill_noalloc(0, xb.p.value, n, None)
         dev.sync()
+    finally:
+        xb.free()
+        cb.free()
+        dev.close()
+        model.free()
+
+
+def test_prefill_noalloc_first_call_shared_stage_kernel():
+    """The first call on a fresh model (no tiled copy yet: the shared-stage kernel) against the allocating prefill
+    (the per-wave kernel) on the same rows, bit for bit; a second, smaller no-allocation call after that (now the
+    per-wave kernel) too."""
+    model = va.Model(va.shape(**va.CONFIGS[4]), 20260106, threads=16)
+    dev = va.Device(model)
+    cfg = model.cfg
+    H, K = cfg.hidden, cfg.n_experts_used
+    n = 600
+    xb = DeviceBuffer(n * H * 4)
+    cb = DeviceBuffer(n * K * 4)
+    try:
+        x = va.normal(900, 3, n * H).reshape(n, H)
+        say("no-alloc prefill on a fresh model, rows", n)
+        xb.put(x)
+        cb.put(np.full((n, K), -1, np.int32))
+        dev.prefill_noalloc(0, xb.p.value, n, cb.p.value)
+        dev.sync()
+        got_x = xb.get((n, H), np.float32)
+        got_ch = cb.get((n, K), np.int32)
+        want_x, want_ch = dev.prefill(0, x)
+        assert np.array_equal(got_ch, want_ch)
+        assert np.array_equal(got_x.view(np.uint32), want_x.view(np.uint32))
+        m = 200
+        xb.put(x[:m])
+        dev.prefill_noalloc(0, xb.p.value, m, None)
+        dev.sync()
+        assert np.array_equal(xb.get((m, H), np.float32).view(np.uint32), want_x[:m].view(np.uint32))
     finally:
         xb.free()
         cb.free()

@@ -30,7 +30,12 @@
 #include <type_traits>
 #include <mutex>
 
-#define ROWS_MAX 256
+/* The most rows a pass takes (the reference's MOE_ROWS, model_cuda.cu:197): model.c runs a prompt in chunks of
+   this many. Scratch for this many rows is allocated with the model. */
+#define ROWS_MAX 1024
+/* With the model's gpu_fast, a pass of at least this many rows runs its experts as the bf16 matrix-core grouped GEMM
+   of the prefill (the reference's FAST_ROWS, model_cuda.cu:204); smaller passes keep the exact kernels. */
+#define FAST_ROWS 64
 
 struct dlayer {
     qmat q, k, v, o;
@@ -66,6 +71,7 @@ struct vitna_cuda_model {
     float *x, *xn, *q, *k, *v, *qp, *att, *act, *ypart, *rlogits, *vocab, *partial;
     route_out* rt;
     route_out* rt_layers; /* the device-routed step's routing of every layer (the last layer's is also in rt) */
+    route_out* rows_rt;   /* the device-routed rows step's routing: [layer][ROWS_MAX] */
     row_rec* rows_dev;
     row_rec* rows_host; /* pinned */
     hipEvent_t rows_copied;
@@ -88,6 +94,7 @@ struct vitna_cuda_model {
     hipGraphExec_t rows_graph;
     int rows_graph_n;           /* the pass the rows graph was captured for: rows, or 0 for none */
     bool rows_graph_shared;
+    bool rows_graph_fast;       /* and whether it ran the pass's experts as the grouped GEMM */
     hipGraphExec_t step_graph;
     bool graph_ready;
     /* the persistent decode step (kernels_step.hip): set up on first use when the model's shape takes it */
@@ -105,6 +112,7 @@ struct vitna_cuda_model {
     uint64_t* step_trace;       /* device: a traced step's phase timeline */
     bool tiled_ready;           /* the multi-row paths' tiled copies made (ensure_tiled) */
     bool lost;
+    bool fast;          /* m->gpu_fast: passes of fast_rows rows or more take the grouped GEMM for their experts */
     size_t fast_rows, long_from;
     int rows_n;         /* rows of the pass in flight (vitna_cuda_moe_rows_*) */
     /* prefill through one MoE layer: buffers for pf_cap rows, allocated on first use */
@@ -427,7 +435,8 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
     g->NL = (int)c->n_layers; g->nh = (int)c->n_heads; g->nkv = (int)c->n_kv_heads; g->hd = (int)c->head_dim;
     g->V = (int)c->vocab; g->ctx = (int)m->ctx; g->seqs = (int)m->seqs; g->renorm = c->renormalize; g->attention = c->n_heads != 0;
     g->eps = c->rms_eps;
-    g->fast_rows = 64;
+    g->fast = m->gpu_fast;
+    g->fast_rows = FAST_ROWS;
     g->long_from = 1024;
     g->embed = {}; g->head = {};
     g->final_norm = nullptr;
@@ -538,6 +547,7 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
          dalloc(g, &g->gm_asum, R * K * (c->intermediate / 16) * 4, "scratch", err, err_len) &&
          dalloc(g, &g->rlogits, 2 * R * E * 4, "scratch", err, err_len) && dalloc(g, &g->rt, R * sizeof(route_out), "scratch", err, err_len) &&
          dalloc(g, &g->rt_layers, c->n_layers * sizeof(route_out), "scratch", err, err_len) &&
+         dalloc(g, &g->rows_rt, c->n_layers * R * sizeof(route_out), "the rows step's routing", err, err_len) &&
          dalloc(g, &g->rows_dev, R * sizeof(row_rec), "scratch", err, err_len) &&
          /* grouped by expert, or by slot when the experts pass through the cache */
          dalloc(g, &g->grp_count, std::max<size_t>(E, g->ec.n_slots) * sizeof(int), "scratch", err, err_len) &&
@@ -631,7 +641,7 @@ static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, 
 
 /* sp: the grouped experts' split of xn_out, run by the top-k kernel (several rows), or null */
 static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, int n_rows, const float* x, float* xn_out, bool topk,
-                                const topk_split* sp = nullptr) {
+                                const topk_split* sp = nullptr, route_out* rt = nullptr) {
     const dlayer& d = g->L[layer];
     route_args r;
     memset(&r, 0, sizeof(r));
@@ -644,7 +654,7 @@ static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, i
     r.eps = g->eps;
     hipError_t e = launch_route(r, g->stream);
     /* one token's top-k runs in the experts' prologue (enqueue_experts); several rows' in a kernel of its own */
-    if (e == hipSuccess && topk && n_rows > 1) e = launch_topk(logits, n_rows, g->E, g->K, g->renorm, g->rt, g->stream, sp);
+    if (e == hipSuccess && topk && n_rows > 1) e = launch_topk(logits, n_rows, g->E, g->K, g->renorm, rt ? rt : g->rt, g->stream, sp);
     return e;
 }
 
@@ -825,7 +835,10 @@ extern "C" const char* vitna_cuda_moe_report(const struct vitna_cuda_model* g, c
 
 extern "C" int vitna_cuda_kv_layers(const struct vitna_cuda_model* g) { return g ? g->NL : 0; }
 extern "C" void vitna_cuda_test_long_from(struct vitna_cuda_model* g, size_t n) { if (g) g->long_from = n; }
-extern "C" void vitna_cuda_test_fast_rows(struct vitna_cuda_model* g, size_t n) { if (g) g->fast_rows = n; }
+/* model_cuda.cu:3517: on a fast model, passes of n rows or more (n under the default) take the grouped GEMM */
+extern "C" void vitna_cuda_test_fast_rows(struct vitna_cuda_model* g, size_t n) {
+    if (g && g->fast && n >= 1 && n < g->fast_rows) g->fast_rows = n;
+}
 
 extern "C" bool vitna_cuda_cpu_experts(struct vitna_cuda_model* g, size_t threads, char* err, size_t err_len) {
     (void)g; (void)threads;
@@ -1287,6 +1300,23 @@ extern "C" bool vitna_hip_step_routing(struct vitna_cuda_model* g, size_t layer,
     return true;
 }
 
+extern "C" bool vitna_hip_rows_routing(struct vitna_cuda_model* g, size_t layer, size_t row, int32_t* chosen, int32_t* ids,
+                                       float* weights, char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no model");
+    if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
+    if (row >= ROWS_MAX) return fail(err, err_len, "row %zu: at most %d", row, ROWS_MAX);
+    HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
+    route_out r;
+    const route_out* src = layer + 1 < (size_t)g->NL ? g->rows_rt + layer * ROWS_MAX + row : g->rt + row;
+    HIP_TRY(hipMemcpy(&r, src, sizeof(r), hipMemcpyDeviceToHost), "copying the routing");
+    for (int k = 0; k < g->K; k++) {
+        if (chosen) chosen[k] = r.chosen[k];
+        if (ids) ids[k] = r.ids[k];
+        if (weights) weights[k] = r.weights[k];
+    }
+    return true;
+}
+
 extern "C" bool vitna_hip_attention_io(struct vitna_cuda_model* g, size_t row, float* q, float* att, char* err, size_t err_len) {
     if (!g || !g->attention) return fail(err, err_len, "no attention");
     if (row >= ROWS_MAX) return fail(err, err_len, "row %zu: at most %d", row, ROWS_MAX);
@@ -1480,6 +1510,12 @@ static bool prefill_reserve(vitna_cuda_model* g, size_t n, char* err, size_t err
     if (!ensure_tiled(g, err, err_len)) return false;
     if (n <= g->pf_cap) return true;
     HIP_TRY(hipStreamSynchronize(g->stream), "waiting before the prefill buffers grow");
+    /* a captured rows step of a fast pass reads these buffers: it is captured again on its next use */
+    if (g->rows_graph_n) {
+        (void)hipGraphExecDestroy(g->rows_graph);
+        (void)hipGraphDestroy(g->rows_graph_src);
+        g->rows_graph_n = 0;
+    }
     for (void* p : g->pf_allocs) (void)hipFree(p);
     g->pf_allocs.clear();
     g->pf_cap = 0;
@@ -1539,11 +1575,7 @@ static bool prefill_check(vitna_cuda_model* g, size_t layer, size_t n, char* err
     if (g->lost) return fail(err, err_len, "the device was lost earlier");
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (n < 1 || n > 65536) return fail(err, err_len, "%zu rows: a prefill takes 1 to 65536", n);
-    const dlayer& d = g->L[layer];
-    if (d.gate.dtype != VITNA_DTYPE_Q8_0 || d.up.dtype != VITNA_DTYPE_Q8_0 || d.down.dtype != VITNA_DTYPE_Q8_0)
-        return fail(err, err_len, "layer %zu: the prefill GEMM serves Q8_0 experts; these are %s/%s/%s", layer, dtype_name(d.gate.dtype),
-                    dtype_name(d.up.dtype), dtype_name(d.down.dtype));
-    if (g->H % 128 || g->I % 64) return fail(err, err_len, "the prefill GEMM needs hidden %% 128 == 0 and expert width %% 64 == 0 (%d, %d)", g->H, g->I);
+    /* every expert set the model check accepts (Q8_0, Q4_K or Q6_K; widths multiples of 256) fits the GEMM */
     return true;
 }
 
@@ -1945,18 +1977,48 @@ static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n, 
     return enqueue_multi(g, go, oimg);
 }
 
+/* --precision fast (model_cuda.cu:5002-5022): a pass of fast_rows rows or more of a gpu_fast model runs its experts as
+   a grouped GEMM on the matrix cores. Its sums run in another order, and its inputs in bf16, so its outputs are close
+   to the exact kernels' but not their bits. */
+static bool rows_fast(const vitna_cuda_model* g, int n) { return g->fast && (size_t)n >= g->fast_rows; }
+
+/* The experts of a fast pass of n rows as rt[0..n) routes them: the normalized rows (g->xn) rounded to bf16, the
+   (row, slot) pairs grouped by expert, the prefill's grouped GEMM (gate/up with SwiGLU, then down times the
+   weight), each row's K parts added onto its residual row in slot order. The working buffers are the prefill's,
+   reserved for n rows beforehand (prefill_reserve). */
+static hipError_t enqueue_fast_experts(vitna_cuda_model* g, int layer, int n, const route_out* rt) {
+    const dlayer& d = g->L[layer];
+    const pf_bufs& b = g->pf;
+    hipStream_t s = g->stream;
+    if ((size_t)n > g->pf_cap) return hipErrorInvalidValue;
+    hipError_t e = launch_prefill_bf16(g->xn, b.xb, (size_t)n * g->H, s);
+    if (e == hipSuccess) e = launch_group(rt, n, g->E, g->K, n, b.count, b.pairs, s);
+    if (e == hipSuccess) e = launch_prefill_plan(b.count, g->E, b.off, b.tiles, b.ntiles, s);
+    prefill_args a;
+    a.gate = d.gate; a.up = d.up; a.down = d.down;
+    a.xb = b.xb; a.rt = rt; a.count = b.count; a.pairs = b.pairs; a.off = b.off;
+    a.tiles = b.tiles; a.n_tiles = b.ntiles; a.act = b.act; a.ypart = b.ypart;
+    a.E = g->E; a.K = g->K; a.cap = n; a.n = n;
+    if (e == hipSuccess) e = launch_prefill_gemm(a, true, s);
+    if (e == hipSuccess) e = launch_prefill_gemm(a, false, s);
+    if (e == hipSuccess) e = launch_prefill_sum(b.ypart, g->x, n, g->K, g->H, s);
+    return e;
+}
+
 /* The grouped experts of the pass's n rows, routed as g->rt[0..n) holds it, added onto the residual rows (or,
    defer_sum, left in g->ypart for the next kernel that reads the rows to add). */
-static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n, bool defer_sum, bool split_done = false) {
+static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n, bool defer_sum, bool split_done = false,
+                                       const route_out* rt = nullptr) {
     const dlayer& d = g->L[layer];
-    hipError_t e = launch_group(g->rt, n, g->E, g->K, ROWS_MAX, g->grp_count, g->grp_pairs, g->stream);
+    if (!rt) rt = g->rt;
+    hipError_t e = launch_group(rt, n, g->E, g->K, ROWS_MAX, g->grp_count, g->grp_pairs, g->stream);
     if (e != hipSuccess) return e;
     /* every expert set check_shapes accepts (quantized, widths multiples of 256) fits the matrix-core kernels */
     if (!gmma_fits(d.gate, d.up, d.down)) return hipErrorInvalidValue;
     if (!split_done) e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
     gmma_args m{};
     m.gate = d.gate; m.up = d.up; m.down = d.down;
-    m.xs = g->gm_xs; m.xsum = g->gm_xsum; m.as = g->gm_as; m.asum = g->gm_asum; m.rt = g->rt; m.count = g->grp_count; m.pairs = g->grp_pairs;
+    m.xs = g->gm_xs; m.xsum = g->gm_xsum; m.as = g->gm_as; m.asum = g->gm_asum; m.rt = rt; m.count = g->grp_count; m.pairs = g->grp_pairs;
     m.E = g->E; m.K = g->K; m.cap = ROWS_MAX; m.n = n; m.ypart = g->ypart;
     if (e == hipSuccess) e = launch_gmma_in(m, g->stream);
     if (e == hipSuccess) e = launch_gmma_down(m, g->stream);
@@ -2141,6 +2203,10 @@ extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t l
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
     if (g->ec.on) return cached_rows_experts(g, (int)layer, (int)n, ids, weights, (int)k, guess, err, err_len);
+    if (rows_fast(g, (int)n)) {
+        if (!prefill_reserve(g, n, err, err_len) || !put_routing(g, n, ids, weights, k, err, err_len)) return false;
+        return check_launch(g, enqueue_fast_experts(g, (int)layer, (int)n, g->rt), "the rows' experts (grouped GEMM)", err, err_len);
+    }
     if (!put_routing(g, n, ids, weights, k, err, err_len)) return false;
     return check_launch(g, enqueue_rows_experts(g, (int)layer, (int)n, false), "the rows' experts", err, err_len);
 }
@@ -2161,24 +2227,39 @@ extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, f
 /* A whole decode step of n rows on the device, routing included. */
 static hipError_t enqueue_rows_step_body(vitna_cuda_model* g, int n) {
     hipError_t e = launch_embed_rows(g->embed, g->rows_dev, n, g->x, g->stream);
-    /* each layer's experts' outputs are added onto the rows by the next layer's (or the head's) norm kernel */
+    const bool fast = rows_fast(g, n);
+    /* each layer's experts' outputs are added onto the rows by the next layer's (or the head's) norm kernel; a fast
+       pass adds them at once */
+    const float* pending = nullptr;
     for (int l = 0; e == hipSuccess && l < g->NL; l++) {
-        e = enqueue_rows_attention(g, l, n, l ? g->ypart : nullptr);
-        /* several rows: the top-k kernel also splits the normed rows for the grouped experts */
+        e = enqueue_rows_attention(g, l, n, pending);
+        /* every layer's routing is kept (rows_rt, the last layer's in rt), the checkers read it */
+        route_out* rt = l + 1 < g->NL ? g->rows_rt + (size_t)l * ROWS_MAX : g->rt;
         const dlayer& d = g->L[l];
+        if (fast) {
+            if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, n, g->x, g->xn, true, nullptr, rt);
+            if (e == hipSuccess && n == 1) e = launch_topk(g->rlogits, 1, g->E, g->K, g->renorm, rt, g->stream);
+            if (e == hipSuccess) e = enqueue_fast_experts(g, l, n, rt);
+            pending = nullptr;
+            continue;
+        }
+        /* several rows: the top-k kernel also splits the normed rows for the grouped experts */
         const bool fused_split = n > 1 && gmma_fits(d.gate, d.up, d.down);
         const topk_split sp = {g->xn, g->gm_xs, g->gm_xsum, (int)g->H, gmma_gran(d.gate.dtype)};
-        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, n, g->x, g->xn, true, fused_split ? &sp : nullptr);
-        if (e == hipSuccess && n == 1) e = launch_topk(g->rlogits, 1, g->E, g->K, g->renorm, g->rt, g->stream);
-        if (e == hipSuccess) e = enqueue_rows_experts(g, l, n, true, fused_split);
+        if (e == hipSuccess) e = enqueue_route(g, l, g->rlogits, n, g->x, g->xn, true, fused_split ? &sp : nullptr, rt);
+        if (e == hipSuccess && n == 1) e = launch_topk(g->rlogits, 1, g->E, g->K, g->renorm, rt, g->stream);
+        if (e == hipSuccess) e = enqueue_rows_experts(g, l, n, true, fused_split, rt);
+        pending = g->ypart;
     }
-    if (e == hipSuccess) e = enqueue_rows_head(g, n, g->NL ? g->ypart : nullptr);
+    if (e == hipSuccess) e = enqueue_rows_head(g, n, pending);
     return e;
 }
 
 static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_len) {
     if (!ensure_tiled(g, err, err_len)) return false;
-    if (g->rows_graph_n == n && g->rows_graph_shared == g->rows_shared_seq) return true;
+    /* a fast pass's working buffers exist before the capture (growing them later would free what the graph uses) */
+    if (rows_fast(g, n) && !prefill_reserve(g, (size_t)n, err, err_len)) return false;
+    if (g->rows_graph_n == n && g->rows_graph_shared == g->rows_shared_seq && g->rows_graph_fast == rows_fast(g, n)) return true;
     if (g->rows_graph_n) {
         HIP_TRY(hipStreamSynchronize(g->stream), "before recapturing the rows step");
         (void)hipGraphExecDestroy(g->rows_graph);
@@ -2197,6 +2278,7 @@ static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_
     HIP_TRY(e3, "instantiating the rows step's graph");
     g->rows_graph_src = graph;
     g->rows_graph_n = n;
+    g->rows_graph_fast = rows_fast(g, n);
     g->rows_graph_shared = g->rows_shared_seq;
     return true;
 }

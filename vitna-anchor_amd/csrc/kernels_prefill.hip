@@ -39,6 +39,7 @@
 
 #include "vitna_kernels.h"
 
+#include <algorithm>
 #include <type_traits>
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -278,7 +279,134 @@ __device__ __forceinline__ void dequant16(const u32x4 q, float d, u32x4& lo, u32
     hi = u32x4{o[4], o[5], o[6], o[7]};
 }
 
-template <bool GU>
+__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 p = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, p);
+}
+
+/* One thread's share of a stage's weights in the shared-stage kernel: 32 consecutive weights of one row (the
+   32-column group g of the row), loaded from the planes a stage ahead and widened into four 16-byte chunks of
+   bf16 (eight weights each, in column order). The widening is the reference's, each weight rounded once more,
+   to bf16, at the end (engine/src/quant.c:40-188):
+     Q8_0  q * d;
+     Q4_K  (d * sc) * q - dmin * mn, the product rounded before the subtraction;
+     Q6_K  (d * sc) * q, q = (low | high << 4) - 32, a scale every 16 weights.
+   Every thread issues the same number of loads a stage (LOADS), which the stage's wait counts. */
+template <int DT>
+struct pf_bgroup;
+
+template <>
+struct pf_bgroup<VITNA_DTYPE_Q8_0> {
+    static constexpr int LOADS = 3;
+    u32x4 q0, q1;
+    uint32_t d;
+    __device__ __forceinline__ void load(const qmat& m, int e, int row, int g) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(m.p[0] + (size_t)e * m.estride[0] + ((size_t)row * m.nb + g) * 32);
+        q0 = src[0];
+        q1 = src[1];
+        d = reinterpret_cast<const uint16_t*>(m.p[1] + (size_t)e * m.estride[1])[(size_t)row * m.nb + g];
+    }
+    __device__ __forceinline__ void widen(u32x4 (&c)[4]) const {
+        const float df = f16_bits_to_f32(d);
+        dequant16(q0, df, c[0], c[1]);
+        dequant16(q1, df, c[2], c[3]);
+    }
+};
+
+template <>
+struct pf_bgroup<VITNA_DTYPE_Q4_K> {
+    static constexpr int LOADS = 3;
+    u32x4 q0, q1, hd; /* the group's 32 quant bytes (one nibble each), the super-block's header */
+    int gi;
+    __device__ __forceinline__ void load(const qmat& m, int e, int row, int g) {
+        const size_t blk = (size_t)row * m.nb + (g >> 3);
+        gi = g & 7;
+        const u32x4* src = reinterpret_cast<const u32x4*>(m.p[0] + (size_t)e * m.estride[0] + blk * 128 + 32 * (gi >> 1));
+        q0 = src[0];
+        q1 = src[1];
+        hd = *reinterpret_cast<const u32x4*>(m.p[1] + (size_t)e * m.estride[1] + blk * 16);
+    }
+    __device__ __forceinline__ void widen(u32x4 (&c)[4]) const {
+        /* header: d, dmin (f16), then twelve bytes of 6-bit scales and mins (quant.c:115) */
+        const uint32_t s03 = hd[1], s47 = hd[2], s8b = hd[3];
+        auto byte = [](uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); };
+        int sc, mn;
+        if (gi < 4) {
+            sc = byte(s03, gi) & 63;
+            mn = byte(s47, gi) & 63;
+        } else {
+            sc = (byte(s8b, gi - 4) & 15) | ((byte(s03, gi - 4) >> 6) << 4);
+            mn = (byte(s8b, gi - 4) >> 4) | ((byte(s47, gi - 4) >> 6) << 4);
+        }
+        const float d1 = f16_bits_to_f32(hd[0] & 0xffffu) * (float)sc, m1 = f16_bits_to_f32(hd[0] >> 16) * (float)mn;
+        const int sh = 4 * (gi & 1);
+        const uint32_t w[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++) {
+            uint32_t o[4];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t v = (w[2 * ch + h] >> sh) & 0x0f0f0f0fu;
+                float f[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float prod = d1 * (float)((v >> (8 * i)) & 0xffu);
+                    f[i] = prod - m1;
+                }
+                o[2 * h] = pack_bf16(f[0], f[1]);
+                o[2 * h + 1] = pack_bf16(f[2], f[3]);
+            }
+            c[ch] = u32x4{o[0], o[1], o[2], o[3]};
+        }
+    }
+};
+
+template <>
+struct pf_bgroup<VITNA_DTYPE_Q6_K> {
+    static constexpr int LOADS = 6;
+    u32x4 l0, l1, h0, h1; /* the group's 32 low-nibble bytes and 32 high-bit bytes */
+    uint32_t sc, d;       /* its two 16-weight scales (int8), the super-block's d (f16) */
+    int r;
+    __device__ __forceinline__ void load(const qmat& m, int e, int row, int g) {
+        const size_t blk = (size_t)row * m.nb + (g >> 3);
+        const int gi = g & 7, h = gi >> 2;
+        r = gi & 3;
+        const u32x4* ql = reinterpret_cast<const u32x4*>(m.p[0] + (size_t)e * m.estride[0] + blk * 128 + 64 * h + 32 * (r & 1));
+        const u32x4* qh = reinterpret_cast<const u32x4*>(m.p[1] + (size_t)e * m.estride[1] + blk * 64 + 32 * h);
+        l0 = ql[0];
+        l1 = ql[1];
+        h0 = qh[0];
+        h1 = qh[1];
+        sc = *reinterpret_cast<const uint16_t*>(m.p[2] + (size_t)e * m.estride[2] + blk * 16 + 8 * h + 2 * r);
+        d = reinterpret_cast<const uint16_t*>(m.p[3] + (size_t)e * m.estride[3])[blk];
+    }
+    __device__ __forceinline__ void widen(u32x4 (&c)[4]) const {
+        const float dd = f16_bits_to_f32(d);
+        const float ds[2] = {dd * (float)(int8_t)(sc & 0xffu), dd * (float)(int8_t)(sc >> 8)};
+        const int sl = 4 * (r >> 1), shh = 2 * r;
+        const uint32_t lw[8] = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+        const uint32_t hw[8] = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+#pragma unroll
+        for (int ch = 0; ch < 4; ch++) {
+            const float s = ds[ch >> 1];
+            uint32_t o[4];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t lo = (lw[2 * ch + h] >> sl) & 0x0f0f0f0fu, hi = (hw[2 * ch + h] >> shh) & 0x03030303u;
+                const uint32_t q = lo | (hi << 4);
+                float f[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) f[i] = s * (float)((int)((q >> (8 * i)) & 0xffu) - 32);
+                o[2 * h] = pack_bf16(f[0], f[1]);
+                o[2 * h + 1] = pack_bf16(f[2], f[3]);
+            }
+            c[ch] = u32x4{o[0], o[1], o[2], o[3]};
+        }
+    }
+};
+
+template <bool GU, int DT>
 __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[(PF_A_STAGES + 2) * PF_TILE_BYTES];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -293,7 +421,6 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
     const int e = tl >> 16, m0 = (tl & 0xffff) * PF_BM;
     const int cnt = a.count[e];
     const int pbase = a.off[e];
-    const int nb = KD / 32;
 
     /* A: this lane's four 16-byte global-to-LDS loads a stage */
     const uint8_t* asrc[4];
@@ -304,12 +431,10 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
         const uint16_t* row = GU ? a.xb + (size_t)(a.pairs[(size_t)e * a.cap + pa] / ROUTE_K_MAX) * H : a.act + (size_t)(pbase + pa) * I;
         asrc[i] = reinterpret_cast<const uint8_t*>(row) + 16 * c;
     }
-    /* B: this thread's weight row bn and block bh of the stage (32 quants, one scale) */
+    /* B: this thread's weight row bn and 32-column half bh of the stage */
     const int bn = tid >> 1, bh = tid & 1;
     const qmat& wmat = GU ? (bn < PF_BN / 2 ? a.gate : a.up) : a.down;
     const int wrow = GU ? nt * (PF_BN / 2) + (bn % (PF_BN / 2)) : nt * PF_BN + bn;
-    const u32x4* bsrc = reinterpret_cast<const u32x4*>(wmat.p[0] + (size_t)e * wmat.estride[0] + ((size_t)wrow * nb + bh) * 32);
-    const uint16_t* dsrc = reinterpret_cast<const uint16_t*>(wmat.p[1] + (size_t)e * wmat.estride[1]) + (size_t)wrow * nb + bh;
 
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
     const uint32_t bstage0 = lds0 + PF_A_STAGES * PF_TILE_BYTES;
@@ -319,24 +444,16 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
         for (int i = 0; i < 4; i++)
             __builtin_amdgcn_global_load_lds((glb_void)(asrc[i] + (size_t)s * 128), (lds_void)(base + (wv * 4 + i) * 1024), 16, 0, 0);
     };
-    u32x4 bq0, bq1;
-    uint32_t bd;
-    auto load_b = [&](int s) {
-        bq0 = bsrc[4 * s];
-        bq1 = bsrc[4 * s + 1];
-        bd = dsrc[2 * s];
-    };
-    /* dequantize the loaded stage into B stage buffer s & 1: row bn, chunks 4 bh .. 4 bh + 3 */
+    pf_bgroup<DT> bw;
+    auto load_b = [&](int s) { bw.load(wmat, e, wrow, 2 * s + bh); };
+    /* widen the loaded stage into B stage buffer s & 1: row bn, chunks 4 bh .. 4 bh + 3 */
     auto store_b = [&](int s) {
-        const float d = f16_bits_to_f32(bd);
-        u32x4 c0, c1, c2, c3;
-        dequant16(bq0, d, c0, c1);
-        dequant16(bq1, d, c2, c3);
+        u32x4 c[4];
+        bw.widen(c);
         const uint32_t rowb = bstage0 + (s & 1) * PF_TILE_BYTES + bn * 128;
-        asm volatile("ds_write_b128 %0, %1" ::"v"(rowb + (chunk_pos(bn, 4 * bh) << 4)), "v"(c0) : "memory");
-        asm volatile("ds_write_b128 %0, %1" ::"v"(rowb + (chunk_pos(bn, 4 * bh + 1) << 4)), "v"(c1) : "memory");
-        asm volatile("ds_write_b128 %0, %1" ::"v"(rowb + (chunk_pos(bn, 4 * bh + 2) << 4)), "v"(c2) : "memory");
-        asm volatile("ds_write_b128 %0, %1" ::"v"(rowb + (chunk_pos(bn, 4 * bh + 3) << 4)), "v"(c3) : "memory");
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            asm volatile("ds_write_b128 %0, %1" ::"v"(rowb + (chunk_pos(bn, 4 * bh + j) << 4)), "v"(c[j]) : "memory");
     };
 
     /* this wave's 64 x 128: A rows wmi * 64 + 32 i + lane % 32; B rows brow[k] (for gate/up: k = 0, 1 gate
@@ -409,7 +526,7 @@ __global__ __launch_bounds__(PF_THREADS) void prefill_gemm_kernel(prefill_args a
     };
     for (int s = 0; s < S; s++) {
         /* A of stage s landed (the seven loads of stage s + 1 may be in flight); this thread's B writes done */
-        if (s + 1 < S) asm volatile("s_waitcnt vmcnt(7) lgkmcnt(0)" ::: "memory");
+        if (s + 1 < S) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(pf_bgroup<DT>::LOADS + 4) : "memory");
         else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         if (first) mma(s);
@@ -764,6 +881,21 @@ hipError_t launch_prefill_norm_router(const float* x, const float* nw, const flo
     return hipGetLastError();
 }
 
+/* The bf16 rounding of n fp32 values (the normalized rows a pass of rows hands the grouped GEMM), four a thread. */
+__global__ __launch_bounds__(256) void prefill_bf16_kernel(const float4* __restrict__ x, uint2* __restrict__ xb, size_t n4) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+        const float4 v = x[i];
+        xb[i] = uint2{bf16_rne(v.x) | (bf16_rne(v.y) << 16), bf16_rne(v.z) | (bf16_rne(v.w) << 16)};
+    }
+}
+
+hipError_t launch_prefill_bf16(const float* x, uint16_t* xb, size_t n, hipStream_t s) {
+    if (!n || n % 4) return hipErrorInvalidValue;
+    const size_t n4 = n / 4, blocks = std::min<size_t>((n4 + 255) / 256, 4096);
+    prefill_bf16_kernel<<<(unsigned)blocks, 256, 0, s>>>(reinterpret_cast<const float4*>(x), reinterpret_cast<uint2*>(xb), n4);
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill_plan(const int* count, int E, int* off, int* tiles, int* n_tiles, hipStream_t s) {
     if (E < 1 || E > ROUTE_E_MAX) return hipErrorInvalidValue;
     prefill_plan_kernel<<<1, 256, 0, s>>>(count, E, off, tiles, n_tiles);
@@ -818,24 +950,38 @@ hipError_t launch_prefill_sum(const uint16_t* ypart, float* x, int n, int K, int
 
 int prefill_max_tiles(int n, int K, int E) { return (n * K + PF_BM - 1) / PF_BM + E; }
 
+template <bool GU>
+static hipError_t launch_shared_stage(const prefill_args& a, int dt, unsigned blocks, hipStream_t s) {
+    switch (dt) {
+        case VITNA_DTYPE_Q8_0: prefill_gemm_kernel<GU, VITNA_DTYPE_Q8_0><<<blocks, PF_THREADS, 0, s>>>(a); break;
+        case VITNA_DTYPE_Q4_K: prefill_gemm_kernel<GU, VITNA_DTYPE_Q4_K><<<blocks, PF_THREADS, 0, s>>>(a); break;
+        case VITNA_DTYPE_Q6_K: prefill_gemm_kernel<GU, VITNA_DTYPE_Q6_K><<<blocks, PF_THREADS, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill_gemm(const prefill_args& a, bool gate_up, hipStream_t s) {
     const int H = a.gate.cols, I = a.gate.rows;
-    const qmat* parts[3] = {&a.gate, &a.up, &a.down};
-    for (const qmat* q : parts)
-        if (q->dtype != VITNA_DTYPE_Q8_0) return hipErrorInvalidValue;
+    auto quant = [](int t) { return t == VITNA_DTYPE_Q8_0 || t == VITNA_DTYPE_Q4_K || t == VITNA_DTYPE_Q6_K; };
+    if (!quant(a.gate.dtype) || a.up.dtype != a.gate.dtype || !quant(a.down.dtype)) return hipErrorInvalidValue;
     if (H % PF_BN || I % (PF_BN / 2) || a.up.rows != I || a.up.cols != H || a.down.rows != H || a.down.cols != I) return hipErrorInvalidValue;
+    /* a K-quant stage (64 columns) lies within one 256-column super-block */
+    if ((a.gate.dtype != VITNA_DTYPE_Q8_0 && H % 256) || (a.down.dtype != VITNA_DTYPE_Q8_0 && I % 256)) return hipErrorInvalidValue;
     if (a.K < 1 || a.K > ROUTE_K_MAX || a.cap > 65536 * PF_BM || a.E > ROUTE_E_MAX) return hipErrorInvalidValue;
     const int NT = gate_up ? I / (PF_BN / 2) : H / PF_BN;
     const size_t blocks = ((size_t)NT * prefill_max_tiles(a.n, a.K, a.E) + 7) / 8 * 8;
     if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    /* the kernel that widens each wave's own weights reads the experts' tiled copy, made by the allocating entry
-       points; without it (the no-allocation entry point before any of them ran) the shared-stage kernel reads
-       the planes. Both give the same bits: the same products, summed in the same order. */
-    const bool wide = a.gate.tiled && a.up.tiled && a.down.tiled && H % 256 == 0 && I % 256 == 0 &&
+    /* Q8_0 experts with their tiled copy (made by the allocating entry points) take the kernel that widens each
+       wave's own weights; K-quant experts, and Q8_0 ones without the copy (the no-allocation entry point before any
+       allocating one ran), the shared-stage kernel, which reads the planes. On Q8_0 the two give the same bits: the
+       same products, summed in the same order. */
+    const bool q8 = a.gate.dtype == VITNA_DTYPE_Q8_0 && a.down.dtype == VITNA_DTYPE_Q8_0;
+    const bool wide = q8 && a.gate.tiled && a.up.tiled && a.down.tiled && H % 256 == 0 && I % 256 == 0 &&
                       (size_t)a.n * a.K * I * 2 < ((size_t)1 << 32) && (size_t)a.n * H * 2 < ((size_t)1 << 32);
     if (wide && gate_up) prefill_wgemm_kernel<true><<<(unsigned)blocks, PW_THREADS, 0, s>>>(a);
     else if (wide) prefill_wgemm_kernel<false><<<(unsigned)blocks, PW_THREADS, 0, s>>>(a);
-    else if (gate_up) prefill_gemm_kernel<true><<<(unsigned)blocks, PF_THREADS, 0, s>>>(a);
-    else prefill_gemm_kernel<false><<<(unsigned)blocks, PF_THREADS, 0, s>>>(a);
+    else if (gate_up) return launch_shared_stage<true>(a, a.gate.dtype, (unsigned)blocks, s);
+    else return launch_shared_stage<false>(a, a.down.dtype, (unsigned)blocks, s);
     return hipGetLastError();
 }

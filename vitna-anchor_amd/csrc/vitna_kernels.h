@@ -286,6 +286,8 @@ hipError_t launch_prefill_router(const float* xn, const float* R, float* logits,
 /* Both in one kernel, the fp32 normalized rows kept in LDS (hidden up to 2048; hipErrorNotSupported above). */
 hipError_t launch_prefill_norm_router(const float* x, const float* nw, const float* R, float* logits, uint16_t* xb, int n, int E,
                                      int H, float eps, hipStream_t s);
+/* xb = the bf16 rounding (to nearest even) of x, n values (n a multiple of 4). */
+hipError_t launch_prefill_bf16(const float* x, uint16_t* xb, size_t n, hipStream_t s);
 hipError_t launch_prefill_plan(const int* count, int E, int* off, int* tiles, int* n_tiles, hipStream_t s);
 int prefill_max_tiles(int n, int K, int E);
 /* x[row] += the sum over slots k (in order) of the bf16 parts ypart[row * K + k]. */

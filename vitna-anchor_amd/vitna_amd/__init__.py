@@ -342,6 +342,9 @@ def _hip():
         "vitna_hip_rows_project": (C.c_bool, [P, C.c_size_t, C.c_int, _FP, C.c_size_t, _FP, *E]),
         "vitna_hip_routing": (C.c_bool, [P, C.c_size_t, _FP, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _FP, *E]),
         "vitna_hip_step_routing": (C.c_bool, [P, C.c_size_t, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _FP, *E]),
+        "vitna_hip_rows_routing": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.POINTER(C.c_int32), C.POINTER(C.c_int32), _FP,
+                                              *E]),
+        "vitna_cuda_test_fast_rows": (None, [P, C.c_size_t]),
         "vitna_hip_attention_io": (C.c_bool, [P, C.c_size_t, _FP, _FP, *E]),
         "vitna_hip_gguf_open": (P, [C.c_char_p, C.POINTER(GgufInfo), *E]),
         "vitna_hip_gguf_count": (C.c_size_t, [P]),
@@ -400,10 +403,12 @@ def _i32(a):
 class Device:
     """A model uploaded to the GPU through vitna_cuda_create."""
 
-    def __init__(self, model, expert_cache_bytes=0):
+    def __init__(self, model, expert_cache_bytes=0, fast=False):
         """expert_cache_bytes: 0 keeps every expert resident; fewer bytes than the experts take puts them behind a
-        cache of slots (the reference's expert cache), served by moe_route / moe_experts."""
+        cache of slots (the reference's expert cache), served by moe_route / moe_experts. fast: the model's gpu_fast
+        (the reference's --precision fast): passes of 64 rows or more run their experts as the grouped GEMM."""
         self.model = model
+        model.m.gpu_fast = bool(fast)
         self.lib = hip()
         self.err = C.create_string_buffer(512)
         cfg = model.cfg
@@ -552,6 +557,22 @@ class Device:
         w = np.empty(K, np.float32)
         self._ok(self.lib.vitna_hip_step_routing(self.g, layer, _i32(ch), _i32(ids), fptr(w), self.err, 512))
         return ch, ids, w
+
+    def rows_routing(self, layer, row):
+        """(chosen largest first, ids in order, weights) of row at layer in the last device-routed rows step."""
+        K = self.model.cfg.n_experts_used
+        ch = np.empty(K, np.int32)
+        ids = np.empty(K, np.int32)
+        w = np.empty(K, np.float32)
+        self._ok(self.lib.vitna_hip_rows_routing(self.g, layer, row, _i32(ch), _i32(ids), fptr(w), self.err, 512))
+        return ch, ids, w
+
+    def rows_max(self):
+        return int(self.lib.vitna_cuda_moe_rows_max(self.g))
+
+    def test_fast_rows(self, n):
+        """The reference's test hook: on a fast model, passes of n rows or more take the grouped GEMM."""
+        self.lib.vitna_cuda_test_fast_rows(self.g, n)
 
     def attention_io(self, row=0):
         """(q before its norm and rotation, attention output) of row at the last layer of the last step or pass."""
