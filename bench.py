@@ -68,7 +68,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-extra", action="store_true", help="measure configs[2] only")
-    ap.add_argument("--only", choices=["0", "1", "3", "4", "cache"],
+    ap.add_argument("--only", choices=["0", "1", "3", "4", "4k", "cache"],
                     help="run one of the other configs alone (profiling), or the expert cache's decode, and print its object")
     ap.add_argument("--cache-frac", type=float, default=0.5, help="--only cache: the share of the experts the cache holds")
     args = ap.parse_args()
@@ -82,6 +82,8 @@ def main():
     if args.only:
         if args.only in ("0", "1"):
             res = bench_layer(va, int(args.only), reps=args.steps)
+        elif args.only == "4k":
+            res = bench_prefill_kquant(va, reps=args.steps)
         elif args.only == "4":
             res = bench_prefill(va, reps=args.steps)
         elif args.only == "cache":
@@ -193,6 +195,7 @@ def main():
         extra = {"3": bench_ragged(va, model, dev, args.steps)}
         dev.close()
         extra["4"] = bench_prefill(va)
+        extra["4_kquant"] = bench_prefill_kquant(va)
         extra["0"] = bench_layer(va, 0)
         extra["1"] = bench_layer(va, 1)
         extra["expert_cache"] = bench_cache(va, 8, 2, 0.5, L, model, kc, vc)
@@ -437,6 +440,32 @@ def bench_prefill(va, reps=10):
                              "note": "both GEMMs: 2 n K (3 I H) flops over their summed duration"},
                 "tflops_whole": round(flops / tot / 1e6, 1),
                 "mfma_probe_TFLOPs": round(probe, 1), "frac_of_probe": round(flops / gemm_us / 1e6 / probe, 4)}
+    finally:
+        dev.close()
+        model.free()
+
+
+def bench_prefill_kquant(va, reps=10):
+    """The same prefill (4096 rows, top-8 of 128, hidden 2048, expert width 768) with Q4_K gate/up and Q6_K down, the
+    Q4_K_M convention: the grouped GEMM's K-quant form, which also serves the reference's fast passes of 64 to 1024
+    rows (gpu_fast). Not a BASELINE config; reported beside configs[4]."""
+    spec = dict(va.CONFIGS[4], dt_gate_up=va.Q4_K, dt_down=va.Q6_K)
+    model = va.Model(va.shape(**spec), 20260105, threads=16)
+    dev = va.Device(model)
+    try:
+        n = 4096
+        tot, ph = dev.time_prefill(0, n, seed=12, reps=reps)
+        cfg = model.cfg
+        flops = 2.0 * n * cfg.n_experts_used * 3 * cfg.intermediate * cfg.hidden
+        gemm_us = ph[2] + ph[3]
+        log("Q4_K/Q6_K prefill of %d rows %.1f us (norm+router %.1f, routing %.1f, gate/up %.1f, down %.1f, sum %.1f)"
+            % (n, tot, *ph))
+        return {"workload": "prefill of 4096 rows through one Qwen3-shaped MoE layer, Q4_K gate/up + Q6_K down experts "
+                            "(the grouped GEMM's K-quant form; not a BASELINE config)", "value": round(n / tot * 1e6, 1),
+                "unit": "tok/s", "us": round(tot, 1), "phases_us": {k: round(v, 1) for k, v in zip(
+                    ["norm+router", "routing+grouping", "gate/up GEMM", "down GEMM", "ordered sum"], ph)},
+                "roofline": {"bound": "mfma", "achieved": round(flops / gemm_us / 1e6, 1), "peak": 2500.0,
+                             "unit": "TFLOP/s", "frac": round(flops / gemm_us / 1e6 / 2500.0, 4)}}
     finally:
         dev.close()
         model.free()
