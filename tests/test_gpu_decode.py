@@ -130,6 +130,14 @@ SMALL = {
     "q4km": dict(n_layers=3, hidden=512, intermediate=256, n_heads=8, n_kv_heads=2, head_dim=128, vocab=1000,
                  n_experts=32, n_experts_used=8, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q6_K, norm_std=0.1,
                  ctx=200, seqs=2, kv_host=1),
+    # expert width 2048 with 8 experts a token: 512 (expert, slice) items a down row, 8 a lane (the down kernel's
+    # one-row-at-a-time form), Q6_K and Q4_K down
+    "wide_i": dict(n_layers=2, hidden=512, intermediate=2048, n_heads=8, n_kv_heads=2, head_dim=128, vocab=1000,
+                   n_experts=16, n_experts_used=8, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q6_K, norm_std=0.1,
+                   ctx=200, seqs=2, kv_host=1),
+    "wide_i_q4": dict(n_layers=2, hidden=512, intermediate=2048, n_heads=8, n_kv_heads=2, head_dim=128, vocab=1000,
+                      n_experts=16, n_experts_used=8, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q4_K, norm_std=0.1,
+                      ctx=200, seqs=2, kv_host=1),
 }
 
 
@@ -150,7 +158,8 @@ def prefilled(name, seed, pos, seq=0):
     return model, dev, kc, vc
 
 
-@pytest.mark.parametrize("name,pos,token", [("q8", 0, 3), ("q8", 65, 17), ("q4km", 130, 999), ("q4km", 63, 4)])
+@pytest.mark.parametrize("name,pos,token", [("q8", 0, 3), ("q8", 65, 17), ("q4km", 130, 999), ("q4km", 63, 4),
+                                            ("wide_i", 90, 12), ("wide_i_q4", 40, 77)])
 def test_abi_step_layer_by_layer(name, pos, token):
     """model.c's moe_step_on_gpu, played by the test: the device runs each layer up to its router, the host routes
     (the reference's rule), the device runs the experts. Router logits bit-exact given the device's residual; the
@@ -198,7 +207,8 @@ def C_f32(addr):
 
 
 @pytest.mark.parametrize("persistent", [False, True], ids=["graph", "persistent"])
-@pytest.mark.parametrize("name,pos,token", [("q4km", 150, 7), ("q8", 79, 250), ("q4km", 192, 11), ("q4km", 199, 5)])
+@pytest.mark.parametrize("name,pos,token", [("q4km", 150, 7), ("q8", 79, 250), ("q4km", 192, 11), ("q4km", 199, 5),
+                                            ("wide_i", 120, 3)])
 def test_device_step_matches_cpu(name, pos, token, persistent):
     """vitna_hip_moe_step (device routing, one graph): logits within tolerance of the CPU step, replayed at two
     positions through the same graph. Cases: mid-chunk; the last position of the context (q8: 79 of 80, q4km:

@@ -394,9 +394,12 @@ hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s) {
 /* One output row a wave: every (expert, slice) item of the row among the 64
    lanes, IPL items a lane, each lane's items fixed for every row, so its
    activations stay in registers. The weighted sum over experts is reduced
-   across the wave. */
+   across the wave. A wave has NR rows' weights in flight at once: two, or one
+   where a lane's items are many (IPL 6 and more: two rows' weights and every
+   item's activations would not fit the registers). */
 template <int DT, int IPL>
 __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) {
+    constexpr int NR = IPL >= 6 ? 1 : 2;
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
     const int H = a.down.rows, I = a.down.cols, S = I / 32, N = a.K * S;
@@ -413,16 +416,16 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
         wk[j] = ok ? a.rt->cw[k] : 0.0f;
         load_xslice(DT, tk[j], a.act + (size_t)k * I, xs[j]);
     }
-    for (int r0 = wave; r0 < H; r0 += 2 * nwaves) {
-        qraw q[2][IPL];
+    for (int r0 = wave; r0 < H; r0 += NR * nwaves) {
+        qraw q[NR][IPL];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < NR; h++) {
             const int r = r0 + h * nwaves < H ? r0 + h * nwaves : H - 1;
 #pragma unroll
             for (int j = 0; j < IPL; j++) slice_load<DT>(a.down, ek[j], r, tk[j], q[h][j]);
         }
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < NR; h++) {
             float p = 0.f;
 #pragma unroll
             for (int j = 0; j < IPL; j++) p = fmaf(wk[j], slice_dot<DT>(q[h][j], tk[j], xs[j]), p);
@@ -435,7 +438,7 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
 
 template <int DT, int IPL>
 static hipError_t edn_launch(const experts_down_args& a, hipStream_t s) {
-    const int waves = (a.down.rows + 1) / 2;
+    const int waves = IPL >= 6 ? a.down.rows : (a.down.rows + 1) / 2;
     experts_down_kernel<DT, IPL><<<(waves + 3) / 4, 256, 0, s>>>(a);
     return hipGetLastError();
 }

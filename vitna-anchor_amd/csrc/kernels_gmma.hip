@@ -271,64 +271,72 @@ template <int DT, int NM, int HALF>
 __device__ __forceinline__ void gcompute(const gstep<DT> s[NM], const u32x4 av[2], const sv<ggran<DT>::per> S[GM_TT],
                                          f32x4 acc[NM]) {
     constexpr int PER = ggran<DT>::per, CPB = ggran<DT>::g / 4; /* scale blocks a step, chunks a block */
-    f32x4 P[PER][NM];
+    /* Scale blocks a pass: Q4_K takes its four at once; Q6_K (eight blocks of 16 columns) and Q8_0 (whose step holds
+       36 registers of quants a matrix) take two at a time, which keeps their sums and weights within the register
+       file (all at once they spilled 632 and 268 bytes a lane). The sums, and the order they are folded into acc,
+       are the same either way. */
+    constexpr int BP = DT == VITNA_DTYPE_Q4_K ? PER : 2;
+    sfor<PER / BP>([&](auto gi) {
+        constexpr int B0 = decltype(gi)::value * BP;
+        f32x4 P[BP][NM];
 #pragma unroll
-    for (int b = 0; b < PER; b++)
+        for (int b = 0; b < BP; b++)
 #pragma unroll
-        for (int k = 0; k < NM; k++) P[b][k] = f32x4{0.f, 0.f, 0.f, 0.f};
-    sfor<CPB>([&](auto ui) {
-        constexpr int U = decltype(ui)::value;
-        u32x2 w[PER][NM];
-        sfor<PER>([&](auto bi) {
-            constexpr int B = decltype(bi)::value;
+            for (int k = 0; k < NM; k++) P[b][k] = f32x4{0.f, 0.f, 0.f, 0.f};
+        sfor<CPB>([&](auto ui) {
+            constexpr int U = decltype(ui)::value;
+            u32x2 w[BP][NM];
+            sfor<BP>([&](auto bi) {
+                constexpr int B = B0 + decltype(bi)::value;
 #pragma unroll
-            for (int k = 0; k < NM; k++) w[B][k] = gweights<DT, B * CPB + U>(s[k]);
+                for (int k = 0; k < NM; k++) w[B - B0][k] = gweights<DT, B * CPB + U>(s[k]);
+            });
+            sfor<BP>([&](auto bi) {
+                constexpr int B = B0 + decltype(bi)::value, T = B * CPB + U;
+                const u32x4 a = av[T >> 4];
+#pragma unroll
+                for (int k = 0; k < NM; k++) P[B - B0][k] = mma4<T & 15>(u32x2{a.x, a.y}, w[B - B0][k], P[B - B0][k]);
+            });
+            sfor<BP>([&](auto bi) {
+                constexpr int B = B0 + decltype(bi)::value, T = B * CPB + U;
+                const u32x4 a = av[T >> 4];
+#pragma unroll
+                for (int k = 0; k < NM; k++) P[B - B0][k] = mma4<T & 15>(u32x2{a.z, a.w}, w[B - B0][k], P[B - B0][k]);
+            });
         });
-        sfor<PER>([&](auto bi) {
-            constexpr int B = decltype(bi)::value, T = B * CPB + U;
-            const u32x4 a = av[T >> 4];
+        sfor<BP>([&](auto bi) {
+            constexpr int B = B0 + decltype(bi)::value;
 #pragma unroll
-            for (int k = 0; k < NM; k++) P[B][k] = mma4<T & 15>(u32x2{a.x, a.y}, w[B][k], P[B][k]);
-        });
-        sfor<PER>([&](auto bi) {
-            constexpr int B = decltype(bi)::value, T = B * CPB + U;
-            const u32x4 a = av[T >> 4];
+            for (int k = 0; k < NM; k++) {
+                if constexpr (DT == VITNA_DTYPE_Q4_K) {
+                    constexpr int g = 4 * HALF + B; /* group of the block */
+                    const uint32_t h0 = s[k].h.x, s03 = s[k].h.y, s47 = s[k].h.z, s8b = s[k].h.w;
+                    uint32_t sc, mn;
+                    if constexpr (g < 4) {
+                        sc = (s03 >> (8 * g)) & 63;
+                        mn = (s47 >> (8 * g)) & 63;
+                    } else {
+                        constexpr int j = g - 4;
+                        sc = ((s8b >> (8 * j)) & 15) | (((s03 >> (8 * j + 6)) & 3) << 4);
+                        mn = ((s8b >> (8 * j + 4)) & 15) | (((s47 >> (8 * j + 6)) & 3) << 4);
+                    }
+                    const float d1 = f16_bits_to_f32(h0 & 0xffffu) * (float)sc;
+                    const float m1 = f16_bits_to_f32(h0 >> 16) * (float)mn;
+                    const float mp = m1 + 128.0f * d1;
 #pragma unroll
-            for (int k = 0; k < NM; k++) P[B][k] = mma4<T & 15>(u32x2{a.z, a.w}, w[B][k], P[B][k]);
-        });
-    });
-    sfor<PER>([&](auto bi) {
-        constexpr int B = decltype(bi)::value;
+                    for (int i = 0; i < 4; i++) acc[k][i] = fmaf(-mp, S[i][B], fmaf(d1, P[B - B0][k][i], acc[k][i]));
+                } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
+                    const uint32_t scw = B < 4 ? s[k].sc.x : s[k].sc.y;
+                    const float ds = f16_bits_to_f32(s[k].d & 0xffffu) * (float)(int8_t)((scw >> (8 * (B & 3))) & 0xff);
 #pragma unroll
-        for (int k = 0; k < NM; k++) {
-            if constexpr (DT == VITNA_DTYPE_Q4_K) {
-                constexpr int g = 4 * HALF + B; /* group of the block */
-                const uint32_t h0 = s[k].h.x, s03 = s[k].h.y, s47 = s[k].h.z, s8b = s[k].h.w;
-                uint32_t sc, mn;
-                if constexpr (g < 4) {
-                    sc = (s03 >> (8 * g)) & 63;
-                    mn = (s47 >> (8 * g)) & 63;
+                    for (int i = 0; i < 4; i++) acc[k][i] = fmaf(ds, fmaf(-160.0f, S[i][B], P[B - B0][k][i]), acc[k][i]);
                 } else {
-                    constexpr int j = g - 4;
-                    sc = ((s8b >> (8 * j)) & 15) | (((s03 >> (8 * j + 6)) & 3) << 4);
-                    mn = ((s8b >> (8 * j + 4)) & 15) | (((s47 >> (8 * j + 6)) & 3) << 4);
+                    const float d = f16_bits_to_f32(s[k].d[B] & 0xffffu);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[k][i] = fmaf(d, fmaf(-128.0f, S[i][B], P[B - B0][k][i]), acc[k][i]);
                 }
-                const float d1 = f16_bits_to_f32(h0 & 0xffffu) * (float)sc;
-                const float m1 = f16_bits_to_f32(h0 >> 16) * (float)mn;
-                const float mp = m1 + 128.0f * d1;
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[k][i] = fmaf(-mp, S[i][B], fmaf(d1, P[B][k][i], acc[k][i]));
-            } else if constexpr (DT == VITNA_DTYPE_Q6_K) {
-                const uint32_t scw = B < 4 ? s[k].sc.x : s[k].sc.y;
-                const float ds = f16_bits_to_f32(s[k].d & 0xffffu) * (float)(int8_t)((scw >> (8 * (B & 3))) & 0xff);
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[k][i] = fmaf(ds, fmaf(-160.0f, S[i][B], P[B][k][i]), acc[k][i]);
-            } else {
-                const float d = f16_bits_to_f32(s[k].d[B] & 0xffffu);
-#pragma unroll
-                for (int i = 0; i < 4; i++) acc[k][i] = fmaf(d, fmaf(-128.0f, S[i][B], P[B][k][i]), acc[k][i]);
             }
-        }
+        });
     });
 }
 
