@@ -168,7 +168,7 @@ class Model:
         self.seed = seed
         self.ptr = synth().vitna_synth_model(C.byref(shp), seed, threads, err, 512)
         if not self.ptr:
-            raise RuntimeError(err.value.decode())
+            raise RuntimeError(err.value.decode(errors="replace"))
         self.m = self.ptr.contents
 
     @property
@@ -207,7 +207,7 @@ def write_gguf(model, directory, norm_dtype=F32, alignment=32):
     """model (a synthetic Model) written into directory as model.gguf and config.json."""
     err = C.create_string_buffer(512)
     if synth().vitna_synth_write_gguf(model.ptr, directory.encode(), norm_dtype, alignment, err, 512):
-        raise VitnaError(err.value.decode())
+        raise VitnaError(err.value.decode(errors="replace"))
     return os.path.join(directory, "model.gguf")
 
 
@@ -272,13 +272,13 @@ class GgufModel:
         self.info = GgufInfo()
         self.g = lib.vitna_hip_gguf_open(path.encode(), C.byref(self.info), self.err, 512)
         if not self.g:
-            raise VitnaError(self.err.value.decode())
+            raise VitnaError(self.err.value.decode(errors="replace"))
         cfg = config if config is not None else config_from_json(os.path.join(os.path.dirname(path), "config.json"))
         self._llama = Llama()
         if not lib.vitna_hip_gguf_llama(self.g, C.byref(cfg), ctx, seqs, C.byref(self._llama), self.err, 512):
             lib.vitna_hip_gguf_close(self.g)
             self.g = None
-            raise VitnaError(self.err.value.decode())
+            raise VitnaError(self.err.value.decode(errors="replace"))
         self.ptr = C.pointer(self._llama)
         self.m = self._llama
 
@@ -419,11 +419,11 @@ class Device:
             c = s = None
         self.g = self.lib.vitna_cuda_create(model.ptr, c, s, expert_cache_bytes, self.err, 512)
         if not self.g:
-            raise VitnaError(self.err.value.decode())
+            raise VitnaError(self.err.value.decode(errors="replace"))
 
     def _ok(self, ok):
         if not ok:
-            raise VitnaError(self.err.value.decode())
+            raise VitnaError(self.err.value.decode(errors="replace"))
 
     def close(self):
         if self.g:
@@ -678,7 +678,7 @@ def widen(matrix):
     out = np.empty(matrix.rows * matrix.cols, np.float32)
     err = C.create_string_buffer(512)
     if not lib.vitna_cuda_widen(C.byref(matrix), fptr(out), err, 512):
-        raise VitnaError(err.value.decode())
+        raise VitnaError(err.value.decode(errors="replace"))
     return out.reshape(matrix.rows, matrix.cols)
 
 
@@ -693,7 +693,7 @@ def expert_check(gate, up, down, norm_w, x, eps):
     xx = np.ascontiguousarray(x, np.float32)
     if not lib.vitna_cuda_expert_check(C.byref(gate), C.byref(up), C.byref(down), fptr(nw), fptr(xx), eps, fptr(xs),
                                        fptr(act), fptr(y), err, 512):
-        raise VitnaError(err.value.decode())
+        raise VitnaError(err.value.decode(errors="replace"))
     return xs, act, y
 
 
@@ -702,7 +702,7 @@ def copy_probe(nbytes, reps=10):
     us = C.c_double()
     err = C.create_string_buffer(512)
     if not hip().vitna_hip_copy_probe(nbytes, reps, C.byref(us), err, 512):
-        raise VitnaError(err.value.decode())
+        raise VitnaError(err.value.decode(errors="replace"))
     return us.value
 
 
@@ -711,7 +711,7 @@ def mfma_probe(blocks=1024, iters=2000, reps=3):
     tf = C.c_double()
     err = C.create_string_buffer(512)
     if not hip().vitna_hip_mfma_probe(blocks, iters, reps, C.byref(tf), err, 512):
-        raise VitnaError(err.value.decode())
+        raise VitnaError(err.value.decode(errors="replace"))
     return tf.value
 
 
@@ -723,7 +723,7 @@ def host_route(logits, k, renormalize):
     w = np.empty(k, np.float32)
     err = C.create_string_buffer(512)
     if not hip().vitna_hip_host_route(fptr(lg), lg.size, k, renormalize, _i32(ch), _i32(order), fptr(w), err, 512):
-        raise VitnaError(err.value.decode())
+        raise VitnaError(err.value.decode(errors="replace"))
     return ch, order, w
 
 
@@ -736,7 +736,7 @@ def route_check(logits, k, renormalize):
     w = np.empty(k, np.float32)
     err = C.create_string_buffer(512)
     if not lib.vitna_hip_route_check(fptr(lg), lg.size, k, renormalize, _i32(ch), _i32(ids), fptr(w), err, 512):
-        raise VitnaError(err.value.decode())
+        raise VitnaError(err.value.decode(errors="replace"))
     return ch, ids, w
 
 
