@@ -51,7 +51,7 @@ METRIC = "Qwen3-30B-A3B Q4_K_M decode tok/s @1 GPU; expert GEMV HBM GB/s (% of p
 # copy_probe_kernel) that roofline.traffic is read from.
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_step_qwen3_hbm_traffic.md")
 KERNELS = {0: "experts_in (gate/up + SiLU)", 1: "experts_down (+ weighted sum)", 2: "route (norm + router + top-k)",
-           3: "q/k/v projections", 4: "attention (+ merge)", 5: "o-projection", 6: "LM head",
+           3: "q/k/v projections", 4: "attention (+ merge and o-projection)", 5: "o-projection alone (GEMV)", 6: "LM head",
            7: "route without top-k", 8: "routing rule alone (1 block)", 9: "tiny launch (floor)"}
 
 

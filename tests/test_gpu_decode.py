@@ -138,6 +138,14 @@ SMALL = {
     "wide_i_q4": dict(n_layers=2, hidden=512, intermediate=2048, n_heads=8, n_kv_heads=2, head_dim=128, vocab=1000,
                       n_experts=16, n_experts_used=8, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q4_K, norm_std=0.1,
                       ctx=200, seqs=2, kv_host=1),
+    # the merged attention and o-projection with a Q6_K o-projection, four head groups (parts) of four heads
+    "q6o": dict(n_layers=2, hidden=512, intermediate=256, n_heads=16, n_kv_heads=4, head_dim=128, vocab=1000,
+                n_experts=16, n_experts_used=4, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q6_K, dt_o=va.Q6_K,
+                norm_std=0.1, ctx=200, seqs=2, kv_host=1),
+    # two query heads: not a whole group of four, so the separate merge and o-projection GEMV
+    "h2": dict(n_layers=2, hidden=256, intermediate=256, n_heads=2, n_kv_heads=1, head_dim=128, vocab=500,
+               n_experts=16, n_experts_used=4, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q6_K, norm_std=0.1,
+               ctx=200, seqs=2, kv_host=1),
 }
 
 
@@ -159,7 +167,7 @@ def prefilled(name, seed, pos, seq=0):
 
 
 @pytest.mark.parametrize("name,pos,token", [("q8", 0, 3), ("q8", 65, 17), ("q4km", 130, 999), ("q4km", 63, 4),
-                                            ("wide_i", 90, 12), ("wide_i_q4", 40, 77)])
+                                            ("wide_i", 90, 12), ("wide_i_q4", 40, 77), ("q6o", 150, 21), ("h2", 130, 8)])
 def test_abi_step_layer_by_layer(name, pos, token):
     """model.c's moe_step_on_gpu, played by the test: the device runs each layer up to its router, the host routes
     (the reference's rule), the device runs the experts. Router logits bit-exact given the device's residual; the
@@ -208,7 +216,7 @@ def C_f32(addr):
 
 @pytest.mark.parametrize("persistent", [False, True], ids=["graph", "persistent"])
 @pytest.mark.parametrize("name,pos,token", [("q4km", 150, 7), ("q8", 79, 250), ("q4km", 192, 11), ("q4km", 199, 5),
-                                            ("wide_i", 120, 3)])
+                                            ("wide_i", 120, 3), ("q6o", 191, 40), ("h2", 64, 9)])
 def test_device_step_matches_cpu(name, pos, token, persistent):
     """vitna_hip_moe_step (device routing, one graph): logits within tolerance of the CPU step, replayed at two
     positions through the same graph. Cases: mid-chunk; the last position of the context (q8: 79 of 80, q4km:

@@ -69,6 +69,10 @@ struct vitna_cuda_model {
     int splits_max;
     /* scratch, ROWS_MAX rows */
     float *x, *xn, *q, *k, *v, *qp, *att, *act, *ypart, *rlogits, *vocab, *partial;
+    /* one row's o-projection in per-head-group parts (launch_attention_oproj), [OPROJ_PARTS_MAX][H]; parts_n > 0
+       while they are still to be added to x (by the router's prologue and the experts' down kernel) */
+    float* parts;
+    int parts_n;
     route_out* rt;
     route_out* rt_layers; /* the device-routed step's routing of every layer (the last layer's is also in rt) */
     route_out* rows_rt;   /* the device-routed rows step's routing: [layer][ROWS_MAX] */
@@ -556,6 +560,7 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
         ok = dalloc(g, &g->q, R * qd * 4, "scratch", err, err_len) && dalloc(g, &g->qp, R * qd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->k, R * kd * 4, "scratch", err, err_len) && dalloc(g, &g->v, R * kd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->att, R * qd * 4, "scratch", err, err_len) &&
+             dalloc(g, &g->parts, (size_t)OPROJ_PARTS_MAX * c->hidden * 4, "scratch", err, err_len) &&
              dalloc(g, &g->vocab, R * c->vocab * 4, "the logits", err, err_len) &&
              dalloc(g, &g->partial, (size_t)R * c->n_kv_heads * g->splits_max * G * (c->head_dim + 4) * 4, "attention partials", err, err_len) &&
              dalloc(g, &g->k_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the key cache", err, err_len) &&
@@ -597,7 +602,9 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
 
 /* ---- per-layer enqueues ---------------------------------------------- */
 
-static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, bool prepared) {
+/* fold: add the o-projection's parts into x here (the ABI's layer-by-layer path, whose caller may read the
+   residual); otherwise they stay pending for the router and the experts (g->parts_n) */
+static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, bool prepared, bool fold = false) {
     const dlayer& d = g->L[layer];
     gemv_args ga;
     memset(&ga, 0, sizeof(ga));
@@ -627,7 +634,17 @@ static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, 
     a.prepared = prepared ? 1 : 0;
     a.mma = 1;
     e = launch_attention(a, g->stream);
-    if (e == hipSuccess) e = launch_attention_merge(a, g->stream);
+    if (e != hipSuccess) return e;
+    g->parts_n = 0;
+    if (attention_oproj_fits(a, d.o)) {
+        e = launch_attention_oproj(a, d.o, g->parts, g->stream);
+        if (e != hipSuccess) return e;
+        const int np = g->nh / ATTN_OPROJ_HEADS;
+        if (fold) return launch_attn_fold(g->x, g->parts, np, g->H, g->stream);
+        g->parts_n = np;
+        return hipSuccess;
+    }
+    e = launch_attention_merge(a, g->stream);
     if (e != hipSuccess) return e;
     gemv_args go;
     memset(&go, 0, sizeof(go));
@@ -652,6 +669,10 @@ static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, i
     r.logits = logits;
     r.H = g->H; r.E = g->E; r.n_rows = n_rows;
     r.eps = g->eps;
+    if (n_rows == 1 && x == g->x && g->parts_n) {
+        r.parts = g->parts;
+        r.n_parts = g->parts_n;
+    }
     hipError_t e = launch_route(r, g->stream);
     /* one token's top-k runs in the experts' prologue (enqueue_experts); several rows' in a kernel of its own */
     if (e == hipSuccess && topk && n_rows > 1) e = launch_topk(logits, n_rows, g->E, g->K, g->renorm, rt ? rt : g->rt, g->stream, sp);
@@ -669,6 +690,13 @@ static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, const float* l
     if (e != hipSuccess) return e;
     experts_down_args ad;
     ad.down = d.down; ad.act = g->act; ad.rt = rt; ad.y = y; ad.K = g->K; ad.add = add;
+    ad.parts = nullptr; ad.n_parts = 0;
+    if (add && y == g->x && g->parts_n) {
+        /* the attention's parts go into the residual with the experts' sum; nothing reads them after */
+        ad.parts = g->parts;
+        ad.n_parts = g->parts_n;
+        g->parts_n = 0;
+    }
     return launch_experts_down(ad, g->stream);
 }
 
@@ -723,7 +751,7 @@ extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int
        slower here (5.3-5.4 against 4.5-4.7 ms a token for configs[2]'s model). */
     hipError_t e = hipSuccess;
     if (layer == 0) e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
-    if (e == hipSuccess) e = enqueue_attention(g, (int)layer, 1, false);
+    if (e == hipSuccess) e = enqueue_attention(g, (int)layer, 1, false, true);
     if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn, false);
     if (e == hipSuccess && nx) e = enqueue_route(g, (int)layer + 1, g->rlogits + g->E, 1, g->x, nullptr, false);
     if (!check_launch(g, e, "the layer up to its router", err, err_len)) return false;
@@ -978,7 +1006,7 @@ extern "C" bool vitna_cuda_expert_check(const vitna_matrix_t* gate, const vitna_
         experts_in_args ai;
         ai.gate = qg; ai.up = qu; ai.xn = dxn; ai.rt = drt; ai.logits = nullptr; ai.E = 1; ai.renorm = 0; ai.act = dact; ai.K = 1;
         experts_down_args ad;
-        ad.down = qd; ad.act = dact; ad.rt = drt; ad.y = dy; ad.K = 1; ad.add = 0;
+        ad.down = qd; ad.act = dact; ad.rt = drt; ad.y = dy; ad.K = 1; ad.add = 0; ad.parts = nullptr; ad.n_parts = 0;
         ok = launch_route(ra, s) == hipSuccess && launch_experts_in(ai, s) == hipSuccess && launch_experts_down(ad, s) == hipSuccess &&
              hipDeviceSynchronize() == hipSuccess;
         if (!ok) fail(err, err_len, "the expert's kernels failed or do not take this shape");
@@ -1416,7 +1444,7 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
                 return enqueue_route(g, l, g->rlogits, 1, g->x, g->xn, false);
             case 1: {
                 experts_down_args ad;
-                ad.down = d.down; ad.act = g->act; ad.rt = g->rt; ad.y = g->ypart; ad.K = K; ad.add = 0;
+                ad.down = d.down; ad.act = g->act; ad.rt = g->rt; ad.y = g->ypart; ad.K = K; ad.add = 0; ad.parts = nullptr; ad.n_parts = 0;
                 b = K * qmat_bytes(d.down) + K * (double)g->I * 4 + H * 4.0;
                 return launch_experts_down(ad, g->stream);
             }
@@ -1442,7 +1470,10 @@ extern "C" bool vitna_hip_time_kernel(struct vitna_cuda_model* g, int which, int
                 a.splits_max = g->splits_max; a.eps = g->eps; a.mma = 1;
                 b = 0; /* set by the caller from the position */
                 const hipError_t e = launch_attention(a, g->stream);
-                return e == hipSuccess ? launch_attention_merge(a, g->stream) : e;
+                if (e != hipSuccess) return e;
+                /* as the step runs it: the merge with the o-projection where the layer takes it */
+                if (attention_oproj_fits(a, d.o)) return launch_attention_oproj(a, d.o, g->parts, g->stream);
+                return launch_attention_merge(a, g->stream);
             }
             case 5: {
                 gemv_args go;

@@ -675,6 +675,175 @@ hipError_t launch_attention_merge(const attn_args& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+/* The merge and the o-projection of one row, a group of HG = ATTN_OPROJ_HEADS query heads a block (blockIdx.x)
+   and a range of 4 RPW U output rows (blockIdx.y). Its weights (the rows' CW = HG HD columns of the group) do not
+   depend on anything before: every wave requests its U units of RPW rows at once. Wave w then merges head w of
+   the group exactly as attention_merge_kernel<1> does (the maximum over the chunks, each chunk's scale
+   exp(m_s - M), the sums in chunk order), so att is the same bits; the HG heads' outputs go to LDS, and each
+   row's dot over the group's columns runs as the dense GEMV's does, LPR = CW / 32 lanes a row, one slice a lane.
+   parts[g][r] holds row r's share of the group. Every block of a group merges the group's heads again (at
+   configs[2], 32 blocks a group, 80 KB of partials each from L2): that costs less than the kernel boundary
+   a separate merge kernel puts in front of the o-projection. More, smaller blocks than the GEMV would take
+   (U = 4: 256 blocks at configs[2]) keep more of the weights in flight: with 128 blocks the pair took 1.4 us
+   more. */
+#define OPROJ_U 4 /* units of RPW rows a wave: 64 rows a block at head size 128, 256 blocks at config 2 */
+#define OPROJ_PRE 36 /* (a multiple of 4) chunks whose values a lane requests in the first round (2,304 positions) */
+template <int DT, int HD>
+__global__ __launch_bounds__(256) void attention_oproj_kernel(attn_args a, qmat o, float* __restrict__ parts) {
+    constexpr int HG = ATTN_OPROJ_HEADS, CW = HG * HD, LPR = CW / 32, RPW = WAVE / LPR, DPT = HD / 64;
+    static_assert(HG == 4 && CW % 256 == 0 && LPR <= WAVE, "one wave a head, whole super-blocks a group");
+    const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = lane / LPR, al = lane % LPR;
+    const int t_abs = g * (CW / 32) + al; /* the lane's slice of a row */
+    const int rbase = blockIdx.y * (4 * RPW * OPROJ_U) + wave * (RPW * OPROJ_U) + sub;
+    /* the position, requested ahead of the weights */
+    const int pos_v = gld<int>(&a.rows[0].pos);
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* then the weights: nothing they need comes from before (the chunk count, which the partials' addresses need,
+       is a dependent load), so they are in flight while that load and the partials' loads run */
+    qraw q[OPROJ_U];
+#pragma unroll
+    for (int u = 0; u < OPROJ_U; u++) {
+        const int r = min(rbase + u * RPW, o.rows - 1);
+        slice_load<DT>(o, 0, r, t_abs, q[u]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* the merge's loads: wave w, head hq = g HG + w, DPT dimensions a lane, the maxima and sums of chunks lane and
+       lane + 64 */
+    __shared__ __attribute__((aligned(16))) float fm[HG][MERGE_MAX];
+    __shared__ __attribute__((aligned(16))) float fl[HG][MERGE_MAX];
+    __shared__ __attribute__((aligned(16))) float sx[CW];
+    const int G = a.n_heads / a.n_kv, hq = g * HG + wave, h = hq / G, gi = hq % G;
+    const int n_act = __builtin_amdgcn_readfirstlane(pos_v) / ATTN_CHUNK + 1;
+    const float* base = a.partial + ((size_t)h * a.splits_max * G + gi) * (HD + 4);
+    const size_t stride = (size_t)G * (HD + 4);
+    const int d0 = lane * DPT;
+    /* (chunks past the last are read as the last, unused: every load unconditional, in one batch) */
+    float v0[OPROJ_PRE][DPT];
+#pragma unroll
+    for (int i = 0; i < OPROJ_PRE; i++) {
+        const float* p = base + (size_t)min(i, n_act - 1) * stride + d0;
+        if constexpr (DPT == 2) {
+            const float2 t = *reinterpret_cast<const float2*>(p);
+            v0[i][0] = t.x;
+            v0[i][1] = t.y;
+        } else {
+            v0[i][0] = p[0];
+        }
+    }
+    float2 ml[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) ml[i] = *reinterpret_cast<const float2*>(base + (size_t)min(lane + WAVE * i, n_act - 1) * stride + HD);
+    /* the merge, as attention_merge_kernel<1> computes it */
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int s = lane + WAVE * i;
+        if (s < n_act) {
+            fm[wave][s] = ml[i].x;
+            fl[wave][s] = ml[i].y;
+            m = fmaxf(m, ml[i].x);
+        }
+    }
+    for (int s = lane + 2 * WAVE; s < n_act; s += WAVE) {
+        fm[wave][s] = base[s * stride + HD];
+        fl[wave][s] = base[s * stride + HD + 1];
+        m = fmaxf(m, fm[wave][s]);
+    }
+    const float M = wave_max_dpp(m);
+    for (int s = lane; s < n_act; s += WAVE) fm[wave][s] = expf(fm[wave][s] - M);
+    __syncthreads();
+    float L = 0.f, acc[DPT];
+#pragma unroll
+    for (int k = 0; k < DPT; k++) acc[k] = 0.f;
+    {
+        /* the first chunks' scales and sums, all read at once (entries past the last chunk are read, not used) */
+        float sf[OPROJ_PRE], sl[OPROJ_PRE];
+#pragma unroll
+        for (int i = 0; i < OPROJ_PRE / 4; i++) {
+            const float4 f4 = reinterpret_cast<const float4*>(fm[wave])[i], l4 = reinterpret_cast<const float4*>(fl[wave])[i];
+            sf[4 * i] = f4.x; sf[4 * i + 1] = f4.y; sf[4 * i + 2] = f4.z; sf[4 * i + 3] = f4.w;
+            sl[4 * i] = l4.x; sl[4 * i + 1] = l4.y; sl[4 * i + 2] = l4.z; sl[4 * i + 3] = l4.w;
+        }
+#pragma unroll
+        for (int i = 0; i < OPROJ_PRE; i++)
+            if (i < n_act) {
+                L = fmaf(sl[i], sf[i], L);
+#pragma unroll
+                for (int k = 0; k < DPT; k++) acc[k] = fmaf(v0[i][k], sf[i], acc[k]);
+            }
+    }
+    int s = OPROJ_PRE;
+    for (; s + 7 < n_act; s += 8) {
+        float v[8][DPT];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int k = 0; k < DPT; k++) v[i][k] = base[(s + i) * stride + d0 + k];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            L = fmaf(fl[wave][s + i], fm[wave][s + i], L);
+#pragma unroll
+            for (int k = 0; k < DPT; k++) acc[k] = fmaf(v[i][k], fm[wave][s + i], acc[k]);
+        }
+    }
+    for (; s < n_act; s++) {
+        L = fmaf(fl[wave][s], fm[wave][s], L);
+#pragma unroll
+        for (int k = 0; k < DPT; k++) acc[k] = fmaf(base[s * stride + d0 + k], fm[wave][s], acc[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < DPT; k++) {
+        const float val = acc[k] / L;
+        sx[wave * HD + d0 + k] = val;
+        if (blockIdx.y == 0) a.att[(size_t)hq * HD + d0 + k] = val;
+    }
+    __syncthreads();
+
+    /* the rows: the lane's slice of the group's columns, then U units of RPW rows */
+    xslice xs;
+    load_xslice(DT, al, sx, xs);
+#pragma unroll
+    for (int u = 0; u < OPROJ_U; u++) {
+        float p = slice_dot<DT>(q[u], t_abs, xs);
+        p = row_sum<LPR>(p);
+        const int r = rbase + u * RPW;
+        if (al == LPR - 1 && r < o.rows) parts[(size_t)g * o.rows + r] = p;
+    }
+}
+
+bool attention_oproj_fits(const attn_args& a, const qmat& o) {
+    return a.n_rows == 1 && !a.prepared && (a.hd == 64 || a.hd == 128) && a.n_kv >= 1 && a.n_heads % a.n_kv == 0 &&
+           a.n_heads % ATTN_OPROJ_HEADS == 0 && a.n_heads / ATTN_OPROJ_HEADS <= OPROJ_PARTS_MAX && a.splits_max <= MERGE_MAX &&
+           o.cols == a.n_heads * a.hd && o.rows >= 256 && o.rows <= ROUTE_PARTS_HMAX &&
+           (o.dtype == VITNA_DTYPE_Q4_K || o.dtype == VITNA_DTYPE_Q6_K || o.dtype == VITNA_DTYPE_Q8_0);
+}
+
+hipError_t launch_attention_oproj(const attn_args& a, const qmat& o, float* parts, hipStream_t s) {
+    if (!attention_oproj_fits(a, o) || !parts) return hipErrorInvalidValue;
+    const int rpw = WAVE / (ATTN_OPROJ_HEADS * a.hd / 32), per_block = 4 * rpw * OPROJ_U;
+    const dim3 grid(a.n_heads / ATTN_OPROJ_HEADS, (o.rows + per_block - 1) / per_block);
+#define OPROJ_CASE(DT, HD) \
+    if (o.dtype == DT && a.hd == HD) { attention_oproj_kernel<DT, HD><<<grid, 256, 0, s>>>(a, o, parts); return hipGetLastError(); }
+    OPROJ_CASE(VITNA_DTYPE_Q4_K, 128) OPROJ_CASE(VITNA_DTYPE_Q6_K, 128) OPROJ_CASE(VITNA_DTYPE_Q8_0, 128)
+    OPROJ_CASE(VITNA_DTYPE_Q4_K, 64) OPROJ_CASE(VITNA_DTYPE_Q6_K, 64) OPROJ_CASE(VITNA_DTYPE_Q8_0, 64)
+#undef OPROJ_CASE
+    return hipErrorInvalidValue;
+}
+
+__global__ __launch_bounds__(256) void attn_fold_kernel(float* __restrict__ x, const float* __restrict__ parts, int n_parts, int H) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < H) x[i] = attn_resid(x[i], parts, n_parts, (size_t)H, (size_t)i);
+}
+
+hipError_t launch_attn_fold(float* x, const float* parts, int n_parts, int H, hipStream_t s) {
+    if (n_parts < 1 || n_parts > OPROJ_PARTS_MAX || H < 1) return hipErrorInvalidValue;
+    attn_fold_kernel<<<(H + 255) / 256, 256, 0, s>>>(x, parts, n_parts, H);
+    return hipGetLastError();
+}
+
 hipError_t launch_attention_prepare(const attn_args& a, hipStream_t s) {
     if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > GMAX || a.n_rows < 1 || !a.q_out) return hipErrorInvalidValue;
     const dim3 grid(a.n_kv, a.n_rows);

@@ -120,42 +120,69 @@ hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_
 /* ------------------------------------------------------------------ */
 
 
-/* One wave a block, four router rows a block (sixteen lanes a row). */
-template <int NCH>
-__global__ __launch_bounds__(64) void route_kernel(route_args a) {
+/* Four router rows a block (sixteen lanes of wave 0 a row). NT threads: 64, or 256 when x's attention parts
+   are still to be added (route_args::parts): the other waves then help load x and the parts, so that every
+   load goes out in one round. */
+template <int NCH, int NT>
+__global__ __launch_bounds__(NT) void route_kernel(route_args a) {
     extern __shared__ float sh[];
     float* sx = sh;             /* H: x */
     float* sxn = sh + a.H;      /* H: normalized */
     __shared__ float chains[16];
     __shared__ float inv_s;
-    const int lane = threadIdx.x, j = lane & 15, rrow = blockIdx.x * 4 + (lane >> 4);
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, rrow = blockIdx.x * 4 + (lane >> 4);
     const int tok = blockIdx.y;
     const float* x = a.x + (size_t)tok * a.H;
-    /* this lane's chain of router weights, loaded before the norm is known */
+    /* this lane's chain of router weights, loaded before the norm is known (wave 0) */
     float w[NCH];
-    const bool has_row = rrow < a.E;
-    const float* wr = a.router + (size_t)(has_row ? rrow : 0) * a.H + j;
+    const bool has_row = tid < 64 && rrow < a.E;
+    if (tid < 64) {
+        const float* wr = a.router + (size_t)(rrow < a.E ? rrow : 0) * a.H + j;
 #pragma unroll
-    for (int m = 0; m < NCH; m++) w[m] = wr[16 * m];
+        for (int m = 0; m < NCH; m++) w[m] = wr[16 * m];
+    }
+    constexpr int NF4 = NCH * 4, X4 = (NF4 + NT - 1) / NT; /* float4 of x, and a thread's share */
+#define X4_OK(i) (NF4 % NT == 0 || tid + NT * (i) < NF4)
     {
-        /* x into LDS: H / 256 = NCH / 16 float4 a lane, all loads issued before any store */
+        /* x into LDS, all loads issued before any store */
         const float4* x4 = reinterpret_cast<const float4*>(x);
-        float4 xv[NCH / 16];
+        float4 xv[X4];
 #pragma unroll
-        for (int i = 0; i < NCH / 16; i++) xv[i] = x4[lane + 64 * i];
+        for (int i = 0; i < X4; i++) xv[i] = X4_OK(i) ? x4[tid + NT * i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (NT > 64 && a.parts) {
+            float4 pv[OPROJ_PARTS_MAX][X4];
+            const float4* p4 = reinterpret_cast<const float4*>(a.parts);
 #pragma unroll
-        for (int i = 0; i < NCH / 16; i++) reinterpret_cast<float4*>(sx)[lane + 64 * i] = xv[i];
+            for (int p = 0; p < OPROJ_PARTS_MAX; p++)
+                if (p < a.n_parts)
+#pragma unroll
+                    for (int i = 0; i < X4; i++)
+                        if (X4_OK(i)) pv[p][i] = p4[(size_t)p * (a.H / 4) + tid + NT * i];
+#pragma unroll
+            for (int i = 0; i < X4; i++) {
+                if (!X4_OK(i)) continue;
+                /* attn_resid, a float4 at a time: the parts in group order, then x */
+                float4 sum = pv[0][i];
+#pragma unroll
+                for (int p = 1; p < OPROJ_PARTS_MAX; p++)
+                    if (p < a.n_parts) { sum.x += pv[p][i].x; sum.y += pv[p][i].y; sum.z += pv[p][i].z; sum.w += pv[p][i].w; }
+                xv[i].x += sum.x; xv[i].y += sum.y; xv[i].z += sum.z; xv[i].w += sum.w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < X4; i++)
+            if (X4_OK(i)) reinterpret_cast<float4*>(sx)[tid + NT * i] = xv[i];
     }
     __syncthreads();
-    if (lane < 16) {
+    if (tid < 16) {
         /* engine/src/kernels.c:115-140: sixteen chains of squares (H a multiple of 16) */
         float acc = 0.0f;
 #pragma unroll 16
-        for (int m = 0; m < NCH; m++) acc = fmaf(sx[16 * m + lane], sx[16 * m + lane], acc);
-        chains[lane] = acc;
+        for (int m = 0; m < NCH; m++) acc = fmaf(sx[16 * m + tid], sx[16 * m + tid], acc);
+        chains[tid] = acc;
     }
     __syncthreads();
-    if (lane == 0) {
+    if (tid == 0) {
         float v[8];
         for (int q = 0; q < 8; q++) v[q] = chains[q] + chains[q + 8];
         const float s0 = v[0] + v[4], s1 = v[1] + v[5], s2 = v[2] + v[6], s3 = v[3] + v[7];
@@ -167,40 +194,50 @@ __global__ __launch_bounds__(64) void route_kernel(route_args a) {
     const float inv = inv_s;
     {
         const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
-        float4 nw[NCH / 16];
+        float4 nw[X4];
 #pragma unroll
-        for (int i = 0; i < NCH / 16; i++) nw[i] = w4[lane + 64 * i];
+        for (int i = 0; i < X4; i++) nw[i] = X4_OK(i) ? w4[tid + NT * i] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int i = 0; i < NCH / 16; i++) {
-            const float4 xv = reinterpret_cast<const float4*>(sx)[lane + 64 * i];
+        for (int i = 0; i < X4; i++) {
+            if (!X4_OK(i)) continue;
+            const float4 xv = reinterpret_cast<const float4*>(sx)[tid + NT * i];
             float4 o;
             o.x = (xv.x * inv) * nw[i].x; o.y = (xv.y * inv) * nw[i].y;
             o.z = (xv.z * inv) * nw[i].z; o.w = (xv.w * inv) * nw[i].w;
-            reinterpret_cast<float4*>(sxn)[lane + 64 * i] = o;
-            if (a.xn_out && blockIdx.x == 0) reinterpret_cast<float4*>(a.xn_out + (size_t)tok * a.H)[lane + 64 * i] = o;
+            reinterpret_cast<float4*>(sxn)[tid + NT * i] = o;
+            if (a.xn_out && blockIdx.x == 0) reinterpret_cast<float4*>(a.xn_out + (size_t)tok * a.H)[tid + NT * i] = o;
         }
     }
     __syncthreads();
+    if (tid >= 64) return;
     float acc = 0.0f;
 #pragma unroll
     for (int m = 0; m < NCH; m++) acc = fmaf(w[m], sxn[16 * m + j], acc);
     const float logit = fold16_lanes(acc);
     if (has_row && j == 0) a.logits[(size_t)tok * a.E + rrow] = logit;
+#undef X4_OK
 }
 
 hipError_t launch_route(const route_args& a, hipStream_t s) {
     if (a.H % 256 || a.E < 1 || a.E > ROUTE_E_MAX || a.n_rows < 1) return hipErrorInvalidValue;
+    if (a.parts && (a.n_rows != 1 || a.n_parts < 1 || a.n_parts > OPROJ_PARTS_MAX)) return hipErrorInvalidValue;
     const dim3 grid((a.E + 3) / 4, a.n_rows);
     const size_t lds = 2 * (size_t)a.H * sizeof(float);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
+    /* with parts: rows of at most ROUTE_PARTS_HMAX (wider ones would hold the router chain and every part's
+       loads past the registers) */
+    if (a.parts && a.H > ROUTE_PARTS_HMAX) return hipErrorInvalidValue;
+#define ROUTE_CASE(N)                                                                   \
+    case N:                                                                             \
+        if (a.parts) route_kernel<N, 256><<<grid, 256, lds, s>>>(a);                   \
+        else route_kernel<N, 64><<<grid, 64, lds, s>>>(a);                              \
+        break;
     switch (a.H / 16) {
-        case 16: route_kernel<16><<<grid, 64, lds, s>>>(a); break;
-        case 32: route_kernel<32><<<grid, 64, lds, s>>>(a); break;
-        case 64: route_kernel<64><<<grid, 64, lds, s>>>(a); break;
-        case 128: route_kernel<128><<<grid, 64, lds, s>>>(a); break;
-        case 256: route_kernel<256><<<grid, 64, lds, s>>>(a); break;
+        ROUTE_CASE(16) ROUTE_CASE(32) ROUTE_CASE(64) ROUTE_CASE(128)
+        case 256: route_kernel<256, 64><<<grid, 64, lds, s>>>(a); break;
         default: return hipErrorInvalidValue;
     }
+#undef ROUTE_CASE
     return hipGetLastError();
 }
 
@@ -416,6 +453,19 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
         wk[j] = ok ? a.rt->cw[k] : 0.0f;
         load_xslice(DT, tk[j], a.act + (size_t)k * I, xs[j]);
     }
+    /* what the sums are added to (the residual, with the attention's parts), requested before the weights so that
+       its loads land under them */
+    __builtin_amdgcn_sched_barrier(0); /* the activations' sums first: their waits then count no later load */
+    /* (without parts the loads read y again, unused: no branch, so the waits below count these loads exactly) */
+    float yx[NR], yp[NR][OPROJ_PARTS_MAX];
+    const float* pp = a.parts ? a.parts : a.y;
+    const int np = a.parts ? a.n_parts : 1;
+#pragma unroll
+    for (int h = 0; h < NR; h++) {
+        const int r = min(wave + h * nwaves, H - 1);
+        yx[h] = a.y[r];
+        attn_parts_load(pp, np, (size_t)H, (size_t)r, yp[h]);
+    }
     for (int r0 = wave; r0 < H; r0 += NR * nwaves) {
         qraw q[NR][IPL];
 #pragma unroll
@@ -431,7 +481,16 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
             for (int j = 0; j < IPL; j++) p = fmaf(wk[j], slice_dot<DT>(q[h][j], tk[j], xs[j]), p);
             p = row_sum<64>(p);
             const int r = r0 + h * nwaves;
-            if (lane == 63 && r < H) a.y[r] = a.add ? a.y[r] + p : p;
+            if (lane == 63 && r < H) {
+                if (!a.add) a.y[r] = p;
+                else if (r0 == wave) {
+                    /* (the empty asm keeps the compiler from summing before the loop, which would wait there) */
+#pragma unroll
+                    for (int i = 0; i < OPROJ_PARTS_MAX; i++) asm volatile("" : "+v"(yp[h][i]));
+                    a.y[r] = (a.parts ? attn_parts_sum(yx[h], yp[h], a.n_parts) : yx[h]) + p;
+                }
+                else a.y[r] = (a.parts ? attn_resid(a.y[r], a.parts, a.n_parts, (size_t)H, (size_t)r) : a.y[r]) + p;
+            }
         }
     }
 }

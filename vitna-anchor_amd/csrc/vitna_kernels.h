@@ -40,6 +40,30 @@ hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_
    router's logits for each row (E of them, the router F32 [E x H]) in the
    reference CPU's order into logits (row stride E). The routing itself
    runs after it (launch_topk). */
+/* The residual after a layer's attention while the o-projection's output is still in per-head-group parts
+   (launch_attention_oproj): x + (((p_0 + p_1) + p_2) + ...), the parts summed in group order, then added. Every
+   kernel that reads that residual forms it with this function, so all of them see the same bits. */
+#define OPROJ_PARTS_MAX 8 /* n_heads / ATTN_OPROJ_HEADS at most: 32 query heads */
+/* attn_resid in two steps, so that a kernel can request the parts early and add them late: the loads (every
+   slot loaded, those past n_parts as the last part, unused; no branch), then the sum */
+__device__ __forceinline__ void attn_parts_load(const float* __restrict__ parts, int n_parts, size_t stride, size_t i,
+                                                float (&v)[OPROJ_PARTS_MAX]) {
+#pragma unroll
+    for (int p = 0; p < OPROJ_PARTS_MAX; p++) v[p] = parts[(size_t)min(p, n_parts - 1) * stride + i];
+}
+__device__ __forceinline__ float attn_parts_sum(float x, const float (&v)[OPROJ_PARTS_MAX], int n_parts) {
+    float s = v[0];
+#pragma unroll
+    for (int p = 1; p < OPROJ_PARTS_MAX; p++) s = p < n_parts ? s + v[p] : s;
+    return x + s;
+}
+__device__ __forceinline__ float attn_resid(float x, const float* __restrict__ parts, int n_parts, size_t stride, size_t i) {
+    float v[OPROJ_PARTS_MAX];
+    attn_parts_load(parts, n_parts, stride, i, v);
+    return attn_parts_sum(x, v, n_parts);
+}
+#define ROUTE_PARTS_HMAX 2048 /* the widest rows the router takes with parts */
+
 struct route_args {
     const float* x;
     const float* norm_w;
@@ -48,6 +72,9 @@ struct route_args {
     float* logits;
     int H, E, n_rows;
     float eps;
+    /* one row only: x's attention parts still to add (n_parts of H floats, part_stride apart), or null */
+    const float* parts;
+    int n_parts;
 };
 hipError_t launch_route(const route_args& a, hipStream_t s);
 
@@ -92,6 +119,9 @@ struct experts_down_args {
     const route_out* rt;
     float* y;
     int K, add;
+    /* with add: the attention parts (attn_resid) added to y before the experts' sum, or null */
+    const float* parts;
+    int n_parts;
 };
 hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s);
 
@@ -172,6 +202,18 @@ struct attn_args {
     img_out img;
 };
 hipError_t launch_attention(const attn_args& a, hipStream_t s);
+/* One row: the chunks' partials merged, as launch_attention_merge merges them (same bits in att), and the
+   o-projection applied group by group: the n_heads / ATTN_OPROJ_HEADS groups of ATTN_OPROJ_HEADS query heads
+   each leave parts[g][r] = o[r][the group's columns] . att[the group's columns]. The residual then is
+   attn_resid(x, parts, n_heads / ATTN_OPROJ_HEADS, o.rows). Each block merges one group's heads and
+   multiplies them into a range of rows, so no kernel waits on another for att. attention_oproj_fits says
+   whether a layer takes it (else: launch_attention_merge, then the o-projection GEMV). */
+#define ATTN_OPROJ_HEADS 4
+bool attention_oproj_fits(const attn_args& a, const qmat& o);
+hipError_t launch_attention_oproj(const attn_args& a, const qmat& o, float* parts, hipStream_t s);
+/* x[i] = attn_resid(x[i], parts, n_parts, H, i): the parts folded into the residual (the ABI's layer-by-layer
+   path, whose caller may read the residual after the router). */
+hipError_t launch_attn_fold(float* x, const float* parts, int n_parts, int H, hipStream_t s);
 /* The chunks' partials of every (row, query head) combined into att. */
 hipError_t launch_attention_merge(const attn_args& a, hipStream_t s);
 /* The prepare pass of prepared = 1: q normalized and rotated into q_out, k
