@@ -133,46 +133,56 @@ __global__ __launch_bounds__(NT) void route_kernel(route_args a) {
     const int tid = threadIdx.x, lane = tid & 63, j = lane & 15, rrow = blockIdx.x * 4 + (lane >> 4);
     const int tok = blockIdx.y;
     const float* x = a.x + (size_t)tok * a.H;
-    /* this lane's chain of router weights, loaded before the norm is known (wave 0) */
-    float w[NCH];
-    const bool has_row = tid < 64 && rrow < a.E;
-    if (tid < 64) {
-        const float* wr = a.router + (size_t)(rrow < a.E ? rrow : 0) * a.H + j;
-#pragma unroll
-        for (int m = 0; m < NCH; m++) w[m] = wr[16 * m];
-    }
     constexpr int NF4 = NCH * 4, X4 = (NF4 + NT - 1) / NT; /* float4 of x, and a thread's share */
 #define X4_OK(i) (NF4 % NT == 0 || tid + NT * (i) < NF4)
-    {
-        /* x into LDS, all loads issued before any store */
-        const float4* x4 = reinterpret_cast<const float4*>(x);
-        float4 xv[X4];
+    /* wave 0's chains of router weights; with parts (NT = 256), after x and the parts, so that the norm, which
+       waits for them, waits for no weight load (at NT = 64 that order leaves the registers short: spills) */
+    float w[NCH];
+    const bool has_row = tid < 64 && rrow < a.E;
+    auto load_router = [&]() {
+        if (tid < 64) {
+            const float* wr = a.router + (size_t)(rrow < a.E ? rrow : 0) * a.H + j;
 #pragma unroll
-        for (int i = 0; i < X4; i++) xv[i] = X4_OK(i) ? x4[tid + NT * i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (NT > 64 && a.parts) {
-            float4 pv[OPROJ_PARTS_MAX][X4];
-            const float4* p4 = reinterpret_cast<const float4*>(a.parts);
-#pragma unroll
-            for (int p = 0; p < OPROJ_PARTS_MAX; p++)
-                if (p < a.n_parts)
-#pragma unroll
-                    for (int i = 0; i < X4; i++)
-                        if (X4_OK(i)) pv[p][i] = p4[(size_t)p * (a.H / 4) + tid + NT * i];
-#pragma unroll
-            for (int i = 0; i < X4; i++) {
-                if (!X4_OK(i)) continue;
-                /* attn_resid, a float4 at a time: the parts in group order, then x */
-                float4 sum = pv[0][i];
-#pragma unroll
-                for (int p = 1; p < OPROJ_PARTS_MAX; p++)
-                    if (p < a.n_parts) { sum.x += pv[p][i].x; sum.y += pv[p][i].y; sum.z += pv[p][i].z; sum.w += pv[p][i].w; }
-                xv[i].x += sum.x; xv[i].y += sum.y; xv[i].z += sum.z; xv[i].w += sum.w;
-            }
+            for (int m = 0; m < NCH; m++) w[m] = wr[16 * m];
         }
+    };
+    if constexpr (NT == 64) load_router();
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    float4 xv[X4];
 #pragma unroll
-        for (int i = 0; i < X4; i++)
-            if (X4_OK(i)) reinterpret_cast<float4*>(sx)[tid + NT * i] = xv[i];
+    for (int i = 0; i < X4; i++) xv[i] = x4[X4_OK(i) ? tid + NT * i : 0];
+    constexpr int NP = NT > 64 ? OPROJ_PARTS_MAX : 1;
+    float4 pv[NP][X4];
+    const bool with_parts = NT > 64 && a.parts;
+    if (with_parts) {
+        /* (every slot loaded, those past n_parts as the last part, unused: no branch between the loads) */
+        const float4* p4 = reinterpret_cast<const float4*>(a.parts);
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+#pragma unroll
+            for (int i = 0; i < X4; i++) pv[p][i] = p4[(size_t)min(p, a.n_parts - 1) * (a.H / 4) + (X4_OK(i) ? tid + NT * i : 0)];
     }
+    if constexpr (NT > 64) {
+        __builtin_amdgcn_sched_barrier(0);
+        load_router();
+    }
+    if (with_parts) {
+#pragma unroll
+        for (int i = 0; i < X4; i++) {
+            /* attn_resid, a float4 at a time: the parts in group order, then x */
+            float4 sum = pv[0][i];
+#pragma unroll
+            for (int p = 1; p < NP; p++) {
+                const bool on = p < a.n_parts;
+                sum.x = on ? sum.x + pv[p][i].x : sum.x; sum.y = on ? sum.y + pv[p][i].y : sum.y;
+                sum.z = on ? sum.z + pv[p][i].z : sum.z; sum.w = on ? sum.w + pv[p][i].w : sum.w;
+            }
+            xv[i].x += sum.x; xv[i].y += sum.y; xv[i].z += sum.z; xv[i].w += sum.w;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < X4; i++)
+        if (X4_OK(i)) reinterpret_cast<float4*>(sx)[tid + NT * i] = xv[i];
     __syncthreads();
     if (tid < 16) {
         /* engine/src/kernels.c:115-140: sixteen chains of squares (H a multiple of 16) */
