@@ -602,9 +602,10 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
 
 /* ---- per-layer enqueues ---------------------------------------------- */
 
-/* fold: add the o-projection's parts into x here (the ABI's layer-by-layer path, whose caller may read the
-   residual); otherwise they stay pending for the router and the experts (g->parts_n) */
-static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, bool prepared, bool fold = false) {
+/* One row's attention and o-projection. Where the layer takes the merged o-projection its parts stay pending
+   (g->parts_n) for the router and the experts' down kernel, which add them to x; vitna_hip_residual adds them when
+   the residual is read before that. */
+static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, bool prepared) {
     const dlayer& d = g->L[layer];
     gemv_args ga;
     memset(&ga, 0, sizeof(ga));
@@ -639,9 +640,7 @@ static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, 
     if (attention_oproj_fits(a, d.o)) {
         e = launch_attention_oproj(a, d.o, g->parts, g->stream);
         if (e != hipSuccess) return e;
-        const int np = g->nh / ATTN_OPROJ_HEADS;
-        if (fold) return launch_attn_fold(g->x, g->parts, np, g->H, g->stream);
-        g->parts_n = np;
+        g->parts_n = g->nh / ATTN_OPROJ_HEADS;
         return hipSuccess;
     }
     e = launch_attention_merge(a, g->stream);
@@ -751,7 +750,7 @@ extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int
        slower here (5.3-5.4 against 4.5-4.7 ms a token for configs[2]'s model). */
     hipError_t e = hipSuccess;
     if (layer == 0) e = launch_embed(g->embed, &g->rows_dev[0].token, 0, g->x, g->stream);
-    if (e == hipSuccess) e = enqueue_attention(g, (int)layer, 1, false, true);
+    if (e == hipSuccess) e = enqueue_attention(g, (int)layer, 1, false);
     if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, 1, g->x, g->xn, false);
     if (e == hipSuccess && nx) e = enqueue_route(g, (int)layer + 1, g->rlogits + g->E, 1, g->x, nullptr, false);
     if (!check_launch(g, e, "the layer up to its router", err, err_len)) return false;
@@ -1262,6 +1261,12 @@ extern "C" bool vitna_hip_residual(struct vitna_cuda_model* g, size_t row, float
     if (!g) return fail(err, err_len, "no model");
     if (row >= ROWS_MAX) return fail(err, err_len, "row %zu: at most %d", row, ROWS_MAX);
     float* d = g->x + row * g->H;
+    if (row == 0 && g->parts_n) {
+        /* the row's attention parts still pending: read, the residual has them; written, the new residual
+           replaces what they would complete */
+        if (!to_device) HIP_TRY(launch_attn_fold(g->x, g->parts, g->parts_n, g->H, g->stream), "adding the attention's parts");
+        g->parts_n = 0;
+    }
     HIP_TRY(hipStreamSynchronize(g->stream), "waiting for the device");
     HIP_TRY(to_device ? hipMemcpy(d, host, g->H * 4, hipMemcpyHostToDevice) : hipMemcpy(host, d, g->H * 4, hipMemcpyDeviceToHost),
             "copying the residual");
@@ -2085,6 +2090,7 @@ static bool set_rows(vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n
     HIP_TRY(hipMemcpyAsync(g->rows_dev, g->rows_host, n * sizeof(row_rec), hipMemcpyHostToDevice, g->stream), "copying the rows");
     HIP_TRY(hipEventRecord(g->rows_copied, g->stream), "recording the row copy");
     g->rows_n = (int)n;
+    g->parts_n = 0; /* a pass of rows owns x's rows: no one row's attention parts are pending any more */
     g->rows_shared_seq = shared;
     return true;
 }

@@ -211,8 +211,8 @@ hipError_t launch_attention(const attn_args& a, hipStream_t s);
 #define ATTN_OPROJ_HEADS 4
 bool attention_oproj_fits(const attn_args& a, const qmat& o);
 hipError_t launch_attention_oproj(const attn_args& a, const qmat& o, float* parts, hipStream_t s);
-/* x[i] = attn_resid(x[i], parts, n_parts, H, i): the parts folded into the residual (the ABI's layer-by-layer
-   path, whose caller may read the residual after the router). */
+/* x[i] = attn_resid(x[i], parts, n_parts, H, i): the parts folded into the residual (for a reader of the
+   residual between the attention and the experts). */
 hipError_t launch_attn_fold(float* x, const float* parts, int n_parts, int H, hipStream_t s);
 /* The chunks' partials of every (row, query head) combined into att. */
 hipError_t launch_attention_merge(const attn_args& a, hipStream_t s);
