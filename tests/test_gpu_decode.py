@@ -142,6 +142,10 @@ SMALL = {
     "q6o": dict(n_layers=2, hidden=512, intermediate=256, n_heads=16, n_kv_heads=4, head_dim=128, vocab=1000,
                 n_experts=16, n_experts_used=4, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q6_K, dt_o=va.Q6_K,
                 norm_std=0.1, ctx=200, seqs=2, kv_host=1),
+    # Q6_K gate/up with Q4_K down (the grouped experts' one-wave-a-SIMD form for Q6_K)
+    "q6gu": dict(n_layers=2, hidden=512, intermediate=256, n_heads=8, n_kv_heads=2, head_dim=128, vocab=1000,
+                 n_experts=16, n_experts_used=4, renormalize=1, dt_gate_up=va.Q6_K, dt_down=va.Q4_K, norm_std=0.1,
+                 ctx=200, seqs=2, kv_host=1),
     # two query heads: not a whole group of four, so the separate merge and o-projection GEMV
     "h2": dict(n_layers=2, hidden=256, intermediate=256, n_heads=2, n_kv_heads=1, head_dim=128, vocab=500,
                n_experts=16, n_experts_used=4, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q6_K, norm_std=0.1,

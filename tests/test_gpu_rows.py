@@ -101,7 +101,7 @@ def test_rows_step_device_routed(name):
         model.free()
 
 
-@pytest.mark.parametrize("name", ["q8", "q4km"])
+@pytest.mark.parametrize("name", ["q8", "q4km", "q6gu"])
 def test_rows_crowded_experts(name):
     """The grouped experts alone, 24 rows on 16 (32) experts: about six tokens an expert, so experts take
     several four-token tiles, and the small models' short rows give the kernels' column split empty and

@@ -422,9 +422,12 @@ __device__ __forceinline__ int pick(gm_int4 v, int i) { return i == 0 ? v.x : i 
 
 /* act[row * K + slot][n] = silu(gate_e[n] . xn[row]) * (up_e[n] . xn[row]), written split, with its sums over
    runs of GO rows. A block: KS waves over one group of 64 weight rows of one expert, wave w taking the w-th
-   of KS contiguous ranges of the columns; wave 0 writes. */
+   of KS contiguous ranges of the columns; wave 0 writes. Q6_K and Q8_0 steps (27 and 36 registers a matrix, two
+   matrices, two steps in flight) do not fit two waves a SIMD: held to that they spilled 548 and 204 bytes a lane
+   inside the column loop; at one wave a SIMD the extra values sit in accumulator registers, and a rows step of
+   32 sequences (8 layers) went 2.74 → 1.76 ms (Q6_K) and 2.10 → 1.94 ms (Q8_0), Q4_K unchanged. */
 template <int DT, int GO, int KS>
-__global__ __launch_bounds__(64 * KS, 8 / KS) void gmma_in_kernel(gmma_args a, int wpe, int ts_n) {
+__global__ __launch_bounds__(64 * KS, DT == VITNA_DTYPE_Q4_K ? 8 / KS : 1) void gmma_in_kernel(gmma_args a, int wpe, int ts_n) {
     __shared__ float red[KS > 1 ? KS * 2 * 4 * 64 : 1];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int per = a.E * wpe, ts = blockIdx.x / per, eb = blockIdx.x - ts * per;
