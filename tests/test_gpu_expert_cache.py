@@ -150,6 +150,11 @@ def test_cache_limits():
                 dev.rows_experts(0, ok, w, guess=outside)
             with pytest.raises(va.VitnaError, match="routes to"):
                 dev.rows_experts(0, ok[:, :K - 1], w[:, :K - 1])
+            # one token's experts: the same checks before any slot is taken
+            with pytest.raises(va.VitnaError, match="named twice"):
+                dev.moe_experts(0, twice[1], w[1])
+            with pytest.raises(va.VitnaError, match="outside"):
+                dev.moe_experts(0, outside[0], w[0])
             _, cnt = dev.expert_cache_state()
             assert cnt["acquired"] == 0 and cnt["copies"] == 0
             dev.rows_experts(0, ok, w, guess=ok)

@@ -802,6 +802,8 @@ extern "C" bool vitna_cuda_moe_experts(struct vitna_cuda_model* g, size_t layer,
     if (k != (size_t)g->K) return fail(err, err_len, "%zu experts given; the model routes to %d", k, g->K);
     for (size_t i = 0; i < k; i++) {
         if (ids[i] < 0 || ids[i] >= g->E) return fail(err, err_len, "expert %d is outside the layer's %d", ids[i], g->E);
+        for (size_t j = 0; j < i; j++)
+            if (ids[j] == ids[i]) return fail(err, err_len, "expert %d is named twice", ids[i]); /* before any slot is taken */
         if (guess && (guess[i] < 0 || guess[i] >= g->E)) return fail(err, err_len, "guessed expert %d is outside the layer's %d", guess[i], g->E);
     }
     int32_t slot_of[ROUTE_K_MAX];
