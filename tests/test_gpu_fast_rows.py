@@ -174,3 +174,47 @@ def test_fast_rows_step_matches_abi():
     finally:
         dev.close()
         model.free()
+
+
+def test_exact_pass_at_rows_max():
+    """A model without gpu_fast at the most rows a pass takes (vitna_cuda_moe_rows_max = 1024, 16 rows of each of
+    64 sequences at consecutive positions): the device-routed rows step (one graph) and the same pass through the
+    ABI layer by layer with the device's routing give the same logits bits, and sampled rows' logits are within
+    1e-3 of max |cpu| of the checker's step over the device's cache."""
+    say("exact pass at rows_max")
+    model, dev = make("q4km", 1618, False)
+    try:
+        cfg = model.cfg
+        n = dev.rows_max()
+        assert n == 1024
+        rows = pass_rows(n, cfg, salt=11)
+        a = np.stack(dev.rows_step(rows))
+        dev_rt = [[dev.rows_routing(l, i) for i in range(n)] for l in range(cfg.n_layers)]
+        for l in range(cfg.n_layers):
+            ids, ws = host_route(dev, rows, l, cfg)
+            d_ids = np.array([dev_rt[l][i][1] for i in range(n)])
+            d_ws = np.array([dev_rt[l][i][2] for i in range(n)])
+            assert np.array_equal(d_ids, ids), ("layer", l)
+            dev.rows_experts(l, d_ids, d_ws)
+        c = np.stack(dev.rows_head(n))
+        assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+        L, kd = cfg.n_layers, cfg.n_kv_heads * cfg.head_dim
+        kc = np.ctypeslib.as_array(model.m.k_cache, shape=(SEQS, L, model.m.ctx, kd))
+        vc = np.ctypeslib.as_array(model.m.v_cache, shape=(SEQS, L, model.m.ctx, kd))
+        worst = 0.0
+        for i in (0, SEQS + 3, n - 1):
+            tok, pos, seq = rows[i]
+            for l in range(L):
+                if pos:
+                    k, v = dev.kv(seq, l, 0, pos)
+                    kc[seq, l, :pos] = k
+                    vc[seq, l, :pos] = v
+            ref, _, tc, _ = oracle.step(model, seq, tok, pos)
+            for l in range(L):
+                assert np.array_equal(np.sort(dev_rt[l][i][1]), np.sort(tc[l])), ("row", i, "layer", l)
+            worst = max(worst, rel(a[i], ref))
+        say("  rows step = ABI bits at 1024 rows; logits rel err against the checker", worst)
+        assert worst <= 1e-3
+    finally:
+        dev.close()
+        model.free()
