@@ -226,3 +226,37 @@ def test_long_context_rows(long_model):
             say("  row %d pos %d: attention rel err %.3g, logits rel err %.3g" % (i, pos, ra, r))
             assert ra <= 1e-4
             assert r <= REL
+
+
+def test_max_context_decode():
+    """The longest context a model takes (1024 chunks of 64 positions): a batch-1 step at its last position, the
+    attention output (merged inside the o-projection from 1024 chunks) against the float64 restatement and the
+    logits against the checker."""
+    spec = dict(LONG, ctx=1024 * 64, seqs=1)
+    model = va.Model(va.shape(**spec), 6553)
+    try:
+        cfg = model.cfg
+        kd = cfg.n_kv_heads * cfg.head_dim
+        kc = np.ctypeslib.as_array(model.m.k_cache, shape=(1, cfg.n_layers, model.m.ctx, kd))
+        vc = np.ctypeslib.as_array(model.m.v_cache, shape=(1, cfg.n_layers, model.m.ctx, kd))
+        kc[:] = va.normal(6553, 101, kc.size).reshape(kc.shape)
+        vc[:] = va.normal(6553, 102, vc.size).reshape(vc.shape)
+        dev = va.Device(model)
+        try:
+            for l in range(cfg.n_layers):
+                dev.kv(0, l, 0, model.m.ctx, kc[0, l], vc[0, l])
+            pos = model.m.ctx - 1
+            say("decode step at position", pos)
+            ref, _, tc, _ = oracle.step(model, 0, 29, pos)
+            logits = dev.step(0, 29, pos)
+            q, att = dev.attention_io(0)
+            ra = rel(att, attention_ref(model, dev, q, 0, cfg.n_layers - 1, pos))
+            r = rel(logits, ref)
+            say("  attention rel err %.3g, logits rel err %.3g" % (ra, r))
+            assert ra <= 1e-4
+            assert np.array_equal(dev.step_routing(cfg.n_layers - 1)[0], tc[-1])
+            assert r <= REL
+        finally:
+            dev.close()
+    finally:
+        model.free()
