@@ -696,35 +696,21 @@ __global__ __launch_bounds__(256) void attention_oproj_kernel(attn_args a, qmat 
     const int sub = lane / LPR, al = lane % LPR;
     const int t_abs = g * (CW / 32) + al; /* the lane's slice of a row */
     const int rbase = blockIdx.y * (4 * RPW * OPROJ_U) + wave * (RPW * OPROJ_U) + sub;
-    /* the position, requested ahead of the weights */
-    const int pos_v = gld<int>(&a.rows[0].pos);
-    __builtin_amdgcn_sched_barrier(0);
-
-    /* then the weights: nothing they need comes from before (the chunk count, which the partials' addresses need,
-       is a dependent load), so they are in flight while that load and the partials' loads run */
-    qraw q[OPROJ_U];
-#pragma unroll
-    for (int u = 0; u < OPROJ_U; u++) {
-        const int r = min(rbase + u * RPW, o.rows - 1);
-        slice_load<DT>(o, 0, r, t_abs, q[u]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    /* the merge's loads: wave w, head hq = g HG + w, DPT dimensions a lane, the maxima and sums of chunks lane and
-       lane + 64 */
+    /* the merge's loads first, none of them waiting for the position: wave w, head hq = g HG + w, DPT dimensions a
+       lane, the values of chunks 0 .. OPROJ_PRE - 1 and the maxima and sums of chunks lane and lane + 64, read
+       whatever the position (those past its last chunk, or past the buffer's chunks as its last, are not used) */
     __shared__ __attribute__((aligned(16))) float fm[HG][MERGE_MAX];
     __shared__ __attribute__((aligned(16))) float fl[HG][MERGE_MAX];
     __shared__ __attribute__((aligned(16))) float sx[CW];
     const int G = a.n_heads / a.n_kv, hq = g * HG + wave, h = hq / G, gi = hq % G;
-    const int n_act = __builtin_amdgcn_readfirstlane(pos_v) / ATTN_CHUNK + 1;
     const float* base = a.partial + ((size_t)h * a.splits_max * G + gi) * (HD + 4);
     const size_t stride = (size_t)G * (HD + 4);
-    const int d0 = lane * DPT;
-    /* (chunks past the last are read as the last, unused: every load unconditional, in one batch) */
+    const int d0 = lane * DPT, last = a.splits_max - 1;
+    const int pos_v = gld<int>(&a.rows[0].pos);
     float v0[OPROJ_PRE][DPT];
 #pragma unroll
     for (int i = 0; i < OPROJ_PRE; i++) {
-        const float* p = base + (size_t)min(i, n_act - 1) * stride + d0;
+        const float* p = base + (size_t)min(i, last) * stride + d0;
         if constexpr (DPT == 2) {
             const float2 t = *reinterpret_cast<const float2*>(p);
             v0[i][0] = t.x;
@@ -735,7 +721,19 @@ __global__ __launch_bounds__(256) void attention_oproj_kernel(attn_args a, qmat 
     }
     float2 ml[2];
 #pragma unroll
-    for (int i = 0; i < 2; i++) ml[i] = *reinterpret_cast<const float2*>(base + (size_t)min(lane + WAVE * i, n_act - 1) * stride + HD);
+    for (int i = 0; i < 2; i++) ml[i] = *reinterpret_cast<const float2*>(base + (size_t)min(lane + WAVE * i, last) * stride + HD);
+    __builtin_amdgcn_sched_barrier(0);
+
+    /* then the weights, which nothing before depends on either: U units of RPW rows a wave */
+    qraw q[OPROJ_U];
+#pragma unroll
+    for (int u = 0; u < OPROJ_U; u++) {
+        const int r = min(rbase + u * RPW, o.rows - 1);
+        slice_load<DT>(o, 0, r, t_abs, q[u]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int n_act = __builtin_amdgcn_readfirstlane(pos_v) / ATTN_CHUNK + 1;
+
     /* the merge, as attention_merge_kernel<1> computes it */
     float m = -INFINITY;
 #pragma unroll
