@@ -482,13 +482,13 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
         for (int h = 0; h < NR; h++) {
             const int r = r0 + h * nwaves < H ? r0 + h * nwaves : H - 1;
 #pragma unroll
-            for (int j = 0; j < IPL; j++) slice_load<DT>(a.down, ek[j], r, tk[j], q[h][j]);
+            for (int j = 0; j < IPL; j++) slice_load<DT, (IPL >= 6)>(a.down, ek[j], r, tk[j], q[h][j]);
         }
 #pragma unroll
         for (int h = 0; h < NR; h++) {
             float p = 0.f;
 #pragma unroll
-            for (int j = 0; j < IPL; j++) p = fmaf(wk[j], slice_dot<DT>(q[h][j], tk[j], xs[j]), p);
+            for (int j = 0; j < IPL; j++) p = fmaf(wk[j], slice_dot<DT, (IPL >= 6)>(q[h][j], tk[j], xs[j]), p);
             p = row_sum<64>(p);
             const int r = r0 + h * nwaves;
             if (lane == 63 && r < H) {

@@ -250,8 +250,10 @@ __device__ __forceinline__ void load_xslice(int dtype, int t, const float* __res
 struct qraw {
     u32x4 a;      /* Q8_0: q[0..15]; Q4_K: q bytes; Q6_K: ql bytes */
     u32x4 b;      /* Q8_0: q[16..31]; Q4_K: header; Q6_K: qh bytes */
-    uint32_t c;   /* Q8_0: d; Q6_K: the two scale bytes (lo run | hi run << 8) */
+    uint32_t c;   /* Q8_0: d; Q6_K: scale bytes 8h .. 8h + 3 of the block (h: the slice's half), or, picked at
+                     the load (PICK), the slice's two (lo run | hi run << 8) */
     uint32_t d;   /* Q6_K: d */
+    uint32_t e;   /* Q6_K: scale bytes 8h + 4 .. 8h + 7 (not PICK) */
 };
 
 /* A load from device memory through a global-address-space pointer: a global_load, counted by vmcnt alone (a
@@ -266,7 +268,10 @@ __device__ __forceinline__ T gld(const void* p) {
     else return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) uint8_t*)p);
 }
 
-template <int DT>
+/* PICK (Q6_K): the slice's two scale bytes picked as they are loaded, one register a slice instead of two, for
+   kernels short of registers; otherwise the half's eight bytes are kept as loaded and picked by slice_dot (picking
+   them at the load makes the wave wait for the load there, and a wait counts every load issued before it). */
+template <int DT, bool PICK = false>
 __device__ __forceinline__ void slice_load(const qmat& m, int e, int row, int t, qraw& r) {
     const size_t blk = (size_t)row * m.nb + (t >> (DT == VITNA_DTYPE_Q8_0 ? 0 : 3));
     if (DT == VITNA_DTYPE_Q8_0) {
@@ -281,18 +286,25 @@ __device__ __forceinline__ void slice_load(const qmat& m, int e, int row, int t,
         const int u = t & 7, h = u >> 2, r0 = (u >> 1) & 1, s = u & 1;
         r.a = gld<u32x4>(m.p[0] + e * m.estride[0] + blk * 128 + 64 * h + 32 * r0 + 16 * s);
         r.b = gld<u32x4>(m.p[1] + e * m.estride[1] + blk * 64 + 32 * h + 16 * s);
-        const uint8_t* sc = m.p[2] + e * m.estride[2] + blk * 16;
-        /* scale of weights i: i / 16 = 8h + 2r + s, for r = r0 and r0 + 2 */
-        r.c = (uint32_t)gld<uint8_t>(sc + 8 * h + 2 * r0 + s) | ((uint32_t)gld<uint8_t>(sc + 8 * h + 2 * r0 + 4 + s) << 8);
+        if constexpr (PICK) {
+            /* scale of weights i: i / 16 = 8h + 2r + s, for r = r0 and r0 + 2 */
+            const uint8_t* sc = m.p[2] + e * m.estride[2] + blk * 16;
+            r.c = (uint32_t)gld<uint8_t>(sc + 8 * h + 2 * r0 + s) | ((uint32_t)gld<uint8_t>(sc + 8 * h + 2 * r0 + 4 + s) << 8);
+        } else {
+            /* the half's eight scale bytes as they lie (one 8-byte load; the planes are 8-byte aligned) */
+            typedef uint32_t w2 __attribute__((ext_vector_type(2)));
+            const w2 sc = gld<w2>(m.p[2] + e * m.estride[2] + blk * 16 + 8 * h);
+            r.c = sc.x;
+            r.e = sc.y;
+        }
         r.d = gld<uint16_t>(m.p[3] + e * m.estride[3] + blk * 2);
-        r.c |= (uint32_t)(2 * r0) << 16; /* the shift of this slice's high bits */
     }
 }
 
 /* The slice's dot product with the lane's activations, fp32 accumulate. The
    per-weight widening w = f(q) is folded: sum (d1 q - m1) x = d1 sum(q x) -
    m1 sum(x), so the inner loop is a byte-to-float convert and one FMA. */
-template <int DT>
+template <int DT, bool PICK = false>
 __device__ __forceinline__ float slice_dot(const qraw& r, int t, const xslice& xs) {
     if (DT == VITNA_DTYPE_Q8_0) {
         /* q + 128 as unsigned bytes, the 128 x sum taken back out */
@@ -347,7 +359,10 @@ __device__ __forceinline__ float slice_dot(const qraw& r, int t, const xslice& x
         return fmaf(d0, acc0, fmaf(d1, acc1, -(m0 * xs.slo + m1 * xs.shi)));
     } else { /* Q6_K */
         const uint32_t ql[4] = {r.a.x, r.a.y, r.a.z, r.a.w}, qh[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-        const int sh = (int)(r.c >> 16);
+        /* slice u = 4h + 2r0 + s: its high bits shifted by 2 r0; weights i / 16 = 8h + 2r + s for r = r0 (scale byte
+           2 r0 + s of the half's first four) and r0 + 2 (the same byte of the next four) */
+        const int u = t & 7, r0 = (u >> 1) & 1, bi = 2 * r0 + (u & 1);
+        const int sh = 2 * r0;
         float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -363,7 +378,8 @@ __device__ __forceinline__ float slice_dot(const qraw& r, int t, const xslice& x
             for (int i = 0; i < 4; i++) acc1 = fmaf(f[i], xs.hi[4 * j + i], acc1);
         }
         const float d = f16_bits_to_f32(r.d);
-        const float s0 = (float)(int8_t)(r.c & 0xff), s1 = (float)(int8_t)((r.c >> 8) & 0xff);
+        const float s0 = (float)(int8_t)((PICK ? r.c : r.c >> (8 * bi)) & 0xff);
+        const float s1 = (float)(int8_t)((PICK ? r.c >> 8 : r.e >> (8 * bi)) & 0xff);
         const float a0 = acc0 - 32.0f * xs.slo, a1 = acc1 - 32.0f * xs.shi;
         return d * fmaf(s0, a0, s1 * a1);
     }
