@@ -302,11 +302,12 @@ hipError_t launch_route_check(const float* logits, int E, int K, int renorm, rou
    consecutive units (one slot, except where a slot ends) and, when it routes the logits itself, runs only the
    selection rounds up to its slot before its loads go out. */
 template <int DT, int LPR, int SPL, int NS>
-__device__ __forceinline__ void experts_in_body(const experts_in_args& a, const xslice (&xs)[SPL], int wave, int lane) {
+__device__ __forceinline__ void experts_in_body(const experts_in_args& a, int wave, int lane) {
     constexpr int RPW = WAVE / LPR;
     const int sub = lane / LPR, al = lane % LPR, wib = threadIdx.x / WAVE;
     const int I = a.gate.rows, units = a.K * I;
     const int b = wave * 2 * RPW; /* this wave's first unit */
+    xslice xs[SPL];
     __shared__ int wch[4][ROUTE_K_MAX];
     __shared__ route_out wrt[4];
     __shared__ float slg[4][NS * 64];
@@ -314,11 +315,20 @@ __device__ __forceinline__ void experts_in_body(const experts_in_args& a, const 
     if (a.logits) {
         /* the selection rounds (the reference's passes, engine/src/model.c:626-650) up to slot kmax */
         float lg[NS];
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const int e = lane + 64 * i;
+            lg[i] = a.logits[e < a.E ? e : 0];
+        }
+        /* the token's activations requested right behind the logits: both were written by the router, and each
+           round trip is long; the selection below waits for the logits only */
+#pragma unroll
+        for (int j = 0; j < SPL; j++) load_xslice(DT, lane % LPR + LPR * j, a.xn, xs[j]);
         bool nan = false;
 #pragma unroll
         for (int i = 0; i < NS; i++) {
             const int e = lane + 64 * i;
-            lg[i] = e < a.E ? a.logits[e] : -INFINITY;
+            lg[i] = e < a.E ? lg[i] : -INFINITY;
             nan |= e < a.E && lg[i] != lg[i];
         }
         if (__any(nan)) {
@@ -347,8 +357,10 @@ __device__ __forceinline__ void experts_in_body(const experts_in_args& a, const 
                 if (lane == 0) wch[wib][k] = pick;
             }
         }
-    } else if (lane < a.K) {
-        wch[wib][lane] = a.rt->chosen[lane];
+    } else {
+#pragma unroll
+        for (int j = 0; j < SPL; j++) load_xslice(DT, lane % LPR + LPR * j, a.xn, xs[j]);
+        if (lane < a.K) wch[wib][lane] = a.rt->chosen[lane];
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -393,13 +405,10 @@ __global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
         }
         return;
     }
-    xslice xs[SPL];
-#pragma unroll
-    for (int j = 0; j < SPL; j++) load_xslice(DT, lane % LPR + LPR * j, a.xn, xs[j]);
-    if (!a.logits || a.E <= 64) experts_in_body<DT, LPR, SPL, 1>(a, xs, wave, lane);
-    else if (a.E <= 128) experts_in_body<DT, LPR, SPL, 2>(a, xs, wave, lane);
-    else if (a.E <= 256) experts_in_body<DT, LPR, SPL, 4>(a, xs, wave, lane);
-    else experts_in_body<DT, LPR, SPL, 8>(a, xs, wave, lane);
+    if (!a.logits || a.E <= 64) experts_in_body<DT, LPR, SPL, 1>(a, wave, lane);
+    else if (a.E <= 128) experts_in_body<DT, LPR, SPL, 2>(a, wave, lane);
+    else if (a.E <= 256) experts_in_body<DT, LPR, SPL, 4>(a, wave, lane);
+    else experts_in_body<DT, LPR, SPL, 8>(a, wave, lane);
 }
 
 template <int DT, int LPR, int SPL>
