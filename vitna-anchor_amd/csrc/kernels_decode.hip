@@ -120,9 +120,9 @@ hipError_t launch_widen_blocks(const uint8_t* src, int dtype, size_t rows, size_
 /* ------------------------------------------------------------------ */
 
 
-/* Four router rows a block (sixteen lanes of wave 0 a row). NT threads: 64, or 256 when x's attention parts
-   are still to be added (route_args::parts): the other waves then help load x and the parts, so that every
-   load goes out in one round. */
+/* Four router rows a block (sixteen lanes of wave 0 a row). NT threads: 64 (a pass of several rows), or 256 for
+   one row: the other waves help load x (and its attention parts, route_args::parts), so that every load goes out
+   in one round, ahead of wave 0's router weights. */
 template <int NCH, int NT>
 __global__ __launch_bounds__(NT) void route_kernel(route_args a) {
     extern __shared__ float sh[];
@@ -239,7 +239,7 @@ hipError_t launch_route(const route_args& a, hipStream_t s) {
     if (a.parts && a.H > ROUTE_PARTS_HMAX) return hipErrorInvalidValue;
 #define ROUTE_CASE(N)                                                                   \
     case N:                                                                             \
-        if (a.parts) route_kernel<N, 256><<<grid, 256, lds, s>>>(a);                   \
+        if (a.parts || a.n_rows == 1) route_kernel<N, 256><<<grid, 256, lds, s>>>(a);  \
         else route_kernel<N, 64><<<grid, 64, lds, s>>>(a);                              \
         break;
     switch (a.H / 16) {
