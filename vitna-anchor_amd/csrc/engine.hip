@@ -700,6 +700,12 @@ static hipError_t enqueue_experts(vitna_cuda_model* g, int layer, const float* l
 }
 
 static hipError_t enqueue_head(vitna_cuda_model* g) {
+    if (g->parts_n) {
+        /* a layer's attention whose experts never ran: its parts still belong in the residual */
+        const hipError_t e = launch_attn_fold(g->x, g->parts, g->parts_n, g->H, g->stream);
+        g->parts_n = 0;
+        if (e != hipSuccess) return e;
+    }
     gemv_args gh;
     memset(&gh, 0, sizeof(gh));
     gh.w[0] = g->head;
