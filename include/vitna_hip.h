@@ -142,6 +142,16 @@ bool vitna_hip_moe_step_async(struct vitna_cuda_model* g, size_t seq, int32_t to
 bool vitna_hip_moe_rows_step(struct vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, float* const* logits, char* err,
                              size_t err_len);
 
+/** Passes of the reference's rows ABI (vitna_cuda_moe_rows_route / _experts / _head) of at most n rows run each
+    row with a single token's kernels, so that every row's logits are the bits a step of that row alone gives
+    (model.c:1052-1190 relies on it for drafted tokens and batched steps); longer passes take the multi-row
+    kernels (within 1e-3 of the CPU, other bits). n is 64 (model.c's PASS_MAX) from vitna_cuda_create; 0 sends
+    every pass to the multi-row kernels (for their tests). At most 64. On a model with an expert cache, such a
+    pass whose experts outnumber one wave of the cache's rule (its slots less k) is taken in groups of consecutive
+    rows that each fit one wave, each group a pass of the cache: the bits stay those of every expert resident, and
+    the cache's counts are those of the groups' passes. */
+bool vitna_hip_set_exact_rows(struct vitna_cuda_model* g, size_t n, char* err, size_t err_len);
+
 /** The mixture-of-experts half of layer (RMSNorm, router, top-k on the
     device, experts, weighted sum) on residual row 0, in place, enqueued. */
 bool vitna_hip_moe_ffn(struct vitna_cuda_model* g, size_t layer, char* err, size_t err_len);

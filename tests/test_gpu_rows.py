@@ -49,12 +49,17 @@ def cpu_rows(model, rows):
 
 
 @pytest.mark.parametrize("name", ["q8", "q4km"])
-def test_rows_abi_layer_by_layer(name):
+@pytest.mark.parametrize("exact", [True, False])
+def test_rows_abi_layer_by_layer(name, exact):
     """model.c's moe_rows_on_gpu played by the test: rows up to the router on the device, the host routes each
-    row, the device runs the grouped experts. Two rows share sequence 1 at consecutive positions."""
-    say("rows abi", name)
+    row, the device runs the experts: a single token's kernels a row (the pass is within vitna_hip_set_exact_rows'
+    limit), or with the limit at 0 the multi-row projections and grouped experts. Two rows share sequence 1 at
+    consecutive positions."""
+    say("rows abi", name, "exact" if exact else "multi-row")
     prefill = [40, 17, 60]
     model, dev = model_with_cache(name, 777, prefill, 3)
+    if not exact:
+        dev.set_exact_rows(0)
     try:
         cfg = model.cfg
         K = cfg.n_experts_used
@@ -103,7 +108,7 @@ def test_rows_step_device_routed(name):
 
 @pytest.mark.parametrize("name", ["q8", "q4km", "q6gu"])
 def test_rows_crowded_experts(name):
-    """The grouped experts alone, 24 rows on 16 (32) experts: about six tokens an expert, so experts take
+    """The grouped experts alone (the rows ABI with vitna_hip_set_exact_rows at 0), 24 rows on 16 (32) experts: about six tokens an expert, so experts take
     several four-token tiles, and the small models' short rows give the kernels' column split empty and
     odd-started ranges. Each layer: the device's residual rows before and after vitna_cuda_moe_rows_experts
     (routed by the host from the device's router logits, as model.c routes), against the CPU checker's
@@ -112,6 +117,7 @@ def test_rows_crowded_experts(name):
     seqs = 24
     prefill = [1 + (7 * s) % 60 for s in range(seqs)]
     model, dev = model_with_cache(name, 999, prefill, seqs)
+    dev.set_exact_rows(0)  # the grouped kernels, not a single token's a row
     try:
         cfg = model.cfg
         H, K = cfg.hidden, cfg.n_experts_used

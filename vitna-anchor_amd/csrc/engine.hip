@@ -36,6 +36,12 @@
 /* With the model's gpu_fast, a pass of at least this many rows runs its experts as the bf16 matrix-core grouped GEMM
    of the prefill (the reference's FAST_ROWS, model_cuda.cu:204); smaller passes keep the exact kernels. */
 #define FAST_ROWS 64
+/* Passes of the rows ABI of at most exact_rows rows (model.c's PASS_MAX, 64: the passes that check drafted tokens
+   and the batched steps of a server, model.c:1052-1190) run each row through the kernels of a single token's step,
+   several rows a launch: a row's logits are then the bits its step alone gives, as model.c expects of them ("every
+   row is the one a step would give", main.c:1003-1007). Longer passes (a prompt's chunks) take the multi-row
+   kernels, within 1e-3 of the checker but not those bits. */
+#define EXACT_ROWS 64
 
 struct dlayer {
     qmat q, k, v, o;
@@ -119,6 +125,8 @@ struct vitna_cuda_model {
     bool fast;          /* m->gpu_fast: passes of fast_rows rows or more take the grouped GEMM for their experts */
     size_t fast_rows, long_from;
     int rows_n;         /* rows of the pass in flight (vitna_cuda_moe_rows_*) */
+    int exact_rows;     /* passes of the rows ABI up to this many rows run the single-token kernels (EXACT_ROWS) */
+    bool pass_exact;    /* and the pass in flight is one */
     /* prefill through one MoE layer: buffers for pf_cap rows, allocated on first use */
     size_t pf_cap;
     std::vector<void*> pf_allocs;
@@ -441,6 +449,7 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
     g->eps = c->rms_eps;
     g->fast = m->gpu_fast;
     g->fast_rows = FAST_ROWS;
+    g->exact_rows = EXACT_ROWS;
     g->long_from = 1024;
     g->embed = {}; g->head = {};
     g->final_norm = nullptr;
@@ -560,7 +569,7 @@ extern "C" struct vitna_cuda_model* vitna_cuda_create(const vitna_llama_t* m, co
         ok = dalloc(g, &g->q, R * qd * 4, "scratch", err, err_len) && dalloc(g, &g->qp, R * qd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->k, R * kd * 4, "scratch", err, err_len) && dalloc(g, &g->v, R * kd * 4, "scratch", err, err_len) &&
              dalloc(g, &g->att, R * qd * 4, "scratch", err, err_len) &&
-             dalloc(g, &g->parts, (size_t)OPROJ_PARTS_MAX * c->hidden * 4, "scratch", err, err_len) &&
+             dalloc(g, &g->parts, (size_t)EXACT_ROWS * OPROJ_PARTS_MAX * c->hidden * 4, "scratch", err, err_len) &&
              dalloc(g, &g->vocab, R * c->vocab * 4, "the logits", err, err_len) &&
              dalloc(g, &g->partial, (size_t)R * c->n_kv_heads * g->splits_max * G * (c->head_dim + 4) * 4, "attention partials", err, err_len) &&
              dalloc(g, &g->k_cache, m->seqs * c->n_layers * g->layer_kv * 4, "the key cache", err, err_len) &&
@@ -768,12 +777,13 @@ extern "C" bool vitna_cuda_moe_route(struct vitna_cuda_model* g, size_t seq, int
 }
 
 /* slots: where the experts are in the expert cache (the kernels' expert index), or null for resident experts */
+/* at: the first of the rows (the routing goes to rt[at .. at + n)) */
 static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const float* weights, size_t k, char* err, size_t err_len,
-                        const int32_t* slots = nullptr) {
+                        const int32_t* slots = nullptr, size_t at = 0) {
     if (k != (size_t)g->K) return fail(err, err_len, "%zu experts given; the model routes to %d", k, g->K);
     /* the previous routing's copy out of the page-locked buffer must have run */
     HIP_TRY(hipEventSynchronize(g->rt_copied), "waiting for the previous routing copy");
-    route_out* ro = g->rt_host;
+    route_out* ro = g->rt_host + at;
     for (size_t t = 0; t < n; t++) {
         memset(&ro[t], 0, sizeof(route_out));
         for (size_t i = 0; i < k; i++) {
@@ -788,7 +798,7 @@ static bool put_routing(vitna_cuda_model* g, size_t n, const int32_t* ids, const
         }
     }
     /* from page-locked memory, in stream order: the kernels after it read it, nothing waits on the host */
-    HIP_TRY(hipMemcpyAsync(g->rt, ro, n * sizeof(route_out), hipMemcpyHostToDevice, g->stream), "copying the routing");
+    HIP_TRY(hipMemcpyAsync(g->rt + at, ro, n * sizeof(route_out), hipMemcpyHostToDevice, g->stream), "copying the routing");
     HIP_TRY(hipEventRecord(g->rt_copied, g->stream), "recording the routing copy");
     return true;
 }
@@ -2081,6 +2091,103 @@ static hipError_t enqueue_rows_head(vitna_cuda_model* g, int n, const float* ypa
     return enqueue_multi(g, gh, img);
 }
 
+/* ---- passes of few rows, each row with a single token's kernels (EXACT_ROWS) ---- */
+
+static bool rows_exact(const vitna_cuda_model* g, int n) { return n <= g->exact_rows && !rows_fast(g, n); }
+
+/* Layer's attention for the pass's n rows as enqueue_attention runs it for one: the q/k/v GEMV with its norm, the
+   attention (rows of one sequence: each row's key and value stored first, with the same arithmetic), the merged
+   o-projection when the layer takes it (its parts then folded into the rows, as the single token's router and
+   experts add them) or else the merge and the o-projection GEMV. */
+static hipError_t enqueue_exact_attention(vitna_cuda_model* g, int layer, int n) {
+    const dlayer& d = g->L[layer];
+    const int qd = g->nh * g->hd, kd = g->nkv * g->hd;
+    gemv_args ga;
+    memset(&ga, 0, sizeof(ga));
+    ga.w[0] = d.q; ga.w[1] = d.k; ga.w[2] = d.v;
+    ga.y[0] = g->q; ga.y[1] = g->k; ga.y[2] = g->v;
+    ga.n = 3;
+    ga.x = g->x;
+    ga.norm_w = d.attn_norm;
+    ga.eps = g->eps;
+    ga.rows = n; ga.xstride = g->H; ga.ystride[0] = qd; ga.ystride[1] = kd; ga.ystride[2] = kd;
+    hipError_t e = launch_gemv(ga, g->stream);
+    if (e != hipSuccess) return e;
+    attn_args a;
+    memset(&a, 0, sizeof(a));
+    a.q_raw = g->q; a.k_raw = g->k; a.v_raw = g->v;
+    a.q_norm = d.q_norm; a.k_norm = d.k_norm;
+    a.cos_tab = g->cos_tab; a.sin_tab = g->sin_tab;
+    a.k_cache = g->k_cache + (size_t)layer * g->layer_kv;
+    a.v_cache = g->v_cache + (size_t)layer * g->layer_kv;
+    a.seq_stride = (size_t)g->NL * g->layer_kv;
+    a.rows = g->rows_dev;
+    a.n_rows = n;
+    a.partial = g->partial;
+    a.att = g->att;
+    a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx; a.splits_max = g->splits_max;
+    a.eps = g->eps;
+    a.mma = 1;
+    if (g->rows_shared_seq) {
+        a.q_out = g->qp;
+        e = launch_attention_prepare(a, g->stream);
+        if (e != hipSuccess) return e;
+        a.q_raw = g->qp;
+        a.prepared = 1;
+    }
+    e = launch_attention(a, g->stream);
+    if (e != hipSuccess) return e;
+    if (attention_oproj_fits(a, d.o)) {
+        const int np = g->nh / ATTN_OPROJ_HEADS;
+        e = launch_attention_oproj(a, d.o, g->parts, g->stream);
+        return e == hipSuccess ? launch_attn_fold(g->x, g->parts, np, g->H, g->stream, n) : e;
+    }
+    e = launch_attention_merge(a, g->stream);
+    if (e != hipSuccess) return e;
+    gemv_args go;
+    memset(&go, 0, sizeof(go));
+    go.w[0] = d.o; go.y[0] = g->x; go.n = 1; go.x = g->att; go.add = 1;
+    go.rows = n; go.xstride = qd; go.ystride[0] = g->H;
+    return launch_gemv(go, g->stream);
+}
+
+/* The experts of the pass's rows at .. at + n - 1 as rt routes them (by slot on a cached model), each row as
+   enqueue_experts runs one token's, added onto its residual row. */
+static hipError_t enqueue_exact_experts(vitna_cuda_model* g, int layer, int n, int at = 0) {
+    const dlayer& d = g->L[layer];
+    const size_t act_row = (size_t)g->K * g->I;
+    experts_in_args ai;
+    ai.gate = d.gate; ai.up = d.up; ai.xn = g->xn + (size_t)at * g->H; ai.rt = g->rt + at; ai.logits = nullptr; ai.E = g->E;
+    ai.renorm = g->renorm; ai.act = g->act + at * act_row; ai.K = g->K;
+    hipError_t e = launch_experts_in(ai, g->stream, n);
+    if (e != hipSuccess) return e;
+    experts_down_args ad;
+    ad.down = d.down; ad.act = g->act + at * act_row; ad.rt = g->rt + at; ad.y = g->x + (size_t)at * g->H; ad.K = g->K; ad.add = 1;
+    ad.parts = nullptr; ad.n_parts = 0;
+    return launch_experts_down(ad, g->stream, n);
+}
+
+/* The head of the pass's n rows as enqueue_head runs one row's. */
+static hipError_t enqueue_exact_head(vitna_cuda_model* g, int n) {
+    gemv_args gh;
+    memset(&gh, 0, sizeof(gh));
+    gh.w[0] = g->head;
+    gh.y[0] = g->vocab;
+    gh.n = 1;
+    gh.x = g->x;
+    gh.norm_w = g->final_norm;
+    gh.eps = g->eps;
+    gh.rows = n; gh.xstride = g->H; gh.ystride[0] = g->V;
+    return launch_gemv(gh, g->stream);
+}
+
+extern "C" bool vitna_hip_set_exact_rows(struct vitna_cuda_model* g, size_t n, char* err, size_t err_len) {
+    if (!g) return fail(err, err_len, "no model");
+    if (n > EXACT_ROWS) return fail(err, err_len, "%zu rows: at most %d take the single-token kernels", n, EXACT_ROWS);
+    g->exact_rows = (int)n;
+    return true;
+}
+
 /* The pass's rows to the device, checked as a step checks its token (model.c:1190-1200). */
 static bool set_rows(vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n, char* err, size_t err_len) {
     if (n < 1 || n > ROWS_MAX) return fail(err, err_len, "%zu rows: 1 to %d a pass", n, ROWS_MAX);
@@ -2098,6 +2205,7 @@ static bool set_rows(vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n
     HIP_TRY(hipMemcpyAsync(g->rows_dev, g->rows_host, n * sizeof(row_rec), hipMemcpyHostToDevice, g->stream), "copying the rows");
     HIP_TRY(hipEventRecord(g->rows_copied, g->stream), "recording the row copy");
     g->rows_n = (int)n;
+    g->pass_exact = false; /* vitna_cuda_moe_rows_route decides at layer 0 */
     g->parts_n = 0; /* a pass of rows owns x's rows: no one row's attention parts are pending any more */
     g->rows_shared_seq = shared;
     return true;
@@ -2112,11 +2220,12 @@ extern "C" bool vitna_cuda_moe_rows_route(struct vitna_cuda_model* g, const vitn
     g->last_step_mega = false;
     if (layer == 0) {
         if (!set_rows(g, rows, n, err, err_len)) return false;
+        g->pass_exact = rows_exact(g, (int)n);
         if (!check_launch(g, launch_embed_rows(g->embed, g->rows_dev, (int)n, g->x, g->stream), "the embeddings", err, err_len)) return false;
     } else if (n != (size_t)g->rows_n) {
         return fail(err, err_len, "%zu rows at layer %zu; the pass took %d at layer 0", n, layer, g->rows_n);
     }
-    hipError_t e = enqueue_rows_attention(g, (int)layer, (int)n, nullptr);
+    hipError_t e = g->pass_exact ? enqueue_exact_attention(g, (int)layer, (int)n) : enqueue_rows_attention(g, (int)layer, (int)n, nullptr);
     if (e == hipSuccess) e = enqueue_route(g, (int)layer, g->rlogits, (int)n, g->x, g->xn, false);
     const bool nx = next && layer + 1 < (size_t)g->NL;
     if (e == hipSuccess && nx) {
@@ -2168,7 +2277,6 @@ static bool cached_rows_experts(vitna_cuda_model* g, int layer, int n, const int
     expert_cache& c = g->ec;
     const dlayer& d = g->L[layer];
     if (k != g->K) return fail(err, err_len, "%d experts given; the model routes to %d", k, g->K);
-    if (!gmma_fits(d.gate, d.up, d.down)) return fail(err, err_len, "layer %d's experts do not fit the grouped kernels", layer);
     std::vector<int32_t> cnt(g->E, 0);
     for (int t = 0; t < n; t++)
         for (int i = 0; i < k; i++) {
@@ -2180,10 +2288,49 @@ static bool cached_rows_experts(vitna_cuda_model* g, int layer, int n, const int
                 return fail(err, err_len, "guessed expert %d is outside the layer's %d", guess[(size_t)t * k + i], g->E);
             cnt[e]++;
         }
-    if (!slot_tiles_for(g, d, err, err_len)) return false;
     std::vector<int32_t> want, slot_of(g->E, -1);
     for (int x = 0; x < g->E; x++)
         if (cnt[x]) want.push_back(x);
+    const int W = c.n_slots - c.K;
+    if (g->pass_exact) {
+        /* each row as a single token's step, from the slots: the rows in groups of consecutive rows whose experts
+           take one wave of the rule (every row's k experts fit one: W >= k), each group a pass of the cache, so
+           that the bits are those of every expert resident whatever the cache's size. A pass whose experts fit one
+           wave is one group: the rule's own pass. */
+        bool ok = true;
+        std::vector<int32_t> gcnt(g->E), slots((size_t)n * k);
+        for (int t0 = 0; ok && t0 < n;) {
+            std::fill(gcnt.begin(), gcnt.end(), 0);
+            int t1 = t0, distinct = 0;
+            for (; t1 < n; t1++) {
+                int fresh = 0;
+                for (int i = 0; i < k; i++) fresh += gcnt[ids[(size_t)t1 * k + i]] == 0;
+                if (t1 > t0 && distinct + fresh > W) break;
+                distinct += fresh;
+                for (int i = 0; i < k; i++) gcnt[ids[(size_t)t1 * k + i]]++;
+            }
+            std::vector<int32_t> gwant;
+            for (int x = 0; x < g->E; x++)
+                if (gcnt[x]) gwant.push_back(x);
+            ec_rows_count(c, layer, gcnt.data());
+            ok = ec_rows_wave(c, layer, gwant.data(), (int)gwant.size(), gcnt.data(), g->stream, slot_of.data(), err, err_len);
+            for (size_t i = 0; ok && i < gwant.size(); i++) {
+                const ec_slot& sl = c.slots[slot_of[gwant[i]]];
+                if (sl.copying && hipStreamWaitEvent(g->stream, sl.landed, 0) != hipSuccess) ok = fail(err, err_len, "waiting for an expert's copy");
+            }
+            for (size_t i = (size_t)t0 * k; i < (size_t)t1 * k; i++) slots[i] = slot_of[ids[i]];
+            ok = ok && put_routing(g, t1 - t0, ids + (size_t)t0 * k, weights + (size_t)t0 * k, k, err, err_len, slots.data() + (size_t)t0 * k, t0) &&
+                 check_launch(g, enqueue_exact_experts(g, layer, t1 - t0, t0), "the rows' experts", err, err_len);
+            /* the holds released whatever happened; the pass's guess after its last group's kernels */
+            const bool last = t1 == n;
+            const bool fin = ec_rows_finish(c, layer, ok && last ? guess : nullptr, last ? n : t1 - t0, k, err, err_len);
+            ok = ok && fin;
+            t0 = t1;
+        }
+        return ok;
+    }
+    if (!gmma_fits(d.gate, d.up, d.down)) return fail(err, err_len, "layer %d's experts do not fit the grouped kernels", layer);
+    if (!slot_tiles_for(g, d, err, err_len)) return false;
     ec_rows_count(c, layer, cnt.data());
     gmma_args m{};
     m.gate = d.gate; m.up = d.up; m.down = d.down;
@@ -2192,7 +2339,6 @@ static bool cached_rows_experts(vitna_cuda_model* g, int layer, int n, const int
     m.E = c.n_slots; m.K = g->K; m.cap = ROWS_MAX; m.n = n; m.ypart = g->ypart;
     hipError_t e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);
     bool ok = check_launch(g, e, "the rows' split", err, err_len);
-    const int W = c.n_slots - c.K;
     std::vector<uint8_t> in_wave(g->E, 0);
     for (size_t w0 = 0; ok && w0 < want.size(); w0 += W) {
         const int nw = (int)std::min<size_t>(W, want.size() - w0);
@@ -2248,6 +2394,9 @@ extern "C" bool vitna_cuda_moe_rows_experts(struct vitna_cuda_model* g, size_t l
     if (layer >= (size_t)g->NL) return fail(err, err_len, "layer %zu: the model has %d", layer, g->NL);
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
     if (g->ec.on) return cached_rows_experts(g, (int)layer, (int)n, ids, weights, (int)k, guess, err, err_len);
+    if (g->pass_exact)
+        return put_routing(g, n, ids, weights, k, err, err_len) &&
+               check_launch(g, enqueue_exact_experts(g, (int)layer, (int)n), "the rows' experts", err, err_len);
     if (rows_fast(g, (int)n)) {
         if (!prefill_reserve(g, n, err, err_len) || !put_routing(g, n, ids, weights, k, err, err_len)) return false;
         return check_launch(g, enqueue_fast_experts(g, (int)layer, (int)n, g->rt), "the rows' experts (grouped GEMM)", err, err_len);
@@ -2261,7 +2410,8 @@ extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, f
     if (!ensure_tiled(g, err, err_len)) return false;
     if (!g->attention) return fail(err, err_len, "this model has no output projection");
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
-    if (!check_launch(g, enqueue_rows_head(g, (int)n, nullptr), "the head", err, err_len)) return false;
+    if (!check_launch(g, g->pass_exact ? enqueue_exact_head(g, (int)n) : enqueue_rows_head(g, (int)n, nullptr), "the head", err, err_len))
+        return false;
     for (size_t i = 0; i < n; i++)
         if (logits && logits[i])
             HIP_TRY(hipMemcpyAsync(logits[i], g->vocab + i * g->V, (size_t)g->V * 4, hipMemcpyDeviceToHost, g->stream), "copying logits");

@@ -61,6 +61,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(gemv_args a) {
     extern __shared__ float sh[];
     const int lane = threadIdx.x & 63;
     const int H = a.w[0].cols;
+    if (blockIdx.y) {
+        /* row blockIdx.y of several: its vector and outputs; the arithmetic is a single vector's */
+        a.x += (size_t)blockIdx.y * a.xstride;
+        for (int i = 0; i < 3; i++) a.y[i] += (size_t)blockIdx.y * a.ystride[i];
+    }
     const float* xin = a.x;
     if (NORM) {
         /* up to eight float4 of x and of the weights a thread (H at most 8192, launch_gemv checks) */
@@ -154,14 +159,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(gemv_args a) {
 
 template <int D0, int D1, int D2, bool NORM, int U>
 static hipError_t gemv_launch(const gemv_args& a, int blocks, size_t lds, hipStream_t s) {
+    const dim3 grid(blocks, a.rows > 1 ? a.rows : 1);
     switch (a.w[0].cols / 32) {
-        case 4: gemv_kernel<D0, D1, D2, 4, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 8: gemv_kernel<D0, D1, D2, 8, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 16: gemv_kernel<D0, D1, D2, 16, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 32: gemv_kernel<D0, D1, D2, 32, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 64: gemv_kernel<D0, D1, D2, 64, 1, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 128: gemv_kernel<D0, D1, D2, 64, 2, NORM, U><<<blocks, 256, lds, s>>>(a); break;
-        case 256: gemv_kernel<D0, D1, D2, 64, 4, NORM, U><<<blocks, 256, lds, s>>>(a); break;
+        case 4: gemv_kernel<D0, D1, D2, 4, 1, NORM, U><<<grid, 256, lds, s>>>(a); break;
+        case 8: gemv_kernel<D0, D1, D2, 8, 1, NORM, U><<<grid, 256, lds, s>>>(a); break;
+        case 16: gemv_kernel<D0, D1, D2, 16, 1, NORM, U><<<grid, 256, lds, s>>>(a); break;
+        case 32: gemv_kernel<D0, D1, D2, 32, 1, NORM, U><<<grid, 256, lds, s>>>(a); break;
+        case 64: gemv_kernel<D0, D1, D2, 64, 1, NORM, U><<<grid, 256, lds, s>>>(a); break;
+        case 128: gemv_kernel<D0, D1, D2, 64, 2, NORM, U><<<grid, 256, lds, s>>>(a); break;
+        case 256: gemv_kernel<D0, D1, D2, 64, 4, NORM, U><<<grid, 256, lds, s>>>(a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -23,46 +23,6 @@
 
 #define GMAX 8
 
-/* RMSNorm and RoPE of NV vectors of HD in LDS (v[i] at vecs + i * HD): the
-   reference's per-head norm (engine/src/model.c:916-921) and vitna_rope_half
-   (engine/src/ops.c:273-281). */
-template <int HD>
-__device__ void norm_rope(float* vecs, int nv, const float* wq, const float* wk, int k_from, float eps, const float* c,
-                          const float* s, float* inv_s) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    constexpr int PL = HD / 64; /* elements a lane */
-    if (wq) {
-        /* a wave a vector: the sum of squares across the wave */
-        for (int v = wave; v < nv; v += 4) {
-            float ss = 0.f;
-#pragma unroll
-            for (int i = 0; i < PL; i++) {
-                const float e = vecs[v * HD + lane + 64 * i];
-                ss = fmaf(e, e, ss);
-            }
-            ss = wave_sum(ss);
-            if (lane == 0) inv_s[v] = 1.0f / sqrtf(ss / (float)HD + eps);
-        }
-        __syncthreads();
-        for (int i = tid; i < nv * HD; i += blockDim.x) {
-            const int g = i / HD, d = i % HD;
-            const float* w = g >= k_from ? wk : wq;
-            vecs[i] = (vecs[i] * inv_s[g]) * w[d];
-        }
-        __syncthreads();
-    }
-    constexpr int HALF = HD / 2;
-    for (int i = tid; i < nv * HALF; i += blockDim.x) {
-        const int g = i / HALF, j = i % HALF;
-        float* v = vecs + g * HD;
-        const float a = v[j], b = v[j + HALF];
-        const float ac = a * c[j], bs = b * s[j], bc = b * c[j], as = a * s[j];
-        v[j] = ac - bs;
-        v[j + HALF] = bc + as;
-    }
-    __syncthreads();
-}
-
 /* Sum over the lanes of one head's float4 group (HD / 4 consecutive lanes: a
    32-lane half for HD 128, a 16-lane row for HD 64), in every lane of it. */
 template <int HD>
@@ -308,27 +268,39 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     }
 }
 
-/* The prepare pass: one block a (row, kv head), its G query heads and its key. */
+/* The prepare pass: one block a (row, kv head), its G query heads and its key, each through head_norm_rope with
+   the lanes the attention kernels give it (thread t: float4 t % (HD / 4) of head t / (HD / 4); wave 0 the key), so
+   that the prepared queries and the stored key are the bits those kernels compute for themselves (a pass of rows
+   then gives each row what a step of that row alone gives). */
 template <int HD>
 __global__ __launch_bounds__(256) void attention_prepare_kernel(attn_args a) {
+    constexpr int QF4 = HD / 4;
     const int h = blockIdx.x, row = blockIdx.y;
     const row_rec rr = a.rows[row];
     const int pos = rr.pos, seq = rr.seq;
     const int G = a.n_heads / a.n_kv, kv_dim = a.n_kv * HD, half = HD / 2;
-    __shared__ float sq[(GMAX + 1) * HD];
-    __shared__ float inv_s[GMAX + 1];
-    const int tid = threadIdx.x;
-    float* nk = sq + G * HD;
-    for (int i = tid; i < G * HD; i += 256) sq[i] = a.q_raw[(size_t)row * a.n_heads * HD + (size_t)h * G * HD + i];
-    if (tid < HD) nk[tid] = a.k_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
-    __syncthreads();
-    norm_rope<HD>(sq, G + 1, a.q_norm, a.k_norm, G, a.eps, a.cos_tab + (size_t)pos * half, a.sin_tab + (size_t)pos * half, inv_s);
-    for (int i = tid; i < G * HD; i += 256) a.q_out[(size_t)row * a.n_heads * HD + (size_t)h * G * HD + i] = sq[i];
-    if (tid < HD) {
-        float* kc = a.k_cache + (size_t)seq * a.seq_stride;
-        float* vc = a.v_cache + (size_t)seq * a.seq_stride;
-        kc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = nk[tid];
-        vc[(size_t)pos * kv_dim + (size_t)h * HD + tid] = a.v_raw[(size_t)row * kv_dim + (size_t)h * HD + tid];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const float* cs = a.cos_tab + (size_t)pos * half;
+    const float* sn = a.sin_tab + (size_t)pos * half;
+    {
+        const int g = tid / QF4, j = tid % QF4;
+        const size_t at = (size_t)row * a.n_heads * HD + (size_t)(h * G + g) * HD;
+        float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (g < G) qv = reinterpret_cast<const float4*>(a.q_raw + at)[j];
+        if (g < GMAX) qv = head_norm_rope<HD>(qv, j, a.q_norm, a.eps, cs, sn);
+        if (g < G) reinterpret_cast<float4*>(a.q_out + at)[j] = qv;
+    }
+    if (wave == 0) {
+        float4 kv4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (lane < QF4) kv4 = reinterpret_cast<const float4*>(a.k_raw + (size_t)row * kv_dim + (size_t)h * HD)[lane];
+        kv4 = head_norm_rope<HD>(kv4, lane % QF4, a.k_norm, a.eps, cs, sn);
+        if (lane < QF4) {
+            float* kc = a.k_cache + (size_t)seq * a.seq_stride;
+            float* vc = a.v_cache + (size_t)seq * a.seq_stride;
+            const float4 vn = reinterpret_cast<const float4*>(a.v_raw + (size_t)row * kv_dim + (size_t)h * HD)[lane];
+            reinterpret_cast<float4*>(kc + (size_t)pos * kv_dim + (size_t)h * HD)[lane] = kv4;
+            reinterpret_cast<float4*>(vc + (size_t)pos * kv_dim + (size_t)h * HD)[lane] = vn;
+        }
     }
 }
 
@@ -692,9 +664,15 @@ template <int DT, int HD>
 __global__ __launch_bounds__(256) void attention_oproj_kernel(attn_args a, qmat o, float* __restrict__ parts) {
     constexpr int HG = ATTN_OPROJ_HEADS, CW = HG * HD, LPR = CW / 32, RPW = WAVE / LPR, DPT = HD / 64;
     static_assert(HG == 4 && CW % 256 == 0 && LPR <= WAVE, "one wave a head, whole super-blocks a group");
-    const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = blockIdx.x, row = blockIdx.z, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = lane / LPR, al = lane % LPR;
     const int t_abs = g * (CW / 32) + al; /* the lane's slice of a row */
+    if (row) {
+        /* row blockIdx.z of a pass: its partials, att and parts; the arithmetic is a single row's */
+        a.partial += (size_t)row * a.n_kv * a.splits_max * (a.n_heads / a.n_kv) * (HD + 4);
+        a.att += (size_t)row * a.n_heads * HD;
+        parts += (size_t)row * (a.n_heads / HG) * o.rows;
+    }
     const int rbase = blockIdx.y * (4 * RPW * OPROJ_U) + wave * (RPW * OPROJ_U) + sub;
     /* the merge's loads first, none of them waiting for the position: wave w, head hq = g HG + w, DPT dimensions a
        lane, the values of chunks 0 .. OPROJ_PRE - 1 and the maxima and sums of chunks lane and lane + 64, read
@@ -706,7 +684,7 @@ __global__ __launch_bounds__(256) void attention_oproj_kernel(attn_args a, qmat 
     const float* base = a.partial + ((size_t)h * a.splits_max * G + gi) * (HD + 4);
     const size_t stride = (size_t)G * (HD + 4);
     const int d0 = lane * DPT, last = a.splits_max - 1;
-    const int pos_v = gld<int>(&a.rows[0].pos);
+    const int pos_v = gld<int>(&a.rows[row].pos);
     float v0[OPROJ_PRE][DPT];
 #pragma unroll
     for (int i = 0; i < OPROJ_PRE; i++) {
@@ -813,7 +791,7 @@ __global__ __launch_bounds__(256) void attention_oproj_kernel(attn_args a, qmat 
 }
 
 bool attention_oproj_fits(const attn_args& a, const qmat& o) {
-    return a.n_rows == 1 && !a.prepared && (a.hd == 64 || a.hd == 128) && a.n_kv >= 1 && a.n_heads % a.n_kv == 0 &&
+    return a.n_rows >= 1 && (a.hd == 64 || a.hd == 128) && a.n_kv >= 1 && a.n_heads % a.n_kv == 0 &&
            a.n_heads % ATTN_OPROJ_HEADS == 0 && a.n_heads / ATTN_OPROJ_HEADS <= OPROJ_PARTS_MAX && a.splits_max <= MERGE_MAX &&
            o.cols == a.n_heads * a.hd && o.rows >= 256 && o.rows <= ROUTE_PARTS_HMAX &&
            (o.dtype == VITNA_DTYPE_Q4_K || o.dtype == VITNA_DTYPE_Q6_K || o.dtype == VITNA_DTYPE_Q8_0);
@@ -822,7 +800,7 @@ bool attention_oproj_fits(const attn_args& a, const qmat& o) {
 hipError_t launch_attention_oproj(const attn_args& a, const qmat& o, float* parts, hipStream_t s) {
     if (!attention_oproj_fits(a, o) || !parts) return hipErrorInvalidValue;
     const int rpw = WAVE / (ATTN_OPROJ_HEADS * a.hd / 32), per_block = 4 * rpw * OPROJ_U;
-    const dim3 grid(a.n_heads / ATTN_OPROJ_HEADS, (o.rows + per_block - 1) / per_block);
+    const dim3 grid(a.n_heads / ATTN_OPROJ_HEADS, (o.rows + per_block - 1) / per_block, a.n_rows);
 #define OPROJ_CASE(DT, HD) \
     if (o.dtype == DT && a.hd == HD) { attention_oproj_kernel<DT, HD><<<grid, 256, 0, s>>>(a, o, parts); return hipGetLastError(); }
     OPROJ_CASE(VITNA_DTYPE_Q4_K, 128) OPROJ_CASE(VITNA_DTYPE_Q6_K, 128) OPROJ_CASE(VITNA_DTYPE_Q8_0, 128)
@@ -833,12 +811,14 @@ hipError_t launch_attention_oproj(const attn_args& a, const qmat& o, float* part
 
 __global__ __launch_bounds__(256) void attn_fold_kernel(float* __restrict__ x, const float* __restrict__ parts, int n_parts, int H) {
     const int i = blockIdx.x * 256 + threadIdx.x;
+    x += (size_t)blockIdx.y * H;
+    parts += (size_t)blockIdx.y * n_parts * H;
     if (i < H) x[i] = attn_resid(x[i], parts, n_parts, (size_t)H, (size_t)i);
 }
 
-hipError_t launch_attn_fold(float* x, const float* parts, int n_parts, int H, hipStream_t s) {
-    if (n_parts < 1 || n_parts > OPROJ_PARTS_MAX || H < 1) return hipErrorInvalidValue;
-    attn_fold_kernel<<<(H + 255) / 256, 256, 0, s>>>(x, parts, n_parts, H);
+hipError_t launch_attn_fold(float* x, const float* parts, int n_parts, int H, hipStream_t s, int n_rows) {
+    if (n_parts < 1 || n_parts > OPROJ_PARTS_MAX || H < 1 || n_rows < 1) return hipErrorInvalidValue;
+    attn_fold_kernel<<<dim3((H + 255) / 256, n_rows), 256, 0, s>>>(x, parts, n_parts, H);
     return hipGetLastError();
 }
 

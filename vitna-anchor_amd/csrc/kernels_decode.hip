@@ -395,6 +395,14 @@ template <int DT, int LPR, int SPL>
 __global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
     constexpr int RPW = WAVE / LPR;
     const int lane = threadIdx.x & 63;
+    if (blockIdx.y) {
+        /* token blockIdx.y of several: its activations, routing (or logits) and outputs; a single token's arithmetic */
+        const size_t r = blockIdx.y;
+        a.xn += r * a.gate.cols;
+        a.rt += r;
+        a.act += r * a.K * a.gate.rows;
+        if (a.logits) a.logits += r * a.E;
+    }
     const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
     const int uwaves = (a.K * a.gate.rows + 2 * RPW - 1) / (2 * RPW); /* waves with units */
     if (wave >= uwaves) {
@@ -412,37 +420,38 @@ __global__ __launch_bounds__(256) void experts_in_kernel(experts_in_args a) {
 }
 
 template <int DT, int LPR, int SPL>
-static hipError_t ein_launch(const experts_in_args& a, hipStream_t s) {
+static hipError_t ein_launch(const experts_in_args& a, hipStream_t s, int n_rows) {
     constexpr int RPW = WAVE / LPR;
     const int units = a.K * a.gate.rows;
     const int waves = (units + 2 * RPW - 1) / (2 * RPW) + 1; /* the last one publishes the routing */
     const int blocks = (waves + 3) / 4;
-    experts_in_kernel<DT, LPR, SPL><<<blocks, 256, 0, s>>>(a);
+    experts_in_kernel<DT, LPR, SPL><<<dim3(blocks, n_rows), 256, 0, s>>>(a);
     return hipGetLastError();
 }
 
 template <int DT>
-static hipError_t ein_dispatch(const experts_in_args& a, hipStream_t s) {
+static hipError_t ein_dispatch(const experts_in_args& a, hipStream_t s, int n) {
     switch (a.gate.cols / 32) {
-        case 4: return ein_launch<DT, 4, 1>(a, s);
-        case 8: return ein_launch<DT, 8, 1>(a, s);
-        case 16: return ein_launch<DT, 16, 1>(a, s);
-        case 32: return ein_launch<DT, 32, 1>(a, s);
-        case 64: return ein_launch<DT, 64, 1>(a, s);
-        case 128: return ein_launch<DT, 64, 2>(a, s);
-        case 256: return ein_launch<DT, 64, 4>(a, s);
+        case 4: return ein_launch<DT, 4, 1>(a, s, n);
+        case 8: return ein_launch<DT, 8, 1>(a, s, n);
+        case 16: return ein_launch<DT, 16, 1>(a, s, n);
+        case 32: return ein_launch<DT, 32, 1>(a, s, n);
+        case 64: return ein_launch<DT, 64, 1>(a, s, n);
+        case 128: return ein_launch<DT, 64, 2>(a, s, n);
+        case 256: return ein_launch<DT, 64, 4>(a, s, n);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s) {
-    if (a.gate.dtype != a.up.dtype || a.gate.rows != a.up.rows || a.gate.cols != a.up.cols || a.K < 1 || a.K > ROUTE_K_MAX)
+hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s, int n_rows) {
+    if (a.gate.dtype != a.up.dtype || a.gate.rows != a.up.rows || a.gate.cols != a.up.cols || a.K < 1 || a.K > ROUTE_K_MAX ||
+        n_rows < 1 || n_rows > 65535)
         return hipErrorInvalidValue;
     if (a.logits && (a.E < a.K || a.E > ROUTE_E_MAX || a.E % 4)) return hipErrorInvalidValue;
     switch (a.gate.dtype) {
-        case VITNA_DTYPE_Q8_0: return ein_dispatch<VITNA_DTYPE_Q8_0>(a, s);
-        case VITNA_DTYPE_Q4_K: return ein_dispatch<VITNA_DTYPE_Q4_K>(a, s);
-        case VITNA_DTYPE_Q6_K: return ein_dispatch<VITNA_DTYPE_Q6_K>(a, s);
+        case VITNA_DTYPE_Q8_0: return ein_dispatch<VITNA_DTYPE_Q8_0>(a, s, n_rows);
+        case VITNA_DTYPE_Q4_K: return ein_dispatch<VITNA_DTYPE_Q4_K>(a, s, n_rows);
+        case VITNA_DTYPE_Q6_K: return ein_dispatch<VITNA_DTYPE_Q6_K>(a, s, n_rows);
         default: return hipErrorInvalidValue;
     }
 }
@@ -459,6 +468,13 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE, nwaves = gridDim.x * (blockDim.x / WAVE);
     const int H = a.down.rows, I = a.down.cols, S = I / 32, N = a.K * S;
+    if (blockIdx.y) {
+        /* token blockIdx.y of several (no parts then): its activations, routing and output row */
+        const size_t r = blockIdx.y;
+        a.act += r * a.K * I;
+        a.rt += r;
+        a.y += r * H;
+    }
     xslice xs[IPL];
     float wk[IPL];
     int ek[IPL], tk[IPL];
@@ -515,33 +531,34 @@ __global__ __launch_bounds__(256) void experts_down_kernel(experts_down_args a) 
 }
 
 template <int DT, int IPL>
-static hipError_t edn_launch(const experts_down_args& a, hipStream_t s) {
+static hipError_t edn_launch(const experts_down_args& a, hipStream_t s, int n_rows) {
     const int waves = IPL >= 6 ? a.down.rows : (a.down.rows + 1) / 2;
-    experts_down_kernel<DT, IPL><<<(waves + 3) / 4, 256, 0, s>>>(a);
+    experts_down_kernel<DT, IPL><<<dim3((waves + 3) / 4, n_rows), 256, 0, s>>>(a);
     return hipGetLastError();
 }
 
 template <int DT>
-static hipError_t edn_dispatch(const experts_down_args& a, hipStream_t s) {
+static hipError_t edn_dispatch(const experts_down_args& a, hipStream_t s, int n) {
     const int N = a.K * (a.down.cols / 32), ipl = (N + 63) / 64;
     switch (ipl) {
-        case 1: return edn_launch<DT, 1>(a, s);
-        case 2: return edn_launch<DT, 2>(a, s);
-        case 3: return edn_launch<DT, 3>(a, s);
-        case 4: return edn_launch<DT, 4>(a, s);
-        case 5: return edn_launch<DT, 5>(a, s);
-        case 6: return edn_launch<DT, 6>(a, s);
-        case 8: return edn_launch<DT, 8>(a, s);
+        case 1: return edn_launch<DT, 1>(a, s, n);
+        case 2: return edn_launch<DT, 2>(a, s, n);
+        case 3: return edn_launch<DT, 3>(a, s, n);
+        case 4: return edn_launch<DT, 4>(a, s, n);
+        case 5: return edn_launch<DT, 5>(a, s, n);
+        case 6: return edn_launch<DT, 6>(a, s, n);
+        case 8: return edn_launch<DT, 8>(a, s, n);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s) {
-    if (a.K < 1 || a.K > ROUTE_K_MAX || a.down.cols % 32) return hipErrorInvalidValue;
+hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s, int n_rows) {
+    if (a.K < 1 || a.K > ROUTE_K_MAX || a.down.cols % 32 || n_rows < 1 || n_rows > 65535 || (n_rows > 1 && a.parts))
+        return hipErrorInvalidValue;
     switch (a.down.dtype) {
-        case VITNA_DTYPE_Q8_0: return edn_dispatch<VITNA_DTYPE_Q8_0>(a, s);
-        case VITNA_DTYPE_Q4_K: return edn_dispatch<VITNA_DTYPE_Q4_K>(a, s);
-        case VITNA_DTYPE_Q6_K: return edn_dispatch<VITNA_DTYPE_Q6_K>(a, s);
+        case VITNA_DTYPE_Q8_0: return edn_dispatch<VITNA_DTYPE_Q8_0>(a, s, n_rows);
+        case VITNA_DTYPE_Q4_K: return edn_dispatch<VITNA_DTYPE_Q4_K>(a, s, n_rows);
+        case VITNA_DTYPE_Q6_K: return edn_dispatch<VITNA_DTYPE_Q6_K>(a, s, n_rows);
         default: return hipErrorInvalidValue;
     }
 }
@@ -576,6 +593,7 @@ hipError_t launch_gemv(const gemv_args& a, hipStream_t s) {
         one.n = 1;
         one.w[0] = a.w[i];
         one.y[0] = a.y[i];
+        one.ystride[0] = a.ystride[i];
         e = launch_gemv(one, s);
         if (e != hipSuccess) return e;
     }

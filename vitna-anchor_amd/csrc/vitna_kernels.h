@@ -109,7 +109,9 @@ struct experts_in_args {
     float* act;
     int K;
 };
-hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s);
+/* n_rows > 1: the same for each of n_rows tokens (xn rows of gate.cols, rt, act rows of K I, logits rows of E),
+   each token's arithmetic that of a single token: its bits. */
+hipError_t launch_experts_in(const experts_in_args& a, hipStream_t s, int n_rows = 1);
 
 /* y[r] (+)= sum_k w_k (down_{ids[k]}[r] . act_k), into y or, with add,
    onto it. */
@@ -123,13 +125,16 @@ struct experts_down_args {
     const float* parts;
     int n_parts;
 };
-hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s);
+/* n_rows > 1 (without parts): the same for each of n_rows tokens (act rows of K cols, rt, y rows of down.rows). */
+hipError_t launch_experts_down(const experts_down_args& a, hipStream_t s, int n_rows = 1);
 
 /* ---- dense projections ---- */
 
 /* Up to three matrices of the same width multiplied by one vector:
    y_i = W_i . xin, where xin = RMSNorm(x, norm_w) when norm_w is set (each
-   block computes it) and x otherwise; with add, y_i += W_i . xin. */
+   block computes it) and x otherwise; with add, y_i += W_i . xin. With rows > 1, the same for each of rows
+   vectors (x at xstride floats apart, y_i at ystride[i]): every row's sums in the order of a single vector's, so
+   a row's result is the bits one call on it alone would give. */
 struct gemv_args {
     qmat w[3];
     float* y[3];
@@ -138,6 +143,8 @@ struct gemv_args {
     const float* norm_w;
     float eps;
     int add;
+    int rows;       /* 0 or 1: one vector */
+    int xstride, ystride[3];
 };
 hipError_t launch_gemv(const gemv_args& a, hipStream_t s);
 
@@ -202,18 +209,18 @@ struct attn_args {
     img_out img;
 };
 hipError_t launch_attention(const attn_args& a, hipStream_t s);
-/* One row: the chunks' partials merged, as launch_attention_merge merges them (same bits in att), and the
+/* Each row: the chunks' partials merged, as launch_attention_merge merges them (same bits in att), and the
    o-projection applied group by group: the n_heads / ATTN_OPROJ_HEADS groups of ATTN_OPROJ_HEADS query heads
-   each leave parts[g][r] = o[r][the group's columns] . att[the group's columns]. The residual then is
-   attn_resid(x, parts, n_heads / ATTN_OPROJ_HEADS, o.rows). Each block merges one group's heads and
+   each leave parts[row][g][r] = o[r][the group's columns] . att[row][the group's columns]. The residual then is
+   attn_resid(x, parts, n_heads / ATTN_OPROJ_HEADS, o.rows). A row of several gets the bits it gets alone. Each block merges one group's heads and
    multiplies them into a range of rows, so no kernel waits on another for att. attention_oproj_fits says
    whether a layer takes it (else: launch_attention_merge, then the o-projection GEMV). */
 #define ATTN_OPROJ_HEADS 4
 bool attention_oproj_fits(const attn_args& a, const qmat& o);
 hipError_t launch_attention_oproj(const attn_args& a, const qmat& o, float* parts, hipStream_t s);
-/* x[i] = attn_resid(x[i], parts, n_parts, H, i): the parts folded into the residual (for a reader of the
-   residual between the attention and the experts). */
-hipError_t launch_attn_fold(float* x, const float* parts, int n_parts, int H, hipStream_t s);
+/* x[row][i] = attn_resid(x[row][i], parts[row], n_parts, H, i) for n_rows rows (parts n_parts H floats a row):
+   the parts folded into the residual (for a reader of the residual between the attention and the experts). */
+hipError_t launch_attn_fold(float* x, const float* parts, int n_parts, int H, hipStream_t s, int n_rows = 1);
 /* The chunks' partials of every (row, query head) combined into att. */
 hipError_t launch_attention_merge(const attn_args& a, hipStream_t s);
 /* The prepare pass of prepared = 1: q normalized and rotated into q_out, k

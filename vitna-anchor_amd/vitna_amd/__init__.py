@@ -354,6 +354,7 @@ def _hip():
         "vitna_hip_gguf_llama_free": (None, [C.POINTER(Llama)]),
         "vitna_hip_gguf_close": (None, [P]),
         "vitna_hip_set_step_kernel": (C.c_bool, [P, C.c_int, C.POINTER(C.c_int), *E]),
+        "vitna_hip_set_exact_rows": (C.c_bool, [P, C.c_size_t, *E]),
         "vitna_hip_step_trace": (C.c_bool, [P, C.c_size_t, C.c_int32, C.c_size_t, C.c_int, C.POINTER(C.c_uint64),
                                              C.c_size_t, *E]),
         "vitna_hip_kv": (C.c_bool, [P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, _FP, _FP, C.c_bool, *E]),
@@ -582,6 +583,10 @@ class Device:
         att = np.empty(qd, np.float32)
         self._ok(self.lib.vitna_hip_attention_io(self.g, row, fptr(q), fptr(att), self.err, 512))
         return q, att
+
+    def set_exact_rows(self, n):
+        """Passes of the rows ABI of at most n rows take the single-token kernels (vitna_hip_set_exact_rows)."""
+        self._ok(self.lib.vitna_hip_set_exact_rows(self.g, n, self.err, 512))
 
     def set_step_kernel(self, on):
         """Decode steps on the persistent step kernel (on) or the per-layer graph (off, the default); returns
