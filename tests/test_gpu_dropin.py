@@ -14,7 +14,8 @@ Bars, each the reference's own promise from its usage text (engine/src/main.c:68
     positions in ten, and not exact's bits; exact run twice gives the same bits (main.c:88-90);
   * `expert-check --device cuda` runs every expert it names through vitna_cuda_expert_check and reports them
     (main.c:1337-1401).
-The engine binary exists only where the build container made it (oracle/_ref, from /root/reference's sources);
+The same checks of logits and generate run on four layers of BASELINE configs[2]'s shape too. The engine binary
+exists only where the build container made it (oracle/_ref, from /root/reference's sources);
 elsewhere these tests skip.
 """
 import json
@@ -154,6 +155,56 @@ def test_precision_fast(model_dir, tmp_path):
     assert not np.array_equal(fast.view(np.uint32), exact.view(np.uint32))
     again = logits(model_dir, tmp_path, "exact2", ids, "--device", "cuda")
     assert np.array_equal(again.view(np.uint32), exact.view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def qwen3_dir(tmp_path_factory):
+    """Four layers of BASELINE configs[2]'s model (Qwen3-30B-A3B's shape: hidden 2048, 128 experts top-8 of width
+    768, 32 query and 4 key-value heads, Q4_K_M with a Q6_K head of 151,936 rows), as a GGUF file of 2 GB."""
+    d = str(tmp_path_factory.mktemp("dropin_qwen3"))
+    m = va.Model(va.shape(n_layers=4, ctx=512), 4321, threads=16)
+    try:
+        va.write_gguf(m, d, va.F32, 32)
+        vocab = m.cfg.vocab
+    finally:
+        m.free()
+    tokenizer(d, vocab)
+    return d
+
+
+@needs_engine
+def test_qwen3_shape_logits_and_generate(qwen3_dir, tmp_path):
+    """configs[2]'s layer shape through the engine: every position's logits within 1e-3 of max |cpu| of the engine's
+    CPU path with the same argmax, and generate's greedy tokens and logits against the CPU's as above."""
+    V = 151936
+    ids = [11, 22, 33, 44, 55, 66, 77, 88]
+    out_c, out_g = str(tmp_path / "c.bin"), str(tmp_path / "g.bin")
+    run(qwen3_dir, "logits", "--ids", ids_arg(ids), "--out", out_c, "--threads", "16", timeout=300)
+    run(qwen3_dir, "logits", "--ids", ids_arg(ids), "--out", out_g, "--device", "cuda", timeout=300)
+    cpu = np.fromfile(out_c, np.float32).reshape(len(ids), V)
+    gpu = np.fromfile(out_g, np.float32).reshape(len(ids), V)
+    r = rel_rows(gpu, cpu)
+    say("  qwen3-shaped logits rel err (max)", float(r.max()))
+    assert r.max() <= 1e-3
+    assert np.array_equal(gpu.argmax(1), cpu.argmax(1))
+    res = {}
+    for dev in ("cpu", "cuda"):
+        lo = str(tmp_path / ("gen_%s.bin" % dev))
+        extra = ["--device", "cuda"] if dev == "cuda" else ["--threads", "16"]
+        p = run(qwen3_dir, "generate", "--ids", ids_arg(ids), "--max-new", "12", "--logits-out", lo, "--timing", *extra,
+                timeout=300)
+        say("  " + dev + ": " + " ".join(l for l in p.stderr.splitlines() if l.startswith("timing")))
+        res[dev] = (json.loads(p.stdout.strip().splitlines()[-1])["ids"], np.fromfile(lo, np.float32).reshape(-1, V))
+    (c_ids, c_lg), (g_ids, g_lg) = res["cpu"], res["cuda"]
+    same = 0
+    while same < len(c_ids) and c_ids[same] == g_ids[same]:
+        same += 1
+    say("  greedy tokens equal for", same, "of", len(c_ids))
+    steps = min(same + 1, len(c_lg), len(g_lg))
+    assert rel_rows(g_lg[:steps], c_lg[:steps]).max() <= 1e-3
+    if same < len(c_ids):
+        top = np.sort(c_lg[same])[-2:]
+        assert top[1] - top[0] <= 2e-3 * np.max(np.abs(c_lg[same])), ("step", same, top)
 
 
 @needs_engine
