@@ -779,25 +779,21 @@ __device__ __forceinline__ void pw_body(const prefill_args& a, int e, int m0, in
                      :
                      : "memory");
 
-    /* accumulator r of a lane: row 8 (r / 4) + 4 kq + r % 4 of the 32 x 32 tile, column l32. The lane's place is
-       taken afresh from the execution mask (mbcnt) and the wave's from a scalar, so that no per-lane value of the
-       prologue stays live through the loop for it (one spilled to scratch) */
-    const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-    const int l32e = lane_e & 31, kqe = lane_e >> 5, wve = __builtin_amdgcn_readfirstlane(wv);
+    /* accumulator r of a lane: row 8 (r / 4) + 4 kq + r % 4 of the 32 x 32 tile, column l32 */
 #pragma unroll
     for (int m = 0; m < ML; m++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int p = m0 + 32 * m + 8 * (r >> 2) + 4 * kqe + (r & 3);
+            const int p = m0 + 32 * m + 8 * (r >> 2) + 4 * kq + (r & 3);
             if (p >= cnt) continue;
             if (GU) {
                 const float gt = acc[m][0][r], up = acc[m][1][r];
                 const float v = pf_swiglu(gt, up);
-                a.act[(size_t)(pbase + p) * I + nt * 128 + wve * 32 + l32e] = (uint16_t)bf16_rne(v);
+                a.act[(size_t)(pbase + p) * I + nt * 128 + wv * 32 + l32] = (uint16_t)bf16_rne(v);
             } else {
                 const int q = p - m0;
                 const float wt = ywt[q];
-                uint16_t* y = a.ypart + (size_t)yrow[q] * H + nt * 256 + wve * 64 + l32e;
+                uint16_t* y = a.ypart + (size_t)yrow[q] * H + nt * 256 + wv * 64 + l32;
 #pragma unroll
                 for (int t = 0; t < 2; t++) y[32 * t] = (uint16_t)bf16_rne(acc[m][t][r] * wt);
             }
