@@ -12,7 +12,8 @@ through vitna_cuda_moe_route / _experts / _head, for:
   * 64 rows of 64 sequences;
   * the merged attention + o-projection (Q4_K, Q6_K and Q8_0 o-projections) and the separate merge + GEMV (two
     query heads);
-  * a model whose experts pass through the expert cache, a pass whose experts fit one wave of its rule.
+  * a model whose experts pass through the expert cache: a pass whose experts fit one wave of its rule, and one
+    taken in groups of rows.
 Each row's router logits at every layer, its final logits and the keys and values it stored are compared.
 """
 import numpy as np
@@ -172,10 +173,12 @@ def test_longer_pass_takes_multi_row_kernels():
         model.free()
 
 
-def test_cached_experts_pass_is_step_bits():
-    """A model with an expert cache of 2K + 20 slots (the rule's waves take 28 experts): a drafted pass of three rows
-    names at most 24, one wave, and gives the steps' bits of the same model with every expert resident."""
-    say("exact rows through the expert cache")
+@pytest.mark.parametrize("extra", [20, 0])
+def test_cached_experts_pass_is_step_bits(extra):
+    """A model with an expert cache of 2K + extra slots, the steps' bits of the same model with every expert
+    resident. With 20 extra (the rule's waves take 28 experts) a drafted pass of three rows names at most 24: one
+    wave. With none (waves of K experts) every row is a group of its own, a pass of the cache each."""
+    say("exact rows through the expert cache, 2K +", extra, "slots")
     spec = dict(SMALL["q4km"])
     from test_gpu_expert_cache import slot_bytes
     model0 = va.Model(va.shape(**spec), 8642)
@@ -183,7 +186,7 @@ def test_cached_experts_pass_is_step_bits():
     model0.free()
     K = spec["n_experts_used"]
     prefill = [50, 30]
-    model, single_dev, pass_dev = make(spec, 8642, prefill, expert_cache_bytes=(2 * K + 20) * sb)
+    model, single_dev, pass_dev = make(spec, 8642, prefill, expert_cache_bytes=(2 * K + extra) * sb)
     try:
         cfg = model.cfg
         for p in (50, 53):
@@ -193,7 +196,7 @@ def test_cached_experts_pass_is_step_bits():
             check(cfg, rows, single, pas, single_dev, pass_dev)
         _, cnt = pass_dev.expert_cache_state()
         say("  cache", cnt)
-        assert cnt["slots"] == 2 * K + 20
+        assert cnt["slots"] == 2 * K + extra
     finally:
         single_dev.close()
         pass_dev.close()
