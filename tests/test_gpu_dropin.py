@@ -12,6 +12,8 @@ Bars, each the reference's own promise from its usage text (engine/src/main.c:68
   * --precision fast on a 96-token prompt: logits close to exact's (bf16 experts: the median position within 1e-2
     of max |exact|, four in five within 3e-2; a near-tied router may take another expert), the same argmax at nine
     positions in ten, and not exact's bits; exact run twice gives the same bits (main.c:88-90);
+  * the routing traces (--router-out, --experts-out) of the GPU against the CPU's, and experts pinned from a file
+    (--experts-in) on both (main.c:809-880);
   * `expert-check --device cuda` runs every expert it names through vitna_cuda_expert_check and reports them
     (main.c:1337-1401).
 The same checks of logits and generate run on four layers of BASELINE configs[2]'s shape too. The engine binary
@@ -155,6 +157,50 @@ def test_precision_fast(model_dir, tmp_path):
     assert not np.array_equal(fast.view(np.uint32), exact.view(np.uint32))
     again = logits(model_dir, tmp_path, "exact2", ids, "--device", "cuda")
     assert np.array_equal(again.view(np.uint32), exact.view(np.uint32))
+
+
+@needs_engine
+def test_routing_traces_and_pins(model_dir, tmp_path):
+    """The engine's routing traces (--router-out, --experts-out: every position's and layer's router logits and
+    chosen experts, main.c:809-880) from the GPU against the CPU's: the same experts everywhere, the logits within
+    1e-4 of each row's largest (the residual they score differs by the fp32 orders, the router itself is exact).
+    Then the experts pinned from a file (--experts-in, each position's and layer's experts: here the CPU's choice
+    shifted by one expert), which model.c hands to vitna_cuda_moe_experts in place of the router's: the GPU's
+    logits within 1e-3 of the CPU's under the same pins, and not the unpinned logits."""
+    E, K, L = SPEC["n_experts"], SPEC["n_experts_used"], SPEC["n_layers"]
+    ids = list(range(4, 60, 5))
+    n = len(ids)
+    tr = {}
+    for dev in ("cpu", "cuda"):
+        r, e, o = (str(tmp_path / ("%s_%s.bin" % (w, dev))) for w in ("router", "experts", "logits"))
+        extra = ["--device", "cuda"] if dev == "cuda" else []
+        run(model_dir, "logits", "--ids", ids_arg(ids), "--out", o, "--router-out", r, "--experts-out", e, *extra)
+        tr[dev] = (np.fromfile(r, np.float32).reshape(n, L, E), np.fromfile(e, np.int32).reshape(n, L, K),
+                   np.fromfile(o, np.float32).reshape(n, SPEC["vocab"]))
+    (cr, ce, cl), (gr, ge, gl) = tr["cpu"], tr["cuda"]
+    assert np.array_equal(ce, ge)
+    rr = np.max(np.abs(gr.astype(np.float64) - cr), axis=2) / np.max(np.abs(cr), axis=2)
+    say("  router logits rel err (max over positions and layers)", float(rr.max()),
+        "bit-equal rows", int(np.sum(np.all(gr.view(np.uint32) == cr.view(np.uint32), axis=2))), "of", n * L)
+    assert rr.max() <= 1e-4
+    pin = (ce + 1) % E
+    # shifting by one may name an expert twice in a layer: keep those rows as chosen
+    for p in range(n):
+        for l in range(L):
+            if len(set(pin[p, l].tolist())) < K:
+                pin[p, l] = ce[p, l]
+    pin_file = str(tmp_path / "pin.bin")
+    pin.astype("<i4").tofile(pin_file)
+    pinned = {}
+    for dev in ("cpu", "cuda"):
+        o = str(tmp_path / ("pinned_%s.bin" % dev))
+        extra = ["--device", "cuda"] if dev == "cuda" else []
+        run(model_dir, "logits", "--ids", ids_arg(ids), "--out", o, "--experts-in", pin_file, *extra)
+        pinned[dev] = np.fromfile(o, np.float32).reshape(n, SPEC["vocab"])
+    r = rel_rows(pinned["cuda"], pinned["cpu"])
+    say("  pinned experts: logits rel err (max)", float(r.max()))
+    assert r.max() <= 1e-3
+    assert not np.allclose(pinned["cuda"], gl)
 
 
 @pytest.fixture(scope="module")
