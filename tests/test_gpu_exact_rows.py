@@ -116,6 +116,16 @@ def test_pass_rows_are_step_bits(name, case):
         single = one_at_a_time(single_dev, cfg, rows)
         pas = as_pass(pass_dev, cfg, rows)
         check(cfg, rows, single, pas, single_dev, pass_dev)
+        # after the pass, a single token's step on each device: the same bits (the pass left nothing behind)
+        tok, pos, seq = max(rows, key=lambda r: (r[2] == rows[0][2], r[1]))
+        nxt = [(tok + 1, pos + 1, seq)]
+        a, b = one_at_a_time(single_dev, cfg, nxt), one_at_a_time(pass_dev, cfg, nxt)
+        assert same_bits(a[0][1], b[0][1]), "the step after the pass"
+        with pytest.raises(va.VitnaError, match="twice"):
+            pass_dev.rows_route(rows, 0)
+            ids = np.tile(np.arange(cfg.n_experts_used), (len(rows), 1))
+            ids[-1, 1] = ids[-1, 0]
+            pass_dev.rows_experts(0, ids, np.full(ids.shape, 0.125))
     finally:
         single_dev.close()
         pass_dev.close()
