@@ -28,7 +28,9 @@ Prints one JSON line. Besides the step throughput it carries:
             layer); configs[4], a prefill of 4096 rows through one
             Qwen3-shaped MoE layer with Q8_0 experts (bf16 MFMA grouped GEMM),
             with the matrix cores' yardstick (back-to-back MFMAs) beside it;
-            configs[0] and [1], one MoE layer of one token; expert_cache,
+            configs[0] and [1], one MoE layer of one token; prompt, a
+            4096-token prompt through configs[2]'s whole model in passes
+            of 1024 rows, exact and --precision fast; expert_cache,
             configs[2]'s model decoded a layer at a time through the
             reference's ABI with every expert resident and with a cache
             holding half of them (copied in from host memory).
@@ -194,6 +196,7 @@ def main():
         log("uploaded for 32 sequences of 8193 positions in %.1f s" % (time.time() - t0))
         extra = {"3": bench_ragged(va, model, dev, args.steps)}
         dev.close()
+        extra["prompt"] = bench_prompt(va, model)
         extra["4"] = bench_prefill(va)
         extra["4_kquant"] = bench_prefill_kquant(va)
         extra["0"] = bench_layer(va, 0)
@@ -304,6 +307,45 @@ def bench_ragged(va, model, dev, steps, reps=None):
             "distinct_experts": {"mean": round(uniq, 2), "min": int(min(distinct)), "max": int(max(distinct))},
             "est_note": "key-value bytes exact; expert bytes for the distinct experts each layer reads, counted "
                         "(%.1f a layer on average)" % uniq}
+
+
+def bench_prompt(va, model, tokens=4096, chunk=1024):
+    """A prompt of `tokens` tokens through configs[2]'s whole model (48 layers and the head), in passes of `chunk`
+    rows of one sequence at consecutive positions, in a cache of `tokens` positions (model.c's default context is the
+    model's, at most 4096), as model.c feeds a prompt in chunks of vitna_cuda_moe_rows_max
+    (the rows step: each row's attention over the keys of the positions before it and its own, device routing,
+    experts grouped), with the exact kernels and with --precision fast (a gpu_fast model: the passes' experts as
+    the bf16 grouped GEMM). The last pass's logits come back. Wall-clock of the second prompt (the first captures
+    the graph and makes the tiled copies)."""
+    cfg = model.cfg
+    out = {"workload": "a %d-token prompt through BASELINE configs[2]'s model (Qwen3-30B-A3B-shaped Q4_K_M, 48 layers), "
+                       "passes of %d rows of one sequence" % (tokens, chunk),
+           "context": "the reference publishes 349 (exact fp32) and 1,014 (--precision fast) tok/s for a 4,096-token "
+                      "Qwen3-30B-A3B Q4_K_M prompt on an RTX 3070 with most experts in host memory (README.md:714); "
+                      "other hardware, not a baseline"}
+    for name, fast in (("exact", False), ("fast", True)):
+        # a device model of one sequence and the context model.c gives by default (at most 4096 positions)
+        saved = (model.m.ctx, model.m.seqs)
+        model.m.ctx, model.m.seqs = tokens, 1
+        try:
+            dev = va.Device(model, fast=fast)
+        finally:
+            model.m.ctx, model.m.seqs = saved
+        try:
+            def prompt():
+                for c in range(tokens // chunk):
+                    rows = [((7 * (c * chunk + i) + 3) % cfg.vocab, c * chunk + i, 0) for i in range(chunk)]
+                    dev.rows_step(rows, logits=(c == tokens // chunk - 1))
+                dev.sync()
+            prompt()
+            t = time.perf_counter()
+            prompt()
+            sec = time.perf_counter() - t
+        finally:
+            dev.close()
+        out[name] = {"value": round(tokens / sec, 1), "unit": "tok/s", "ms": round(sec * 1e3, 1)}
+        log("prompt of %d tokens, %s: %.1f ms, %.0f tok/s" % (tokens, name, sec * 1e3, tokens / sec))
+    return out
 
 
 def bench_cache(va, tokens, warmup, frac, layers, model=None, kc=None, vc=None):

@@ -42,6 +42,8 @@
    row is the one a step would give", main.c:1003-1007). Longer passes (a prompt's chunks) take the multi-row
    kernels, within 1e-3 of the checker but not those bits. */
 #define EXACT_ROWS 64
+/* rows step graphs kept at once: a prompt's passes take up to three attention grids, and a ragged step a fourth */
+#define ROWS_GRAPHS 4
 
 struct dlayer {
     qmat q, k, v, o;
@@ -100,11 +102,17 @@ struct vitna_cuda_model {
     uint16_t *gm_xs, *gm_as;    /* the grouped experts' split activations: [ROWS_MAX][2H], [ROWS_MAX * K][2I] */
     float *gm_xsum, *gm_asum;   /* and their sums over runs of 16 or more columns */
     bool rows_shared_seq;       /* the pass's rows include two of one sequence (attention prepares first) */
-    hipGraph_t rows_graph_src;
-    hipGraphExec_t rows_graph;
-    int rows_graph_n;           /* the pass the rows graph was captured for: rows, or 0 for none */
-    bool rows_graph_shared;
-    bool rows_graph_fast;       /* and whether it ran the pass's experts as the grouped GEMM */
+    /* the rows step's captured graphs, a few kept (least recently used replaced): one a pass shape */
+    struct rows_graph_t {
+        hipGraph_t src;
+        hipGraphExec_t exec;
+        int n;                  /* rows, or 0 for an empty entry */
+        bool shared, fast;      /* rows of one sequence; the experts as the grouped GEMM */
+        int splits;             /* the attention's grid */
+        uint64_t used;
+    } rg[ROWS_GRAPHS];
+    uint64_t rg_clock;
+    int rg_cur;                 /* the entry the last ensure_rows_graph chose */
     hipGraphExec_t step_graph;
     bool graph_ready;
     /* the persistent decode step (kernels_step.hip): set up on first use when the model's shape takes it */
@@ -126,6 +134,10 @@ struct vitna_cuda_model {
     size_t fast_rows, long_from;
     int rows_n;         /* rows of the pass in flight (vitna_cuda_moe_rows_*) */
     int exact_rows;     /* passes of the rows ABI up to this many rows run the single-token kernels (EXACT_ROWS) */
+    /* the attention's grid for the row(s) set last: the power of two of chunks at or above the most any row needs
+       (at most splits_max), so that a short position in a long cache launches few blocks past its last chunk;
+       the graphs are captured for one such size (graph_splits, rows_graph_t::splits) */
+    int splits_grid, graph_splits;
     bool pass_exact;    /* and the pass in flight is one */
     /* prefill through one MoE layer: buffers for pf_cap rows, allocated on first use */
     size_t pf_cap;
@@ -409,6 +421,15 @@ extern "C" int vitna_cuda_devices(vitna_cuda_device_t* out, int max) {
     return k;
 }
 
+static void drop_rows_graphs(vitna_cuda_model* g) {
+    for (auto& r : g->rg) {
+        if (!r.n) continue;
+        (void)hipGraphExecDestroy(r.exec);
+        (void)hipGraphDestroy(r.src);
+        r.n = 0;
+    }
+}
+
 extern "C" void vitna_cuda_free(struct vitna_cuda_model* g) {
     if (!g) return;
     (void)hipSetDevice(g->device);
@@ -417,10 +438,7 @@ extern "C" void vitna_cuda_free(struct vitna_cuda_model* g) {
         (void)hipGraphExecDestroy(g->step_graph);
         (void)hipGraphDestroy(g->step_graph_src);
     }
-    if (g->rows_graph_n) {
-        (void)hipGraphExecDestroy(g->rows_graph);
-        (void)hipGraphDestroy(g->rows_graph_src);
-    }
+    drop_rows_graphs(g);
     for (void* p : g->allocs) (void)hipFree(p);
     for (void* p : g->pf_allocs) (void)hipFree(p);
     if (g->rows_host) (void)hipHostFree(g->rows_host);
@@ -640,6 +658,7 @@ static hipError_t enqueue_attention(vitna_cuda_model* g, int layer, int n_rows, 
     a.partial = g->partial;
     a.att = g->att;
     a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx; a.splits_max = g->splits_max;
+    a.splits_grid = g->splits_grid;
     a.eps = g->eps;
     a.prepared = prepared ? 1 : 0;
     a.mma = 1;
@@ -733,11 +752,19 @@ static bool check_launch(vitna_cuda_model* g, hipError_t e, const char* what, ch
     return fail_hip(err, err_len, what, e);
 }
 
+static int splits_bucket(const vitna_cuda_model* g, int max_pos) {
+    const int need = max_pos / ATTN_CHUNK + 1;
+    int b = 1;
+    while (b < need) b <<= 1;
+    return b < g->splits_max ? b : g->splits_max;
+}
+
 static bool set_row(vitna_cuda_model* g, size_t seq, int32_t token, size_t pos, char* err, size_t err_len) {
     if (seq >= (size_t)g->seqs) return fail(err, err_len, "sequence %zu: the cache holds %d", seq, g->seqs);
     if (pos >= (size_t)g->ctx) return fail(err, err_len, "position %zu: the cache holds %d", pos, g->ctx);
     if (g->attention && (token < 0 || token >= g->V)) return fail(err, err_len, "token %d is outside the vocabulary of %d", token, g->V);
     const row_rec r = {token, (int32_t)pos, (int32_t)seq};
+    g->splits_grid = splits_bucket(g, (int)pos);
     /* the layers of one token after the first find their row in place */
     if (g->row_set && g->row_last.token == r.token && g->row_last.pos == r.pos && g->row_last.seq == r.seq) return true;
     /* the previous copy out of the page-locked row must have run */
@@ -1182,8 +1209,14 @@ static hipError_t enqueue_step_body(vitna_cuda_model* g) {
 }
 
 static bool ensure_graph(vitna_cuda_model* g, char* err, size_t err_len) {
-    if (g->graph_ready) return true;
+    if (g->graph_ready && g->graph_splits == g->splits_grid) return true;
     HIP_TRY(hipStreamSynchronize(g->stream), "before capturing the step");
+    if (g->graph_ready) {
+        /* captured for another attention grid: captured again for this one */
+        (void)hipGraphExecDestroy(g->step_graph);
+        (void)hipGraphDestroy(g->step_graph_src);
+        g->graph_ready = false;
+    }
     HIP_TRY(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "capturing the step");
     const hipError_t e = enqueue_step_body(g);
     hipGraph_t graph = nullptr;
@@ -1195,6 +1228,7 @@ static bool ensure_graph(vitna_cuda_model* g, char* err, size_t err_len) {
     HIP_TRY(e3, "instantiating the step's graph");
     g->step_graph_src = graph;
     g->graph_ready = true;
+    g->graph_splits = g->splits_grid;
     return true;
 }
 
@@ -1211,8 +1245,8 @@ extern "C" bool vitna_hip_moe_step_async(struct vitna_cuda_model* g, size_t seq,
         g->last_step_mega = true;
         return check_launch(g, e, "the step", err, err_len);
     }
-    if (!ensure_graph(g, err, err_len)) return false;
     if (!set_row(g, seq, token, pos, err, err_len)) return false;
+    if (!ensure_graph(g, err, err_len)) return false;
     HIP_TRY(hipGraphLaunch(g->step_graph, g->stream), "launching the step");
     g->last_step_mega = false;
     return true;
@@ -1565,11 +1599,7 @@ static bool prefill_reserve(vitna_cuda_model* g, size_t n, char* err, size_t err
     if (n <= g->pf_cap) return true;
     HIP_TRY(hipStreamSynchronize(g->stream), "waiting before the prefill buffers grow");
     /* a captured rows step of a fast pass reads these buffers: it is captured again on its next use */
-    if (g->rows_graph_n) {
-        (void)hipGraphExecDestroy(g->rows_graph);
-        (void)hipGraphDestroy(g->rows_graph_src);
-        g->rows_graph_n = 0;
-    }
+    drop_rows_graphs(g);
     for (void* p : g->pf_allocs) (void)hipFree(p);
     g->pf_allocs.clear();
     g->pf_cap = 0;
@@ -1758,9 +1788,9 @@ extern "C" bool vitna_hip_time_steps(struct vitna_cuda_model* g, size_t seq, int
     if (steps < 1) return fail(err, err_len, "at least one step");
     bool mega;
     if (!use_step(g, &mega, err, err_len)) return false;
-    if (!mega && !ensure_graph(g, err, err_len)) return false;
     /* every timed step decodes the same row, copied in once */
     if (!set_row(g, seq, token, pos, err, err_len)) return false;
+    if (!mega && !ensure_graph(g, err, err_len)) return false;
     event_pair ev;
     HIP_TRY(ev.make(), "events");
     HIP_TRY(hipStreamSynchronize(g->stream), "before timing");
@@ -2008,6 +2038,7 @@ static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n, 
     a.partial = g->partial;
     a.att = g->att;
     a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx; a.splits_max = g->splits_max;
+    a.splits_grid = g->splits_grid;
     a.eps = g->eps;
     /* several rows: the score and value products on the matrix cores */
     a.mma = n > 1 ? 1 : 0;
@@ -2126,6 +2157,7 @@ static hipError_t enqueue_exact_attention(vitna_cuda_model* g, int layer, int n)
     a.partial = g->partial;
     a.att = g->att;
     a.n_heads = g->nh; a.n_kv = g->nkv; a.hd = g->hd; a.ctx = g->ctx; a.splits_max = g->splits_max;
+    a.splits_grid = g->splits_grid;
     a.eps = g->eps;
     a.mma = 1;
     if (g->rows_shared_seq) {
@@ -2201,7 +2233,12 @@ static bool set_rows(vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n
     }
     HIP_TRY(hipEventSynchronize(g->rows_copied), "waiting for the previous row copy");
     g->row_set = false;
-    for (size_t i = 0; i < n; i++) g->rows_host[i] = {rows[i].token, rows[i].pos, rows[i].seq};
+    int max_pos = 0;
+    for (size_t i = 0; i < n; i++) {
+        g->rows_host[i] = {rows[i].token, rows[i].pos, rows[i].seq};
+        max_pos = std::max(max_pos, (int)rows[i].pos);
+    }
+    g->splits_grid = splits_bucket(g, max_pos);
     HIP_TRY(hipMemcpyAsync(g->rows_dev, g->rows_host, n * sizeof(row_rec), hipMemcpyHostToDevice, g->stream), "copying the rows");
     HIP_TRY(hipEventRecord(g->rows_copied, g->stream), "recording the row copy");
     g->rows_n = (int)n;
@@ -2454,27 +2491,40 @@ static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_
     if (!ensure_tiled(g, err, err_len)) return false;
     /* a fast pass's working buffers exist before the capture (growing them later would free what the graph uses) */
     if (rows_fast(g, n) && !prefill_reserve(g, (size_t)n, err, err_len)) return false;
-    if (g->rows_graph_n == n && g->rows_graph_shared == g->rows_shared_seq && g->rows_graph_fast == rows_fast(g, n)) return true;
-    if (g->rows_graph_n) {
-        HIP_TRY(hipStreamSynchronize(g->stream), "before recapturing the rows step");
-        (void)hipGraphExecDestroy(g->rows_graph);
-        (void)hipGraphDestroy(g->rows_graph_src);
-        g->rows_graph_n = 0;
+    const bool fast = rows_fast(g, n);
+    int pick = 0;
+    for (int i = 0; i < ROWS_GRAPHS; i++) {
+        const auto& r = g->rg[i];
+        if (r.n == n && r.shared == g->rows_shared_seq && r.fast == fast && r.splits == g->splits_grid) {
+            g->rg[i].used = ++g->rg_clock;
+            g->rg_cur = i;
+            return true;
+        }
+        if (!r.n || (g->rg[pick].n && r.used < g->rg[pick].used)) pick = i;
     }
+    auto& r = g->rg[pick];
     HIP_TRY(hipStreamSynchronize(g->stream), "before capturing the rows step");
+    if (r.n) {
+        (void)hipGraphExecDestroy(r.exec);
+        (void)hipGraphDestroy(r.src);
+        r.n = 0;
+    }
     HIP_TRY(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "capturing the rows step");
     const hipError_t e = enqueue_rows_step_body(g, n);
     hipGraph_t graph = nullptr;
     const hipError_t e2 = hipStreamEndCapture(g->stream, &graph);
     if (e != hipSuccess) { if (graph) (void)hipGraphDestroy(graph); return check_launch(g, e, "capturing the rows step", err, err_len); }
     HIP_TRY(e2, "ending the capture of the rows step");
-    const hipError_t e3 = hipGraphInstantiate(&g->rows_graph, graph, nullptr, nullptr, 0);
+    const hipError_t e3 = hipGraphInstantiate(&r.exec, graph, nullptr, nullptr, 0);
     if (e3 != hipSuccess) (void)hipGraphDestroy(graph);
     HIP_TRY(e3, "instantiating the rows step's graph");
-    g->rows_graph_src = graph;
-    g->rows_graph_n = n;
-    g->rows_graph_fast = rows_fast(g, n);
-    g->rows_graph_shared = g->rows_shared_seq;
+    r.src = graph;
+    r.n = n;
+    r.fast = fast;
+    r.shared = g->rows_shared_seq;
+    r.splits = g->splits_grid;
+    r.used = ++g->rg_clock;
+    g->rg_cur = pick;
     return true;
 }
 
@@ -2485,7 +2535,7 @@ extern "C" bool vitna_hip_moe_rows_step(struct vitna_cuda_model* g, const vitna_
     if (!g->attention) return fail(err, err_len, "this model has no attention");
     if (!set_rows(g, rows, n, err, err_len)) return false;
     if (!ensure_rows_graph(g, (int)n, err, err_len)) return false;
-    HIP_TRY(hipGraphLaunch(g->rows_graph, g->stream), "launching the rows step");
+    HIP_TRY(hipGraphLaunch(g->rg[g->rg_cur].exec, g->stream), "launching the rows step");
     g->last_step_mega = false;
     for (size_t i = 0; i < n; i++)
         if (logits && logits[i])
@@ -2504,10 +2554,10 @@ extern "C" bool vitna_hip_time_rows(struct vitna_cuda_model* g, const vitna_cuda
     if (!ensure_rows_graph(g, (int)n, err, err_len)) return false;
     event_pair ev;
     HIP_TRY(ev.make(), "events");
-    HIP_TRY(hipGraphLaunch(g->rows_graph, g->stream), "launching the rows step"); /* warm-up */
+    HIP_TRY(hipGraphLaunch(g->rg[g->rg_cur].exec, g->stream), "launching the rows step"); /* warm-up */
     HIP_TRY(hipStreamSynchronize(g->stream), "before timing");
     HIP_TRY(hipEventRecord(ev.t0, g->stream), "events");
-    for (int i = 0; i < steps; i++) HIP_TRY(hipGraphLaunch(g->rows_graph, g->stream), "launching the rows step");
+    for (int i = 0; i < steps; i++) HIP_TRY(hipGraphLaunch(g->rg[g->rg_cur].exec, g->stream), "launching the rows step");
     HIP_TRY(hipEventRecord(ev.t1, g->stream), "events");
     HIP_TRY(hipEventSynchronize(ev.t1), "timing the rows steps");
     float ms = 0;

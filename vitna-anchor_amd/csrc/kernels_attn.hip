@@ -515,8 +515,8 @@ __global__ __launch_bounds__(256, ATTN_MMA_OCC) void attention_mma_kernel(attn_a
 
 hipError_t launch_attention(const attn_args& a, hipStream_t s) {
     if (a.n_kv < 1 || a.n_heads % a.n_kv || a.n_heads / a.n_kv > GMAX || a.n_rows < 1) return hipErrorInvalidValue;
-    if (a.splits_max * ATTN_CHUNK < a.ctx) return hipErrorInvalidValue;
-    const dim3 grid(a.splits_max, a.n_kv, a.n_rows);
+    if (a.splits_max * ATTN_CHUNK < a.ctx || a.splits_grid < 0) return hipErrorInvalidValue;
+    const dim3 grid(a.splits_grid > 0 && a.splits_grid < a.splits_max ? a.splits_grid : a.splits_max, a.n_kv, a.n_rows);
     const int G = a.n_heads / a.n_kv;
     if (a.mma && a.hd == 128) {
 #define ATTN_MMA(GG) \

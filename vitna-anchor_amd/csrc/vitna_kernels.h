@@ -195,6 +195,9 @@ struct attn_args {
     float* partial;        /* [n_rows][n_kv][splits_max][G][hd + 4]: values, max, sum, padding */
     float* att;            /* [n_rows][n_heads * hd] */
     int n_heads, n_kv, hd, ctx, splits_max;
+    /* chunks the launch covers (the grid's first dimension): at least the most any row of the pass has, at most
+       splits_max; 0: splits_max. Blocks past a row's last chunk return at once, but they still take a dispatch. */
+    int splits_grid;
     float eps;
     /* 0: this kernel normalizes and rotates q and k and stores k and v at
        each row's position itself (rows of distinct sequences). 1: q_raw holds
