@@ -1,0 +1,113 @@
+"""A prompt through the rows path: passes of many rows of ONE sequence at consecutive positions, as model.c feeds
+a prompt in chunks of vitna_cuda_moe_rows_max (engine/src/model.c:1006-1030). Such a pass (more rows than
+vitna_hip_set_exact_rows' limit) takes the attention kernel that reads each chunk of keys and values once for a tile
+of rows (attention_run_kernel), where passes of rows of several sequences read them once a row.
+
+Bars:
+  * a 1024-row pass and a 90-row pass after it, as the device-routed rows step and through the ABI layer by layer
+    with the routing the step chose (the host's rule picks the same experts): the same logits bits (the same
+    kernels), and every layer's experts identical to the checker's step of sampled rows over the device's cache,
+    their logits within 1e-3 of max |cpu|;
+  * query groups of 4 (tiles of 16 rows) and of 8 query heads a key-value head (tiles of 8 rows), and a pass whose
+    row count leaves the last tile part-filled;
+  * the same pass with every row of another sequence added to it takes the per-row kernel: the one-sequence rows
+    within 1e-3 of that pass's (sums in another order).
+"""
+import numpy as np
+import pytest
+
+import oracle
+import vitna_amd as va
+from test_gpu_decode import SMALL, rel, say
+
+pytestmark = pytest.mark.gpu
+
+SPECS = {
+    "g4": dict(SMALL["q4km"], seqs=2, ctx=1200),
+    "g8": dict(n_layers=2, hidden=512, intermediate=256, n_heads=16, n_kv_heads=2, head_dim=128, vocab=1000,
+               n_experts=16, n_experts_used=4, renormalize=1, dt_gate_up=va.Q4_K, dt_down=va.Q6_K, norm_std=0.1,
+               ctx=1200, seqs=2, kv_host=1),
+}
+
+
+def abi_pass(dev, cfg, rows, dev_rt):
+    """The rows through the ABI layer by layer, each row given the routing the device-routed step chose (the host's
+    rule picks the same experts from the same logits; the device's weights are used so that the same kernels see
+    the same inputs)."""
+    K, ren = cfg.n_experts_used, bool(cfg.renormalize)
+    chosen = []
+    for l in range(cfg.n_layers):
+        lg = dev.rows_route(rows, l)
+        ids = np.array([dev_rt[l][i][1] for i in range(len(rows))])
+        ws = np.array([dev_rt[l][i][2] for i in range(len(rows))])
+        ch = []
+        for i in range(len(rows)):
+            c, order, w = oracle.route(lg[i], K, ren)
+            assert np.array_equal(order, ids[i]), ("layer", l, "row", i)
+            ch.append(c)
+        dev.rows_experts(l, ids, ws)
+        chosen.append(ch)
+    return dev.rows_head(len(rows)), chosen
+
+
+def check_rows(model, dev, rows, logits, chosen, sample):
+    cfg = model.cfg
+    L, kd = cfg.n_layers, cfg.n_kv_heads * cfg.head_dim
+    kc = np.ctypeslib.as_array(model.m.k_cache, shape=(model.m.seqs, L, model.m.ctx, kd))
+    vc = np.ctypeslib.as_array(model.m.v_cache, shape=(model.m.seqs, L, model.m.ctx, kd))
+    worst = 0.0
+    for i in sample:
+        tok, pos, seq = rows[i]
+        for l in range(L):
+            if pos:
+                k, v = dev.kv(seq, l, 0, pos)
+                kc[seq, l, :pos] = k
+                vc[seq, l, :pos] = v
+        ref, _, tc, _ = oracle.step(model, seq, tok, pos)
+        for l in range(L):
+            assert np.array_equal(np.sort(chosen[l][i]), np.sort(tc[l])), ("row", i, "layer", l)
+        worst = max(worst, rel(logits[i], ref))
+    return worst
+
+
+@pytest.mark.parametrize("name", ["g4", "g8"])
+def test_prompt_passes(name):
+    say("prompt passes", name)
+    model = va.Model(va.shape(**SPECS[name]), 777)
+    a, b = va.Device(model), va.Device(model)
+    try:
+        cfg = model.cfg
+        worst = 0.0
+        for start, n in ((0, 1024), (1024, 90)):
+            rows = [((13 * (start + i) + 5) % cfg.vocab, start + i, 0) for i in range(n)]
+            lb = np.stack(b.rows_step(rows))
+            dev_rt = [[b.rows_routing(l, i) for i in range(n)] for l in range(cfg.n_layers)]
+            la, chosen = abi_pass(a, cfg, rows, dev_rt)
+            assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), ("pass at", start)
+            worst = max(worst, check_rows(model, a, rows, la, chosen, (0, 1, 63, 64, n // 2, n - 2, n - 1)))
+        say("  logits rel err against the checker (sampled rows)", worst)
+        assert worst <= 1e-3
+    finally:
+        a.close()
+        b.close()
+        model.free()
+
+
+def test_prompt_against_per_row_kernel():
+    """A 300-row pass of sequence 0 (tiles) against the same rows with one row of sequence 1 appended (the per-row
+    kernel for every row): the sequence-0 rows within 1e-3 of max |logits| of each other."""
+    say("prompt tiles against the per-row kernel")
+    model = va.Model(va.shape(**SPECS["g8"]), 4321)
+    a, b = va.Device(model), va.Device(model)
+    try:
+        cfg = model.cfg
+        rows = [((11 * i + 3) % cfg.vocab, i, 0) for i in range(300)]
+        la = np.stack(a.rows_step(rows))
+        lb = np.stack(b.rows_step(rows + [(7, 0, 1)]))[:300]
+        worst = max(rel(la[i], lb[i]) for i in range(300))
+        say("  tiles against per-row: max rel diff", worst)
+        assert worst <= 1e-3
+    finally:
+        a.close()
+        b.close()
+        model.free()

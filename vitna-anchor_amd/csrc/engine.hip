@@ -102,6 +102,7 @@ struct vitna_cuda_model {
     uint16_t *gm_xs, *gm_as;    /* the grouped experts' split activations: [ROWS_MAX][2H], [ROWS_MAX * K][2I] */
     float *gm_xsum, *gm_asum;   /* and their sums over runs of 16 or more columns */
     bool rows_shared_seq;       /* the pass's rows include two of one sequence (attention prepares first) */
+    bool rows_one_seq;          /* every row of the pass is of one sequence (a prompt's chunk: tiles of rows) */
     /* the rows step's captured graphs, a few kept (least recently used replaced): one a pass shape */
     struct rows_graph_t {
         hipGraph_t src;
@@ -2055,7 +2056,8 @@ static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n, 
     go.w[0] = d.o; go.y[0] = g->x; go.nm = 1; go.x = g->att; go.n = n; go.xstride = g->nh * g->hd; go.add = 1;
     /* the merge writes the o-projection's operands too */
     const bool oimg = multi_exact(go);
-    e = launch_attention(a, g->stream);
+    /* a pass of one sequence (a prompt's chunk): tiles of rows read each chunk once */
+    e = g->rows_one_seq && n > 1 && attention_run_fits(a) ? launch_attention_run(a, g->stream) : launch_attention(a, g->stream);
     if (oimg) a.img = model_img(g);
     if (e == hipSuccess) e = launch_attention_merge(a, g->stream);
     if (e != hipSuccess) return e;
@@ -2242,6 +2244,8 @@ static bool set_rows(vitna_cuda_model* g, const vitna_cuda_row_t* rows, size_t n
     HIP_TRY(hipMemcpyAsync(g->rows_dev, g->rows_host, n * sizeof(row_rec), hipMemcpyHostToDevice, g->stream), "copying the rows");
     HIP_TRY(hipEventRecord(g->rows_copied, g->stream), "recording the row copy");
     g->rows_n = (int)n;
+    g->rows_one_seq = true;
+    for (size_t i = 1; i < n; i++) g->rows_one_seq &= rows[i].seq == rows[0].seq;
     g->pass_exact = false; /* vitna_cuda_moe_rows_route decides at layer 0 */
     g->parts_n = 0; /* a pass of rows owns x's rows: no one row's attention parts are pending any more */
     g->rows_shared_seq = shared;
