@@ -3,6 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
     python bench.py --only 0|1|3|4 [--steps K] one of the other configs alone (profiling)
     python bench.py --only cache [--cache-frac F] configs[2]'s decode through the expert cache
+    python bench.py --only prompt                 a 4096-token prompt through configs[2]'s model
 
 Workload: a full 48-layer Qwen3-30B-A3B-shaped model
 with seeded random weights (Q4_K gate/up/q/k/o, Q6_K down/v/LM head, Q4_K
@@ -70,7 +71,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-extra", action="store_true", help="measure configs[2] only")
-    ap.add_argument("--only", choices=["0", "1", "3", "4", "4k", "cache"],
+    ap.add_argument("--only", choices=["0", "1", "3", "4", "4k", "cache", "prompt"],
                     help="run one of the other configs alone (profiling), or the expert cache's decode, and print its object")
     ap.add_argument("--cache-frac", type=float, default=0.5, help="--only cache: the share of the experts the cache holds")
     args = ap.parse_args()
@@ -90,6 +91,10 @@ def main():
             res = bench_prefill(va, reps=args.steps)
         elif args.only == "cache":
             res = bench_cache(va, args.steps, args.warmup, args.cache_frac, args.layers)
+        elif args.only == "prompt":
+            model = va.Model(va.shape(n_layers=args.layers, ctx=4096, seqs=1, kv_host=0), 20260101, threads=16)
+            res = bench_prompt(va, model)
+            model.free()
         else:
             model = va.Model(va.shape(n_layers=args.layers, ctx=8193, seqs=32, kv_host=0), 20260101, threads=16)
             dev = va.Device(model)
@@ -315,8 +320,8 @@ def bench_prompt(va, model, tokens=4096, chunk=1024):
     model's, at most 4096), as model.c feeds a prompt in chunks of vitna_cuda_moe_rows_max
     (the rows step: each row's attention over the keys of the positions before it and its own, device routing,
     experts grouped), with the exact kernels and with --precision fast (a gpu_fast model: the passes' experts as
-    the bf16 grouped GEMM). The last pass's logits come back. Wall-clock of the second prompt (the first captures
-    the graph and makes the tiled copies)."""
+    the bf16 grouped GEMM). The last position's logits come back, as model.c asks of a prompt. Wall-clock of the
+    second prompt (the first captures the graphs and makes the tiled copies)."""
     cfg = model.cfg
     out = {"workload": "a %d-token prompt through BASELINE configs[2]'s model (Qwen3-30B-A3B-shaped Q4_K_M, 48 layers), "
                        "passes of %d rows of one sequence" % (tokens, chunk),
@@ -335,7 +340,8 @@ def bench_prompt(va, model, tokens=4096, chunk=1024):
             def prompt():
                 for c in range(tokens // chunk):
                     rows = [((7 * (c * chunk + i) + 3) % cfg.vocab, c * chunk + i, 0) for i in range(chunk)]
-                    dev.rows_step(rows, logits=(c == tokens // chunk - 1))
+                    # the last position's logits, as model.c asks of a prompt
+                    dev.rows_step(rows, logits=(c == tokens // chunk - 1), only=[chunk - 1])
                 dev.sync()
             prompt()
             t = time.perf_counter()

@@ -508,10 +508,13 @@ class Device:
         self._ok(self.lib.vitna_cuda_moe_rows_head(self.g, n, ptrs, self.err, 512))
         return out
 
-    def rows_step(self, rows, logits=True):
+    def rows_step(self, rows, logits=True, only=None):
+        """logits of every row (or, with only, of the rows it lists, the others' pointers NULL: their rows of the
+        result stay unset) or none."""
         n = len(rows)
         out = np.empty((n, self.model.cfg.vocab), np.float32) if logits else None
-        ptrs = (_FP * n)(*[out[i].ctypes.data_as(_FP) for i in range(n)]) if logits else None
+        want = set(range(n)) if only is None else set(only)
+        ptrs = (_FP * n)(*[out[i].ctypes.data_as(_FP) if i in want else None for i in range(n)]) if logits else None
         self._ok(self.lib.vitna_hip_moe_rows_step(self.g, self._rows(rows), n, ptrs, self.err, 512))
         return out
 
