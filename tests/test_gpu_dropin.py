@@ -16,7 +16,8 @@ Bars, each the reference's own promise from its usage text (engine/src/main.c:68
     (--experts-in) on both (main.c:809-880);
   * `expert-check --device cuda` runs every expert it names through vitna_cuda_expert_check and reports them
     (main.c:1337-1401).
-The same checks of logits and generate run on four layers of BASELINE configs[2]'s shape too. The engine binary
+A prompt of 1100 tokens (two chunks of rows) is checked the same way. The same checks of logits and generate run
+on four layers of BASELINE configs[2]'s shape too. The engine binary
 exists only where the build container made it (oracle/_ref, from /root/reference's sources);
 elsewhere these tests skip.
 """
@@ -201,6 +202,43 @@ def test_routing_traces_and_pins(model_dir, tmp_path):
     say("  pinned experts: logits rel err (max)", float(r.max()))
     assert r.max() <= 1e-3
     assert not np.allclose(pinned["cuda"], gl)
+
+
+@needs_engine
+def test_long_prompt(tmp_path_factory, tmp_path):
+    """A prompt of 1100 tokens: model.c feeds it in chunks of vitna_cuda_moe_rows_max (1024 rows of one sequence,
+    asking no logits, then 76 asking the last), model.c:1000-1020. The GPU's greedy tokens and logits against the
+    CPU's, as above."""
+    d = str(tmp_path_factory.mktemp("dropin_long"))
+    m = va.Model(va.shape(**dict(SPEC, ctx=2048)), 99)
+    try:
+        va.write_gguf(m, d, va.F32, 32)
+    finally:
+        m.free()
+    tokenizer(d, SPEC["vocab"])
+    ids = [(17 * i + 5) % SPEC["vocab"] for i in range(1100)]
+    ids_file = str(tmp_path / "ids.txt")
+    with open(ids_file, "w") as f:
+        f.write(ids_arg(ids))
+    res = {}
+    for dev in ("cpu", "cuda"):
+        lo = str(tmp_path / ("long_%s.bin" % dev))
+        extra = ["--device", "cuda"] if dev == "cuda" else ["--threads", "16"]
+        p = run(d, "generate", "--ids-file", ids_file, "--max-new", "8", "--logits-out", lo, "--timing", *extra, timeout=300)
+        say("  " + dev + ": " + " ".join(l for l in p.stderr.splitlines() if l.startswith("timing")))
+        res[dev] = (json.loads(p.stdout.strip().splitlines()[-1])["ids"], np.fromfile(lo, np.float32).reshape(-1, SPEC["vocab"]))
+    (c_ids, c_lg), (g_ids, g_lg) = res["cpu"], res["cuda"]
+    same = 0
+    while same < len(c_ids) and c_ids[same] == g_ids[same]:
+        same += 1
+    say("  greedy tokens equal for", same, "of", len(c_ids))
+    steps = min(same + 1, len(c_lg), len(g_lg))
+    r = rel_rows(g_lg[:steps], c_lg[:steps])
+    say("  logits rel err (max)", float(r.max()))
+    assert r.max() <= 1e-3
+    if same < len(c_ids):
+        top = np.sort(c_lg[same])[-2:]
+        assert top[1] - top[0] <= 2e-3 * np.max(np.abs(c_lg[same])), ("step", same, top)
 
 
 @pytest.fixture(scope="module")

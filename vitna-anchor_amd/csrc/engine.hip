@@ -2451,6 +2451,10 @@ extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, f
     if (!ensure_tiled(g, err, err_len)) return false;
     if (!g->attention) return fail(err, err_len, "this model has no output projection");
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
+    /* a prompt's chunks before its last ask no logits (model.c:1011): then the head has nothing to do */
+    bool any = false;
+    for (size_t i = 0; logits && i < n; i++) any |= logits[i] != nullptr;
+    if (!any) return true;
     if (!check_launch(g, g->pass_exact ? enqueue_exact_head(g, (int)n) : enqueue_rows_head(g, (int)n, nullptr), "the head", err, err_len))
         return false;
     for (size_t i = 0; i < n; i++)
