@@ -1,7 +1,7 @@
 """A prompt through the rows path: passes of many rows of ONE sequence at consecutive positions, as model.c feeds
 a prompt in chunks of vitna_cuda_moe_rows_max (engine/src/model.c:1006-1030). Such a pass (more rows than
 vitna_hip_set_exact_rows' limit) takes the attention kernel that reads each chunk of keys and values once for a tile
-of rows (attention_run_kernel), where passes of rows of several sequences read them once a row.
+of rows (attention_flash_kernel), where passes of rows of several sequences read them once a row.
 
 Bars:
   * a 1024-row pass and a 90-row pass after it, as the device-routed rows step and through the ABI layer by layer

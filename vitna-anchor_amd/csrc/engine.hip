@@ -2056,8 +2056,13 @@ static hipError_t enqueue_rows_attention(vitna_cuda_model* g, int layer, int n, 
     go.w[0] = d.o; go.y[0] = g->x; go.nm = 1; go.x = g->att; go.n = n; go.xstride = g->nh * g->hd; go.add = 1;
     /* the merge writes the o-projection's operands too */
     const bool oimg = multi_exact(go);
-    /* a pass of one sequence (a prompt's chunk): tiles of rows read each chunk once */
-    e = g->rows_one_seq && n > 1 && attention_run_fits(a) ? launch_attention_run(a, g->stream) : launch_attention(a, g->stream);
+    if (g->rows_one_seq && n > 1 && attention_run_fits(a)) {
+        /* a pass of one sequence (a prompt's chunk): tiles of rows, each chunk read once a tile, att written by the
+           attention itself; the o-projection's operands split from it */
+        e = launch_attention_flash(a, g->stream);
+        return e == hipSuccess ? enqueue_multi(g, go, false) : e;
+    }
+    e = launch_attention(a, g->stream);
     if (oimg) a.img = model_img(g);
     if (e == hipSuccess) e = launch_attention_merge(a, g->stream);
     if (e != hipSuccess) return e;

@@ -536,40 +536,32 @@ hipError_t launch_attention(const attn_args& a, hipStream_t s) {
 /* ---- passes of many rows of one sequence (a prompt's chunks): a tile of rows a block ----
    The per-row kernels read a chunk's keys and values once for every row, so a prompt pass of 1024 rows of one
    sequence reads each chunk up to 1024 times (from the memory-side cache; the L2 of an XCD holds 4 MB of a layer's
-   16 MB). Here a block takes one chunk of 64 positions of one kv head for a tile of TQ = 4 * 16 / G rows: the chunk's
-   keys and values go to LDS once (64 KB, float4 chunks XOR-swizzled by position so that the fragment reads do
-   not share banks), and wave w takes 16 query columns, RW = 16 / G rows of the tile times the G heads, against all
-   64 positions: scores on v_mfma_f32_16x16x4_f32 (lane (c, kq) multiplies dimensions 32 kq .. 32 kq + 31 of key
-   row c and of column c), the softmax over the chunk per column, then P . V as the decode kernel takes it, and
-   the chunk's partial (max, sum, weighted values) per (row, head), the layout attention_merge_kernel reads. The
-   queries come prepared (launch_attention_prepare), each row masked to the positions up to its own. */
+   16 MB). Here a block takes one kv head for a tile of TQ = 4 * 16 / G rows and loops over the chunks up to the
+   tile's last position: each chunk's keys and values go to LDS once (64 KB, float4 chunks XOR-swizzled by position
+   so that the fragment reads do not share banks), and wave w takes 16 query columns, RW = 16 / G rows of the tile
+   times the G heads, against the chunk's 64 positions: scores on v_mfma_f32_16x16x4_f32 (lane (c, kq) multiplies
+   dimensions 32 kq .. 32 kq + 31 of key row c and of column c), each row masked to the positions up to its own,
+   then P . V as the decode kernel takes it. The queries come prepared (launch_attention_prepare). The scores of
+   each chunk fold into a running maximum and sum per column, the values into O rescaled as the maximum grows,
+   and the block writes att itself (O / sum): no chunk leaves a partial and no merge runs. A chunk's keys and
+   values are requested before the barrier that frees the LDS of the previous one; the other block of the CU
+   covers the wait. */
 #define RUN_CHUNKS 32 /* float4 chunks of a head's 128 dimensions */
 template <int G>
-__global__ __launch_bounds__(256, 2) void attention_run_kernel(attn_args a) {
-    constexpr int HD = 128, PS = HD + 4, RW = 16 / G, TQ = 4 * RW;
-    const int split = blockIdx.x, h = blockIdx.y, tile = blockIdx.z;
+__global__ __launch_bounds__(256, 2) void attention_flash_kernel(attn_args a) {
+    constexpr int HD = 128, RW = 16 / G, TQ = 4 * RW;
+    const int h = blockIdx.x, tile = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c16 = lane & 15, kq = lane >> 4;
     const int r_first = tile * TQ, r_end = min(a.n_rows, r_first + TQ);
     int pmax = 0;
     for (int r = r_first; r < r_end; r++) pmax = max(pmax, a.rows[r].pos);
-    if (split > pmax / ATTN_CHUNK) return;
-    const int seq = a.rows[r_first].seq, kv_dim = a.n_kv * HD, t0 = split * ATTN_CHUNK;
+    const int nch = pmax / ATTN_CHUNK + 1;
+    const int seq = a.rows[r_first].seq, kv_dim = a.n_kv * HD;
     const float* kc = a.k_cache + (size_t)seq * a.seq_stride;
     const float* vc = a.v_cache + (size_t)seq * a.seq_stride;
     __shared__ __attribute__((aligned(16))) float sk[ATTN_CHUNK * HD];
     __shared__ __attribute__((aligned(16))) float sv[ATTN_CHUNK * HD];
 
-    /* the chunk's keys and values, positions past the tile's last as zeros: 8 float4 of each a thread */
-    float4 kr[8], vr[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int idx = tid + 256 * i, p = idx >> 5, c = idx & 31, pos = t0 + p;
-        const bool ok = pos <= pmax;
-        const size_t at = (size_t)(ok ? pos : t0) * kv_dim + (size_t)h * HD + 4 * c;
-        kr[i] = ok ? *reinterpret_cast<const float4*>(kc + at) : make_float4(0.f, 0.f, 0.f, 0.f);
-        vr[i] = ok ? *reinterpret_cast<const float4*>(vc + at) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    /* this lane's query column: row rr of the tile, head g; dimensions 32 kq .. 32 kq + 31, scaled by 1 / sqrt(hd) */
     const int rr = r_first + wave * RW + c16 / G, g = c16 % G;
     const bool colv = rr < r_end;
     const int prow = colv ? a.rows[rr].pos : -1;
@@ -584,103 +576,123 @@ __global__ __launch_bounds__(256, 2) void attention_run_kernel(attn_args a) {
             qv[4 * i] = v.x * sc; qv[4 * i + 1] = v.y * sc; qv[4 * i + 2] = v.z * sc; qv[4 * i + 3] = v.w * sc;
         }
     }
+    float4 kr[8], vr[8];
+    auto fetch = [&](int c) {
+        const int t0 = c * ATTN_CHUNK;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int idx = tid + 256 * i, p = idx >> 5, c = idx & 31, pc = c ^ (p & 31);
-        reinterpret_cast<float4*>(sk)[p * RUN_CHUNKS + pc] = kr[i];
-        reinterpret_cast<float4*>(sv)[p * RUN_CHUNKS + pc] = vr[i];
-    }
-    __syncthreads();
-
-    /* scores: S[pt] holds positions 16 pt + 4 kq + i (i < 4) of column c16 */
-    at_f4 S[4];
-#pragma unroll
-    for (int pt = 0; pt < 4; pt++) {
-        const int p = 16 * pt + c16;
-        at_f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const float4 k4 = reinterpret_cast<const float4*>(sk)[p * RUN_CHUNKS + ((8 * kq + q) ^ (p & 31))];
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qv[4 * q], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qv[4 * q + 1], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qv[4 * q + 2], acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qv[4 * q + 3], acc, 0, 0, 0);
+        for (int i = 0; i < 8; i++) {
+            const int idx = tid + 256 * i, p = idx >> 5, cc = idx & 31, pos = t0 + p;
+            const bool ok = pos <= pmax;
+            const size_t at = (size_t)(ok ? pos : 0) * kv_dim + (size_t)h * HD + 4 * cc;
+            kr[i] = ok ? *reinterpret_cast<const float4*>(kc + at) : make_float4(0.f, 0.f, 0.f, 0.f);
+            vr[i] = ok ? *reinterpret_cast<const float4*>(vc + at) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        S[pt] = acc;
-    }
-    /* the softmax over the chunk, per column (lanes c16, c16 + 16, + 32, + 48 hold one column) */
-    float m = -INFINITY;
-#pragma unroll
-    for (int pt = 0; pt < 4; pt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const bool ok = t0 + 16 * pt + 4 * kq + i <= prow;
-            S[pt][i] = ok ? S[pt][i] : -INFINITY;
-            m = fmaxf(m, S[pt][i]);
-        }
-    m = fmaxf(m, __shfl_xor(m, 16, WAVE));
-    m = fmaxf(m, __shfl_xor(m, 32, WAVE));
-    float l = 0.0f;
-#pragma unroll
-    for (int pt = 0; pt < 4; pt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            S[pt][i] = S[pt][i] == -INFINITY ? 0.0f : __expf(S[pt][i] - m);
-            l += S[pt][i];
-        }
-    l += __shfl_xor(l, 16, WAVE);
-    l += __shfl_xor(l, 32, WAVE);
-
-    /* values: O[j] column tile j of dimension VDIM(j, c); step (pt, i) takes position 16 pt + 4 (lane / 16) + i */
+    };
+    float m_run = -INFINITY, l_run = 0.0f;
     at_f4 O[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) O[j] = at_f4{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nch; c++) {
+        fetch(c);
+        __syncthreads(); /* the previous chunk's fragment reads are done */
 #pragma unroll
-    for (int pt = 0; pt < 4; pt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int p = 16 * pt + 4 * kq + i;
-            const float4 v0 = reinterpret_cast<const float4*>(sv)[p * RUN_CHUNKS + (c16 ^ (p & 31))];
-            const float4 v1 = reinterpret_cast<const float4*>(sv)[p * RUN_CHUNKS + ((16 + c16) ^ (p & 31))];
-            const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) O[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(S[pt][i], vv[j], O[j], 0, 0, 0);
+        for (int i = 0; i < 8; i++) {
+            const int idx = tid + 256 * i, p = idx >> 5, cc = idx & 31, pc = cc ^ (p & 31);
+            reinterpret_cast<float4*>(sk)[p * RUN_CHUNKS + pc] = kr[i];
+            reinterpret_cast<float4*>(sv)[p * RUN_CHUNKS + pc] = vr[i];
         }
-    /* the partials: lane (c16, kq) holds O of columns 4 kq + i at dimensions VDIM(j, c16) */
+        __syncthreads();
+        const int t0 = c * ATTN_CHUNK;
+        at_f4 S[4];
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++) {
+            const int p = 16 * pt + c16;
+            at_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float4 k4 = reinterpret_cast<const float4*>(sk)[p * RUN_CHUNKS + ((8 * kq + q) ^ (p & 31))];
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qv[4 * q], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qv[4 * q + 1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qv[4 * q + 2], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qv[4 * q + 3], acc, 0, 0, 0);
+            }
+            S[pt] = acc;
+        }
+        float m = m_run;
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const bool ok = t0 + 16 * pt + 4 * kq + i <= prow;
+                S[pt][i] = ok ? S[pt][i] : -INFINITY;
+                m = fmaxf(m, S[pt][i]);
+            }
+        m = fmaxf(m, __shfl_xor(m, 16, WAVE));
+        m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+        /* the column's rescale of what came before (0 when nothing did) */
+        const float f = m == -INFINITY || m_run == -INFINITY ? 0.0f : __expf(m_run - m);
+        float l = 0.0f;
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                S[pt][i] = S[pt][i] == -INFINITY ? 0.0f : __expf(S[pt][i] - m);
+                l += S[pt][i];
+            }
+        l += __shfl_xor(l, 16, WAVE);
+        l += __shfl_xor(l, 32, WAVE);
+        l_run = fmaf(l_run, f, l);
+        m_run = m;
+        /* O's rows are the columns 4 kq + i: their rescales from the lanes that hold those columns */
+        float fo[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) fo[i] = __shfl(f, 4 * kq + i, WAVE);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) O[j][i] *= fo[i];
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = 16 * pt + 4 * kq + i;
+                const float4 v0 = reinterpret_cast<const float4*>(sv)[p * RUN_CHUNKS + (c16 ^ (p & 31))];
+                const float4 v1 = reinterpret_cast<const float4*>(sv)[p * RUN_CHUNKS + ((16 + c16) ^ (p & 31))];
+                const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) O[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(S[pt][i], vv[j], O[j], 0, 0, 0);
+            }
+    }
+    /* att = O / sum, column 4 kq + i of the lane's O at dimensions VDIM(j, c16) */
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int cc = 4 * kq + i, rw = r_first + wave * RW + cc / G, gc = cc % G;
+        const float lsum = __shfl(l_run, cc, WAVE);
         if (rw < r_end) {
-            float* part = a.partial + ((((size_t)rw * a.n_kv + h) * a.splits_max + split) * G + gc) * PS;
+            float* out = a.att + (size_t)rw * a.n_heads * HD + (size_t)(h * G + gc) * HD;
 #pragma unroll
-            for (int j = 0; j < 8; j++) part[VDIM(j, c16)] = O[j][i];
+            for (int j = 0; j < 8; j++) out[VDIM(j, c16)] = O[j][i] / lsum;
         }
     }
-    if (kq == 0 && colv) {
-        float* part = a.partial + ((((size_t)rr * a.n_kv + h) * a.splits_max + split) * G + g) * PS;
-        part[HD] = m;
-        part[HD + 1] = l;
+}
+
+hipError_t launch_attention_flash(const attn_args& a, hipStream_t s) {
+    if (!attention_run_fits(a) || a.n_rows < 1) return hipErrorInvalidValue;
+    const int G = a.n_heads / a.n_kv, tq = 4 * (16 / G);
+    const dim3 grid(a.n_kv, (a.n_rows + tq - 1) / tq);
+    switch (G) {
+        case 8: attention_flash_kernel<8><<<grid, 256, 0, s>>>(a); break;
+        case 4: attention_flash_kernel<4><<<grid, 256, 0, s>>>(a); break;
+        case 2: attention_flash_kernel<2><<<grid, 256, 0, s>>>(a); break;
+        case 1: attention_flash_kernel<1><<<grid, 256, 0, s>>>(a); break;
+        default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
 }
 
 bool attention_run_fits(const attn_args& a) {
     return a.hd == 128 && a.prepared && a.n_kv >= 1 && a.n_heads % a.n_kv == 0 && 16 % (a.n_heads / a.n_kv) == 0 &&
            a.n_heads / a.n_kv <= GMAX;
-}
-
-hipError_t launch_attention_run(const attn_args& a, hipStream_t s) {
-    if (!attention_run_fits(a) || a.n_rows < 1 || a.splits_max * ATTN_CHUNK < a.ctx || a.splits_grid < 0) return hipErrorInvalidValue;
-    const int G = a.n_heads / a.n_kv, tq = 4 * (16 / G);
-    const dim3 grid(a.splits_grid > 0 && a.splits_grid < a.splits_max ? a.splits_grid : a.splits_max, a.n_kv,
-                    (a.n_rows + tq - 1) / tq);
-    switch (G) {
-        case 8: attention_run_kernel<8><<<grid, 256, 0, s>>>(a); break;
-        case 4: attention_run_kernel<4><<<grid, 256, 0, s>>>(a); break;
-        case 2: attention_run_kernel<2><<<grid, 256, 0, s>>>(a); break;
-        case 1: attention_run_kernel<1><<<grid, 256, 0, s>>>(a); break;
-        default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
 }
 
 /* One block per (query head, row): the chunks' maxima and sums read in parallel, each chunk's scale

@@ -224,11 +224,12 @@ hipError_t launch_attention_oproj(const attn_args& a, const qmat& o, float* part
 /* x[row][i] = attn_resid(x[row][i], parts[row], n_parts, H, i) for n_rows rows (parts n_parts H floats a row):
    the parts folded into the residual (for a reader of the residual between the attention and the experts). */
 hipError_t launch_attn_fold(float* x, const float* parts, int n_parts, int H, hipStream_t s, int n_rows = 1);
-/* Rows of ONE sequence (prepared: queries in q_raw, every row's key and value stored), head dimension 128: the
-   chunks' partials of every (row, query head), as launch_attention leaves them, from tiles of 4 * 16 / G rows that
-   read each chunk's keys and values once (a prompt's passes). Sums in another order than launch_attention's. */
+/* Rows of ONE sequence (prepared: queries in q_raw, every row's key and value stored), head dimension 128: att of
+   every (row, query head) from tiles of 4 * 16 / G rows, each block a tile's chunks in a loop with the softmax
+   folded across them, each chunk's keys and values read once a tile (a prompt's passes). No partials, no merge;
+   sums in another order than launch_attention's and the merge's. attention_run_fits says whether a pass takes it. */
 bool attention_run_fits(const attn_args& a);
-hipError_t launch_attention_run(const attn_args& a, hipStream_t s);
+hipError_t launch_attention_flash(const attn_args& a, hipStream_t s);
 /* The chunks' partials of every (row, query head) combined into att. */
 hipError_t launch_attention_merge(const attn_args& a, hipStream_t s);
 /* The prepare pass of prepared = 1: q normalized and rotated into q_out, k
