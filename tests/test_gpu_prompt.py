@@ -6,7 +6,8 @@ of rows (attention_flash_kernel), where passes of rows of several sequences read
 Bars:
   * a 1024-row pass and a 90-row pass after it, as the device-routed rows step and through the ABI layer by layer
     with the routing the step chose (the host's rule picks the same experts): the same logits bits (the same
-    kernels), and every layer's experts identical to the checker's step of sampled rows over the device's cache,
+    kernels); sampled rows' router logits bit-exact against the checker's norm and router on the device's residual
+    (a pass of 128 rows or more takes the prefill's norm and router kernels); every layer's experts identical to the checker's step of sampled rows over the device's cache,
     their logits within 1e-3 of max |cpu|;
   * query groups of 4 (tiles of 16 rows) and of 8 query heads a key-value head (tiles of 8 rows), and a pass whose
     row count leaves the last tile part-filled;
@@ -18,7 +19,7 @@ import pytest
 
 import oracle
 import vitna_amd as va
-from test_gpu_decode import SMALL, rel, say
+from test_gpu_decode import C_f32, SMALL, rel, same_bits, say
 
 pytestmark = pytest.mark.gpu
 
@@ -30,14 +31,22 @@ SPECS = {
 }
 
 
-def abi_pass(dev, cfg, rows, dev_rt):
+def abi_pass(model, dev, rows, dev_rt):
     """The rows through the ABI layer by layer, each row given the routing the device-routed step chose (the host's
     rule picks the same experts from the same logits; the device's weights are used so that the same kernels see
     the same inputs)."""
+    cfg = model.cfg
     K, ren = cfg.n_experts_used, bool(cfg.renormalize)
+    E, H = cfg.n_experts, cfg.hidden
     chosen = []
     for l in range(cfg.n_layers):
         lg = dev.rows_route(rows, l)
+        # router logits bit-exact against the checker's norm and router on the device's residual rows
+        norm = np.ctypeslib.as_array(model.m.layers[l].mlp_norm, shape=(H,))
+        router = np.ctypeslib.as_array(C_f32(model.m.layers[l].router.data), shape=(E * H,))
+        for i in (0, len(rows) // 3, len(rows) - 1):
+            xn = oracle.rmsnorm(dev.residual(i), norm, cfg.rms_eps)
+            assert same_bits(lg[i], oracle.matvec(router, va.F32, xn, E, H)), ("router logits", "layer", l, "row", i)
         ids = np.array([dev_rt[l][i][1] for i in range(len(rows))])
         ws = np.array([dev_rt[l][i][2] for i in range(len(rows))])
         ch = []
@@ -82,7 +91,7 @@ def test_prompt_passes(name):
             rows = [((13 * (start + i) + 5) % cfg.vocab, start + i, 0) for i in range(n)]
             lb = np.stack(b.rows_step(rows))
             dev_rt = [[b.rows_routing(l, i) for i in range(n)] for l in range(cfg.n_layers)]
-            la, chosen = abi_pass(a, cfg, rows, dev_rt)
+            la, chosen = abi_pass(model, a, rows, dev_rt)
             assert np.array_equal(la.view(np.uint32), lb.view(np.uint32)), ("pass at", start)
             worst = max(worst, check_rows(model, a, rows, la, chosen, (0, 1, 63, 64, n // 2, n - 2, n - 1)))
         say("  logits rel err against the checker (sampled rows)", worst)

@@ -42,6 +42,8 @@
    row is the one a step would give", main.c:1003-1007). Longer passes (a prompt's chunks) take the multi-row
    kernels, within 1e-3 of the checker but not those bits. */
 #define EXACT_ROWS 64
+/* passes of at least this many rows take the prefill's norm and router kernels for their routers */
+#define ROUTE_WIDE_ROWS 128
 /* rows step graphs kept at once: a prompt's passes take up to three attention grids, and a ragged step a fourth */
 #define ROWS_GRAPHS 4
 
@@ -701,7 +703,15 @@ static hipError_t enqueue_route(vitna_cuda_model* g, int layer, float* logits, i
         r.parts = g->parts;
         r.n_parts = g->parts_n;
     }
-    hipError_t e = launch_route(r, g->stream);
+    hipError_t e;
+    if (n_rows >= ROUTE_WIDE_ROWS && xn_out && !r.parts) {
+        /* many rows (a prompt's chunk): the prefill's norm, then its router over the normalized rows, eight rows by
+           eight experts a lane group (the same sums in the same order as route_kernel's, so the same bits) */
+        e = launch_prefill_norm(x, d.mlp_norm, xn_out, nullptr, n_rows, g->H, g->eps, g->stream);
+        if (e == hipSuccess) e = launch_prefill_router(xn_out, d.router, logits, n_rows, g->E, g->H, g->stream);
+    } else {
+        e = launch_route(r, g->stream);
+    }
     /* one token's top-k runs in the experts' prologue (enqueue_experts); several rows' in a kernel of its own */
     if (e == hipSuccess && topk && n_rows > 1) e = launch_topk(logits, n_rows, g->E, g->K, g->renorm, rt ? rt : g->rt, g->stream, sp);
     return e;

@@ -88,6 +88,7 @@ __global__ __launch_bounds__(64) void prefill_norm_kernel(const float* __restric
         o.x = (v.x * inv) * nw.x; o.y = (v.y * inv) * nw.y;
         o.z = (v.z * inv) * nw.z; o.w = (v.w * inv) * nw.w;
         reinterpret_cast<float4*>(xn + r * H)[i] = o;
+        if (!xb) continue;
         uint2 b;
         b.x = bf16_rne(o.x) | (bf16_rne(o.y) << 16);
         b.y = bf16_rne(o.z) | (bf16_rne(o.w) << 16);

@@ -339,6 +339,8 @@ struct prefill_args {
     uint16_t* ypart;        /* bf16 [n * K][H], row * K + slot: each pair's weighted expert output */
     int E, K, cap, n;
 };
+/* xn = RMSNorm(x) * w in the sixteen-chain order (route_kernel's, the same bits), and its bf16 rounding into xb
+   unless xb is null. */
 hipError_t launch_prefill_norm(const float* x, const float* w, float* xn, uint16_t* xb, int n, int H, float eps, hipStream_t s);
 hipError_t launch_prefill_router(const float* xn, const float* R, float* logits, int n, int E, int H, hipStream_t s);
 /* Both in one kernel, the fp32 normalized rows kept in LDS (hidden up to 2048; hipErrorNotSupported above). */
