@@ -230,6 +230,27 @@ def test_rows_projections_isolated(name):
         model.free()
 
 
+@pytest.mark.parametrize("name", ["q4km", "q8", "wide_k"])
+def test_rows_projections_token_tiles(name):
+    """A pass of 200 rows (seven token tiles: the exact kernel takes two a block, the weights loaded once for both)
+    against the same rows projected 32 at a time (one token tile a block): the same bits, q, k, v, o and the head."""
+    say("rows projections, token tiles", name)
+    spec = dict(WIDE, seqs=1) if name == "wide_k" else dict(SMALL[name])
+    model = va.Model(va.shape(**spec), 6161)
+    dev = va.Device(model)
+    try:
+        rng = np.random.RandomState(3)
+        for which in range(5):
+            mat = _matrix(model, 0, which)
+            x = rng.standard_normal((200, mat.cols)).astype(np.float32)
+            y = dev.rows_project(0, which, x)
+            y32 = np.concatenate([dev.rows_project(0, which, x[i:i + 32]) for i in range(0, 200, 32)])
+            assert np.array_equal(y.view(np.uint32), y32.view(np.uint32)), ("matrix", which)
+    finally:
+        dev.close()
+        model.free()
+
+
 NARROW = dict(n_layers=2, hidden=256, intermediate=256, n_heads=2, n_kv_heads=1, head_dim=64, vocab=300, n_experts=8,
               n_experts_used=2, renormalize=0, rms_eps=1e-5, rope_theta=10000.0, dt_gate_up=va.Q8_0, dt_down=va.Q8_0,
               dt_q=va.Q8_0, dt_k=va.Q8_0, dt_v=va.Q8_0, dt_o=va.Q8_0, dt_head=va.Q8_0, dt_embed=va.Q8_0, norm_std=0.1,

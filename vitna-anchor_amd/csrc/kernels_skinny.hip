@@ -37,6 +37,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define SK_TOK 32
+#define SK_NT 2 /* token tiles a block of the exact kernel takes when a pass has many */
 
 /* ---- activations, split ------------------------------------------------- */
 
@@ -579,26 +580,34 @@ __device__ __forceinline__ void sx_compute(const sx_w<DT>& w, const sx_a& x, int
     }
 }
 
-/* Superblock b of the lane's weight row: every weight load issued first, the activations two units ahead. */
-template <int DT>
-__device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& w, int tile, int tt, int b, int lane, f32x16& acc) {
+/* Superblock b of the lane's weight row against NT token tiles tt0, tt0 + 1, ... (those below mt): every weight
+   load issued first, then each tile's activations two units ahead; the weights stay in registers across the
+   tiles, and each tile's sums run as they would for that tile alone. */
+template <int DT, int NT>
+__device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& w, int tile, int tt0, int mt, int b, int lane,
+                                              f32x16 (&acc)[NT]) {
     const int kq = lane >> 5;
     const int K = w.cols;
-    float cs[8];
     sx_w<DT> W;
-    sx_a x0, x1;
     sx_load_w<DT>(w, tile, b, lane, W);
-    sx_load_a<DT, 0>(a, tt, K, b, lane, x0);
-    sx_load_a<DT, 1>(a, tt, K, b, lane, x1);
-    __builtin_amdgcn_sched_barrier(0);
-    sx_compute<DT, 0>(W, x0, kq, acc, cs);
-    sx_load_a<DT, 2>(a, tt, K, b, lane, x0);
-    __builtin_amdgcn_sched_barrier(0);
-    sx_compute<DT, 1>(W, x1, kq, acc, cs);
-    sx_load_a<DT, 3>(a, tt, K, b, lane, x1);
-    __builtin_amdgcn_sched_barrier(0);
-    sx_compute<DT, 2>(W, x0, kq, acc, cs);
-    sx_compute<DT, 3>(W, x1, kq, acc, cs);
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int tt = tt0 + t;
+        if (tt >= mt) break;
+        float cs[8];
+        sx_a x0, x1;
+        sx_load_a<DT, 0>(a, tt, K, b, lane, x0);
+        sx_load_a<DT, 1>(a, tt, K, b, lane, x1);
+        __builtin_amdgcn_sched_barrier(0);
+        sx_compute<DT, 0>(W, x0, kq, acc[t], cs);
+        sx_load_a<DT, 2>(a, tt, K, b, lane, x0);
+        __builtin_amdgcn_sched_barrier(0);
+        sx_compute<DT, 1>(W, x1, kq, acc[t], cs);
+        sx_load_a<DT, 3>(a, tt, K, b, lane, x1);
+        __builtin_amdgcn_sched_barrier(0);
+        sx_compute<DT, 2>(W, x0, kq, acc[t], cs);
+        sx_compute<DT, 3>(W, x1, kq, acc[t], cs);
+    }
 }
 
 /*
@@ -608,6 +617,7 @@ __device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& 
  * counter in cnt[]) adds the splits' sums in split order, writes the result and clears the counter, so the
  * result does not depend on which block finishes last.
  */
+template <int NT>
 __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     extern __shared__ float red[]; /* [KS][16][64] */
     __shared__ int last;
@@ -622,65 +632,76 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     }
     const qmat& w = a.w[mi];
     const int splits = a.splits[mi], sp = bx % splits, tile = bx / splits;
-    const int row0 = 32 * tile, tok0 = blockIdx.y * SK_TOK;
+    const int row0 = 32 * tile, mt = (a.n + SK_TOK - 1) / SK_TOK, tt0 = blockIdx.y * NT;
     const int b = 8 * sp + wv;
-    f32x16 acc = {};
+    f32x16 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = f32x16{};
     if (b < w.cols / 256) {
-        if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K>(a, w, tile, blockIdx.y, b, lane, acc);
-        else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K>(a, w, tile, blockIdx.y, b, lane, acc);
-        else sx_superblock<VITNA_DTYPE_Q8_0>(a, w, tile, blockIdx.y, b, lane, acc);
+        if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K, NT>(a, w, tile, tt0, mt, b, lane, acc);
+        else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K, NT>(a, w, tile, tt0, mt, b, lane, acc);
+        else sx_superblock<VITNA_DTYPE_Q8_0, NT>(a, w, tile, tt0, mt, b, lane, acc);
     }
 
-    /* accumulator r of a lane: token 8 (r / 4) + 4 (lane / 32) + r % 4 of the tile, weight row lane % 32 */
     float* y = a.y[mi];
-    auto put = [&](int r, float v) {
-        const int n = row0 + l32;
-        const int tk = tok0 + 8 * (r >> 2) + 4 * kq + (r & 3);
-        if (n < w.rows && tk < a.n) {
-            float* o = y + (size_t)tk * w.rows + n;
-            *o = a.add ? *o + v : v;
-        }
-    };
-    if (KS > 1) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) red[(wv * 16 + r) * 64 + lane] = acc[r];
-        __syncthreads();
-    }
-    if (splits == 1) {
-        if (KS == 1) {
+    for (int t = 0; t < NT; t++) {
+        const int tt = tt0 + t;
+        if (tt >= mt) break;
+        /* accumulator r of a lane: token 8 (r / 4) + 4 (lane / 32) + r % 4 of the tile, weight row lane % 32 */
+        const int tok0 = tt * SK_TOK;
+        auto put = [&](int r, float v) {
+            const int n = row0 + l32;
+            const int tk = tok0 + 8 * (r >> 2) + 4 * kq + (r & 3);
+            if (n < w.rows && tk < a.n) {
+                float* o = y + (size_t)tk * w.rows + n;
+                *o = a.add ? *o + v : v;
+            }
+        };
+        if (KS > 1) {
+            if (t) __syncthreads(); /* the previous tile's sums are read */
 #pragma unroll
-            for (int r = 0; r < 16; r++) put(r, acc[r]);
-            return;
+            for (int r = 0; r < 16; r++) red[(wv * 16 + r) * 64 + lane] = acc[t][r];
+            __syncthreads();
         }
+        if (splits == 1) {
+            if (KS == 1) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) put(r, acc[t][r]);
+                continue;
+            }
+            for (int r = wv; r < 16; r += KS) {
+                float v = 0.0f;
+                for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
+                put(r, v);
+            }
+            continue;
+        }
+        /* several splits: this block's sum of the tile into part[], then the last block of the tile adds them */
+        const size_t slot = (size_t)tt * a.tiles + tile0 + tile; /* the tile's counter */
+        float* part = a.part + slot * a.split_max * 1024;
+        /* The sums are stored as agent-scope atomics (written through this XCD's L2 to where every XCD reads);
+           the counter's increment releases them and the last block's acquires them, at agent scope, so the last
+           block reads every split's sums (the workgroup barrier carries thread 0's acquire to the others). */
         for (int r = wv; r < 16; r += KS) {
             float v = 0.0f;
             for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
-            put(r, v);
+            __hip_atomic_store(part + (size_t)sp * 1024 + r * 64 + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        return;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* every wave's stores complete before the barrier */
+        __syncthreads();
+        if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + slot, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+        __syncthreads();
+        if (last) {
+            for (int r = wv; r < 16; r += KS) {
+                float v = 0.0f;
+                for (int u = 0; u < splits; u++)
+                    v += __hip_atomic_load(part + (size_t)u * 1024 + r * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                put(r, v);
+            }
+            if (threadIdx.x == 0) __hip_atomic_store(a.cnt + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
-    /* several splits: this block's sum of the tile into part[], then the last block of the tile adds them */
-    const size_t slot = (size_t)blockIdx.y * a.tiles + tile0 + tile; /* the tile's counter */
-    float* part = a.part + slot * a.split_max * 1024;
-    /* The sums are stored as agent-scope atomics (written through this XCD's L2 to where every XCD reads);
-       the counter's increment releases them and the last block's acquires them, at agent scope, so the last
-       block reads every split's sums (the workgroup barrier carries thread 0's acquire to the others). */
-    for (int r = wv; r < 16; r += KS) {
-        float v = 0.0f;
-        for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
-        __hip_atomic_store(part + (size_t)sp * 1024 + r * 64 + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* every wave's stores complete before the barrier */
-    __syncthreads();
-    if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + slot, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
-    __syncthreads();
-    if (!last) return;
-    for (int r = wv; r < 16; r += KS) {
-        float v = 0.0f;
-        for (int u = 0; u < splits; u++) v += __hip_atomic_load(part + (size_t)u * 1024 + r * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        put(r, v);
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* ---- wide matrices (the LM head): activations staged in LDS ---------------- */
@@ -818,7 +839,10 @@ static hipError_t launch_skinny_exact(const skinny_args& a0, hipStream_t s) {
     }
     if (split_max > 1 && (!a.part || !a.cnt || (size_t)mt * tiles > a.cnt_cap || (size_t)mt * tiles * split_max * 1024 > a.part_cap))
         return hipErrorInvalidValue;
-    skinny_exact_kernel<<<dim3(blocks, mt), 64 * ks, (size_t)ks * 16 * 64 * sizeof(float), s>>>(a);
+    /* many token tiles (a prompt's chunk): each block takes SK_NT of them, the weights loaded once for all */
+    const size_t lds = (size_t)ks * 16 * 64 * sizeof(float);
+    if (mt >= 2 * SK_NT) skinny_exact_kernel<SK_NT><<<dim3(blocks, (mt + SK_NT - 1) / SK_NT), 64 * ks, lds, s>>>(a);
+    else skinny_exact_kernel<1><<<dim3(blocks, mt), 64 * ks, lds, s>>>(a);
     return hipGetLastError();
 }
 
