@@ -88,7 +88,10 @@ __global__ __launch_bounds__(256) void attention_kernel(attn_args a) {
     constexpr int VPL = HD / 64; /* dimensions a lane in the values */
     constexpr int QF4 = HD / 4;  /* float4 of a head */
     constexpr int PS = HD + 4;   /* floats of a (chunk, query head) partial */
-    const int split = blockIdx.x, h = blockIdx.y, row = blockIdx.z;
+    /* blocks go to the eight XCDs in turn by their linear index; the chunk a block takes is rotated by its
+       (head, row) so that the leftover chunks of ragged rows do not all fall on the first XCDs */
+    const int split = (int)((blockIdx.x + blockIdx.y + gridDim.y * blockIdx.z) % gridDim.x);
+    const int h = blockIdx.y, row = blockIdx.z;
     const row_rec rr = a.rows[row];
     const int pos = rr.pos, seq = rr.seq;
     const int n_act = pos / ATTN_CHUNK + 1;
@@ -326,7 +329,10 @@ typedef float at_f4 __attribute__((ext_vector_type(4)));
 template <int G>
 __global__ __launch_bounds__(256, ATTN_MMA_OCC) void attention_mma_kernel(attn_args a) {
     constexpr int HD = 128, QF4 = HD / 4, PS = HD + 4;
-    const int split = blockIdx.x, h = blockIdx.y, row = blockIdx.z;
+    /* blocks go to the eight XCDs in turn by their linear index; the chunk a block takes is rotated by its
+       (head, row) so that the leftover chunks of ragged rows do not all fall on the first XCDs */
+    const int split = (int)((blockIdx.x + blockIdx.y + gridDim.y * blockIdx.z) % gridDim.x);
+    const int h = blockIdx.y, row = blockIdx.z;
     const row_rec rr = a.rows[row];
     const int pos = rr.pos, seq = rr.seq;
     const int n_act = pos / ATTN_CHUNK + 1;
