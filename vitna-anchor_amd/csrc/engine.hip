@@ -33,6 +33,11 @@
 /* The most rows a pass takes (the reference's MOE_ROWS, model_cuda.cu:197): model.c runs a prompt in chunks of
    this many. Scratch for this many rows is allocated with the model. */
 #define ROWS_MAX 1024
+/* passes of this many rows or more, of a model whose experts are resident, take the grouped kernels on tiles of
+   32 pairs (launch_gsx) instead of four (launch_gmma_in / _down). At top-8 of 128 experts (a 4096-token prompt
+   in chunks, same box): 96-row chunks 961 -> 781 ms, 128 903 -> 707, 256 635 -> 433, 1024 415 -> 250; the
+   32 rows of a ragged step (two pairs an expert) 12.55 -> 17.74 ms, so they keep the four-pair tiles */
+#define GSX_ROWS 64
 /* With the model's gpu_fast, a pass of at least this many rows runs its experts as the bf16 matrix-core grouped GEMM
    of the prefill (the reference's FAST_ROWS, model_cuda.cu:204); smaller passes keep the exact kernels. */
 #define FAST_ROWS 64
@@ -52,6 +57,8 @@ struct dlayer {
     float *attn_norm, *mlp_norm, *q_norm, *k_norm;
     float* router;
     qmat gate, up, down;
+    /* the experts' copies tiled for the crowded passes' grouped kernels (launch_gsx), or null */
+    const uint8_t *sx_gate, *sx_up, *sx_down;
 };
 
 /* A prefill's working buffers for n rows (everything but the rows themselves), carved from one region by
@@ -103,6 +110,12 @@ struct vitna_cuda_model {
     size_t sk_part_cap, sk_cnt_cap;
     uint16_t *gm_xs, *gm_as;    /* the grouped experts' split activations: [ROWS_MAX][2H], [ROWS_MAX * K][2I] */
     float *gm_xsum, *gm_asum;   /* and their sums over runs of 16 or more columns */
+    /* the crowded passes' grouped experts (launch_gsx), made with the tiled copies: tile offsets and experts,
+       operand images and sums of the pairs' rows and of the SwiGLU output, that output */
+    int *gsx_toff, *gsx_te;
+    uint32_t *gsx_img_in, *gsx_img_act;
+    uint16_t *gsx_s32, *gsx_s16;
+    float* gsx_act;
     bool rows_shared_seq;       /* the pass's rows include two of one sequence (attention prepares first) */
     bool rows_one_seq;          /* every row of the pass is of one sequence (a prompt's chunk: tiles of rows) */
     /* the rows step's captured graphs, a few kept (least recently used replaced): one a pass shape */
@@ -389,6 +402,28 @@ static bool ensure_tiled(vitna_cuda_model* g, char* err, size_t err_len) {
                 HIP_TRY(launch_gmma_tile(*sets[i], g->E, t, g->stream), "tiling the experts");
                 HIP_TRY(hipStreamSynchronize(g->stream), "tiling the experts");
                 sets[i]->tiled = t;
+            }
+        }
+        if (!g->ec.on && g->E <= ROUTE_E_MAX && gsx_fits(d.gate, d.up, d.down)) {
+            const qmat* sets[3] = {&d.gate, &d.up, &d.down};
+            const uint8_t** dst[3] = {&d.sx_gate, &d.sx_up, &d.sx_down};
+            for (int i = 0; i < 3; i++) {
+                uint8_t* t;
+                if (!dalloc(g, &t, gsx_tiled_bytes(*sets[i], g->E), "the experts' copy for crowded passes", err, err_len)) return false;
+                HIP_TRY(launch_gsx_tile(*sets[i], g->E, t, g->stream), "tiling the experts");
+                HIP_TRY(hipStreamSynchronize(g->stream), "tiling the experts");
+                *dst[i] = t;
+            }
+            if (!g->gsx_te) {
+                const size_t T = (size_t)gsx_max_tiles(ROWS_MAX, g->K, g->E), H = g->H, I = d.gate.rows, W = std::max(H, I);
+                if (!(dalloc(g, &g->gsx_toff, (g->E + 1) * sizeof(int), "scratch", err, err_len) &&
+                      dalloc(g, &g->gsx_te, T * sizeof(int), "scratch", err, err_len) &&
+                      dalloc(g, &g->gsx_img_in, 32 * T * H * 4, "scratch", err, err_len) &&
+                      dalloc(g, &g->gsx_img_act, 32 * T * I * 4, "scratch", err, err_len) &&
+                      dalloc(g, &g->gsx_s32, T * (W / 256) * 1536, "scratch", err, err_len) &&
+                      dalloc(g, &g->gsx_s16, T * (W / 128) * 1536, "scratch", err, err_len) &&
+                      dalloc(g, &g->gsx_act, 32 * T * I * 4, "scratch", err, err_len)))
+                    return false;
             }
         }
     }
@@ -2115,6 +2150,21 @@ static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n, bo
     if (!rt) rt = g->rt;
     hipError_t e = launch_group(rt, n, g->E, g->K, ROWS_MAX, g->grp_count, g->grp_pairs, g->stream);
     if (e != hipSuccess) return e;
+    if (n >= GSX_ROWS && d.sx_gate) {
+        /* a crowded pass: tiles of 32 pairs of one expert */
+        gsx_args x{};
+        x.gate = d.gate; x.gate.tiled = d.sx_gate;
+        x.up = d.up; x.up.tiled = d.sx_up;
+        x.down = d.down; x.down.tiled = d.sx_down;
+        x.xn = g->xn; x.rt = rt; x.count = g->grp_count; x.pairs = g->grp_pairs;
+        x.E = g->E; x.K = g->K; x.cap = ROWS_MAX; x.n = n;
+        x.toff = g->gsx_toff; x.te = g->gsx_te; x.max_tiles = gsx_max_tiles(ROWS_MAX, g->K, g->E);
+        x.img_in = g->gsx_img_in; x.img_act = g->gsx_img_act; x.s32 = g->gsx_s32; x.s16 = g->gsx_s16;
+        x.act = g->gsx_act; x.ypart = g->ypart;
+        e = launch_gsx(x, g->stream);
+        if (e == hipSuccess && !defer_sum) e = launch_reduce_rows(g->ypart, g->x, n, g->K, g->H, g->stream);
+        return e;
+    }
     /* every expert set check_shapes accepts (quantized, widths multiples of 256) fits the matrix-core kernels */
     if (!gmma_fits(d.gate, d.up, d.down)) return hipErrorInvalidValue;
     if (!split_done) e = launch_gmma_split(g->xn, n, g->H, g->H, gmma_gran(d.gate.dtype), g->gm_xs, g->gm_xsum, g->stream);

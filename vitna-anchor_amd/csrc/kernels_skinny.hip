@@ -879,3 +879,248 @@ hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
     else skinny_kernel<1><<<grid, 64 * ks, lds, s>>>(a);
     return hipGetLastError();
 }
+
+/* ---- grouped experts of crowded passes ------------------------------------ */
+
+/*
+ * A pass whose experts hold many pairs each (a prompt's chunk: 1024 rows of top-8 over 128 experts, 64 pairs an
+ * expert) runs its experts with the exact arithmetic above on tiles of 32 pairs of one expert, instead of the
+ * four-pair tiles of kernels_gmma.hip, so that an expert's weights are read once per 32 pairs rather than once
+ * per four. The pairs of each expert (launch_group's lists) are cut into tiles; tile t (of one expert, te[t])
+ * is the virtual token tile t of the operand images, which a gather writes from the normalized rows. Gate and up
+ * run in one block over the same activations; the block writes the SwiGLU output of its 32 x 32 (pair, row)
+ * tile in fp32, whose images the same gather writes for down; down multiplies by the pair's weight into ypart,
+ * as kernels_gmma.hip does. The weights come from a copy tiled as the dense matrices' are, experts back to back
+ * (expert e's 32-row tile x is tile e I / 32 + x).
+ */
+
+/* One block a (expert, 32-row tile, superblock): the expert's planes as a matrix of its own. */
+__global__ void gsx_tile_kernel(qmat m, int tiles, uint8_t* __restrict__ dst) {
+    const int S = m.cols / 256, b = blockIdx.x % S, tile = (blockIdx.x / S) % tiles, e = blockIdx.x / (S * tiles);
+    qmat me = m;
+#pragma unroll
+    for (int i = 0; i < 4; i++) me.p[i] = m.p[i] ? m.p[i] + (size_t)e * m.estride[i] : nullptr;
+    const int tb = (int)tile_bytes(m.dtype);
+    uint8_t* out = dst + (size_t)blockIdx.x * tb;
+    for (int o = threadIdx.x; o < tb; o += blockDim.x) out[o] = (uint8_t)tile_src(me, tile, b, o);
+}
+
+size_t gsx_tiled_bytes(const qmat& m, int n_experts) {
+    return tile_bytes(m.dtype) * (size_t)(m.rows / 32) * (m.cols / 256) * n_experts;
+}
+
+hipError_t launch_gsx_tile(const qmat& m, int n_experts, uint8_t* dst, hipStream_t s) {
+    if (!tile_bytes(m.dtype) || m.cols % 256 || m.rows % 32 || n_experts < 1) return hipErrorInvalidValue;
+    const int tiles = m.rows / 32;
+    gsx_tile_kernel<<<n_experts * tiles * (m.cols / 256), 256, 0, s>>>(m, tiles, dst);
+    return hipGetLastError();
+}
+
+bool gsx_fits(const qmat& gate, const qmat& up, const qmat& down) {
+    auto dt = [](int d) { return d == VITNA_DTYPE_Q8_0 || d == VITNA_DTYPE_Q4_K || d == VITNA_DTYPE_Q6_K; };
+    const int H = gate.cols, I = gate.rows;
+    /* whole superblocks, at most eight a row (one block's waves), whole 32-row tiles */
+    return dt(gate.dtype) && up.dtype == gate.dtype && dt(down.dtype) && up.rows == I && up.cols == H && down.rows == H &&
+           down.cols == I && H % 256 == 0 && I % 256 == 0 && H <= 2048 && I <= 2048;
+}
+
+int gsx_max_tiles(int n, int K, int E) { return (n * K + 31) / 32 + E; }
+
+/* Tile offsets of the experts' pair lists (toff[E + 1]) and the expert of each tile (te[max_tiles], -1 past the
+   last): one block, the first wave scanning the tile counts 64 experts at a time. */
+__global__ __launch_bounds__(256) void gsx_plan_kernel(const int* __restrict__ count, int E, int* __restrict__ toff,
+                                                       int* __restrict__ te, int max_tiles) {
+    __shared__ int off[ROUTE_E_MAX + 1];
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid < 64) {
+        int run = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + lane;
+            const int c = e < E ? (count[e] + 31) / 32 : 0;
+            int v = c; /* inclusive scan across the wave */
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int o = __shfl_up(v, d, WAVE);
+                if (lane >= d) v += o;
+            }
+            if (e < E) off[e] = run + v - c;
+            run += __shfl(v, 63, WAVE);
+        }
+        if (lane == 0) off[E] = run;
+    }
+    __syncthreads();
+    for (int e = tid; e <= E; e += blockDim.x) toff[e] = off[e];
+    for (int e = tid; e < E; e += blockDim.x)
+        for (int t = off[e]; t < off[e + 1]; t++) te[t] = e;
+    for (int t = off[E] + tid; t < max_tiles; t += blockDim.x) te[t] = -1;
+}
+
+/* The operand images (one column order) and group sums of the virtual token tiles: block (b, t) takes superblock
+   b of tile t. With pairs, token l of tile t is pair toff-relative index 32 (t - toff[e]) + l of expert te[t]
+   (past its count: the last pair again), read from row pair / ROUTE_K_MAX of x; without, it is row 32 t + l of x. */
+__global__ void gsx_image_kernel(const float* __restrict__ x, int K, const int* __restrict__ pairs, const int* __restrict__ count,
+                                 int cap, const int* __restrict__ toff, const int* __restrict__ te, u32x4* __restrict__ imga,
+                                 u32x4* __restrict__ imgb, uint16_t* __restrict__ s32, uint16_t* __restrict__ s16) {
+    const int b = blockIdx.x, t = blockIdx.y;
+    const int e = te[t];
+    if (e < 0) return;
+    const int j0 = 32 * (t - toff[e]), c = count[e];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int item = threadIdx.x + 256 * j, l = item >> 5, c8 = 32 * b + (item & 31);
+        const int row = 32 * t + l;
+        size_t src_row = (size_t)row;
+        if (pairs) src_row = (size_t)(pairs[(size_t)e * cap + min(j0 + l, c - 1)] / ROUTE_K_MAX);
+        const float4* src = reinterpret_cast<const float4*>(x + src_row * K + 8 * c8);
+        const float4 v0 = src[0], v1 = src[1];
+        const float ev[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        u32x4 vh, vl;
+        float sum;
+        img_split8(ev, vh, vl, sum);
+        img_put(imga, imgb, row, K, c8, vh, vl);
+        const float t16 = sum + __shfl_xor(sum, 1, WAVE);
+        const float t32 = t16 + __shfl_xor(t16, 2, WAVE);
+        if (!(c8 & 1)) img_sum16(s16, row, K, c8 >> 1, t16);
+        if (!(c8 & 3)) img_sum32(s32, row, K, c8 >> 2, t32);
+    }
+}
+
+/* The KS waves' tiles added in wave order through red ([KS][16][64]); wave wv returns the sums of accumulators
+   wv, wv + KS, ... in out[0], out[1], ... */
+__device__ __forceinline__ void gsx_reduce(const f32x16& acc, float* red, int KS, int wv, int lane, float out[16]) {
+    __syncthreads(); /* red is free */
+#pragma unroll
+    for (int r = 0; r < 16; r++) red[(wv * 16 + r) * 64 + lane] = acc[r];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int r = wv + i * KS;
+        if (r < 16) {
+            float v = 0.0f;
+            for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
+            out[i] = v;
+        }
+    }
+}
+
+/* act[32 t + token][32 x + row] = silu(gate . x) * (up . x) for virtual tile t (expert te[t]) and 32-row tile x
+   (blockIdx.x) of the expert's I rows: KS = H / 256 waves, wave wv on superblock wv of both matrices, each unit's
+   activations loaded once for both. */
+template <int DT>
+__global__ __launch_bounds__(512) void gsx_in_kernel(qmat gate, qmat up, skinny_args sa, const int* __restrict__ te,
+                                                     float* __restrict__ act) {
+    extern __shared__ float red[];
+    const int t = blockIdx.y, e = te[t];
+    if (e < 0) return;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, KS = blockDim.x >> 6, kq = lane >> 5, l32 = lane & 31;
+    const int H = gate.cols, I = gate.rows, x = blockIdx.x, tile = e * (I / 32) + x, b = wv;
+    f32x16 ag = {}, au = {};
+    {
+        sx_w<DT> Wg, Wu;
+        sx_load_w<DT>(gate, tile, b, lane, Wg);
+        sx_load_w<DT>(up, tile, b, lane, Wu);
+        float cg[8], cu[8];
+        sx_a x0, x1;
+        sx_load_a<DT, 0>(sa, t, H, b, lane, x0);
+        sx_load_a<DT, 1>(sa, t, H, b, lane, x1);
+        __builtin_amdgcn_sched_barrier(0);
+        sx_compute<DT, 0>(Wg, x0, kq, ag, cg);
+        sx_compute<DT, 0>(Wu, x0, kq, au, cu);
+        sx_load_a<DT, 2>(sa, t, H, b, lane, x0);
+        __builtin_amdgcn_sched_barrier(0);
+        sx_compute<DT, 1>(Wg, x1, kq, ag, cg);
+        sx_compute<DT, 1>(Wu, x1, kq, au, cu);
+        sx_load_a<DT, 3>(sa, t, H, b, lane, x1);
+        __builtin_amdgcn_sched_barrier(0);
+        sx_compute<DT, 2>(Wg, x0, kq, ag, cg);
+        sx_compute<DT, 2>(Wu, x0, kq, au, cu);
+        sx_compute<DT, 3>(Wg, x1, kq, ag, cg);
+        sx_compute<DT, 3>(Wu, x1, kq, au, cu);
+    }
+    float g[16], u[16];
+    gsx_reduce(ag, red, KS, wv, lane, g);
+    gsx_reduce(au, red, KS, wv, lane, u);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int r = wv + i * KS;
+        if (r < 16) {
+            /* accumulator r: token 8 (r / 4) + 4 kq + r % 4 of the tile, row l32 of the tile */
+            const int tok = 8 * (r >> 2) + 4 * kq + (r & 3);
+            const float v = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+            act[(size_t)(32 * t + tok) * I + 32 * x + l32] = v;
+        }
+    }
+}
+
+/* ypart[(row K + slot) H + n] = w_slot (down_e[n] . act[pair]) for the pairs of virtual tile t (past the expert's
+   count: none written) and 32-row tile x of the H rows: KS = I / 256 waves, wave wv on superblock wv. */
+template <int DT>
+__global__ __launch_bounds__(512) void gsx_down_kernel(qmat down, skinny_args sa, const int* __restrict__ te,
+                                                       const int* __restrict__ toff, const int* __restrict__ count,
+                                                       const int* __restrict__ pairs, int cap, const route_out* __restrict__ rt,
+                                                       int K, float* __restrict__ ypart) {
+    extern __shared__ float red[];
+    const int t = blockIdx.y, e = te[t];
+    if (e < 0) return;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, KS = blockDim.x >> 6, kq = lane >> 5, l32 = lane & 31;
+    const int H = down.rows, I = down.cols, x = blockIdx.x;
+    f32x16 acc[1] = {f32x16{}};
+    sx_superblock<DT, 1>(sa, down, e * (H / 32) + x, t, t + 1, wv, lane, acc);
+    float v[16];
+    gsx_reduce(acc[0], red, KS, wv, lane, v);
+    const int j0 = 32 * (t - toff[e]), c = count[e];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int r = wv + i * KS;
+        if (r < 16) {
+            const int j = j0 + 8 * (r >> 2) + 4 * kq + (r & 3);
+            if (j < c) {
+                const int p = pairs[(size_t)e * cap + j], row = p / ROUTE_K_MAX, slot = p % ROUTE_K_MAX;
+                ypart[((size_t)row * K + slot) * H + 32 * x + l32] = rt[row].weights[slot] * v[i];
+            }
+        }
+    }
+    (void)I;
+}
+
+hipError_t launch_gsx(const gsx_args& a, hipStream_t s) {
+    if (!gsx_fits(a.gate, a.up, a.down) || !a.gate.tiled || !a.up.tiled || !a.down.tiled || a.K < 1 || a.K > ROUTE_K_MAX ||
+        a.E < 1 || a.E > ROUTE_E_MAX || a.n < 1 || a.cap < a.n || a.max_tiles < gsx_max_tiles(a.n, a.K, a.E))
+        return hipErrorInvalidValue;
+    const int H = a.gate.cols, I = a.gate.rows, T = gsx_max_tiles(a.n, a.K, a.E);
+    gsx_plan_kernel<<<1, 256, 0, s>>>(a.count, a.E, a.toff, a.te, T);
+    const bool in_b = a.gate.dtype == VITNA_DTYPE_Q6_K, dn_b = a.down.dtype == VITNA_DTYPE_Q6_K;
+    u32x4* ii = reinterpret_cast<u32x4*>(a.img_in);
+    u32x4* ia = reinterpret_cast<u32x4*>(a.img_act);
+    gsx_image_kernel<<<dim3(H / 256, T), 256, 0, s>>>(a.xn, H, a.pairs, a.count, a.cap, a.toff, a.te, in_b ? nullptr : ii,
+                                                      in_b ? ii : nullptr, a.s32, a.s16);
+    skinny_args si{};
+    si.img[0] = si.img[1] = a.img_in;
+    si.s32 = reinterpret_cast<const uint32_t*>(a.s32);
+    si.s16 = reinterpret_cast<const uint32_t*>(a.s16);
+    const int ksi = H / 256, ksd = I / 256;
+    const dim3 gi(I / 32, T), gd(H / 32, T);
+    switch (a.gate.dtype) {
+    case VITNA_DTYPE_Q4_K: gsx_in_kernel<VITNA_DTYPE_Q4_K><<<gi, 64 * ksi, ksi * 4096, s>>>(a.gate, a.up, si, a.te, a.act); break;
+    case VITNA_DTYPE_Q6_K: gsx_in_kernel<VITNA_DTYPE_Q6_K><<<gi, 64 * ksi, ksi * 4096, s>>>(a.gate, a.up, si, a.te, a.act); break;
+    default: gsx_in_kernel<VITNA_DTYPE_Q8_0><<<gi, 64 * ksi, ksi * 4096, s>>>(a.gate, a.up, si, a.te, a.act); break;
+    }
+    gsx_image_kernel<<<dim3(I / 256, T), 256, 0, s>>>(a.act, I, nullptr, a.count, a.cap, a.toff, a.te, dn_b ? nullptr : ia,
+                                                      dn_b ? ia : nullptr, a.s32, a.s16);
+    skinny_args sd{};
+    sd.img[0] = sd.img[1] = a.img_act;
+    sd.s32 = reinterpret_cast<const uint32_t*>(a.s32);
+    sd.s16 = reinterpret_cast<const uint32_t*>(a.s16);
+    switch (a.down.dtype) {
+    case VITNA_DTYPE_Q4_K:
+        gsx_down_kernel<VITNA_DTYPE_Q4_K><<<gd, 64 * ksd, ksd * 4096, s>>>(a.down, sd, a.te, a.toff, a.count, a.pairs, a.cap, a.rt, a.K, a.ypart);
+        break;
+    case VITNA_DTYPE_Q6_K:
+        gsx_down_kernel<VITNA_DTYPE_Q6_K><<<gd, 64 * ksd, ksd * 4096, s>>>(a.down, sd, a.te, a.toff, a.count, a.pairs, a.cap, a.rt, a.K, a.ypart);
+        break;
+    default:
+        gsx_down_kernel<VITNA_DTYPE_Q8_0><<<gd, 64 * ksd, ksd * 4096, s>>>(a.down, sd, a.te, a.toff, a.count, a.pairs, a.cap, a.rt, a.K, a.ypart);
+        break;
+    }
+    return hipGetLastError();
+}

@@ -37,17 +37,17 @@ __device__ __forceinline__ void img_split8(const float e[8], u32x4& vh, u32x4& v
     sum = s;
 }
 
-/* columns 8 c8 .. 8 c8 + 7 of row `row` (a row K columns wide) into both images */
+/* columns 8 c8 .. 8 c8 + 7 of row `row` (a row K columns wide) into both images (or the one that is not null) */
 __device__ __forceinline__ void img_put(u32x4* imga, u32x4* imgb, int row, int K, int c8, const u32x4& vh, const u32x4& vl) {
     const int tt = row >> 5, l = row & 31, b = c8 >> 5, c = 8 * (c8 & 31);
     const size_t base = ((size_t)tt * (K / 256) + b) * 2048;
-    {
+    if (imga) {
         const int U = c >> 6, r = c & 63, i = ((r >> 5) << 1) | ((r >> 3) & 1), kq = (r >> 4) & 1;
         const size_t q = base + (size_t)((U * 4 + i) * 2) * 64 + l + 32 * kq;
         imga[q] = vh;
         imga[q + 64] = vl;
     }
-    {
+    if (imgb) {
         const int r = c & 127, U = 2 * (c >> 7) + ((r >> 5) & 1), i = ((r >> 4) & 1) + 2 * (r >> 6), kq = (r >> 3) & 1;
         const size_t q = base + (size_t)((U * 4 + i) * 2) * 64 + l + 32 * kq;
         imgb[q] = vh;

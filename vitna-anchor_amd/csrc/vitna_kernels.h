@@ -312,6 +312,30 @@ int gmma_gran(int dtype);
 hipError_t launch_gmma_split(const float* x, int n, int K, int xstride, int gran, uint16_t* xs, float* sums, hipStream_t s);
 hipError_t launch_gmma_in(const gmma_args& a, hipStream_t s);
 hipError_t launch_gmma_down(const gmma_args& a, hipStream_t s);
+/* The grouped experts of a crowded pass (kernels_skinny.hip): tiles of 32 pairs of one expert on the exact
+   bf16 arithmetic of the multi-row projections. gate, up and down carry in .tiled their per-expert tiled copies
+   (gsx_tiled_bytes, launch_gsx_tile); the pairs are launch_group's lists. Leaves ypart as launch_gmma_down does. */
+struct gsx_args {
+    qmat gate, up, down;
+    const float* xn;       /* the normalized rows [n][H] */
+    const route_out* rt;   /* [n] */
+    const int* count;      /* [E] */
+    const int* pairs;      /* [E][cap] */
+    int E, K, cap, n;
+    int *toff, *te;        /* [E + 1], [max_tiles] */
+    int max_tiles;         /* at least gsx_max_tiles(n, K, E) */
+    uint32_t* img_in;      /* operand images of the tiles' rows: 32 max_tiles x H x 4 bytes */
+    uint32_t* img_act;     /* of the SwiGLU output: 32 max_tiles x I x 4 bytes */
+    uint16_t *s32, *s16;   /* group sums: max_tiles x (max(H, I) / 256) x 1536 bytes, and twice that */
+    float* act;            /* the SwiGLU output [32 max_tiles][I] */
+    float* ypart;          /* [n][K][H] */
+};
+bool gsx_fits(const qmat& gate, const qmat& up, const qmat& down);
+int gsx_max_tiles(int n, int K, int E);
+size_t gsx_tiled_bytes(const qmat& m, int n_experts);
+hipError_t launch_gsx_tile(const qmat& m, int n_experts, uint8_t* dst, hipStream_t s);
+hipError_t launch_gsx(const gsx_args& a, hipStream_t s);
+
 /* x[row] += the row's K outputs in ypart, added in slot order. */
 hipError_t launch_reduce_rows(const float* ypart, float* x, int n, int K, int H, hipStream_t s);
 
