@@ -26,6 +26,9 @@
  *     each slice, as the activations' lanes do for token lane % 32.
  * Both stay within 1e-3 of the CPU checker; each projection alone is held to
  * 2e-5 of max |ref| against the widened matrix in float64.
+ *
+ * The same exact arithmetic serves the grouped experts of crowded passes (64
+ * rows and more) on tiles of 32 pairs of one expert (launch_gsx, at the end).
  */
 
 #include "vitna_kernels.h"
@@ -892,6 +895,10 @@ hipError_t launch_skinny(const skinny_args& a, hipStream_t s) {
  * tile in fp32, whose images the same gather writes for down; down multiplies by the pair's weight into ypart,
  * as kernels_gmma.hip does. The weights come from a copy tiled as the dense matrices' are, experts back to back
  * (expert e's 32-row tile x is tile e I / 32 + x).
+ *
+ * Reference counterparts: experts_in_rows_kernel model_cuda.cu:2071 and experts_down_rows_kernel
+ * model_cuda.cu:2101; the CPU arithmetic checked against is mixture_of_experts engine/src/model.c:745-761 and
+ * vitna_silu_mul engine/src/ops.c:283, one row at a time.
  */
 
 /* One block a (expert, 32-row tile, superblock): the expert's planes as a matrix of its own. */
