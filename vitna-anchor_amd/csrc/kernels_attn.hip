@@ -543,16 +543,40 @@ hipError_t launch_attention(const attn_args& a, hipStream_t s) {
    The per-row kernels read a chunk's keys and values once for every row, so a prompt pass of 1024 rows of one
    sequence reads each chunk up to 1024 times (from the memory-side cache; the L2 of an XCD holds 4 MB of a layer's
    16 MB). Here a block takes one kv head for a tile of TQ = 4 * 16 / G rows and loops over the chunks up to the
-   tile's last position: each chunk's keys and values go to LDS once (64 KB, float4 chunks XOR-swizzled by position
-   so that the fragment reads do not share banks), and wave w takes 16 query columns, RW = 16 / G rows of the tile
-   times the G heads, against the chunk's 64 positions: scores on v_mfma_f32_16x16x4_f32 (lane (c, kq) multiplies
-   dimensions 32 kq .. 32 kq + 31 of key row c and of column c), each row masked to the positions up to its own,
-   then P . V as the decode kernel takes it. The queries come prepared (launch_attention_prepare). The scores of
-   each chunk fold into a running maximum and sum per column, the values into O rescaled as the maximum grows,
-   and the block writes att itself (O / sum): no chunk leaves a partial and no merge runs. A chunk's keys and
-   values are requested before the barrier that frees the LDS of the previous one; the other block of the CU
-   covers the wait. */
-#define RUN_CHUNKS 32 /* float4 chunks of a head's 128 dimensions */
+   tile's last position: each chunk's keys and values go to LDS once (64 KB), and wave w takes 16 query columns,
+   RW = 16 / G rows of the tile times the G heads, against the chunk's 64 positions, each row masked to the
+   positions up to its own. The queries come prepared (launch_attention_prepare). The scores of each chunk fold
+   into a running maximum and sum per column, the values into O rescaled as the maximum grows, and the block
+   writes att itself (O / sum): no chunk leaves a partial and no merge runs. A chunk's keys and values are
+   requested before the barrier that frees the LDS of the previous one; the other block of the CU covers the
+   wait. Passes of more than 64 rows reach it (the exact-rows limit), so it is held to 1e-3, not to a step's
+   bits.
+
+   The products run on the bf16 matrix cores. Each operand is split into bf16 hi + lo (lo the rounding of what hi
+   leaves) and each product taken as hi*hi + hi*lo + lo*hi on v_mfma_f32_16x16x32_bf16, summed in fp32: about
+   2^-15 of |a||b| a product against fp32's 2^-24, at a sixteenth of the fp32 unit's cycles an operation. (The
+   same loop on v_mfma_f32_16x16x4_f32 took a 4096-token prompt 255 ms exact and 212 ms fast, against 226 and 183
+   here, same box, twice each.) The keys go to LDS split, position-major (16-byte chunks of eight dimensions,
+   XOR-swizzled by position); the values split and transposed, dimension-major (8-byte chunks of four positions,
+   swizzled by dimension), so that a lane's eight positions of one dimension are two reads. A thread of the fetch
+   holds four consecutive positions of four dimensions, which it transposes in registers. The scores come out with
+   lane (c16, kq) holding position 16 pt + 4 kq + i of column c16; the weighted values take positions
+   16 pt + 4 kq + i of pt in {2 s, 2 s + 1} as the eight k-slots of MFMA s, on both operands. */
+typedef __bf16 fl_bf8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ uint32_t fl_pack(__bf16 a, __bf16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+/* four floats as bf16 hi and lo, packed in order */
+__device__ __forceinline__ void fl_split4(float x0, float x1, float x2, float x3, uint2& hi, uint2& lo) {
+    const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1, h2 = (__bf16)x2, h3 = (__bf16)x3;
+    hi = make_uint2(fl_pack(h0, h1), fl_pack(h2, h3));
+    lo = make_uint2(fl_pack((__bf16)(x0 - (float)h0), (__bf16)(x1 - (float)h1)),
+                    fl_pack((__bf16)(x2 - (float)h2), (__bf16)(x3 - (float)h3)));
+}
+__device__ __forceinline__ fl_bf8 fl_join(uint2 a, uint2 b) { return __builtin_bit_cast(fl_bf8, u32x4{a.x, a.y, b.x, b.y}); }
+#define FL_MMA(A, B, C) __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, C, 0, 0, 0)
+
 template <int G>
 __global__ __launch_bounds__(256, 2) void attention_flash_kernel(attn_args a) {
     constexpr int HD = 128, RW = 16 / G, TQ = 4 * RW;
@@ -565,29 +589,39 @@ __global__ __launch_bounds__(256, 2) void attention_flash_kernel(attn_args a) {
     const int seq = a.rows[r_first].seq, kv_dim = a.n_kv * HD;
     const float* kc = a.k_cache + (size_t)seq * a.seq_stride;
     const float* vc = a.v_cache + (size_t)seq * a.seq_stride;
-    __shared__ __attribute__((aligned(16))) float sk[ATTN_CHUNK * HD];
-    __shared__ __attribute__((aligned(16))) float sv[ATTN_CHUNK * HD];
+    /* keys [position][16 chunks of 8 dimensions], values [dimension][16 chunks of 4 positions], hi and lo */
+    __shared__ __attribute__((aligned(16))) uint32_t skh[64 * 64], skl[64 * 64];
+    __shared__ __attribute__((aligned(16))) uint32_t svh[128 * 32], svl[128 * 32];
 
     const int rr = r_first + wave * RW + c16 / G, g = c16 % G;
     const bool colv = rr < r_end;
     const int prow = colv ? a.rows[rr].pos : -1;
-    float qv[32];
+    /* the column's query, scaled: dimensions 32 s + 8 kq .. + 7 as the B operand of step s */
+    fl_bf8 qh[4], ql[4];
     {
         const float sc = 1.0f / sqrtf((float)HD);
         const float4* q4 = reinterpret_cast<const float4*>(a.q_raw + (size_t)(colv ? rr : r_first) * a.n_heads * HD +
-                                                           (size_t)(h * G + g) * HD + 32 * kq);
+                                                           (size_t)(h * G + g) * HD);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 v = colv ? q4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-            qv[4 * i] = v.x * sc; qv[4 * i + 1] = v.y * sc; qv[4 * i + 2] = v.z * sc; qv[4 * i + 3] = v.w * sc;
+        for (int s = 0; s < 4; s++) {
+            const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 v0 = colv ? q4[8 * s + 2 * kq] : z, v1 = colv ? q4[8 * s + 2 * kq + 1] : z;
+            uint2 h0, l0, h1, l1;
+            fl_split4(v0.x * sc, v0.y * sc, v0.z * sc, v0.w * sc, h0, l0);
+            fl_split4(v1.x * sc, v1.y * sc, v1.z * sc, v1.w * sc, h1, l1);
+            qh[s] = fl_join(h0, h1);
+            ql[s] = fl_join(l0, l1);
         }
     }
+    /* a thread's fetch: positions 32 (i / 4) + 4 pg + i % 4 of the chunk, dimensions 4 cc .. 4 cc + 3 (a wave's
+       load is two whole 512-byte rows) */
+    const int pg = tid >> 5, cc = tid & 31;
     float4 kr[8], vr[8];
     auto fetch = [&](int c) {
         const int t0 = c * ATTN_CHUNK;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int idx = tid + 256 * i, p = idx >> 5, cc = idx & 31, pos = t0 + p;
+            const int p = 32 * (i >> 2) + 4 * pg + (i & 3), pos = t0 + p;
             const bool ok = pos <= pmax;
             const size_t at = (size_t)(ok ? pos : 0) * kv_dim + (size_t)h * HD + 4 * cc;
             kr[i] = ok ? *reinterpret_cast<const float4*>(kc + at) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -603,9 +637,29 @@ __global__ __launch_bounds__(256, 2) void attention_flash_kernel(attn_args a) {
         __syncthreads(); /* the previous chunk's fragment reads are done */
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int idx = tid + 256 * i, p = idx >> 5, cc = idx & 31, pc = cc ^ (p & 31);
-            reinterpret_cast<float4*>(sk)[p * RUN_CHUNKS + pc] = kr[i];
-            reinterpret_cast<float4*>(sv)[p * RUN_CHUNKS + pc] = vr[i];
+            const int p = 32 * (i >> 2) + 4 * pg + (i & 3);
+            uint2 hh, ll;
+            fl_split4(kr[i].x, kr[i].y, kr[i].z, kr[i].w, hh, ll);
+            const int ka = (p * 16 + ((cc >> 1) ^ (p & 15))) * 4 + 2 * (cc & 1);
+            *reinterpret_cast<uint2*>(&skh[ka]) = hh;
+            *reinterpret_cast<uint2*>(&skl[ka]) = ll;
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int pc = 8 * q + pg; /* the chunk of positions 32 q + 4 pg .. + 3 */
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const float4 *v = vr + 4 * q;
+                const float x0 = d == 0 ? v[0].x : d == 1 ? v[0].y : d == 2 ? v[0].z : v[0].w;
+                const float x1 = d == 0 ? v[1].x : d == 1 ? v[1].y : d == 2 ? v[1].z : v[1].w;
+                const float x2 = d == 0 ? v[2].x : d == 1 ? v[2].y : d == 2 ? v[2].z : v[2].w;
+                const float x3 = d == 0 ? v[3].x : d == 1 ? v[3].y : d == 2 ? v[3].z : v[3].w;
+                uint2 hh, ll;
+                fl_split4(x0, x1, x2, x3, hh, ll);
+                const int dim = 4 * cc + d, va = (dim * 16 + (pc ^ (dim & 15))) * 2;
+                *reinterpret_cast<uint2*>(&svh[va]) = hh;
+                *reinterpret_cast<uint2*>(&svl[va]) = ll;
+            }
         }
         __syncthreads();
         const int t0 = c * ATTN_CHUNK;
@@ -615,12 +669,13 @@ __global__ __launch_bounds__(256, 2) void attention_flash_kernel(attn_args a) {
             const int p = 16 * pt + c16;
             at_f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const float4 k4 = reinterpret_cast<const float4*>(sk)[p * RUN_CHUNKS + ((8 * kq + q) ^ (p & 31))];
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qv[4 * q], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qv[4 * q + 1], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qv[4 * q + 2], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qv[4 * q + 3], acc, 0, 0, 0);
+            for (int s = 0; s < 4; s++) {
+                const int ka = (p * 16 + ((4 * s + kq) ^ (p & 15))) * 4;
+                const fl_bf8 kh = *reinterpret_cast<const fl_bf8*>(&skh[ka]);
+                const fl_bf8 kl = *reinterpret_cast<const fl_bf8*>(&skl[ka]);
+                acc = FL_MMA(kh, qh[s], acc);
+                acc = FL_MMA(kh, ql[s], acc);
+                acc = FL_MMA(kl, qh[s], acc);
             }
             S[pt] = acc;
         }
@@ -635,7 +690,6 @@ __global__ __launch_bounds__(256, 2) void attention_flash_kernel(attn_args a) {
             }
         m = fmaxf(m, __shfl_xor(m, 16, WAVE));
         m = fmaxf(m, __shfl_xor(m, 32, WAVE));
-        /* the column's rescale of what came before (0 when nothing did) */
         const float f = m == -INFINITY || m_run == -INFINITY ? 0.0f : __expf(m_run - m);
         float l = 0.0f;
 #pragma unroll
@@ -649,7 +703,6 @@ __global__ __launch_bounds__(256, 2) void attention_flash_kernel(attn_args a) {
         l += __shfl_xor(l, 32, WAVE);
         l_run = fmaf(l_run, f, l);
         m_run = m;
-        /* O's rows are the columns 4 kq + i: their rescales from the lanes that hold those columns */
         float fo[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) fo[i] = __shfl(f, 4 * kq + i, WAVE);
@@ -658,26 +711,33 @@ __global__ __launch_bounds__(256, 2) void attention_flash_kernel(attn_args a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) O[j][i] *= fo[i];
 #pragma unroll
-        for (int pt = 0; pt < 4; pt++)
+        for (int s = 0; s < 2; s++) {
+            uint2 ph0, pl0, ph1, pl1;
+            fl_split4(S[2 * s][0], S[2 * s][1], S[2 * s][2], S[2 * s][3], ph0, pl0);
+            fl_split4(S[2 * s + 1][0], S[2 * s + 1][1], S[2 * s + 1][2], S[2 * s + 1][3], ph1, pl1);
+            const fl_bf8 ph = fl_join(ph0, ph1), pl = fl_join(pl0, pl1);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = 16 * pt + 4 * kq + i;
-                const float4 v0 = reinterpret_cast<const float4*>(sv)[p * RUN_CHUNKS + (c16 ^ (p & 31))];
-                const float4 v1 = reinterpret_cast<const float4*>(sv)[p * RUN_CHUNKS + ((16 + c16) ^ (p & 31))];
-                const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-                for (int j = 0; j < 8; j++) O[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(S[pt][i], vv[j], O[j], 0, 0, 0);
+            for (int j = 0; j < 8; j++) {
+                const int dim = 16 * j + c16;
+                const int va0 = (dim * 16 + ((8 * s + kq) ^ (dim & 15))) * 2;
+                const int va1 = (dim * 16 + ((8 * s + 4 + kq) ^ (dim & 15))) * 2;
+                const fl_bf8 vh = fl_join(*reinterpret_cast<const uint2*>(&svh[va0]), *reinterpret_cast<const uint2*>(&svh[va1]));
+                const fl_bf8 vl = fl_join(*reinterpret_cast<const uint2*>(&svl[va0]), *reinterpret_cast<const uint2*>(&svl[va1]));
+                O[j] = FL_MMA(ph, vh, O[j]);
+                O[j] = FL_MMA(ph, vl, O[j]);
+                O[j] = FL_MMA(pl, vh, O[j]);
             }
+        }
     }
-    /* att = O / sum, column 4 kq + i of the lane's O at dimensions VDIM(j, c16) */
+    /* att = O / sum: column 4 kq + i of the lane's O, dimension 16 j + c16 */
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int cc = 4 * kq + i, rw = r_first + wave * RW + cc / G, gc = cc % G;
-        const float lsum = __shfl(l_run, cc, WAVE);
+        const int ccol = 4 * kq + i, rw = r_first + wave * RW + ccol / G, gc = ccol % G;
+        const float lsum = __shfl(l_run, ccol, WAVE);
         if (rw < r_end) {
             float* out = a.att + (size_t)rw * a.n_heads * HD + (size_t)(h * G + gc) * HD;
 #pragma unroll
-            for (int j = 0; j < 8; j++) out[VDIM(j, c16)] = O[j][i] / lsum;
+            for (int j = 0; j < 8; j++) out[16 * j + c16] = O[j][i] / lsum;
         }
     }
 }
