@@ -41,6 +41,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define SK_TOK 32
 #define SK_NT 2 /* token tiles a block of the exact kernel takes when a pass has many */
+#ifndef SK_NR
+#define SK_NR 2
+#endif
 
 /* ---- activations, split ------------------------------------------------- */
 
@@ -583,33 +586,44 @@ __device__ __forceinline__ void sx_compute(const sx_w<DT>& w, const sx_a& x, int
     }
 }
 
-/* Superblock b of the lane's weight row against NT token tiles tt0, tt0 + 1, ... (those below mt): every weight
-   load issued first, then each tile's activations two units ahead; the weights stay in registers across the
-   tiles, and each tile's sums run as they would for that tile alone. */
-template <int DT, int NT>
-__device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& w, int tile, int tt0, int mt, int b, int lane,
-                                              f32x16 (&acc)[NT]) {
+/* Superblock b of the lane's weight rows of NR consecutive 32-row tiles (those of them below nr) against NT
+   token tiles tt0, tt0 + 1, ... (those below mt): every weight load issued first, then each token tile's
+   activations two units ahead, each unit's activations used for all NR weight tiles; the weights stay in
+   registers across the token tiles, and each (weight tile, token tile)'s sums run as they would alone. */
+template <int DT, int NT, int NR>
+__device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& w, int tile, int nr, int tt0, int mt, int b,
+                                              int lane, f32x16 (&acc)[NR][NT]) {
     const int kq = lane >> 5;
     const int K = w.cols;
-    sx_w<DT> W;
-    sx_load_w<DT>(w, tile, b, lane, W);
+    sx_w<DT> W[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++)
+        if (r < nr) sx_load_w<DT>(w, tile + r, b, lane, W[r]);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const int tt = tt0 + t;
         if (tt >= mt) break;
-        float cs[8];
+        float cs[NR][8];
         sx_a x0, x1;
         sx_load_a<DT, 0>(a, tt, K, b, lane, x0);
         sx_load_a<DT, 1>(a, tt, K, b, lane, x1);
         __builtin_amdgcn_sched_barrier(0);
-        sx_compute<DT, 0>(W, x0, kq, acc[t], cs);
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+            if (r < nr) sx_compute<DT, 0>(W[r], x0, kq, acc[r][t], cs[r]);
         sx_load_a<DT, 2>(a, tt, K, b, lane, x0);
         __builtin_amdgcn_sched_barrier(0);
-        sx_compute<DT, 1>(W, x1, kq, acc[t], cs);
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+            if (r < nr) sx_compute<DT, 1>(W[r], x1, kq, acc[r][t], cs[r]);
         sx_load_a<DT, 3>(a, tt, K, b, lane, x1);
         __builtin_amdgcn_sched_barrier(0);
-        sx_compute<DT, 2>(W, x0, kq, acc[t], cs);
-        sx_compute<DT, 3>(W, x1, kq, acc[t], cs);
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+            if (r < nr) sx_compute<DT, 2>(W[r], x0, kq, acc[r][t], cs[r]);
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+            if (r < nr) sx_compute<DT, 3>(W[r], x1, kq, acc[r][t], cs[r]);
     }
 }
 
@@ -620,7 +634,7 @@ __device__ __forceinline__ void sx_superblock(const skinny_args& a, const qmat& 
  * counter in cnt[]) adds the splits' sums in split order, writes the result and clears the counter, so the
  * result does not depend on which block finishes last.
  */
-template <int NT>
+template <int NT, int NR>
 __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     extern __shared__ float red[]; /* [KS][16][64] */
     __shared__ int last;
@@ -628,81 +642,90 @@ __global__ __launch_bounds__(512) void skinny_exact_kernel(skinny_args a) {
     const int l32 = lane & 31, kq = lane >> 5;
     int bx = blockIdx.x, mi = 0, tile0 = 0;
     for (; mi < a.nm - 1; mi++) {
-        const int nb = (a.w[mi].rows + 31) / 32 * a.splits[mi];
+        const int nb = ((a.w[mi].rows + 31) / 32 + NR - 1) / NR * a.splits[mi];
         if (bx < nb) break;
         bx -= nb;
         tile0 += (a.w[mi].rows + 31) / 32;
     }
     const qmat& w = a.w[mi];
-    const int splits = a.splits[mi], sp = bx % splits, tile = bx / splits;
-    const int row0 = 32 * tile, mt = (a.n + SK_TOK - 1) / SK_TOK, tt0 = blockIdx.y * NT;
+    const int splits = a.splits[mi], sp = bx % splits, tile = bx / splits * NR;
+    const int nr = min(NR, (w.rows + 31) / 32 - tile); /* this block's weight tiles */
+    const int mt = (a.n + SK_TOK - 1) / SK_TOK, tt0 = blockIdx.y * NT;
     const int b = 8 * sp + wv;
-    f32x16 acc[NT];
+    f32x16 acc[NR][NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) acc[t] = f32x16{};
+    for (int r = 0; r < NR; r++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[r][t] = f32x16{};
     if (b < w.cols / 256) {
-        if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K, NT>(a, w, tile, tt0, mt, b, lane, acc);
-        else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K, NT>(a, w, tile, tt0, mt, b, lane, acc);
-        else sx_superblock<VITNA_DTYPE_Q8_0, NT>(a, w, tile, tt0, mt, b, lane, acc);
+        if (w.dtype == VITNA_DTYPE_Q4_K) sx_superblock<VITNA_DTYPE_Q4_K, NT, NR>(a, w, tile, nr, tt0, mt, b, lane, acc);
+        else if (w.dtype == VITNA_DTYPE_Q6_K) sx_superblock<VITNA_DTYPE_Q6_K, NT, NR>(a, w, tile, nr, tt0, mt, b, lane, acc);
+        /* (two Q8_0 weight tiles a block do not fit the registers: the launch keeps Q8_0 to one) */
+        else if constexpr (NR == 1) sx_superblock<VITNA_DTYPE_Q8_0, NT, NR>(a, w, tile, nr, tt0, mt, b, lane, acc);
     }
 
     float* y = a.y[mi];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int tt = tt0 + t;
-        if (tt >= mt) break;
-        /* accumulator r of a lane: token 8 (r / 4) + 4 (lane / 32) + r % 4 of the tile, weight row lane % 32 */
-        const int tok0 = tt * SK_TOK;
-        auto put = [&](int r, float v) {
-            const int n = row0 + l32;
-            const int tk = tok0 + 8 * (r >> 2) + 4 * kq + (r & 3);
-            if (n < w.rows && tk < a.n) {
-                float* o = y + (size_t)tk * w.rows + n;
-                *o = a.add ? *o + v : v;
+    for (int wr = 0; wr < NR; wr++) {
+        if (wr >= nr) break;
+        const int row0 = 32 * (tile + wr);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int tt = tt0 + t;
+            if (tt >= mt) break;
+            /* accumulator r of a lane: token 8 (r / 4) + 4 (lane / 32) + r % 4 of the tile, weight row lane % 32 */
+            const int tok0 = tt * SK_TOK;
+            auto put = [&](int r, float v) {
+                const int n = row0 + l32;
+                const int tk = tok0 + 8 * (r >> 2) + 4 * kq + (r & 3);
+                if (n < w.rows && tk < a.n) {
+                    float* o = y + (size_t)tk * w.rows + n;
+                    *o = a.add ? *o + v : v;
+                }
+            };
+            if (KS > 1) {
+                if (t || wr) __syncthreads(); /* the previous tile's sums are read */
+#pragma unroll
+                for (int r = 0; r < 16; r++) red[(wv * 16 + r) * 64 + lane] = acc[wr][t][r];
+                __syncthreads();
             }
-        };
-        if (KS > 1) {
-            if (t) __syncthreads(); /* the previous tile's sums are read */
+            if (splits == 1) {
+                if (KS == 1) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) red[(wv * 16 + r) * 64 + lane] = acc[t][r];
-            __syncthreads();
-        }
-        if (splits == 1) {
-            if (KS == 1) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) put(r, acc[t][r]);
+                    for (int r = 0; r < 16; r++) put(r, acc[wr][t][r]);
+                    continue;
+                }
+                for (int r = wv; r < 16; r += KS) {
+                    float v = 0.0f;
+                    for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
+                    put(r, v);
+                }
                 continue;
             }
+            /* several splits: this block's sum of the tile into part[], then the last block of the tile adds them */
+            const size_t slot = (size_t)tt * a.tiles + tile0 + tile + wr; /* the tile's counter */
+            float* part = a.part + slot * a.split_max * 1024;
+            /* The sums are stored as agent-scope atomics (written through this XCD's L2 to where every XCD reads);
+               the counter's increment releases them and the last block's acquires them, at agent scope, so the last
+               block reads every split's sums (the workgroup barrier carries thread 0's acquire to the others). */
             for (int r = wv; r < 16; r += KS) {
                 float v = 0.0f;
                 for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
-                put(r, v);
+                __hip_atomic_store(part + (size_t)sp * 1024 + r * 64 + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            continue;
-        }
-        /* several splits: this block's sum of the tile into part[], then the last block of the tile adds them */
-        const size_t slot = (size_t)tt * a.tiles + tile0 + tile; /* the tile's counter */
-        float* part = a.part + slot * a.split_max * 1024;
-        /* The sums are stored as agent-scope atomics (written through this XCD's L2 to where every XCD reads);
-           the counter's increment releases them and the last block's acquires them, at agent scope, so the last
-           block reads every split's sums (the workgroup barrier carries thread 0's acquire to the others). */
-        for (int r = wv; r < 16; r += KS) {
-            float v = 0.0f;
-            for (int u = 0; u < KS; u++) v += red[(u * 16 + r) * 64 + lane];
-            __hip_atomic_store(part + (size_t)sp * 1024 + r * 64 + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* every wave's stores complete before the barrier */
-        __syncthreads();
-        if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + slot, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
-        __syncthreads();
-        if (last) {
-            for (int r = wv; r < 16; r += KS) {
-                float v = 0.0f;
-                for (int u = 0; u < splits; u++)
-                    v += __hip_atomic_load(part + (size_t)u * 1024 + r * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                put(r, v);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* every wave's stores complete before the barrier */
+            __syncthreads();
+            if (threadIdx.x == 0) last = __hip_atomic_fetch_add(a.cnt + slot, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == splits - 1;
+            __syncthreads();
+            if (last) {
+                for (int r = wv; r < 16; r += KS) {
+                    float v = 0.0f;
+                    for (int u = 0; u < splits; u++)
+                        v += __hip_atomic_load(part + (size_t)u * 1024 + r * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    put(r, v);
+                }
+                if (threadIdx.x == 0) __hip_atomic_store(a.cnt + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (threadIdx.x == 0) __hip_atomic_store(a.cnt + slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -842,10 +865,22 @@ static hipError_t launch_skinny_exact(const skinny_args& a0, hipStream_t s) {
     }
     if (split_max > 1 && (!a.part || !a.cnt || (size_t)mt * tiles > a.cnt_cap || (size_t)mt * tiles * split_max * 1024 > a.part_cap))
         return hipErrorInvalidValue;
-    /* many token tiles (a prompt's chunk): each block takes SK_NT of them, the weights loaded once for all */
+    /* many token tiles (a prompt's chunk): each block takes SK_NT of them, the weights loaded once for all, or
+       two weight tiles against the same token tile, each unit's activations loaded once for both */
     const size_t lds = (size_t)ks * 16 * 64 * sizeof(float);
-    if (mt >= 2 * SK_NT) skinny_exact_kernel<SK_NT><<<dim3(blocks, (mt + SK_NT - 1) / SK_NT), 64 * ks, lds, s>>>(a);
-    else skinny_exact_kernel<1><<<dim3(blocks, mt), 64 * ks, lds, s>>>(a);
+    if (mt >= 2 * SK_NT) {
+        bool q8 = false;
+        for (int i = 0; i < a.nm; i++) q8 |= a.w[i].dtype == VITNA_DTYPE_Q8_0;
+        if (SK_NR == 2 && !q8) {
+            int b2 = 0;
+            for (int i = 0; i < a.nm; i++) b2 += ((a.w[i].rows + 31) / 32 + 1) / 2 * a.splits[i];
+            skinny_exact_kernel<1, 2><<<dim3(b2, mt), 64 * ks, lds, s>>>(a);
+        } else {
+            skinny_exact_kernel<SK_NT, 1><<<dim3(blocks, (mt + SK_NT - 1) / SK_NT), 64 * ks, lds, s>>>(a);
+        }
+    } else {
+        skinny_exact_kernel<1, 1><<<dim3(blocks, mt), 64 * ks, lds, s>>>(a);
+    }
     return hipGetLastError();
 }
 
@@ -1060,8 +1095,9 @@ __global__ __launch_bounds__(512) void gsx_in_kernel(qmat gate, qmat up, skinny_
 }
 
 /* ypart[(row K + slot) H + n] = w_slot (down_e[n] . act[pair]) for the pairs of virtual tile t (past the expert's
-   count: none written) and 32-row tile x of the H rows: KS = I / 256 waves, wave wv on superblock wv. */
-template <int DT>
+   count: none written) and NR 32-row tiles from NR x of the H rows (each unit's activations loaded once for
+   them): KS = I / 256 waves, wave wv on superblock wv. */
+template <int DT, int NR>
 __global__ __launch_bounds__(512) void gsx_down_kernel(qmat down, skinny_args sa, const int* __restrict__ te,
                                                        const int* __restrict__ toff, const int* __restrict__ count,
                                                        const int* __restrict__ pairs, int cap, const route_out* __restrict__ rt,
@@ -1070,24 +1106,28 @@ __global__ __launch_bounds__(512) void gsx_down_kernel(qmat down, skinny_args sa
     const int t = blockIdx.y, e = te[t];
     if (e < 0) return;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, KS = blockDim.x >> 6, kq = lane >> 5, l32 = lane & 31;
-    const int H = down.rows, I = down.cols, x = blockIdx.x;
-    f32x16 acc[1] = {f32x16{}};
-    sx_superblock<DT, 1>(sa, down, e * (H / 32) + x, t, t + 1, wv, lane, acc);
-    float v[16];
-    gsx_reduce(acc[0], red, KS, wv, lane, v);
+    const int H = down.rows, x0 = NR * blockIdx.x;
+    f32x16 acc[NR][1];
+#pragma unroll
+    for (int r = 0; r < NR; r++) acc[r][0] = f32x16{};
+    sx_superblock<DT, 1, NR>(sa, down, e * (H / 32) + x0, NR, t, t + 1, wv, lane, acc);
     const int j0 = 32 * (t - toff[e]), c = count[e];
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int r = wv + i * KS;
-        if (r < 16) {
-            const int j = j0 + 8 * (r >> 2) + 4 * kq + (r & 3);
-            if (j < c) {
-                const int p = pairs[(size_t)e * cap + j], row = p / ROUTE_K_MAX, slot = p % ROUTE_K_MAX;
-                ypart[((size_t)row * K + slot) * H + 32 * x + l32] = rt[row].weights[slot] * v[i];
+    for (int wr = 0; wr < NR; wr++) {
+        float v[16];
+        gsx_reduce(acc[wr][0], red, KS, wv, lane, v);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = wv + i * KS;
+            if (r < 16) {
+                const int j = j0 + 8 * (r >> 2) + 4 * kq + (r & 3);
+                if (j < c) {
+                    const int p = pairs[(size_t)e * cap + j], row = p / ROUTE_K_MAX, slot = p % ROUTE_K_MAX;
+                    ypart[((size_t)row * K + slot) * H + 32 * (x0 + wr) + l32] = rt[row].weights[slot] * v[i];
+                }
             }
         }
     }
-    (void)I;
 }
 
 hipError_t launch_gsx(const gsx_args& a, hipStream_t s) {
@@ -1118,15 +1158,17 @@ hipError_t launch_gsx(const gsx_args& a, hipStream_t s) {
     sd.img[0] = sd.img[1] = a.img_act;
     sd.s32 = reinterpret_cast<const uint32_t*>(a.s32);
     sd.s16 = reinterpret_cast<const uint32_t*>(a.s16);
+    /* two 32-row tiles a block for K-quant down weights (Q8_0's two do not fit the registers) */
+    const dim3 gd2(H / 64, T);
     switch (a.down.dtype) {
     case VITNA_DTYPE_Q4_K:
-        gsx_down_kernel<VITNA_DTYPE_Q4_K><<<gd, 64 * ksd, ksd * 4096, s>>>(a.down, sd, a.te, a.toff, a.count, a.pairs, a.cap, a.rt, a.K, a.ypart);
+        gsx_down_kernel<VITNA_DTYPE_Q4_K, 2><<<gd2, 64 * ksd, ksd * 4096, s>>>(a.down, sd, a.te, a.toff, a.count, a.pairs, a.cap, a.rt, a.K, a.ypart);
         break;
     case VITNA_DTYPE_Q6_K:
-        gsx_down_kernel<VITNA_DTYPE_Q6_K><<<gd, 64 * ksd, ksd * 4096, s>>>(a.down, sd, a.te, a.toff, a.count, a.pairs, a.cap, a.rt, a.K, a.ypart);
+        gsx_down_kernel<VITNA_DTYPE_Q6_K, 2><<<gd2, 64 * ksd, ksd * 4096, s>>>(a.down, sd, a.te, a.toff, a.count, a.pairs, a.cap, a.rt, a.K, a.ypart);
         break;
     default:
-        gsx_down_kernel<VITNA_DTYPE_Q8_0><<<gd, 64 * ksd, ksd * 4096, s>>>(a.down, sd, a.te, a.toff, a.count, a.pairs, a.cap, a.rt, a.K, a.ypart);
+        gsx_down_kernel<VITNA_DTYPE_Q8_0, 1><<<gd, 64 * ksd, ksd * 4096, s>>>(a.down, sd, a.te, a.toff, a.count, a.pairs, a.cap, a.rt, a.K, a.ypart);
         break;
     }
     return hipGetLastError();
