@@ -4,6 +4,7 @@
     python bench.py --only 0|1|3|4 [--steps K] one of the other configs alone (profiling)
     python bench.py --only cache [--cache-frac F] configs[2]'s decode through the expert cache
     python bench.py --only prompt                 a 4096-token prompt through configs[2]'s model
+    python bench.py --only prompt-abi             the same prompt layer by layer through the ABI (model.c's path)
 
 Workload: a full 48-layer Qwen3-30B-A3B-shaped model
 with seeded random weights (Q4_K gate/up/q/k/o, Q6_K down/v/LM head, Q4_K
@@ -71,7 +72,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-extra", action="store_true", help="measure configs[2] only")
-    ap.add_argument("--only", choices=["0", "1", "3", "4", "4k", "cache", "prompt"],
+    ap.add_argument("--only", choices=["0", "1", "3", "4", "4k", "cache", "prompt", "prompt-abi"],
                     help="run one of the other configs alone (profiling), or the expert cache's decode, and print its object")
     ap.add_argument("--cache-frac", type=float, default=0.5, help="--only cache: the share of the experts the cache holds")
     args = ap.parse_args()
@@ -91,9 +92,9 @@ def main():
             res = bench_prefill(va, reps=args.steps)
         elif args.only == "cache":
             res = bench_cache(va, args.steps, args.warmup, args.cache_frac, args.layers)
-        elif args.only == "prompt":
+        elif args.only in ("prompt", "prompt-abi"):
             model = va.Model(va.shape(n_layers=args.layers, ctx=4096, seqs=1, kv_host=0), 20260101, threads=16)
-            res = bench_prompt(va, model)
+            res = bench_prompt(va, model) if args.only == "prompt" else bench_prompt_abi(va, model)
             model.free()
         else:
             model = va.Model(va.shape(n_layers=args.layers, ctx=8193, seqs=32, kv_host=0), 20260101, threads=16)
@@ -351,6 +352,50 @@ def bench_prompt(va, model, tokens=4096, chunk=1024):
             dev.close()
         out[name] = {"value": round(tokens / sec, 1), "unit": "tok/s", "ms": round(sec * 1e3, 1)}
         log("prompt of %d tokens, %s: %.1f ms, %.0f tok/s" % (tokens, name, sec * 1e3, tokens / sec))
+    return out
+
+
+def bench_prompt_abi(va, model, tokens=4096, chunk=1024):
+    """The same prompt as bench_prompt, fed as model.c feeds it: layer by layer through the ABI
+    (vitna_cuda_moe_rows_route, then the host's routing of every row, then vitna_cuda_moe_rows_experts;
+    vitna_cuda_moe_rows_head for the last position), engine/src/model.c:1006-1030 and moe_rows_on_gpu
+    :1052-1190. The host routing here is a vectorized top-k of the device's logits (largest first, ties to the
+    lower index) with the softmax over the chosen (Qwen3 renormalizes), so the time is the device's and the ABI's,
+    not a Python loop's. No graph is replayed, so this is the form the prompt is profiled in."""
+    cfg = model.cfg
+    K, L = cfg.n_experts_used, cfg.n_layers
+    out = {"workload": "a %d-token prompt through BASELINE configs[2]'s model, passes of %d rows, layer by layer "
+                       "through the ABI with host routing" % (tokens, chunk)}
+    for name, fast in (("exact", False), ("fast", True)):
+        saved = (model.m.ctx, model.m.seqs)
+        model.m.ctx, model.m.seqs = tokens, 1
+        try:
+            dev = va.Device(model, fast=fast)
+        finally:
+            model.m.ctx, model.m.seqs = saved
+        try:
+            def prompt():
+                for c in range(tokens // chunk):
+                    rows = [((7 * (c * chunk + i) + 3) % cfg.vocab, c * chunk + i, 0) for i in range(chunk)]
+                    for l in range(L):
+                        lg = dev.rows_route(rows, l)
+                        ids = np.argsort(-lg, axis=1, kind="stable")[:, :K].astype(np.int32)
+                        top = np.take_along_axis(lg, ids, axis=1).astype(np.float64)
+                        w = np.exp(top - top[:, :1])
+                        w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+                        order = np.argsort(ids, axis=1)
+                        dev.rows_experts(l, np.take_along_axis(ids, order, axis=1), np.take_along_axis(w, order, axis=1))
+                    if c == tokens // chunk - 1:
+                        dev.rows_head(chunk, only=[chunk - 1])
+                dev.sync()
+            prompt()
+            t = time.perf_counter()
+            prompt()
+            sec = time.perf_counter() - t
+        finally:
+            dev.close()
+        out[name] = {"value": round(tokens / sec, 1), "unit": "tok/s", "ms": round(sec * 1e3, 1)}
+        log("prompt of %d tokens through the ABI, %s: %.1f ms, %.0f tok/s" % (tokens, name, sec * 1e3, tokens / sec))
     return out
 
 

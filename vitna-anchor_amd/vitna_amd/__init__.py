@@ -501,10 +501,12 @@ class Device:
         self._ok(self.lib.vitna_cuda_moe_rows_experts(self.g, layer, n, _i32(ids), fptr(w), k,
                                                       _i32(g) if g is not None else None, self.err, 512))
 
-    def rows_head(self, n):
+    def rows_head(self, n, only=None):
+        """logits of every row, or (only) of the rows it lists: the others' pointers NULL, their rows unset."""
         V = self.model.cfg.vocab
         out = np.empty((n, V), np.float32)
-        ptrs = (_FP * n)(*[out[i].ctypes.data_as(_FP) for i in range(n)])
+        want = set(range(n)) if only is None else set(only)
+        ptrs = (_FP * n)(*[out[i].ctypes.data_as(_FP) if i in want else None for i in range(n)])
         self._ok(self.lib.vitna_cuda_moe_rows_head(self.g, n, ptrs, self.err, 512))
         return out
 
