@@ -861,6 +861,13 @@ double mfma_probe_flops(int blocks, int iters) { return (double)blocks * 4 * ite
 
 /* ---- launches ----------------------------------------------------------- */
 
+/* Experts a 16-lane group of the routers. At 128 experts the plain router's groups of 8 left one block column:
+   1024 rows were 128 blocks (a prompt of 4096 tokens 210.6 -> 208.4 ms exact with 2). The fused kernel
+   normalizes its rows in every block of a row tile, so it keeps 8 (config 4: 73 us, against 101 with 4 and 155
+   with 2). Each (row, expert) chain runs the same either way: the same bits. */
+#define PR_RE 2
+#define NR_RE 8
+
 hipError_t launch_prefill_norm(const float* x, const float* w, float* xn, uint16_t* xb, int n, int H, float eps, hipStream_t s) {
     if (n < 1 || H % 16 || H > 8192) return hipErrorInvalidValue;
     prefill_norm_kernel<<<n, 64, H * 4, s>>>(x, w, xn, xb, H, eps);
@@ -869,7 +876,7 @@ hipError_t launch_prefill_norm(const float* x, const float* w, float* xn, uint16
 
 hipError_t launch_prefill_router(const float* xn, const float* R, float* logits, int n, int E, int H, hipStream_t s) {
     if (n < 1 || E < 1 || H % 16) return hipErrorInvalidValue;
-    constexpr int RT = 8, RE = 8;
+    constexpr int RT = 8, RE = PR_RE;
     prefill_router_kernel<RT, RE><<<dim3((E + 16 * RE - 1) / (16 * RE), (n + RT - 1) / RT), 256, 0, s>>>(xn, R, logits, n, E, H);
     return hipGetLastError();
 }
@@ -878,7 +885,7 @@ hipError_t launch_prefill_norm_router(const float* x, const float* nw, const flo
                                      int H, float eps, hipStream_t s) {
     if (n < 1 || E < 1 || H % 16) return hipErrorInvalidValue;
     if (H > NR_HMAX) return hipErrorNotSupported; /* the two-kernel form */
-    constexpr int RT = 8, RE = 8;
+    constexpr int RT = 8, RE = NR_RE;
     prefill_norm_router_kernel<RT, RE><<<dim3((E + 16 * RE - 1) / (16 * RE), (n + RT - 1) / RT), 256, 0, s>>>(x, nw, R, logits, xb, n, E, H, eps);
     return hipGetLastError();
 }
