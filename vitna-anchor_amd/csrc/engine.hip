@@ -404,30 +404,43 @@ static bool ensure_tiled(vitna_cuda_model* g, char* err, size_t err_len) {
                 sets[i]->tiled = t;
             }
         }
-        if (!g->ec.on && g->E <= ROUTE_E_MAX && gsx_fits(d.gate, d.up, d.down)) {
-            const qmat* sets[3] = {&d.gate, &d.up, &d.down};
-            const uint8_t** dst[3] = {&d.sx_gate, &d.sx_up, &d.sx_down};
-            for (int i = 0; i < 3; i++) {
-                uint8_t* t;
-                if (!dalloc(g, &t, gsx_tiled_bytes(*sets[i], g->E), "the experts' copy for crowded passes", err, err_len)) return false;
-                HIP_TRY(launch_gsx_tile(*sets[i], g->E, t, g->stream), "tiling the experts");
-                HIP_TRY(hipStreamSynchronize(g->stream), "tiling the experts");
-                *dst[i] = t;
-            }
-            if (!g->gsx_te) {
-                const size_t T = (size_t)gsx_max_tiles(ROWS_MAX, g->K, g->E), H = g->H, I = d.gate.rows, W = std::max(H, I);
-                if (!(dalloc(g, &g->gsx_toff, (g->E + 1) * sizeof(int), "scratch", err, err_len) &&
-                      dalloc(g, &g->gsx_te, T * sizeof(int), "scratch", err, err_len) &&
-                      dalloc(g, &g->gsx_img_in, 32 * T * H * 4, "scratch", err, err_len) &&
-                      dalloc(g, &g->gsx_img_act, 32 * T * I * 4, "scratch", err, err_len) &&
-                      dalloc(g, &g->gsx_s32, T * (W / 256) * 1536, "scratch", err, err_len) &&
-                      dalloc(g, &g->gsx_s16, T * (W / 128) * 1536, "scratch", err, err_len) &&
-                      dalloc(g, &g->gsx_act, 32 * T * I * 4, "scratch", err, err_len)))
-                    return false;
+    }
+    if (g->attention && !make_tiled(g, &g->head, "the output projection", err, err_len)) return false;
+    /* the crowded passes' copy of the experts and its buffers, when the device has room for them all (1 GB to
+       spare): without it those passes keep the four-pair kernels */
+    if (!g->ec.on && g->E <= ROUTE_E_MAX && gsx_fits(g->L[0].gate, g->L[0].up, g->L[0].down)) {
+        const size_t T = (size_t)gsx_max_tiles(ROWS_MAX, g->K, g->E), H = g->H, I = g->L[0].gate.rows, W = std::max(H, I);
+        size_t need = (g->E + 1 + T) * sizeof(int) + 32 * T * (H + 2 * I) * 4 + T * (W / 256) * 1536 * 3;
+        for (int l = 0; l < g->NL; l++) {
+            const dlayer& d = g->L[l];
+            if (gsx_fits(d.gate, d.up, d.down))
+                need += gsx_tiled_bytes(d.gate, g->E) + gsx_tiled_bytes(d.up, g->E) + gsx_tiled_bytes(d.down, g->E);
+        }
+        size_t fr = 0, tot = 0;
+        if (hipMemGetInfo(&fr, &tot) == hipSuccess && need + ((size_t)1 << 30) <= fr) {
+            if (!(dalloc(g, &g->gsx_toff, (g->E + 1) * sizeof(int), "scratch", err, err_len) &&
+                  dalloc(g, &g->gsx_te, T * sizeof(int), "scratch", err, err_len) &&
+                  dalloc(g, &g->gsx_img_in, 32 * T * H * 4, "scratch", err, err_len) &&
+                  dalloc(g, &g->gsx_img_act, 32 * T * I * 4, "scratch", err, err_len) &&
+                  dalloc(g, &g->gsx_s32, T * (W / 256) * 1536, "scratch", err, err_len) &&
+                  dalloc(g, &g->gsx_s16, T * (W / 128) * 1536, "scratch", err, err_len) &&
+                  dalloc(g, &g->gsx_act, 32 * T * I * 4, "scratch", err, err_len)))
+                return false;
+            for (int l = 0; l < g->NL; l++) {
+                dlayer& d = g->L[l];
+                if (!gsx_fits(d.gate, d.up, d.down)) continue;
+                const qmat* sets[3] = {&d.gate, &d.up, &d.down};
+                const uint8_t** dst[3] = {&d.sx_gate, &d.sx_up, &d.sx_down};
+                for (int i = 0; i < 3; i++) {
+                    uint8_t* t;
+                    if (!dalloc(g, &t, gsx_tiled_bytes(*sets[i], g->E), "the experts' copy for crowded passes", err, err_len)) return false;
+                    HIP_TRY(launch_gsx_tile(*sets[i], g->E, t, g->stream), "tiling the experts");
+                    HIP_TRY(hipStreamSynchronize(g->stream), "tiling the experts");
+                    *dst[i] = t;
+                }
             }
         }
     }
-    if (g->attention && !make_tiled(g, &g->head, "the output projection", err, err_len)) return false;
     g->tiled_ready = true;
     return true;
 }
