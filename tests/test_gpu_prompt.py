@@ -120,3 +120,28 @@ def test_prompt_against_per_row_kernel():
         a.close()
         b.close()
         model.free()
+
+
+def test_prompt_head_rows():
+    """A pass of more rows than the exact limit that asks one row's logits (a prompt's last chunk, model.c:1011)
+    runs the head on that row alone, and one that asks none runs no head: the asked row's logits within 1e-5 of
+    max |logits| of the all-rows head (another kernel), and after a pass with no logits and one with one row, the
+    all-rows pass gives its first bits again (each head form its own captured graph)."""
+    say("prompt head rows")
+    model = va.Model(va.shape(**SPECS["g8"]), 2468)
+    dev = va.Device(model)
+    try:
+        cfg = model.cfg
+        n = 200
+        rows = [((17 * i + 1) % cfg.vocab, i, 0) for i in range(n)]
+        full = np.stack(dev.rows_step(rows))
+        dev.rows_step(rows, logits=False)
+        one = dev.rows_step(rows, only=[n - 1])[n - 1]
+        r = float(np.max(np.abs(one - full[n - 1])) / np.max(np.abs(full[n - 1])))
+        say("  one row's head against the all-rows head: rel diff", r)
+        assert r <= 1e-5
+        again = np.stack(dev.rows_step(rows))
+        assert np.array_equal(again.view(np.uint32), full.view(np.uint32))
+    finally:
+        dev.close()
+        model.free()

@@ -125,6 +125,7 @@ struct vitna_cuda_model {
         int n;                  /* rows, or 0 for an empty entry */
         bool shared, fast;      /* rows of one sequence; the experts as the grouped GEMM */
         int splits;             /* the attention's grid */
+        int head;               /* the head's rows: HEAD_ALL, HEAD_NONE or the one row */
         uint64_t used;
     } rg[ROWS_GRAPHS];
     uint64_t rg_clock;
@@ -2191,15 +2192,35 @@ static hipError_t enqueue_rows_experts(vitna_cuda_model* g, int layer, int n, bo
     return e;
 }
 
-static hipError_t enqueue_rows_head(vitna_cuda_model* g, int n, const float* ypart) {
+/* The head's rows: every row's, none (the final norm only, so the residual rows hold the pass's sums), or the one
+   row a prompt's last chunk asks for (model.c:1011), the head then a single row's GEMM. */
+#define HEAD_ALL (-1)
+#define HEAD_NONE (-2)
+
+static hipError_t enqueue_rows_head(vitna_cuda_model* g, int n, const float* ypart, int head = HEAD_ALL) {
     gemv_multi_args gh;
     memset(&gh, 0, sizeof(gh));
     gh.w[0] = g->head; gh.y[0] = g->vocab; gh.nm = 1; gh.x = g->xn; gh.n = n; gh.xstride = g->H;
-    const bool img = multi_exact(gh);
+    if (head >= 0) {
+        gh.x = g->xn + (size_t)head * g->H;
+        gh.y[0] = g->vocab + (size_t)head * g->V;
+        gh.n = 1;
+    }
+    const bool img = head == HEAD_ALL && multi_exact(gh);
     hipError_t e = launch_residual_norm(g->x, ypart, g->K, g->final_norm, g->xn, n, g->H, g->eps,
                                         img ? model_img(g) : img_out{nullptr, nullptr, nullptr, nullptr}, g->stream);
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || head == HEAD_NONE) return e;
     return enqueue_multi(g, gh, img);
+}
+
+/* The head's rows a call's logits pointers ask for: none, the one (passes past the exact-rows limit, whose logits
+   are not a step's bits anyway), or every row. */
+static int head_rows(const vitna_cuda_model* g, size_t n, float* const* logits) {
+    int asked = 0, last = -1;
+    for (size_t i = 0; logits && i < n; i++)
+        if (logits[i]) { asked++; last = (int)i; }
+    if (!asked) return HEAD_NONE;
+    return asked == 1 && n > (size_t)EXACT_ROWS ? last : HEAD_ALL;
 }
 
 /* ---- passes of few rows, each row with a single token's kernels (EXACT_ROWS) ---- */
@@ -2530,10 +2551,9 @@ extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, f
     if (!g->attention) return fail(err, err_len, "this model has no output projection");
     if (n != (size_t)g->rows_n) return fail(err, err_len, "%zu rows; the pass has %d", n, g->rows_n);
     /* a prompt's chunks before its last ask no logits (model.c:1011): then the head has nothing to do */
-    bool any = false;
-    for (size_t i = 0; logits && i < n; i++) any |= logits[i] != nullptr;
-    if (!any) return true;
-    if (!check_launch(g, g->pass_exact ? enqueue_exact_head(g, (int)n) : enqueue_rows_head(g, (int)n, nullptr), "the head", err, err_len))
+    const int head = head_rows(g, n, logits);
+    if (head == HEAD_NONE) return true;
+    if (!check_launch(g, g->pass_exact ? enqueue_exact_head(g, (int)n) : enqueue_rows_head(g, (int)n, nullptr, head), "the head", err, err_len))
         return false;
     for (size_t i = 0; i < n; i++)
         if (logits && logits[i])
@@ -2543,7 +2563,7 @@ extern "C" bool vitna_cuda_moe_rows_head(struct vitna_cuda_model* g, size_t n, f
 }
 
 /* A whole decode step of n rows on the device, routing included. */
-static hipError_t enqueue_rows_step_body(vitna_cuda_model* g, int n) {
+static hipError_t enqueue_rows_step_body(vitna_cuda_model* g, int n, int head) {
     hipError_t e = launch_embed_rows(g->embed, g->rows_dev, n, g->x, g->stream);
     const bool fast = rows_fast(g, n);
     /* each layer's experts' outputs are added onto the rows by the next layer's (or the head's) norm kernel; a fast
@@ -2569,11 +2589,11 @@ static hipError_t enqueue_rows_step_body(vitna_cuda_model* g, int n) {
         if (e == hipSuccess) e = enqueue_rows_experts(g, l, n, true, fused_split, rt);
         pending = g->ypart;
     }
-    if (e == hipSuccess) e = enqueue_rows_head(g, n, pending);
+    if (e == hipSuccess) e = enqueue_rows_head(g, n, pending, head);
     return e;
 }
 
-static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_len) {
+static bool ensure_rows_graph(vitna_cuda_model* g, int n, int head, char* err, size_t err_len) {
     if (!ensure_tiled(g, err, err_len)) return false;
     /* a fast pass's working buffers exist before the capture (growing them later would free what the graph uses) */
     if (rows_fast(g, n) && !prefill_reserve(g, (size_t)n, err, err_len)) return false;
@@ -2581,7 +2601,7 @@ static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_
     int pick = 0;
     for (int i = 0; i < ROWS_GRAPHS; i++) {
         const auto& r = g->rg[i];
-        if (r.n == n && r.shared == g->rows_shared_seq && r.fast == fast && r.splits == g->splits_grid) {
+        if (r.n == n && r.shared == g->rows_shared_seq && r.fast == fast && r.splits == g->splits_grid && r.head == head) {
             g->rg[i].used = ++g->rg_clock;
             g->rg_cur = i;
             return true;
@@ -2596,7 +2616,7 @@ static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_
         r.n = 0;
     }
     HIP_TRY(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal), "capturing the rows step");
-    const hipError_t e = enqueue_rows_step_body(g, n);
+    const hipError_t e = enqueue_rows_step_body(g, n, head);
     hipGraph_t graph = nullptr;
     const hipError_t e2 = hipStreamEndCapture(g->stream, &graph);
     if (e != hipSuccess) { if (graph) (void)hipGraphDestroy(graph); return check_launch(g, e, "capturing the rows step", err, err_len); }
@@ -2609,6 +2629,7 @@ static bool ensure_rows_graph(vitna_cuda_model* g, int n, char* err, size_t err_
     r.fast = fast;
     r.shared = g->rows_shared_seq;
     r.splits = g->splits_grid;
+    r.head = head;
     r.used = ++g->rg_clock;
     g->rg_cur = pick;
     return true;
@@ -2620,7 +2641,7 @@ extern "C" bool vitna_hip_moe_rows_step(struct vitna_cuda_model* g, const vitna_
     if (!g || g->lost) return fail(err, err_len, "the device model is not usable");
     if (!g->attention) return fail(err, err_len, "this model has no attention");
     if (!set_rows(g, rows, n, err, err_len)) return false;
-    if (!ensure_rows_graph(g, (int)n, err, err_len)) return false;
+    if (!ensure_rows_graph(g, (int)n, head_rows(g, n, logits), err, err_len)) return false;
     HIP_TRY(hipGraphLaunch(g->rg[g->rg_cur].exec, g->stream), "launching the rows step");
     g->last_step_mega = false;
     for (size_t i = 0; i < n; i++)
@@ -2637,7 +2658,7 @@ extern "C" bool vitna_hip_time_rows(struct vitna_cuda_model* g, const vitna_cuda
     if (!g->attention) return fail(err, err_len, "this model has no attention");
     if (steps < 1) return fail(err, err_len, "at least one step");
     if (!set_rows(g, rows, n, err, err_len)) return false;
-    if (!ensure_rows_graph(g, (int)n, err, err_len)) return false;
+    if (!ensure_rows_graph(g, (int)n, HEAD_ALL, err, err_len)) return false;
     event_pair ev;
     HIP_TRY(ev.make(), "events");
     HIP_TRY(hipGraphLaunch(g->rg[g->rg_cur].exec, g->stream), "launching the rows step"); /* warm-up */
